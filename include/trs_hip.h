@@ -1,0 +1,201 @@
+/*
+ * trs_hip.h -- C ABI of libtrs_hip.so, the MI355X (gfx950) device backend for
+ * the pytorch-rs tensor hot path: strided/broadcast pointwise ops, the
+ * pointwise fusion compiler, fp32 matmul and the backward helpers autograd
+ * needs.
+ *
+ * The reference (bobrenjc93/pytorch-rs) has no FFI or plugin boundary for
+ * this path: arithmetic is called directly from Tensor methods in
+ * src/tensor.rs, and the storage seam is the (device, dtype) match in
+ * Storage::from_owned (src/storage.rs:116-124).  Each entry point below names
+ * the reference function whose per-element work it replaces.
+ *
+ * Conventions
+ *   - Every function returns int: 0 on success, a negative TRS_E_* code on
+ *     failure; trs_last_error() then holds a thread-local message.  The codes
+ *     mirror TensorError (src/tensor_error.rs:7-108).  No C++ exception
+ *     crosses this boundary.
+ *   - Tensor operands are (base pointer, trs_layout): `base` is element 0 of
+ *     the storage and layout.offset the element offset of the view, as in the
+ *     reference Tensor struct (src/tensor.rs:212-221).  Strides are in
+ *     elements and never negative.
+ *   - The caller allocates every output (trs_alloc) and computes its layout;
+ *     the output layout of the reference's planner (elementwise_output_strides,
+ *     src/tensor.rs:4249-4312) is a host-side property.
+ *   - All work is queued in order on one HIP stream per device (trs_stream);
+ *     only trs_memcpy_d2h and trs_synchronize block the host.
+ *   - Callable from any thread; the allocator and the fusion cache are
+ *     internally locked.
+ */
+#ifndef TRS_HIP_H
+#define TRS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRS_MAX_RANK 8
+
+/* Status codes (TensorError variants, src/tensor_error.rs:7-108). */
+#define TRS_OK 0
+#define TRS_E_ALLOCATION_FAILED (-1)      /* AllocationFailed */
+#define TRS_E_INDEX_OVERFLOW (-2)         /* IndexCalculationOverflow */
+#define TRS_E_STRIDE_OVERFLOW (-3)        /* StrideCalculationOverflow */
+#define TRS_E_SHAPE_MISMATCH (-4)         /* ShapeMismatch */
+#define TRS_E_MATMUL_INNER_MISMATCH (-5)  /* MatmulInnerDimensionMismatch */
+#define TRS_E_MATMUL_REQUIRES_MATRICES (-6) /* MatmulRequiresMatrices */
+#define TRS_E_INVALID_ARGUMENT (-7)       /* bad op code, rank > 8, null pointer */
+#define TRS_E_HIP (-8)                    /* HIP runtime failure */
+#define TRS_E_FUSION (-9)                 /* fusion IR parse or hipRTC failure */
+#define TRS_E_NO_DEVICE (-10)             /* no usable gfx950 device */
+
+/* A strided view: rank <= 8, shape/stride/offset in elements (the Tensor
+ * metadata of src/tensor.rs:212-221). */
+typedef struct trs_layout {
+    int32_t rank;
+    int32_t reserved;
+    int64_t shape[TRS_MAX_RANK];
+    int64_t stride[TRS_MAX_RANK];
+    int64_t offset;
+} trs_layout;
+
+/* ---- device and memory (Storage / Device: src/storage.rs:7-18, src/device.rs:5-9) */
+
+/* Initialise HIP, select device 0 and create its stream.  Idempotent. */
+int trs_init(void);
+int trs_device_count(int *count);
+int trs_set_device(int device);
+int trs_get_device(int *device);
+/* Device name, CU count and max engine clock (kHz) of the current device. */
+int trs_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz);
+/* Storage allocation (filled_storage, src/tensor.rs:4434-4442, without the fill). */
+int trs_alloc(size_t bytes, void **ptr);
+int trs_free(void *ptr);
+/* Host <-> device copies on the device stream; d2h blocks until done. */
+int trs_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int trs_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int trs_memcpy_d2d(void *dst, const void *src, size_t bytes);
+/* Zero `bytes` with a fill kernel (no hipMemset node, so it is graph-safe). */
+int trs_memset_zero(void *dst, size_t bytes);
+int trs_synchronize(void);
+/* The hipStream_t all entry points enqueue on (for event timing). */
+int trs_stream(void **stream);
+/* Thread-local message for the last failing call on this thread. */
+const char *trs_last_error(void);
+
+/* ---- pointwise (zip_map / map_scalar / unary_map, src/tensor.rs:2535-2794) */
+
+/* Tensor-tensor ops: add/sub/mul/div (src/tensor.rs:2197-2247). */
+#define TRS_ADD 0
+#define TRS_SUB 1
+#define TRS_MUL 2
+#define TRS_DIV 3
+/* Tensor-scalar ops (src/tensor.rs:2254-2372): v+s, v-s, v*s, v/s, s-v,
+ * and s*(1/v) (scalar_div's reciprocal multiplication). */
+#define TRS_S_ADD 0
+#define TRS_S_SUB 1
+#define TRS_S_MUL 2
+#define TRS_S_DIV 3
+#define TRS_S_RSUB 4
+#define TRS_S_RDIV 5
+/* Unary ops: exp (src/tensor.rs:2398), relu (:2378, relu_value :4392-4400),
+ * neg (negate_value :4388-4390), copy (materialize_with_strides :1805-1838,
+ * used by contiguous()/clone). */
+#define TRS_EXP 0
+#define TRS_RELU 1
+#define TRS_NEG 2
+#define TRS_COPY 3
+
+/* out = op(a, b) elementwise.  `lo` is the output layout; a and b broadcast
+ * to lo's shape by right alignment (BroadcastPlan, src/tensor.rs:3601-3693).
+ * Replaces zip_map (src/tensor.rs:2535-2716) and its trailing fast paths
+ * (:3376-3543) and odometer (:3546-3599).  Bit-exact: one IEEE op each. */
+int trs_binary_f32(int op, const float *a, const trs_layout *la, const float *b,
+                   const trs_layout *lb, float *out, const trs_layout *lo);
+/* out = op(a, s) elementwise; replaces map_scalar (src/tensor.rs:2718-2735). */
+int trs_binary_scalar_f32(int op, const float *a, const trs_layout *la, float s, float *out,
+                          const trs_layout *lo);
+/* out = op(a) elementwise; replaces unary_map + materialize_with_strides
+ * (src/tensor.rs:2737-2749, 1805-1838). */
+int trs_unary_f32(int op, const float *a, const trs_layout *la, float *out,
+                  const trs_layout *lo);
+/* Dropout-apply with a precomputed keep-mask: out = (h * f32(mask)) * scale,
+ * two roundings.  Replaces the reference composition mul (src/tensor.rs:2217)
+ * then mul_scalar (:2274) of a mask ingested as f32 0/1
+ * (src/python.rs:10396-10444); the mask stays uint8 in HBM. */
+int trs_mask_apply_f32(const float *h, const trs_layout *lh, const uint8_t *mask,
+                       const trs_layout *lm, float scale, float *out, const trs_layout *lo);
+
+/* ---- reductions and backward helpers (src/tensor.rs:2413-2431, 2881-3341) */
+
+/* *out (one device float) = sum of x.  Replaces Tensor::sum
+ * (src/tensor.rs:2413-2431); a fixed-order two-level tree rather than the
+ * reference's sequential fold, so it matches within the float summation
+ * bound, not bit for bit. */
+int trs_sum_f32(const float *x, const trs_layout *lx, float *out);
+/* out[0..n) = *value (a device float): the Sum VJP fill (src/tensor.rs:3008-3013). */
+int trs_fill_from_device_f32(float *out, size_t n, const float *value);
+/* out[0..n) = value. */
+int trs_fill_f32(float *out, size_t n, float value);
+/* grad (input-logical order) = relu'(input) * up; apply_relu_vjp
+ * (src/tensor.rs:3161-3176) with relu_backward_value (:4422-4432).  `up` is
+ * contiguous in the input's logical order. */
+int trs_relu_backward_f32(const float *input, const trs_layout *li, const float *up,
+                          float *grad);
+/* One operand's Multiply VJP (src/tensor.rs:3031-3097) with the
+ * GradientAccumulator rule (:3204-3228): grad[j] = sum over output indices o
+ * that read operand element j, in row-major order, of up[o] * other[o];
+ * no-broadcast operands store the single contribution as is, broadcast ones
+ * accumulate from +0.0.  `up` is contiguous with shape lout; `grad` is
+ * contiguous with the operand shape lself (only rank/shape read). */
+int trs_mul_backward_f32(const float *up, const trs_layout *lout, const float *other,
+                         const trs_layout *lother, const trs_layout *lself, float *grad);
+/* grad = up summed over the dims lself was broadcast along, from +0.0 in
+ * row-major output order (the add VJP; the reference records none for
+ * tensor-tensor add, src/tensor.rs:2197-2209). */
+int trs_reduce_to_shape_f32(const float *up, const trs_layout *lout, const trs_layout *lself,
+                            float *grad);
+/* dst[i] += src[i]; add_gradient and accumulate_leaf_gradient
+ * (src/tensor.rs:3302-3341, src/storage.rs:85-100). */
+int trs_accumulate_f32(float *dst, const float *src, size_t n);
+
+/* ---- matmul (Tensor::matmul, src/tensor.rs:2453-2533, 3872-3994) */
+
+/* C = A @ B in fp32 on CDNA4 FP32 MFMA.  Rank 2 ([M,K] @ [K,N]) or rank 3
+ * ([b,M,K] @ [b,K,N], the batch the reference spells as rank-2 calls).
+ * Operands may be transposed views (unit stride in either matrix dim,
+ * e.g. `.mT`); other strides are packed first.  `lc` must be contiguous.
+ * Tolerance versus the reference's sequential order: |dC| <= 1e-5*sqrt(K) *
+ * (|A||B|) elementwise. */
+int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
+                   float *c, const trs_layout *lc);
+
+/* ---- pointwise fusion compiler (new; no counterpart in the reference) */
+
+/* Compile a pointwise IR program to a gfx950 kernel with hipRTC (-O3,
+ * -ffp-contract=off), cached by IR text.  IR grammar, one instruction per
+ * line, values numbered from 0 in order of definition:
+ *     in f32 | in u8           -- next kernel input
+ *     const <hex f32 bits>     -- scalar constant
+ *     add|sub|mul|div %a %b    -- binary32 op, one rounding
+ *     exp|relu|neg %a          -- unary op with the reference semantics
+ *     out %a                   -- the (single) output
+ * Each instruction rounds exactly as the eager op it mirrors, so a fused
+ * chain is bit-identical to the eager chain except through exp. */
+int trs_fusion_compile(const char *ir, size_t ir_len, uint64_t *kernel_id);
+/* Launch a compiled program: inputs broadcast to lo's shape. */
+int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *inputs,
+                      const trs_layout *in_layouts, float *out, const trs_layout *lo);
+/* Generated HIP C++ source of a compiled program (for inspection). */
+int trs_fusion_source(uint64_t kernel_id, char *buf, size_t buf_len, size_t *needed);
+/* Milliseconds spent in hipRTC for this program (reported apart from timings). */
+int trs_fusion_compile_ms(uint64_t kernel_id, double *ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRS_HIP_H */

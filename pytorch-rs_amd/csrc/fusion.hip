@@ -1,0 +1,315 @@
+// fusion.hip -- the pointwise fusion compiler: IR text -> HIP C++ -> hipRTC
+// (gfx950) -> cached module -> launch through the shared pointwise engine.
+//
+// The reference has no fusion (torch.jit.strict_fusion is a warning-only
+// no-op and torch.compile is unsupported, README.md:178); this component is
+// new.  A program is a straight-line DAG of reference ops; the generated
+// functor evaluates it per element with one IEEE rounding per op, exactly as
+// the eager chain would, and is instantiated into the same kernel bodies the
+// eager ops use (pw_core.h), so fused and eager runs differ only in that
+// intermediates never touch HBM.
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "pw_host.h"
+#include "trs_internal.h"
+
+namespace trs {
+
+namespace {
+
+// pw_core.h as a string literal, generated at build time.
+const char kPwCoreSource[] =
+#include "pw_core_src.inc"
+    ;
+
+struct Program {
+    std::string ir;
+    std::string source;
+    int nin = 0;
+    unsigned u8mask = 0;
+    double compile_ms = 0.0;
+    std::vector<char> code;
+    hipModule_t module[16] = {};
+    std::map<std::string, hipFunction_t> functions[16];
+};
+
+std::mutex g_mu;
+std::vector<std::unique_ptr<Program>> g_programs;  // kernel_id = index + 1
+std::map<std::string, uint64_t> g_by_ir;
+
+struct Instr {
+    std::string op;
+    std::vector<int> args;
+    uint32_t bits = 0;
+};
+
+int parse_value(const std::string &tok, int defined, int *out) {
+    if (tok.size() < 2 || tok[0] != '%') return -1;
+    char *end = nullptr;
+    long v = std::strtol(tok.c_str() + 1, &end, 10);
+    if (*end != '\0' || v < 0 || v >= defined) return -1;
+    *out = (int)v;
+    return 0;
+}
+
+// Parses the IR, emits the functor and the extern "C" kernel wrappers.
+int generate(const std::string &ir, Program *prog) {
+    std::istringstream in(ir);
+    std::string line;
+    std::vector<Instr> code;
+    int defined = 0, nin = 0, result = -1, lineno = 0;
+    unsigned u8mask = 0;
+    while (std::getline(in, line)) {
+        lineno++;
+        const size_t hash = line.find('#');
+        if (hash != std::string::npos) line.resize(hash);
+        std::istringstream ls(line);
+        std::string op;
+        if (!(ls >> op)) continue;
+        if (result >= 0) return set_error(TRS_E_FUSION, "line %d: instruction after 'out'", lineno);
+        Instr ins;
+        ins.op = op;
+        std::vector<std::string> toks;
+        std::string t;
+        while (ls >> t) toks.push_back(t);
+        if (op == "in") {
+            if (toks.size() != 1 || (toks[0] != "f32" && toks[0] != "u8"))
+                return set_error(TRS_E_FUSION, "line %d: expected 'in f32' or 'in u8'", lineno);
+            if (nin >= kMaxIn) return set_error(TRS_E_FUSION, "line %d: more than %d inputs", lineno, kMaxIn);
+            if (toks[0] == "u8") u8mask |= 1u << nin;
+            ins.args.push_back(nin++);
+            code.push_back(ins);
+            defined++;
+        } else if (op == "const") {
+            if (toks.size() != 1) return set_error(TRS_E_FUSION, "line %d: expected 'const 0x<bits>'", lineno);
+            char *end = nullptr;
+            unsigned long v = std::strtoul(toks[0].c_str(), &end, 0);
+            if (*end != '\0' || v > 0xffffffffUL)
+                return set_error(TRS_E_FUSION, "line %d: bad constant '%s'", lineno, toks[0].c_str());
+            ins.bits = (uint32_t)v;
+            code.push_back(ins);
+            defined++;
+        } else if (op == "add" || op == "sub" || op == "mul" || op == "div") {
+            if (toks.size() != 2) return set_error(TRS_E_FUSION, "line %d: '%s' takes two values", lineno, op.c_str());
+            for (auto &tk : toks) {
+                int v;
+                if (parse_value(tk, defined, &v))
+                    return set_error(TRS_E_FUSION, "line %d: bad operand '%s'", lineno, tk.c_str());
+                ins.args.push_back(v);
+            }
+            code.push_back(ins);
+            defined++;
+        } else if (op == "exp" || op == "relu" || op == "neg") {
+            int v;
+            if (toks.size() != 1 || parse_value(toks[0], defined, &v))
+                return set_error(TRS_E_FUSION, "line %d: '%s' takes one value", lineno, op.c_str());
+            ins.args.push_back(v);
+            code.push_back(ins);
+            defined++;
+        } else if (op == "out") {
+            int v;
+            if (toks.size() != 1 || parse_value(toks[0], defined, &v))
+                return set_error(TRS_E_FUSION, "line %d: 'out' takes one value", lineno);
+            result = v;
+        } else {
+            return set_error(TRS_E_FUSION, "line %d: unknown instruction '%s'", lineno, op.c_str());
+        }
+    }
+    if (result < 0) return set_error(TRS_E_FUSION, "program has no 'out'");
+    if (nin == 0) return set_error(TRS_E_FUSION, "program has no inputs");
+
+    std::ostringstream s;
+    s << "// generated by libtrs_hip fusion compiler\n";
+    s << "struct TrsFused {\n  static constexpr int NIN = " << nin << ";\n";
+    s << "  __device__ __forceinline__ float operator()(const float *a) const {\n";
+    for (size_t i = 0; i < code.size(); i++) {
+        const Instr &c = code[i];
+        s << "    const float v" << i << " = ";
+        if (c.op == "in") s << "a[" << c.args[0] << "]";
+        else if (c.op == "const") {
+            char buf[32];
+            std::snprintf(buf, sizeof buf, "0x%08xu", c.bits);
+            s << "__uint_as_float(" << buf << ")";
+        } else if (c.op == "add") s << "v" << c.args[0] << " + v" << c.args[1];
+        else if (c.op == "sub") s << "v" << c.args[0] << " - v" << c.args[1];
+        else if (c.op == "mul") s << "v" << c.args[0] << " * v" << c.args[1];
+        else if (c.op == "div") s << "v" << c.args[0] << " / v" << c.args[1];
+        else if (c.op == "exp") s << "trs::exp_value(v" << c.args[0] << ")";
+        else if (c.op == "relu") s << "trs::relu_value(v" << c.args[0] << ")";
+        else if (c.op == "neg") s << "trs::negate_value(v" << c.args[0] << ")";
+        s << ";\n";
+    }
+    s << "    return v" << result << ";\n  }\n};\n";
+    const std::string mask = std::to_string(u8mask) + "u";
+    auto wrap = [&](const char *name, const std::string &body) {
+        s << "extern \"C\" __global__ void __launch_bounds__(256) " << name
+          << "(trs::PwGeom g, trs::PwPtrs p) { " << body << "(TrsFused{}, g, p); }\n";
+    };
+    wrap("trs_fused_flat_v", "trs::pw_flat_body<TrsFused, " + mask + ", true>");
+    wrap("trs_fused_flat_s", "trs::pw_flat_body<TrsFused, " + mask + ", false>");
+    wrap("trs_fused_rows_v", "trs::pw_rows_body<TrsFused, " + mask + ", true>");
+    wrap("trs_fused_rows_s", "trs::pw_rows_body<TrsFused, " + mask + ", false>");
+    wrap("trs_fused_generic", "trs::pw_generic_body<TrsFused, " + mask + ">");
+    for (int nt = 1; nt <= nin && nt <= 4; nt++) {
+        const std::string v = "trs_fused_tiled_v" + std::to_string(nt);
+        const std::string sc = "trs_fused_tiled_s" + std::to_string(nt);
+        wrap(v.c_str(), "trs::pw_tiled_body<TrsFused, " + mask + ", true, " + std::to_string(nt) + ">");
+        wrap(sc.c_str(), "trs::pw_tiled_body<TrsFused, " + mask + ", false, " + std::to_string(nt) + ">");
+    }
+    prog->nin = nin;
+    prog->u8mask = u8mask;
+    prog->source = s.str();
+    return TRS_OK;
+}
+
+int compile(Program *prog) {
+    std::string full = std::string(kPwCoreSource) + "\n" + prog->source;
+    hiprtcProgram rp;
+    hiprtcResult r = hiprtcCreateProgram(&rp, full.c_str(), "trs_fused.hip", 0, nullptr, nullptr);
+    if (r != HIPRTC_SUCCESS) return set_error(TRS_E_FUSION, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
+    const char *opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-std=c++20", "-DTRS_RTC",
+                          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-w"};
+    const auto t0 = std::chrono::steady_clock::now();
+    r = hiprtcCompileProgram(rp, (int)(sizeof opts / sizeof opts[0]), opts);
+    prog->compile_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    if (r != HIPRTC_SUCCESS) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(rp, &n);
+        std::string log(n + 1, '\0');
+        hiprtcGetProgramLog(rp, &log[0]);
+        hiprtcDestroyProgram(&rp);
+        return set_error(TRS_E_FUSION, "hipRTC compile failed: %.900s", log.c_str());
+    }
+    size_t n = 0;
+    hiprtcGetCodeSize(rp, &n);
+    prog->code.resize(n);
+    hiprtcGetCode(rp, prog->code.data());
+    hiprtcDestroyProgram(&rp);
+    return TRS_OK;
+}
+
+Program *lookup(uint64_t id) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (id == 0 || id > g_programs.size()) return nullptr;
+    return g_programs[id - 1].get();
+}
+
+int get_function(Program *prog, DeviceState *dev, const std::string &name, hipFunction_t *fn) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    const int d = dev->index;
+    if (!prog->module[d]) TRS_HIP_CHECK(hipModuleLoadData(&prog->module[d], prog->code.data()), "hipModuleLoadData");
+    auto it = prog->functions[d].find(name);
+    if (it != prog->functions[d].end()) {
+        *fn = it->second;
+        return TRS_OK;
+    }
+    TRS_HIP_CHECK(hipModuleGetFunction(fn, prog->module[d], name.c_str()), "hipModuleGetFunction");
+    prog->functions[d][name] = *fn;
+    return TRS_OK;
+}
+
+}  // namespace
+
+}  // namespace trs
+
+using namespace trs;
+
+extern "C" {
+
+int trs_fusion_compile(const char *ir, size_t ir_len, uint64_t *kernel_id) {
+    if (!ir || !kernel_id) return set_error(TRS_E_INVALID_ARGUMENT, "null IR or kernel id pointer");
+    const std::string text(ir, ir_len);
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        auto it = g_by_ir.find(text);
+        if (it != g_by_ir.end()) {
+            *kernel_id = it->second;
+            return TRS_OK;
+        }
+    }
+    auto prog = std::make_unique<Program>();
+    prog->ir = text;
+    int rc = generate(text, prog.get());
+    if (rc) return rc;
+    rc = compile(prog.get());
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(g_mu);
+    auto it = g_by_ir.find(text);  // another thread may have won the race
+    if (it != g_by_ir.end()) {
+        *kernel_id = it->second;
+        return TRS_OK;
+    }
+    g_programs.push_back(std::move(prog));
+    *kernel_id = g_programs.size();
+    g_by_ir[text] = *kernel_id;
+    return TRS_OK;
+}
+
+int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *inputs, const trs_layout *in_layouts,
+                      float *out, const trs_layout *lo) {
+    Program *prog = lookup(kernel_id);
+    if (!prog) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id %llu", (unsigned long long)kernel_id);
+    if (n_inputs != prog->nin)
+        return set_error(TRS_E_INVALID_ARGUMENT, "program takes %d inputs, got %d", prog->nin, n_inputs);
+    if (!inputs || !in_layouts) return set_error(TRS_E_INVALID_ARGUMENT, "null inputs");
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    const trs_layout *ls[kMaxIn];
+    int eb[kMaxIn];
+    for (int i = 0; i < n_inputs; i++) {
+        ls[i] = &in_layouts[i];
+        eb[i] = ((prog->u8mask >> i) & 1u) ? 1 : 4;
+    }
+    PwPlan pl;
+    int rc = plan_pointwise(lo, out, n_inputs, inputs, ls, eb, dev->cu_count, &pl);
+    if (rc) return rc;
+    std::string name;
+    switch (pl.variant) {
+    case PwVariant::Empty: return TRS_OK;
+    case PwVariant::Flat: name = pl.vec ? "trs_fused_flat_v" : "trs_fused_flat_s"; break;
+    case PwVariant::Rows: name = pl.vec ? "trs_fused_rows_v" : "trs_fused_rows_s"; break;
+    case PwVariant::Tiled:
+        name = std::string(pl.vec ? "trs_fused_tiled_v" : "trs_fused_tiled_s") + std::to_string(pl.ntransposed);
+        break;
+    case PwVariant::Generic: name = "trs_fused_generic"; break;
+    }
+    hipFunction_t fn;
+    rc = get_function(prog, dev, name, &fn);
+    if (rc) return rc;
+    void *args[] = {(void *)&pl.g, (void *)&pl.p};
+    TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, 256, 1, 1, 0, dev->stream, args, nullptr),
+                  "hipModuleLaunchKernel");
+    return TRS_OK;
+}
+
+int trs_fusion_source(uint64_t kernel_id, char *buf, size_t buf_len, size_t *needed) {
+    Program *prog = lookup(kernel_id);
+    if (!prog) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id");
+    if (needed) *needed = prog->source.size() + 1;
+    if (buf && buf_len) {
+        const size_t n = std::min(buf_len - 1, prog->source.size());
+        std::memcpy(buf, prog->source.data(), n);
+        buf[n] = '\0';
+    }
+    return TRS_OK;
+}
+
+int trs_fusion_compile_ms(uint64_t kernel_id, double *ms) {
+    Program *prog = lookup(kernel_id);
+    if (!prog || !ms) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id");
+    *ms = prog->compile_ms;
+    return TRS_OK;
+}
+
+}  // extern "C"

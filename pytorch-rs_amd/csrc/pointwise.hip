@@ -1,0 +1,484 @@
+// pointwise.hip -- ahead-of-time pointwise, reduction and backward kernels.
+//
+// Each entry point replaces the per-element loop of one reference function
+// (cited at the entry point) and runs it through the shared engine in
+// pw_core.h.  Ops are functors with the reference's scalar semantics; the
+// file is compiled with -ffp-contract=off so `a * b + c` is never fused.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "pw_core.h"
+#include "pw_host.h"
+#include "trs_internal.h"
+
+namespace trs {
+
+// ---- op functors ----------------------------------------------------------
+
+template <int OP>
+struct BinaryF {
+    static constexpr int NIN = 2;
+    __device__ __forceinline__ float operator()(const float *a) const {
+        if constexpr (OP == TRS_ADD) return a[0] + a[1];
+        else if constexpr (OP == TRS_SUB) return a[0] - a[1];
+        else if constexpr (OP == TRS_MUL) return a[0] * a[1];
+        else return a[0] / a[1];
+    }
+};
+
+template <int OP>
+struct ScalarF {
+    static constexpr int NIN = 1;
+    float s;
+    __device__ __forceinline__ float operator()(const float *a) const {
+        if constexpr (OP == TRS_S_ADD) return a[0] + s;
+        else if constexpr (OP == TRS_S_SUB) return a[0] - s;
+        else if constexpr (OP == TRS_S_MUL) return a[0] * s;
+        else if constexpr (OP == TRS_S_DIV) return a[0] / s;
+        else if constexpr (OP == TRS_S_RSUB) return s - a[0];
+        else return s * (1.0f / a[0]);  // scalar_div: reciprocal multiplication
+    }
+};
+
+template <int OP>
+struct UnaryF {
+    static constexpr int NIN = 1;
+    __device__ __forceinline__ float operator()(const float *a) const {
+        if constexpr (OP == TRS_EXP) return exp_value(a[0]);
+        else if constexpr (OP == TRS_RELU) return relu_value(a[0]);
+        else if constexpr (OP == TRS_NEG) return negate_value(a[0]);
+        else return a[0];
+    }
+};
+
+// (h * mask) * scale with the mask read as uint8 (input 1).
+struct MaskApplyF {
+    static constexpr int NIN = 2;
+    float scale;
+    __device__ __forceinline__ float operator()(const float *a) const {
+        const float t = a[0] * a[1];
+        return t * scale;
+    }
+};
+
+struct ReluBackwardF {
+    static constexpr int NIN = 2;  // (saved input, upstream)
+    __device__ __forceinline__ float operator()(const float *a) const {
+        return relu_backward_value(a[0], a[1]);
+    }
+};
+
+// ---- AOT wrappers -----------------------------------------------------------
+
+template <class F, unsigned M, bool V>
+__global__ void __launch_bounds__(256) k_flat(F f, PwGeom g, PwPtrs p) { pw_flat_body<F, M, V>(f, g, p); }
+template <class F, unsigned M, bool V>
+__global__ void __launch_bounds__(256) k_rows(F f, PwGeom g, PwPtrs p) { pw_rows_body<F, M, V>(f, g, p); }
+template <class F, unsigned M, bool V, int NT>
+__global__ void __launch_bounds__(256) k_tiled(F f, PwGeom g, PwPtrs p) { pw_tiled_body<F, M, V, NT>(f, g, p); }
+template <class F, unsigned M>
+__global__ void __launch_bounds__(256) k_generic(F f, PwGeom g, PwPtrs p) { pw_generic_body<F, M>(f, g, p); }
+
+template <class F, unsigned M>
+int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
+    const dim3 grid((unsigned)pl.grid), block(256);
+    switch (pl.variant) {
+    case PwVariant::Empty:
+        return TRS_OK;
+    case PwVariant::Flat:
+        if (pl.vec) hipLaunchKernelGGL((k_flat<F, M, true>), grid, block, 0, s, f, pl.g, pl.p);
+        else hipLaunchKernelGGL((k_flat<F, M, false>), grid, block, 0, s, f, pl.g, pl.p);
+        break;
+    case PwVariant::Rows:
+        if (pl.vec) hipLaunchKernelGGL((k_rows<F, M, true>), grid, block, 0, s, f, pl.g, pl.p);
+        else hipLaunchKernelGGL((k_rows<F, M, false>), grid, block, 0, s, f, pl.g, pl.p);
+        break;
+    case PwVariant::Tiled:
+        if constexpr (F::NIN >= 2) {
+            if (pl.ntransposed == 2) {
+                if (pl.vec) hipLaunchKernelGGL((k_tiled<F, M, true, 2>), grid, block, 0, s, f, pl.g, pl.p);
+                else hipLaunchKernelGGL((k_tiled<F, M, false, 2>), grid, block, 0, s, f, pl.g, pl.p);
+                break;
+            }
+        }
+        if (pl.vec) hipLaunchKernelGGL((k_tiled<F, M, true, 1>), grid, block, 0, s, f, pl.g, pl.p);
+        else hipLaunchKernelGGL((k_tiled<F, M, false, 1>), grid, block, 0, s, f, pl.g, pl.p);
+        break;
+    case PwVariant::Generic:
+        hipLaunchKernelGGL((k_generic<F, M>), grid, block, 0, s, f, pl.g, pl.p);
+        break;
+    }
+    TRS_LAUNCH_CHECK("pointwise kernel launch");
+    return TRS_OK;
+}
+
+template <class F, unsigned M = 0u>
+int run_pointwise(const F &f, const trs_layout *lo, float *out, int nin, const void *const *bases,
+                  const trs_layout *const *lins, const int *eb) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    PwPlan pl;
+    int rc = plan_pointwise(lo, out, nin, bases, lins, eb, dev->cu_count, &pl);
+    if (rc) return rc;
+    return launch_planned<F, M>(f, pl, dev->stream);
+}
+
+// ---- reductions -------------------------------------------------------------
+
+constexpr int kSumBlocks = 1024;
+
+// Fixed-order two-level sum.  Pass 1: block b sums the contiguous element
+// range [b*chunk, (b+1)*chunk) -- lane l adds elements l, l+256, ... in order,
+// then a fixed shuffle/LDS tree over the 256 lanes.  Pass 2 sums the block
+// partials in the same way.  The order depends only on the element count.
+template <bool CONTIG>
+__global__ void __launch_bounds__(256) sum_pass1(const float *x, PwGeom g, int64_t chunk, float *partial) {
+    __shared__ float red[256];
+    const int64_t begin = (int64_t)blockIdx.x * chunk;
+    const int64_t end = begin + chunk < g.numel ? begin + chunk : g.numel;
+    float acc = 0.0f;
+    for (int64_t e = begin + threadIdx.x; e < end; e += 256) {
+        int64_t off;
+        if constexpr (CONTIG) {
+            off = g.ioff[0] + e;
+        } else {
+            int64_t oo, io[1];
+            decode_outer<1>(g, g.rank, e, oo, io);
+            off = io[0];
+        }
+        acc += x[off];
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+__global__ void __launch_bounds__(256) sum_pass2(const float *partial, int n, float *out) {
+    __shared__ float red[256];
+    float acc = 0.0f;
+    for (int e = threadIdx.x; e < n; e += 256) acc += partial[e];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = red[0];
+}
+
+__global__ void __launch_bounds__(256) fill_kernel(float *out, size_t n, float value, const float *src) {
+    const float v = src ? src[0] : value;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = v;
+}
+
+// Broadcast-reduction: grad[j] = sum over the reduced dims (row-major order)
+// of up[o] * (other ? other[o] : 1), accumulated from +0.0, one thread per
+// operand element j.  `kept` dims are the operand's non-broadcast dims of the
+// output; `red` dims are the dims it was broadcast along.
+struct ReduceGeom {
+    int32_t nkept;
+    int32_t nred;
+    int64_t kept_size[kMaxRank];
+    int64_t kept_up[kMaxRank];     // strides of up (output-contiguous) per kept dim
+    int64_t kept_other[kMaxRank];  // strides of other per kept dim
+    int64_t red_size[kMaxRank];
+    int64_t red_up[kMaxRank];
+    int64_t red_other[kMaxRank];
+    int64_t nself;
+    int64_t nred_total;
+    int64_t other_off;
+};
+
+template <bool HAS_OTHER>
+__global__ void __launch_bounds__(256) reduce_bcast_kernel(const float *up, const float *other, ReduceGeom rg,
+                                                           float *grad) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < rg.nself; j += stride) {
+        int64_t ub = 0, ob = rg.other_off, rem = j;
+        for (int d = rg.nkept - 1; d >= 0; d--) {
+            const int64_t c = rem % rg.kept_size[d];
+            rem /= rg.kept_size[d];
+            ub += c * rg.kept_up[d];
+            ob += c * rg.kept_other[d];
+        }
+        float acc = 0.0f;
+        int64_t cnt[kMaxRank];
+        for (int d = 0; d < rg.nred; d++) cnt[d] = 0;
+        int64_t uo = ub, oo = ob;
+        for (int64_t r = 0; r < rg.nred_total; r++) {
+            float c = up[uo];
+            if constexpr (HAS_OTHER) c = c * other[oo];
+            acc += c;
+            // odometer over reduced dims, innermost last
+            for (int d = rg.nred - 1; d >= 0; d--) {
+                if (++cnt[d] < rg.red_size[d]) {
+                    uo += rg.red_up[d];
+                    oo += rg.red_other[d];
+                    break;
+                }
+                cnt[d] = 0;
+                uo -= rg.red_up[d] * (rg.red_size[d] - 1);
+                oo -= rg.red_other[d] * (rg.red_size[d] - 1);
+            }
+        }
+        grad[j] = acc;
+    }
+}
+
+int reduce_to_operand(const float *up, const trs_layout *lout, const float *other,
+                      const trs_layout *lother, const trs_layout *lself, float *grad) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    int rc = check_layout(lout, "output");
+    if (!rc) rc = check_layout(lself, "operand");
+    if (!rc && other) rc = check_layout(lother, "other");
+    if (rc) return rc;
+    if (lself->rank > lout->rank) return set_error(TRS_E_SHAPE_MISMATCH, "operand rank above output rank");
+    ReduceGeom rg{};
+    const int lead = lout->rank - lself->rank;
+    const int olead = other ? lout->rank - lother->rank : 0;
+    int64_t ustride[kMaxRank];
+    {
+        int64_t s = 1;
+        for (int d = lout->rank - 1; d >= 0; d--) {
+            ustride[d] = s;
+            s *= lout->shape[d];
+        }
+    }
+    for (int d = 0; d < lout->rank; d++) {
+        const int64_t osz = lout->shape[d];
+        const bool self_bcast = d < lead || (lself->shape[d - lead] == 1 && osz != 1);
+        if (d >= lead && lself->shape[d - lead] != osz && lself->shape[d - lead] != 1)
+            return set_error(TRS_E_SHAPE_MISMATCH, "operand does not broadcast to the output");
+        int64_t ost = 0;
+        if (other && d >= olead) {
+            const int64_t s = lother->shape[d - olead];
+            if (s != osz && s != 1) return set_error(TRS_E_SHAPE_MISMATCH, "other does not broadcast");
+            ost = (s == 1) ? 0 : lother->stride[d - olead];
+        }
+        if (self_bcast) {
+            if (osz == 1) continue;
+            rg.red_size[rg.nred] = osz;
+            rg.red_up[rg.nred] = ustride[d];
+            rg.red_other[rg.nred] = ost;
+            rg.nred++;
+        } else {
+            rg.kept_size[rg.nkept] = osz;
+            rg.kept_up[rg.nkept] = ustride[d];
+            rg.kept_other[rg.nkept] = ost;
+            rg.nkept++;
+        }
+    }
+    rg.nself = layout_numel(lself);
+    rg.nred_total = 1;
+    for (int d = 0; d < rg.nred; d++) rg.nred_total *= rg.red_size[d];
+    rg.other_off = other ? lother->offset : 0;
+    if (rg.nself == 0) return TRS_OK;
+    if (layout_numel(lout) == 0) {  // nothing reaches the operand: +0.0
+        const int64_t grid = std::min<int64_t>((rg.nself + 255) / 256, (int64_t)dev->cu_count * 8);
+        hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream, grad,
+                           (size_t)rg.nself, 0.0f, (const float *)nullptr);
+        TRS_LAUNCH_CHECK("fill kernel");
+        return TRS_OK;
+    }
+    const int64_t grid = std::min<int64_t>((rg.nself + 255) / 256, (int64_t)dev->cu_count * 8);
+    if (other)
+        hipLaunchKernelGGL(reduce_bcast_kernel<true>, dim3((unsigned)grid), dim3(256), 0, dev->stream, up,
+                           other, rg, grad);
+    else
+        hipLaunchKernelGGL(reduce_bcast_kernel<false>, dim3((unsigned)grid), dim3(256), 0, dev->stream, up,
+                           (const float *)nullptr, rg, grad);
+    TRS_LAUNCH_CHECK("broadcast reduction kernel");
+    return TRS_OK;
+}
+
+// Contiguous layout of `shape` (for gradients, which are logical-order).
+trs_layout contiguous_like(const trs_layout *l) {
+    trs_layout c{};
+    c.rank = l->rank;
+    int64_t s = 1;
+    for (int d = l->rank - 1; d >= 0; d--) {
+        c.shape[d] = l->shape[d];
+        c.stride[d] = s;
+        s *= l->shape[d];
+    }
+    c.offset = 0;
+    return c;
+}
+
+}  // namespace trs
+
+using namespace trs;
+
+extern "C" {
+
+int trs_binary_f32(int op, const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
+                   float *out, const trs_layout *lo) {
+    const void *bases[2] = {a, b};
+    const trs_layout *ls[2] = {la, lb};
+    const int eb[2] = {4, 4};
+    switch (op) {
+    case TRS_ADD: return run_pointwise(BinaryF<TRS_ADD>{}, lo, out, 2, bases, ls, eb);
+    case TRS_SUB: return run_pointwise(BinaryF<TRS_SUB>{}, lo, out, 2, bases, ls, eb);
+    case TRS_MUL: return run_pointwise(BinaryF<TRS_MUL>{}, lo, out, 2, bases, ls, eb);
+    case TRS_DIV: return run_pointwise(BinaryF<TRS_DIV>{}, lo, out, 2, bases, ls, eb);
+    default: return set_error(TRS_E_INVALID_ARGUMENT, "unknown binary op %d", op);
+    }
+}
+
+int trs_binary_scalar_f32(int op, const float *a, const trs_layout *la, float s, float *out,
+                          const trs_layout *lo) {
+    const void *bases[1] = {a};
+    const trs_layout *ls[1] = {la};
+    const int eb[1] = {4};
+    if (la && lo && la->rank != lo->rank)
+        return set_error(TRS_E_SHAPE_MISMATCH, "scalar op output rank differs from input rank");
+    switch (op) {
+    case TRS_S_ADD: return run_pointwise(ScalarF<TRS_S_ADD>{s}, lo, out, 1, bases, ls, eb);
+    case TRS_S_SUB: return run_pointwise(ScalarF<TRS_S_SUB>{s}, lo, out, 1, bases, ls, eb);
+    case TRS_S_MUL: return run_pointwise(ScalarF<TRS_S_MUL>{s}, lo, out, 1, bases, ls, eb);
+    case TRS_S_DIV: return run_pointwise(ScalarF<TRS_S_DIV>{s}, lo, out, 1, bases, ls, eb);
+    case TRS_S_RSUB: return run_pointwise(ScalarF<TRS_S_RSUB>{s}, lo, out, 1, bases, ls, eb);
+    case TRS_S_RDIV: return run_pointwise(ScalarF<TRS_S_RDIV>{s}, lo, out, 1, bases, ls, eb);
+    default: return set_error(TRS_E_INVALID_ARGUMENT, "unknown scalar op %d", op);
+    }
+}
+
+int trs_unary_f32(int op, const float *a, const trs_layout *la, float *out, const trs_layout *lo) {
+    const void *bases[1] = {a};
+    const trs_layout *ls[1] = {la};
+    const int eb[1] = {4};
+    if (la && lo && la->rank != lo->rank)
+        return set_error(TRS_E_SHAPE_MISMATCH, "unary op output rank differs from input rank");
+    switch (op) {
+    case TRS_EXP: return run_pointwise(UnaryF<TRS_EXP>{}, lo, out, 1, bases, ls, eb);
+    case TRS_RELU: return run_pointwise(UnaryF<TRS_RELU>{}, lo, out, 1, bases, ls, eb);
+    case TRS_NEG: return run_pointwise(UnaryF<TRS_NEG>{}, lo, out, 1, bases, ls, eb);
+    case TRS_COPY: return run_pointwise(UnaryF<TRS_COPY>{}, lo, out, 1, bases, ls, eb);
+    default: return set_error(TRS_E_INVALID_ARGUMENT, "unknown unary op %d", op);
+    }
+}
+
+int trs_mask_apply_f32(const float *h, const trs_layout *lh, const uint8_t *mask, const trs_layout *lm,
+                       float scale, float *out, const trs_layout *lo) {
+    const void *bases[2] = {h, mask};
+    const trs_layout *ls[2] = {lh, lm};
+    const int eb[2] = {4, 1};
+    return run_pointwise<MaskApplyF, 2u>(MaskApplyF{scale}, lo, out, 2, bases, ls, eb);
+}
+
+int trs_relu_backward_f32(const float *input, const trs_layout *li, const float *up, float *grad) {
+    int rc = check_layout(li, "input");
+    if (rc) return rc;
+    const trs_layout lc = contiguous_like(li);
+    const void *bases[2] = {input, up};
+    const trs_layout *ls[2] = {li, &lc};
+    const int eb[2] = {4, 4};
+    return run_pointwise(ReluBackwardF{}, &lc, grad, 2, bases, ls, eb);
+}
+
+int trs_accumulate_f32(float *dst, const float *src, size_t n) {
+    trs_layout l{};
+    l.rank = 1;
+    l.shape[0] = (int64_t)n;
+    l.stride[0] = 1;
+    const void *bases[2] = {dst, src};
+    const trs_layout *ls[2] = {&l, &l};
+    const int eb[2] = {4, 4};
+    return run_pointwise(BinaryF<TRS_ADD>{}, &l, dst, 2, bases, ls, eb);
+}
+
+int trs_fill_f32(float *out, size_t n, float value) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (n == 0) return TRS_OK;
+    if (!out) return set_error(TRS_E_INVALID_ARGUMENT, "null output");
+    const int64_t grid = std::min<int64_t>(((int64_t)n + 255) / 256, (int64_t)dev->cu_count * 8);
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream, out, n, value,
+                       (const float *)nullptr);
+    TRS_LAUNCH_CHECK("fill kernel");
+    return TRS_OK;
+}
+
+int trs_fill_from_device_f32(float *out, size_t n, const float *value) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (n == 0) return TRS_OK;
+    if (!out || !value) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer");
+    const int64_t grid = std::min<int64_t>(((int64_t)n + 255) / 256, (int64_t)dev->cu_count * 8);
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream, out, n, 0.0f, value);
+    TRS_LAUNCH_CHECK("fill kernel");
+    return TRS_OK;
+}
+
+int trs_mul_backward_f32(const float *up, const trs_layout *lout, const float *other, const trs_layout *lother,
+                         const trs_layout *lself, float *grad) {
+    int rc = check_layout(lout, "output");
+    if (!rc) rc = check_layout(lself, "operand");
+    if (rc) return rc;
+    if (!other) return set_error(TRS_E_INVALID_ARGUMENT, "null other operand");
+    if (layout_numel(lself) == layout_numel(lout)) {
+        // No broadcast: one contribution per element, stored as is.
+        const trs_layout lc = contiguous_like(lout);
+        const void *bases[2] = {up, other};
+        const trs_layout *ls[2] = {&lc, lother};
+        const int eb[2] = {4, 4};
+        return run_pointwise(BinaryF<TRS_MUL>{}, &lc, grad, 2, bases, ls, eb);
+    }
+    return reduce_to_operand(up, lout, other, lother, lself, grad);
+}
+
+int trs_reduce_to_shape_f32(const float *up, const trs_layout *lout, const trs_layout *lself, float *grad) {
+    int rc = check_layout(lout, "output");
+    if (!rc) rc = check_layout(lself, "operand");
+    if (rc) return rc;
+    if (layout_numel(lself) == layout_numel(lout)) {
+        const size_t n = (size_t)layout_numel(lout);
+        return trs_memcpy_d2d(grad, up, n * sizeof(float));
+    }
+    return reduce_to_operand(up, lout, nullptr, nullptr, lself, grad);
+}
+
+int trs_sum_f32(const float *x, const trs_layout *lx, float *out) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    int rc = check_layout(lx, "input");
+    if (rc) return rc;
+    if (!out) return set_error(TRS_E_INVALID_ARGUMENT, "null output");
+    const int64_t n = layout_numel(lx);
+    if (n == 0) return trs_fill_f32(out, 1, -0.0f);
+    if (!x) return set_error(TRS_E_INVALID_ARGUMENT, "null input");
+    // Geometry for logical-order decode of a strided input.
+    PwGeom g;
+    std::memset(&g, 0, sizeof g);
+    g.numel = n;
+    g.rank = lx->rank;
+    g.ioff[0] = lx->offset;
+    for (int d = 0; d < lx->rank; d++) {
+        g.size[d] = lx->shape[d];
+        g.istride[0][d] = lx->stride[d];
+        if (lx->shape[d] > (int64_t)UINT32_MAX) g.wide = 1;
+        g.fd[d] = make_fast_div(lx->shape[d] > (int64_t)UINT32_MAX ? 1u : (uint32_t)lx->shape[d]);
+    }
+    rc = ensure_scratch(dev, kSumBlocks * sizeof(float));
+    if (rc) return rc;
+    const int64_t chunk = (n + kSumBlocks - 1) / kSumBlocks;
+    const int blocks = (int)((n + chunk - 1) / chunk);
+    float *partial = (float *)dev->scratch;
+    if (layout_is_contiguous(lx))
+        hipLaunchKernelGGL(sum_pass1<true>, dim3(blocks), dim3(256), 0, dev->stream, x, g, chunk, partial);
+    else
+        hipLaunchKernelGGL(sum_pass1<false>, dim3(blocks), dim3(256), 0, dev->stream, x, g, chunk, partial);
+    TRS_LAUNCH_CHECK("sum pass 1");
+    hipLaunchKernelGGL(sum_pass2, dim3(1), dim3(256), 0, dev->stream, partial, blocks, out);
+    TRS_LAUNCH_CHECK("sum pass 2");
+    return TRS_OK;
+}
+
+}  // extern "C"

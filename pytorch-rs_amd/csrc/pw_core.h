@@ -1,0 +1,437 @@
+// pw_core.h -- device-side pointwise engine for gfx950 (CDNA4).
+//
+// Shared verbatim by the ahead-of-time kernels (pointwise.hip) and by the
+// runtime fusion compiler (fusion.cpp embeds this file and compiles it with
+// hipRTC), so an eager op and a fused chain run the same index machinery.
+//
+// The host normalises every launch first (pw_host.h): operands are aligned
+// to the output rank with zero strides on broadcast dims, size-1 dims are
+// dropped, dims are ordered by decreasing output stride and adjacent dims
+// that are contiguous for every operand are merged.  The kernels below then
+// cover four cases:
+//   pw_flat  -- rank 1, every operand unit-stride or broadcast: 16-byte
+//               vector loads/stores in a grid-stride loop.
+//   pw_rows  -- innermost dim unit-stride or broadcast for every operand:
+//               one (outer row, 1024-column chunk) tile per block iteration;
+//               the outer-row decode is wave-uniform (scalar registers), the
+//               lanes stream 16-byte vectors along the row.
+//   pw_tiled -- an operand is unit-stride along another dim (a transposed or
+//               permuted view such as c.mT): 64x64 tiles staged through LDS
+//               so both its reads and the output writes are coalesced.
+//   pw_generic -- any strides: per-element decode with magic-number division.
+//
+// Every op is written so that hipcc and hipRTC (both run with
+// -ffp-contract=off) emit exactly one IEEE binary32 rounding per reference op.
+#pragma once
+#ifndef TRS_RTC
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#else
+// hipRTC provides the fixed-width integer types in __hip_internal.
+using __hip_internal::int32_t;
+using __hip_internal::int64_t;
+using __hip_internal::uint32_t;
+using __hip_internal::uint64_t;
+using __hip_internal::uint8_t;
+#endif
+
+#pragma clang fp contract(off)
+
+namespace trs {
+
+constexpr int kMaxRank = 8;
+constexpr int kMaxIn = 8;
+constexpr int kRowChunk = 1024;  // columns per pw_rows tile (256 lanes x 4)
+constexpr int kTile = 64;        // pw_tiled tile edge
+
+// Unsigned 32-bit division by a runtime-invariant divisor (Granlund-Montgomery
+// round-up method): q = (umulhi(n, mul) + n) >> shift, exact for all n < 2^32.
+struct FastDiv {
+    uint32_t div;
+    uint32_t mul;
+    uint32_t shift;
+    uint32_t pad;
+};
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &d) {
+    uint32_t t = __umulhi(n, d.mul);
+    return (uint32_t)(((uint64_t)t + n) >> d.shift);
+}
+
+struct PwGeom {
+    int32_t rank;   // >= 1 after normalisation
+    int32_t tdim;   // pw_tiled: dim along which transposed operands are unit-stride
+    int32_t wide;   // a dim exceeds 32 bits: always decode with 64-bit division
+    int32_t pad0;
+    int64_t numel;
+    int64_t size[kMaxRank];
+    FastDiv fd[kMaxRank];
+    int64_t ostride[kMaxRank];
+    int64_t istride[kMaxIn][kMaxRank];
+    int64_t ooff;
+    int64_t ioff[kMaxIn];
+    uint32_t transposed;  // pw_tiled: bit i set when input i goes through LDS
+    uint32_t streamed;    // bit i set when input i is read once (no broadcast dim)
+    int64_t rows;         // pw_rows / pw_tiled: number of outer index tuples
+    int64_t chunks;       // pw_rows: column chunks per row; pw_tiled: tiles per outer tuple
+    int64_t ttiles;       // pw_tiled: tiles along tdim
+};
+
+typedef float vf4 __attribute__((ext_vector_type(4)));
+typedef uint8_t vu8x4 __attribute__((ext_vector_type(4)));
+
+struct PwPtrs {
+    float *out;
+    const void *in[kMaxIn];
+};
+
+// ---- element loads --------------------------------------------------------
+
+template <unsigned U8MASK, int I>
+__device__ __forceinline__ float ld1(const PwPtrs &p, int64_t off) {
+    if constexpr (((U8MASK >> I) & 1u) != 0u) {
+        return (float)(((const uint8_t *)p.in[I])[off]);
+    } else {
+        return ((const float *)p.in[I])[off];
+    }
+}
+
+// Four consecutive elements (unit stride) or one broadcast element (stride 0).
+// Operands read exactly once use non-temporal loads; re-read (broadcast)
+// operands keep normal caching.
+template <unsigned U8MASK, int I>
+__device__ __forceinline__ void ld4(const PwPtrs &p, int64_t off, bool unit, float *v,
+                                    bool stream = false) {
+    if (!unit) {
+        float s = ld1<U8MASK, I>(p, off);
+        v[0] = s; v[1] = s; v[2] = s; v[3] = s;
+        return;
+    }
+    if constexpr (((U8MASK >> I) & 1u) != 0u) {
+        vu8x4 q = *(const vu8x4 *)(((const uint8_t *)p.in[I]) + off);
+        v[0] = (float)q.x; v[1] = (float)q.y; v[2] = (float)q.z; v[3] = (float)q.w;
+    } else {
+        const vf4 *src = (const vf4 *)(((const float *)p.in[I]) + off);
+        vf4 q = stream ? __builtin_nontemporal_load(src) : *src;
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    }
+}
+
+__device__ __forceinline__ void st4(float *dst, const float *v) {
+    vf4 q = {v[0], v[1], v[2], v[3]};
+    __builtin_nontemporal_store(q, (vf4 *)dst);
+}
+
+// Compile-time loop over inputs.
+template <int N, int I = 0, class Fn>
+__device__ __forceinline__ void static_for(Fn &&fn) {
+    if constexpr (I < N) {
+        fn.template operator()<I>();
+        static_for<N, I + 1>(fn);
+    }
+}
+
+// Offsets of output and inputs for a logical index tuple given by the first
+// `ndims` dims of the decomposition of `outer` (row-major over dims
+// [0, ndims)).  Uses 32-bit magic division when `outer` fits in 32 bits.
+template <int NIN>
+__device__ __forceinline__ void decode_outer(const PwGeom &g, int ndims, int64_t outer,
+                                             int64_t &oo, int64_t *io) {
+    oo = g.ooff;
+    for (int i = 0; i < NIN; i++) io[i] = g.ioff[i];
+    if (!g.wide && outer < 0x100000000LL) {
+        uint32_t rem = (uint32_t)outer;
+        for (int d = ndims - 1; d >= 0; d--) {
+            uint32_t q = fast_div(rem, g.fd[d]);
+            uint32_t c = rem - q * g.fd[d].div;
+            rem = q;
+            oo += (int64_t)c * g.ostride[d];
+            for (int i = 0; i < NIN; i++) io[i] += (int64_t)c * g.istride[i][d];
+        }
+    } else {
+        int64_t rem = outer;
+        for (int d = ndims - 1; d >= 0; d--) {
+            int64_t q = rem / g.size[d];
+            int64_t c = rem - q * g.size[d];
+            rem = q;
+            oo += c * g.ostride[d];
+            for (int i = 0; i < NIN; i++) io[i] += c * g.istride[i][d];
+        }
+    }
+}
+
+// Kernel bodies are __device__ functions so that the ahead-of-time wrappers
+// (templates) and the hipRTC-generated wrappers (extern "C") share them.
+
+// ---- pw_flat --------------------------------------------------------------
+// rank 1; ostride 1; istride in {0, 1}.  VEC requires numel % 4 == 0 is NOT
+// assumed: the vector body covers floor(numel/4) groups and a scalar tail the
+// rest.  VEC is chosen by the host only when every unit-stride operand and
+// the output are 16-byte aligned (4-byte for u8).
+template <class F, unsigned U8MASK, bool VEC>
+__device__ __forceinline__ void pw_flat_body(const F &f, const PwGeom &g, const PwPtrs &p) {
+    constexpr int NIN = F::NIN;
+    const int64_t n = g.numel;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+    bool unit[NIN > 0 ? NIN : 1];
+    for (int i = 0; i < NIN; i++) unit[i] = g.istride[i][0] != 0;
+    float *out = p.out + g.ooff;
+    int64_t tail_start = 0;
+    if constexpr (VEC) {
+        const int64_t groups = n >> 2;
+        constexpr int U = 4;  // float4 groups in flight per thread
+        int64_t gi = tid;
+        for (; gi + (int64_t)(U - 1) * nthreads < groups; gi += (int64_t)U * nthreads) {
+            float v[U][NIN > 0 ? NIN : 1][4];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int64_t e = (gi + (int64_t)u * nthreads) << 2;
+                static_for<NIN>([&]<int I>() {
+                    ld4<U8MASK, I>(p, g.ioff[I] + (unit[I] ? e : 0), unit[I], v[u][I], (g.streamed >> I) & 1u);
+                });
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int64_t e = (gi + (int64_t)u * nthreads) << 2;
+                float r[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    float a[NIN > 0 ? NIN : 1];
+#pragma unroll
+                    for (int i = 0; i < NIN; i++) a[i] = v[u][i][k];
+                    r[k] = f(a);
+                }
+                st4(out + e, r);
+            }
+        }
+        for (; gi < groups; gi += nthreads) {
+            const int64_t e = gi << 2;
+            float v[NIN > 0 ? NIN : 1][4];
+            static_for<NIN>([&]<int I>() {
+                ld4<U8MASK, I>(p, g.ioff[I] + (unit[I] ? e : 0), unit[I], v[I], (g.streamed >> I) & 1u);
+            });
+            float r[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float a[NIN > 0 ? NIN : 1];
+#pragma unroll
+                for (int i = 0; i < NIN; i++) a[i] = v[i][k];
+                r[k] = f(a);
+            }
+            st4(out + e, r);
+        }
+        tail_start = groups << 2;
+    }
+    for (int64_t e = tail_start + tid; e < n; e += nthreads) {
+        float a[NIN > 0 ? NIN : 1];
+        static_for<NIN>([&]<int I>() { a[I] = ld1<U8MASK, I>(p, g.ioff[I] + (unit[I] ? e : 0)); });
+        out[e] = f(a);
+    }
+}
+
+// ---- pw_rows --------------------------------------------------------------
+// Innermost dim (size[rank-1] columns) has ostride 1 and istride in {0, 1}.
+// g.rows = product of the outer dims, g.chunks = ceil(cols / kRowChunk).
+// VEC: cols % 4 == 0 and every unit-stride row start 16-byte aligned.
+template <class F, unsigned U8MASK, bool VEC>
+__device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const PwPtrs &p) {
+    constexpr int NIN = F::NIN;
+    const int inner = g.rank - 1;
+    const int64_t cols = g.size[inner];
+    const int64_t ntiles = g.rows * g.chunks;
+    bool unit[NIN > 0 ? NIN : 1];
+    for (int i = 0; i < NIN; i++) unit[i] = g.istride[i][inner] != 0;
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        // Wave-uniform decode of the outer tuple (held in scalar registers).
+        const int64_t row = tile / g.chunks;
+        const int64_t chunk = tile - row * g.chunks;
+        int64_t oo, io[NIN > 0 ? NIN : 1];
+        decode_outer<NIN>(g, inner, row, oo, io);
+        const int64_t c0 = chunk * kRowChunk;
+        if constexpr (VEC) {
+            const int64_t c = c0 + (int64_t)threadIdx.x * 4;
+            if (c < cols) {
+                float v[NIN > 0 ? NIN : 1][4];
+                static_for<NIN>([&]<int I>() {
+                    ld4<U8MASK, I>(p, io[I] + (unit[I] ? c : 0), unit[I], v[I], (g.streamed >> I) & 1u);
+                });
+                float r[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    float a[NIN > 0 ? NIN : 1];
+#pragma unroll
+                    for (int i = 0; i < NIN; i++) a[i] = v[i][k];
+                    r[k] = f(a);
+                }
+                st4(p.out + oo + c, r);
+            }
+        } else {
+            for (int k = 0; k < 4; k++) {
+                const int64_t c = c0 + (int64_t)k * 256 + threadIdx.x;
+                if (c < cols) {
+                    float a[NIN > 0 ? NIN : 1];
+                    static_for<NIN>([&]<int I>() {
+                        a[I] = ld1<U8MASK, I>(p, io[I] + (unit[I] ? c : 0));
+                    });
+                    p.out[oo + c] = f(a);
+                }
+            }
+        }
+    }
+}
+
+// ---- pw_tiled -------------------------------------------------------------
+// Output unit-stride along the innermost dim `x` (size[rank-1]); operands in
+// g.transposed are unit-stride along dim `t` = g.tdim (< rank-1) instead and
+// are staged through a 64x65 LDS tile per operand (padding keeps both the
+// column writes and the row reads free of bank conflicts).  Other operands
+// have stride 0 or 1 along x.  Block = 256 lanes; one 64(t) x 64(x) tile per
+// block iteration.  g.rows = product of the remaining dims, g.ttiles = tiles
+// along t, g.chunks = ttiles * tiles along x.
+template <class F, unsigned U8MASK, bool VEC, int NT>
+__device__ __forceinline__ void pw_tiled_body(const F &f, const PwGeom &g, const PwPtrs &p) {
+    constexpr int NIN = F::NIN;
+    __shared__ float lds[NT > 0 ? NT : 1][kTile][kTile + 1];
+    const int xd = g.rank - 1;
+    const int td = g.tdim;
+    const int64_t xs = g.size[xd], ts = g.size[td];
+    const int64_t ntiles = g.rows * g.chunks;
+    const int lane = threadIdx.x;
+    // Map transposed input index -> LDS slot.
+    int slot[NIN > 0 ? NIN : 1];
+    {
+        int s = 0;
+        for (int i = 0; i < NIN; i++) slot[i] = ((g.transposed >> i) & 1u) ? s++ : -1;
+    }
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t outer = tile / g.chunks;
+        const int64_t rest = tile - outer * g.chunks;
+        const int64_t tt = rest % g.ttiles;
+        const int64_t xt = rest / g.ttiles;
+        // Decode the outer tuple over all dims except t and x (wave-uniform).
+        int64_t oo = g.ooff, io[NIN > 0 ? NIN : 1];
+        for (int i = 0; i < NIN; i++) io[i] = g.ioff[i];
+        {
+            int64_t rem = outer;
+            for (int d = xd - 1; d >= 0; d--) {
+                if (d == td) continue;
+                const int64_t c = rem % g.size[d];
+                rem /= g.size[d];
+                oo += c * g.ostride[d];
+                for (int i = 0; i < NIN; i++) io[i] += c * g.istride[i][d];
+            }
+        }
+        const int64_t t0 = tt * kTile, x0 = xt * kTile;
+        // Stage transposed operands: lane reads 4 consecutive t at one x.
+        if constexpr (NT > 0) {
+            const int a = lane & 15;  // t group
+            const int b0 = lane >> 4; // x row (0..15), +16j
+            static_for<NIN>([&]<int I>() {
+                if (slot[I] >= 0) {
+                    for (int j = 0; j < 4; j++) {
+                        const int xb = b0 + 16 * j;
+                        const int64_t x = x0 + xb;
+                        const int64_t t = t0 + 4 * a;
+                        const int64_t base = io[I] + x * g.istride[I][xd] + t;
+                        if (VEC && x < xs && t + 3 < ts) {
+                            float v[4];
+                            ld4<U8MASK, I>(p, base, true, v, (g.streamed >> I) & 1u);
+                            for (int k = 0; k < 4; k++) lds[slot[I]][4 * a + k][xb] = v[k];
+                        } else {
+                            for (int k = 0; k < 4; k++) {
+                                lds[slot[I]][4 * a + k][xb] =
+                                    (x < xs && t + k < ts) ? ld1<U8MASK, I>(p, base + k) : 0.0f;
+                            }
+                        }
+                    }
+                }
+            });
+            __syncthreads();
+        }
+        // Compute: lane handles 4 consecutive x at t rows (lane>>4) + 16j.
+        {
+            const int c = lane & 15;
+            const int r0 = lane >> 4;
+            for (int j = 0; j < 4; j++) {
+                const int tb = r0 + 16 * j;
+                const int64_t t = t0 + tb;
+                const int64_t x = x0 + 4 * c;
+                if (t >= ts) continue;
+                const int64_t ob = oo + t * g.ostride[td] + x;
+                float v[NIN > 0 ? NIN : 1][4];
+                const bool full = VEC && x + 3 < xs;
+                static_for<NIN>([&]<int I>() {
+                    if (slot[I] >= 0) {
+                        for (int k = 0; k < 4; k++) v[I][k] = lds[slot[I]][tb][4 * c + k];
+                    } else {
+                        const bool unit = g.istride[I][xd] != 0;
+                        const int64_t base = io[I] + t * g.istride[I][td] + (unit ? x : 0);
+                        if (full) {
+                            ld4<U8MASK, I>(p, base, unit, v[I], (g.streamed >> I) & 1u);
+                        } else {
+                            for (int k = 0; k < 4; k++)
+                                v[I][k] = (x + k < xs) ? ld1<U8MASK, I>(p, base + (unit ? k : 0)) : 0.0f;
+                        }
+                    }
+                });
+                float r[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    float a[NIN > 0 ? NIN : 1];
+#pragma unroll
+                    for (int i = 0; i < NIN; i++) a[i] = v[i][k];
+                    r[k] = f(a);
+                }
+                if (full) {
+                    st4(p.out + ob, r);
+                } else {
+                    for (int k = 0; k < 4; k++)
+                        if (x + k < xs) p.out[ob + k] = r[k];
+                }
+            }
+        }
+        if constexpr (NT > 0) __syncthreads();
+    }
+}
+
+// ---- pw_generic -----------------------------------------------------------
+template <class F, unsigned U8MASK>
+__device__ __forceinline__ void pw_generic_body(const F &f, const PwGeom &g, const PwPtrs &p) {
+    constexpr int NIN = F::NIN;
+    const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < g.numel; e += nthreads) {
+        int64_t oo, io[NIN > 0 ? NIN : 1];
+        decode_outer<NIN>(g, g.rank, e, oo, io);
+        float a[NIN > 0 ? NIN : 1];
+        static_for<NIN>([&]<int I>() { a[I] = ld1<U8MASK, I>(p, io[I]); });
+        p.out[oo] = f(a);
+    }
+}
+
+// ---- scalar semantics of the reference ------------------------------------
+
+// relu_value (src/tensor.rs:4392-4400): exact zeros (either sign) pass
+// through; otherwise max(v, 0) with NaN -> +0.0.
+__device__ __forceinline__ float relu_value(float v) {
+    if ((__float_as_uint(v) & 0x7fffffffu) == 0u) return v;
+    return v > 0.0f ? v : 0.0f;
+}
+
+// relu_backward_value (src/tensor.rs:4422-4432).
+__device__ __forceinline__ float relu_backward_value(float input, float up) {
+    const uint32_t bits = __float_as_uint(input);
+    const uint32_t mag = bits & 0x7fffffffu;
+    const bool pass = mag > 0x7f800000u || ((bits & 0x80000000u) == 0u && mag != 0u);
+    return pass ? up : 0.0f;
+}
+
+// negate_value (src/tensor.rs:4388-4390): sign-bit flip.
+__device__ __forceinline__ float negate_value(float v) {
+    return __uint_as_float(__float_as_uint(v) ^ 0x80000000u);
+}
+
+// exp: the device libm expf (ocml, about 1 ulp, denormal outputs kept).
+__device__ __forceinline__ float exp_value(float v) { return expf(v); }
+
+}  // namespace trs

@@ -1,0 +1,243 @@
+// pw_host.h -- host-side launch planning for the pointwise engine (pw_core.h).
+//
+// plan_pointwise() turns (output layout, input layouts) into a normalised
+// PwGeom and picks the kernel variant:
+//   1. align inputs to the output rank (right-aligned broadcasting,
+//      BroadcastPlan in src/tensor.rs:3601-3693): stride 0 on broadcast dims;
+//   2. drop size-1 dims, order dims by decreasing output stride so the kernel
+//      walks the output in physical order, and merge adjacent dims that are
+//      contiguous for every operand;
+//   3. choose flat / rows / tiled / generic and whether 16-byte vector
+//      accesses are legal (alignment of every unit-stride operand).
+#pragma once
+
+#include <cstdint>
+#include <cstring>
+
+#include "pw_core.h"
+#include "trs_internal.h"
+
+namespace trs {
+
+enum class PwVariant { Empty, Flat, Rows, Tiled, Generic };
+
+struct PwPlan {
+    PwVariant variant = PwVariant::Empty;
+    bool vec = false;
+    int ntransposed = 0;
+    int nin = 0;
+    int64_t grid = 0;
+    PwGeom g;
+    PwPtrs p;
+};
+
+inline FastDiv make_fast_div(uint32_t d) {
+    FastDiv f{};
+    f.div = d;
+    uint32_t shift = 0;
+    while (shift < 32 && (1ull << shift) < d) shift++;
+    const uint64_t two32 = 1ull << 32;
+    const uint64_t m = (two32 * ((1ull << shift) - d)) / d + 1;
+    f.mul = (uint32_t)m;
+    f.shift = shift;
+    return f;
+}
+
+// `elem_bytes[i]` is 4 for f32 inputs and 1 for u8 inputs.
+inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void *const *bases,
+                          const trs_layout *const *lins, const int *elem_bytes, int cu_count,
+                          PwPlan *plan) {
+    int rc = check_layout(lo, "output");
+    if (rc) return rc;
+    if (nin > kMaxIn) return set_error(TRS_E_INVALID_ARGUMENT, "too many pointwise inputs (%d)", nin);
+    for (int i = 0; i < nin; i++) {
+        rc = check_layout(lins[i], "input");
+        if (rc) return rc;
+        if (lins[i]->rank > lo->rank)
+            return set_error(TRS_E_SHAPE_MISMATCH, "input %d has rank %d above the output rank %d", i,
+                             lins[i]->rank, lo->rank);
+        const int lead = lo->rank - lins[i]->rank;
+        for (int d = 0; d < lins[i]->rank; d++) {
+            const int64_t s = lins[i]->shape[d], o = lo->shape[lead + d];
+            if (s != o && s != 1)
+                return set_error(TRS_E_SHAPE_MISMATCH,
+                                 "The size of tensor a (%lld) must match the size of tensor b "
+                                 "(%lld) at non-singleton dimension %d",
+                                 (long long)s, (long long)o, lead + d);
+        }
+    }
+    *plan = PwPlan{};
+    plan->nin = nin;
+    PwGeom &g = plan->g;
+    std::memset(&g, 0, sizeof(g));
+    plan->p.out = out;
+    for (int i = 0; i < nin; i++) plan->p.in[i] = bases[i];
+
+    int64_t numel = layout_numel(lo);
+    if (numel == 0) {
+        plan->variant = PwVariant::Empty;
+        return TRS_OK;
+    }
+    if (out == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "null output pointer");
+    for (int i = 0; i < nin; i++)
+        if (bases[i] == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "null input pointer %d", i);
+
+    // 1-2. align, drop singleton dims.
+    int rank = 0;
+    int64_t size[kMaxRank], os[kMaxRank], is[kMaxIn][kMaxRank];
+    for (int d = 0; d < lo->rank; d++) {
+        if (lo->shape[d] == 1) continue;
+        size[rank] = lo->shape[d];
+        os[rank] = lo->stride[d];
+        for (int i = 0; i < nin; i++) {
+            const int lead = lo->rank - lins[i]->rank;
+            is[i][rank] = (d < lead || lins[i]->shape[d - lead] == 1) ? 0 : lins[i]->stride[d - lead];
+        }
+        rank++;
+    }
+    // Order by decreasing output stride (stable insertion sort).
+    for (int a = 1; a < rank; a++) {
+        for (int b = a; b > 0 && os[b - 1] < os[b]; b--) {
+            std::swap(size[b - 1], size[b]);
+            std::swap(os[b - 1], os[b]);
+            for (int i = 0; i < nin; i++) std::swap(is[i][b - 1], is[i][b]);
+        }
+    }
+    // The output must not overlap itself (each element written once).
+    for (int d = 0; d + 1 < rank; d++) {
+        if (os[d] < os[d + 1] * size[d + 1])
+            return set_error(TRS_E_INVALID_ARGUMENT, "output layout overlaps itself");
+    }
+    if (rank > 0 && os[rank - 1] == 0)
+        return set_error(TRS_E_INVALID_ARGUMENT, "output layout overlaps itself");
+    // Merge dims that are contiguous for every operand.
+    {
+        int w = rank - 1;  // merge outward into the innermost kept dim
+        int64_t nsize[kMaxRank], nos[kMaxRank], nis[kMaxIn][kMaxRank];
+        int nr = 0;
+        // Walk from innermost to outermost, building reversed list.
+        for (int d = rank - 1; d >= 0; d--) {
+            if (nr > 0) {
+                const int q = nr - 1;
+                bool ok = os[d] == nos[q] * nsize[q];
+                for (int i = 0; ok && i < nin; i++) ok = is[i][d] == nis[i][q] * nsize[q];
+                if (ok) {
+                    nsize[q] *= size[d];
+                    continue;
+                }
+            }
+            nsize[nr] = size[d];
+            nos[nr] = os[d];
+            for (int i = 0; i < nin; i++) nis[i][nr] = is[i][d];
+            nr++;
+        }
+        (void)w;
+        rank = nr;
+        for (int d = 0; d < rank; d++) {
+            size[d] = nsize[rank - 1 - d];
+            os[d] = nos[rank - 1 - d];
+            for (int i = 0; i < nin; i++) is[i][d] = nis[i][rank - 1 - d];
+        }
+    }
+    if (rank == 0) {  // a single element
+        rank = 1;
+        size[0] = 1;
+        os[0] = 1;
+        for (int i = 0; i < nin; i++) is[i][0] = 0;
+    }
+
+    g.rank = rank;
+    g.numel = numel;
+    g.ooff = lo->offset;
+    for (int d = 0; d < rank; d++) {
+        g.size[d] = size[d];
+        g.ostride[d] = os[d];
+        if (size[d] > (int64_t)UINT32_MAX) g.wide = 1;
+        g.fd[d] = make_fast_div(size[d] > (int64_t)UINT32_MAX ? 1u : (uint32_t)size[d]);
+    }
+    for (int i = 0; i < nin; i++) {
+        g.ioff[i] = lins[i]->offset;
+        bool bcast = false;
+        for (int d = 0; d < rank; d++) {
+            g.istride[i][d] = is[i][d];
+            bcast |= is[i][d] == 0;
+        }
+        if (!bcast) g.streamed |= 1u << i;
+    }
+
+    // Alignment of a unit-stride access along dim `ud` for operand bytes.
+    auto aligned = [&](const void *base, int64_t off, const int64_t *strides, int ud, int eb) {
+        const uint64_t addr = (uint64_t)(uintptr_t)base + (uint64_t)off * (uint64_t)eb;
+        if (addr % (uint64_t)(4 * eb) != 0) return false;
+        for (int d = 0; d < rank; d++)
+            if (d != ud && strides[d] % 4 != 0) return false;
+        return true;
+    };
+
+    const int inner = rank - 1;
+    bool unit_or_bcast = os[inner] == 1;
+    for (int i = 0; i < nin; i++) unit_or_bcast &= is[i][inner] == 0 || is[i][inner] == 1;
+    const int64_t want = (int64_t)cu_count * 16;
+
+    if (unit_or_bcast) {
+        bool vec = aligned(out, lo->offset, os, inner, 4);
+        for (int i = 0; i < nin; i++)
+            if (is[i][inner] == 1) vec &= aligned(bases[i], g.ioff[i], is[i], inner, elem_bytes[i]);
+        if (rank == 1) {
+            plan->variant = PwVariant::Flat;
+            plan->vec = vec;
+            const int64_t work = vec ? (numel / 4) / 4 : numel;
+            plan->grid = std::min<int64_t>(std::max<int64_t>(1, (work + 255) / 256), want);
+        } else {
+            plan->variant = PwVariant::Rows;
+            plan->vec = vec && size[inner] % 4 == 0;
+            g.rows = numel / size[inner];
+            g.chunks = (size[inner] + kRowChunk - 1) / kRowChunk;
+            plan->grid = std::min<int64_t>(g.rows * g.chunks, want);
+        }
+        return TRS_OK;
+    }
+
+    // Transposed operands: unit stride along one common dim t < inner.
+    if (os[inner] == 1 && rank >= 2) {
+        int tdim = -1;
+        bool ok = true;
+        uint32_t tmask = 0;
+        for (int i = 0; i < nin && ok; i++) {
+            if (is[i][inner] == 0 || is[i][inner] == 1) continue;
+            int t = -1;
+            for (int d = 0; d < inner; d++)
+                if (is[i][d] == 1) t = d;
+            if (t < 0 || (tdim >= 0 && t != tdim)) ok = false;
+            tdim = t;
+            tmask |= 1u << i;
+        }
+        int nt = __builtin_popcount(tmask);
+        if (ok && tdim >= 0 && nt <= 4) {
+            plan->variant = PwVariant::Tiled;
+            plan->ntransposed = nt;
+            g.tdim = tdim;
+            g.transposed = tmask;
+            bool vec = aligned(out, lo->offset, os, inner, 4);
+            for (int i = 0; i < nin; i++) {
+                if ((tmask >> i) & 1u) {
+                    vec &= aligned(bases[i], g.ioff[i], is[i], tdim, elem_bytes[i]);
+                } else if (is[i][inner] == 1) {
+                    vec &= aligned(bases[i], g.ioff[i], is[i], inner, elem_bytes[i]);
+                }
+            }
+            plan->vec = vec;
+            g.ttiles = (size[tdim] + kTile - 1) / kTile;
+            const int64_t xtiles = (size[inner] + kTile - 1) / kTile;
+            g.chunks = g.ttiles * xtiles;
+            g.rows = numel / (size[tdim] * size[inner]);
+            plan->grid = std::min<int64_t>(g.rows * g.chunks, want);
+            return TRS_OK;
+        }
+    }
+    plan->variant = PwVariant::Generic;
+    plan->grid = std::min<int64_t>(std::max<int64_t>(1, (numel + 255) / 256), want);
+    return TRS_OK;
+}
+
+}  // namespace trs

@@ -1,0 +1,296 @@
+// runtime.hip -- device selection, memory and streams for libtrs_hip.so.
+//
+// Replaces the reference's storage/device layer (src/storage.rs:7-18,
+// src/device.rs:5-9), which only knows a CPU Vec<f32>: here storage is HBM
+// owned by the caller through trs_alloc/trs_free, and all work is ordered on
+// one stream per device.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "trs_internal.h"
+
+namespace trs {
+
+namespace {
+
+thread_local std::string g_last_error;
+thread_local int g_device = 0;
+
+constexpr int kMaxDevices = 16;
+DeviceState g_devices[kMaxDevices];
+std::mutex g_init_mu;
+int g_device_count = -1;
+
+__global__ void __launch_bounds__(256) fill_u32_kernel(uint32_t *dst, size_t n, uint32_t value) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = value;
+}
+
+__global__ void __launch_bounds__(256) fill_u8_kernel(uint8_t *dst, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = 0;
+}
+
+int count_devices() {
+    std::lock_guard<std::mutex> lock(g_init_mu);
+    if (g_device_count < 0) {
+        int n = 0;
+        hipError_t e = hipGetDeviceCount(&n);
+        if (e != hipSuccess) {
+            g_device_count = 0;
+            return set_error(TRS_E_NO_DEVICE, "hipGetDeviceCount failed: %s", hipGetErrorString(e));
+        }
+        g_device_count = n < kMaxDevices ? n : kMaxDevices;
+    }
+    return TRS_OK;
+}
+
+}  // namespace
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return set_error(TRS_E_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+int check_layout(const trs_layout *l, const char *what) {
+    if (l == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "%s layout is null", what);
+    if (l->rank < 0 || l->rank > TRS_MAX_RANK)
+        return set_error(TRS_E_INVALID_ARGUMENT, "%s rank %d outside [0, 8]", what, l->rank);
+    if (l->offset < 0) return set_error(TRS_E_INVALID_ARGUMENT, "%s offset is negative", what);
+    for (int d = 0; d < l->rank; d++) {
+        if (l->shape[d] < 0 || l->stride[d] < 0)
+            return set_error(TRS_E_INVALID_ARGUMENT, "%s dim %d has a negative size or stride", what, d);
+    }
+    return TRS_OK;
+}
+
+int64_t layout_numel(const trs_layout *l) {
+    int64_t n = 1;
+    for (int d = 0; d < l->rank; d++) n *= l->shape[d];
+    return n;
+}
+
+bool layout_is_contiguous(const trs_layout *l) {
+    if (layout_numel(l) == 0) return true;
+    int64_t expected = 1;
+    for (int d = l->rank - 1; d >= 0; d--) {
+        if (l->shape[d] == 1) continue;
+        if (l->stride[d] != expected) return false;
+        expected *= l->shape[d];
+    }
+    return true;
+}
+
+DeviceState *device_state() {
+    if (count_devices() != TRS_OK) return nullptr;
+    if (g_device_count == 0) {
+        set_error(TRS_E_NO_DEVICE, "no HIP device is visible");
+        return nullptr;
+    }
+    if (g_device < 0 || g_device >= g_device_count) {
+        set_error(TRS_E_INVALID_ARGUMENT, "device %d out of range", g_device);
+        return nullptr;
+    }
+    DeviceState *dev = &g_devices[g_device];
+    std::lock_guard<std::mutex> lock(dev->mu);
+    if (dev->ready) {
+        if (hipSetDevice(g_device) != hipSuccess) {
+            set_error(TRS_E_HIP, "hipSetDevice(%d) failed", g_device);
+            return nullptr;
+        }
+        return dev;
+    }
+    hipError_t e = hipSetDevice(g_device);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipSetDevice");
+        return nullptr;
+    }
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, g_device);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipGetDeviceProperties");
+        return nullptr;
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_error(TRS_E_NO_DEVICE, "device %d is %s; this library is built for gfx950 only", g_device,
+                  prop.gcnArchName);
+        return nullptr;
+    }
+    // Default-priority stream (never a prioritised one).
+    e = hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipStreamCreate");
+        return nullptr;
+    }
+    dev->index = g_device;
+    dev->cu_count = prop.multiProcessorCount;
+    dev->clock_khz = prop.clockRate;
+    std::snprintf(dev->name, sizeof dev->name, "%s", prop.name);
+    dev->ready = true;
+    return dev;
+}
+
+int ensure_scratch(DeviceState *dev, size_t bytes) {
+    std::lock_guard<std::mutex> lock(dev->mu);
+    if (dev->scratch_bytes >= bytes) return TRS_OK;
+    if (dev->scratch) {
+        // Stream-ordered reuse: wait for queued users before replacing it.
+        TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "scratch sync");
+        TRS_HIP_CHECK(hipFree(dev->scratch), "scratch free");
+        dev->scratch = nullptr;
+        dev->scratch_bytes = 0;
+    }
+    TRS_HIP_CHECK(hipMalloc(&dev->scratch, bytes), "scratch alloc");
+    dev->scratch_bytes = bytes;
+    return TRS_OK;
+}
+
+}  // namespace trs
+
+using namespace trs;
+
+extern "C" {
+
+const char *trs_last_error(void) { return g_last_error.c_str(); }
+
+int trs_init(void) {
+    DeviceState *dev = device_state();
+    return dev ? TRS_OK : TRS_E_NO_DEVICE;
+}
+
+int trs_device_count(int *count) {
+    if (!count) return set_error(TRS_E_INVALID_ARGUMENT, "null count");
+    int rc = count_devices();
+    *count = g_device_count < 0 ? 0 : g_device_count;
+    return rc;
+}
+
+int trs_set_device(int device) {
+    int rc = count_devices();
+    if (rc) return rc;
+    if (device < 0 || device >= g_device_count)
+        return set_error(TRS_E_INVALID_ARGUMENT, "device %d out of range [0, %d)", device, g_device_count);
+    g_device = device;
+    return device_state() ? TRS_OK : TRS_E_HIP;
+}
+
+int trs_get_device(int *device) {
+    if (!device) return set_error(TRS_E_INVALID_ARGUMENT, "null device");
+    *device = g_device;
+    return TRS_OK;
+}
+
+int trs_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (name && name_len) std::snprintf(name, name_len, "%s", dev->name);
+    if (cu_count) *cu_count = dev->cu_count;
+    if (clock_khz) *clock_khz = dev->clock_khz;
+    return TRS_OK;
+}
+
+int trs_alloc(size_t bytes, void **ptr) {
+    if (!ptr) return set_error(TRS_E_INVALID_ARGUMENT, "null out pointer");
+    *ptr = nullptr;
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (bytes == 0) return TRS_OK;
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess) {
+        *ptr = nullptr;
+        (void)hipGetLastError();
+        return set_error(TRS_E_ALLOCATION_FAILED, "hipMalloc of %zu bytes failed: %s", bytes,
+                         hipGetErrorString(e));
+    }
+    return TRS_OK;
+}
+
+int trs_free(void *ptr) {
+    if (!ptr) return TRS_OK;
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    // Memory may still be read by queued work: drain the stream first.
+    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "free sync");
+    TRS_HIP_CHECK(hipFree(ptr), "hipFree");
+    return TRS_OK;
+}
+
+int trs_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (bytes == 0) return TRS_OK;
+    if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in h2d copy");
+    // Pageable host memory: the runtime stages the copy; returning after
+    // hipMemcpyAsync means `src` has been consumed.
+    TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream), "h2d copy");
+    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "h2d sync");
+    return TRS_OK;
+}
+
+int trs_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (bytes == 0) return TRS_OK;
+    if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in d2h copy");
+    TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream), "d2h copy");
+    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "d2h sync");
+    return TRS_OK;
+}
+
+int trs_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (bytes == 0) return TRS_OK;
+    if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in d2d copy");
+    TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev->stream), "d2d copy");
+    return TRS_OK;
+}
+
+int trs_memset_zero(void *dst, size_t bytes) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (bytes == 0) return TRS_OK;
+    if (!dst) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in memset");
+    const int64_t want = (int64_t)dev->cu_count * 8;
+    if (bytes % 4 == 0 && ((uintptr_t)dst % 4) == 0) {
+        const size_t n = bytes / 4;
+        const int64_t grid = std::min<int64_t>(std::max<int64_t>(1, (int64_t)((n + 255) / 256)), want);
+        hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream,
+                           (uint32_t *)dst, n, 0u);
+    } else {
+        const int64_t grid = std::min<int64_t>(std::max<int64_t>(1, (int64_t)((bytes + 255) / 256)), want);
+        hipLaunchKernelGGL(fill_u8_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream,
+                           (uint8_t *)dst, bytes);
+    }
+    TRS_LAUNCH_CHECK("memset kernel");
+    return TRS_OK;
+}
+
+int trs_synchronize(void) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "synchronize");
+    return TRS_OK;
+}
+
+int trs_stream(void **stream) {
+    if (!stream) return set_error(TRS_E_INVALID_ARGUMENT, "null stream out pointer");
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    *stream = (void *)dev->stream;
+    return TRS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,56 @@
+// trs_internal.h -- host-side internals shared by the libtrs_hip.so sources.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <mutex>
+
+#include "trs_hip.h"
+
+namespace trs {
+
+// Per-device state: one in-order stream carries every entry point's work, so
+// stream order gives the reference's eager semantics.
+struct DeviceState {
+    int index = -1;
+    bool ready = false;
+    hipStream_t stream = nullptr;
+    int cu_count = 0;
+    int clock_khz = 0;
+    char name[256] = {0};
+    // Stream-ordered scratch for multi-pass kernels (partial sums).  Reused in
+    // stream order; guarded by `mu` only for (re)allocation.
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+    std::mutex mu;
+};
+
+// Returns the current device's state, initialising it on first use.
+// On failure returns nullptr with the error recorded.
+DeviceState *device_state();
+
+// Ensures dev->scratch holds at least `bytes`; returns TRS_OK or an error.
+int ensure_scratch(DeviceState *dev, size_t bytes);
+
+// Records a thread-local error message and returns `code`.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps a HIP failure to TRS_E_HIP with the runtime's message.
+int hip_fail(hipError_t e, const char *what);
+
+// Validates rank (0..8), non-negative shape/stride/offset.
+int check_layout(const trs_layout *l, const char *what);
+int64_t layout_numel(const trs_layout *l);
+bool layout_is_contiguous(const trs_layout *l);
+
+#define TRS_HIP_CHECK(expr, what)                 \
+    do {                                          \
+        hipError_t trs_e_ = (expr);               \
+        if (trs_e_ != hipSuccess) return ::trs::hip_fail(trs_e_, what); \
+    } while (0)
+
+// A launch's error surfaces from hipGetLastError right after the launch.
+#define TRS_LAUNCH_CHECK(what) TRS_HIP_CHECK(hipGetLastError(), what)
+
+}  // namespace trs

@@ -1,0 +1,161 @@
+"""Secondary benchmark configurations reported under bench.py's "extra".
+
+Each returns device-time figures measured with HIP events on the library
+stream.  Working sets that fit the 256 MB Infinity Cache are rotated over
+several buffer sets so the GB/s figures reflect HBM.
+"""
+from __future__ import annotations
+
+import ctypes
+import statistics
+
+import numpy as np
+
+from . import abi
+from .abi import DeviceArray, check, layout_of
+from .configs import generate
+from .timing import time_launches
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def _fusion(ir: str) -> int:
+    kid = ctypes.c_uint64()
+    check(abi.lib.trs_fusion_compile(ir.encode(), len(ir), ctypes.byref(kid)))
+    return kid.value
+
+
+def _fuse_launch(kid, devs, lays, out, lo):
+    n = len(devs)
+    ptrs = (ctypes.c_void_p * n)(*[d.addr for d in devs])
+    la = (abi.Layout * n)(*lays)
+    check(abi.lib.trs_fusion_launch(kid, n, ptrs, la, out.ptr, ctypes.byref(lo)))
+
+
+def relu_bias(log, reps: int = 20, sets: int = 3) -> dict:
+    """Config 0: relu(x + b), x [4096,4096], b [4096] row-broadcast, seed 0."""
+    R = C = 4096
+    x = generate("relu_bias", "x")
+    b = generate("relu_bias", "b")
+    xs = [DeviceArray.from_numpy(x) for _ in range(sets)]
+    outs = [DeviceArray(R * C * 4) for _ in range(sets)]
+    tmp = [DeviceArray(R * C * 4) for _ in range(sets)]
+    db = DeviceArray.from_numpy(b)
+    lx, lb = layout_of((R, C)), layout_of((C,))
+    algo = 2 * R * C * 4 + C * 4
+    i = [0]
+
+    def eager():
+        k = i[0] % sets
+        i[0] += 1
+        check(abi.lib.trs_binary_f32(0, xs[k].ptr, ctypes.byref(lx), db.ptr, ctypes.byref(lb), tmp[k].ptr,
+                                     ctypes.byref(lx)))
+        check(abi.lib.trs_unary_f32(1, tmp[k].ptr, ctypes.byref(lx), outs[k].ptr, ctypes.byref(lx)))
+
+    kid = _fusion("in f32\nin f32\nadd %0 %1\nrelu %2\nout %3\n")
+
+    def fused():
+        k = i[0] % sets
+        i[0] += 1
+        _fuse_launch(kid, [xs[k], db], [lx, lb], outs[k], lx)
+
+    e = statistics.median(time_launches(eager, reps))
+    f = statistics.median(time_launches(fused, reps))
+    log(f"relu_bias: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us")
+    return {"relu_bias": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
+                          "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
+                          "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+
+
+def broadcast_strided(log, reps: int = 20, sets: int = 2) -> dict:
+    """Config 2: (a + b) * c.mT, a [64,1,1024], b [1,512,1024], c [64,1024,512]."""
+    B, M, N = 64, 512, 1024
+    a = generate("broadcast_strided", "a")
+    b = generate("broadcast_strided", "b")
+    c = generate("broadcast_strided", "c")
+    da, db = DeviceArray.from_numpy(a), DeviceArray.from_numpy(b)
+    dcs = [DeviceArray.from_numpy(c) for _ in range(sets)]
+    outs = [DeviceArray(B * M * N * 4) for _ in range(sets)]
+    tmps = [DeviceArray(B * M * N * 4) for _ in range(sets)]
+    la, lb = layout_of((B, 1, N)), layout_of((1, M, N))
+    lc = layout_of((B, M, N), (N * M, 1, M))
+    lo = layout_of((B, M, N))
+    algo = (B * N + M * N + B * N * M + B * M * N) * 4
+    i = [0]
+
+    def eager():
+        k = i[0] % sets
+        i[0] += 1
+        check(abi.lib.trs_binary_f32(0, da.ptr, ctypes.byref(la), db.ptr, ctypes.byref(lb), tmps[k].ptr,
+                                     ctypes.byref(lo)))
+        check(abi.lib.trs_binary_f32(2, tmps[k].ptr, ctypes.byref(lo), dcs[k].ptr, ctypes.byref(lc), outs[k].ptr,
+                                     ctypes.byref(lo)))
+
+    kid = _fusion("in f32\nin f32\nin f32\nadd %0 %1\nmul %3 %2\nout %4\n")
+
+    def fused():
+        k = i[0] % sets
+        i[0] += 1
+        _fuse_launch(kid, [da, db, dcs[k]], [la, lb, lc], outs[k], lo)
+
+    e = statistics.median(time_launches(eager, reps))
+    f = statistics.median(time_launches(fused, reps))
+    log(f"broadcast_strided: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us")
+    return {"broadcast_strided": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
+                                  "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
+                                  "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+
+
+def matmul(log, reps: int = 10) -> dict:
+    """Config 3: A @ B 4096^3 and batched [32,512,512]^2, fp32, N(0, 1/sqrt(K)), seed 3."""
+    out = {}
+    K = 4096
+    A, Bm = generate("matmul", "A"), generate("matmul", "B")
+    dA, dB, dC = DeviceArray.from_numpy(A), DeviceArray.from_numpy(Bm), DeviceArray(K * K * 4)
+    l = layout_of((K, K))
+
+    def mm():
+        check(abi.lib.trs_matmul_f32(dA.ptr, ctypes.byref(l), dB.ptr, ctypes.byref(l), dC.ptr, ctypes.byref(l)))
+
+    t = time_launches(mm, reps)
+    med = statistics.median(t)
+    tf = 2 * K ** 3 / (med * 1e-3) / 1e12
+    out["matmul_4096"] = {"ms_median": med, "ms_min": min(t), "TFLOPS": tf, "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS}
+    log(f"matmul 4096^3: {med:.3f} ms, {tf:.1f} TFLOPS")
+    Ab, Bb = generate("matmul", "Ab"), generate("matmul", "Bb")
+    dAb, dBb, dCb = DeviceArray.from_numpy(Ab), DeviceArray.from_numpy(Bb), DeviceArray(32 * 512 * 512 * 4)
+    lb = layout_of((32, 512, 512))
+
+    def bmm():
+        check(abi.lib.trs_matmul_f32(dAb.ptr, ctypes.byref(lb), dBb.ptr, ctypes.byref(lb), dCb.ptr,
+                                     ctypes.byref(lb)))
+
+    t = time_launches(bmm, reps * 3)
+    med = statistics.median(t)
+    tf = 2 * 32 * 512 ** 3 / (med * 1e-3) / 1e12
+    out["matmul_batched_32x512"] = {"ms_median": med, "ms_min": min(t), "TFLOPS": tf,
+                                    "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS}
+    log(f"batched matmul 32x512^3: {med:.3f} ms, {tf:.1f} TFLOPS")
+    return out
+
+
+def mlp(log, reps: int = 5) -> dict:
+    """Config 4: 2-layer MLP forward+backward through the torch_rs API on the device."""
+    try:
+        import torch_rs  # noqa: F401
+    except Exception as exc:  # the host engine is optional for this report
+        return {"mlp": {"skipped": repr(exc)}}
+    from . import mlp_bench
+    return {"mlp": mlp_bench.run(log, reps)}
+
+
+def run_all(log) -> dict:
+    res = {}
+    for fn in (relu_bias, broadcast_strided, matmul, mlp):
+        try:
+            res.update(fn(log))
+        except Exception as exc:
+            res[fn.__name__] = {"error": repr(exc)}
+            log(f"{fn.__name__} failed: {exc!r}")
+    return res

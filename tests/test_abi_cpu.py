@@ -1,0 +1,103 @@
+"""Host-only checks of the C ABI library and the input generator (no GPU)."""
+import ctypes
+import hashlib
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import golden
+from trs_backend import abi
+from trs_backend.configs import CONFIGS, generate
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_functions():
+    text = (ROOT / "include" / "trs_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(trs_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_entry_point():
+    names = declared_functions()
+    assert len(names) >= 30
+    for name in names:
+        assert hasattr(abi.lib, name), name
+        assert name in abi._SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_binding_declares_nothing_the_header_lacks():
+    assert set(abi._SIGNATURES) <= set(declared_functions())
+
+
+def test_layout_struct_matches_header_size():
+    # int32 rank, int32 reserved, int64 shape[8], int64 stride[8], int64 offset
+    assert ctypes.sizeof(abi.Layout) == 4 + 4 + 8 * 8 + 8 * 8 + 8
+
+
+def test_philox_known_answer_vectors():
+    # Random123 kat_vectors for philox4x32 with 10 rounds.
+    assert abi.philox((0, 0, 0, 0), (0, 0)) == (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)
+    assert abi.philox((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2) == (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)
+    assert abi.philox((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0)) == (
+        0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)
+
+
+def test_generated_inputs_match_committed_hashes():
+    ref = golden("input_sha256.json")
+    for cfg, spec in CONFIGS.items():
+        for name, *_ in spec["tensors"]:
+            arr = generate(cfg, name, ref["prefix_elements"])
+            assert hashlib.sha256(arr.tobytes()).hexdigest() == ref["hashes"][f"{cfg}.{name}"], f"{cfg}.{name}"
+
+
+def test_generator_is_thread_count_independent_and_distributed():
+    a = abi.gen_normal(4, 0, 0.0, 1.0, 300_001, threads=1)
+    b = abi.gen_normal(4, 0, 0.0, 1.0, 300_001, threads=7)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert abs(a.mean()) < 0.01 and abs(a.std() - 1.0) < 0.01
+    u = abi.gen_uniform(1, 2, -4.0, 4.0, 200_000, threads=3)
+    assert u.min() >= -4.0 and u.max() < 4.0 and abs(u.mean()) < 0.05
+    m = abi.gen_mask(4, 3, 0.9, 200_000)
+    assert set(np.unique(m)) <= {0, 1} and abs(m.mean() - 0.9) < 0.005
+
+
+def _compile(ir: str):
+    kid = ctypes.c_uint64()
+    rc = abi.lib.trs_fusion_compile(ir.encode(), len(ir), ctypes.byref(kid))
+    return rc, kid.value
+
+
+def test_fusion_compiler_generates_and_compiles_on_the_host():
+    ir = "in f32\nin f32\nin f32\nmul %0 %1\nadd %3 %2\nexp %4\nconst 0x3f800000\nsub %5 %6\nrelu %7\nout %8\n"
+    rc, kid = _compile(ir)
+    abi.check(rc)
+    n = ctypes.c_size_t()
+    abi.check(abi.lib.trs_fusion_source(kid, None, 0, ctypes.byref(n)))
+    buf = ctypes.create_string_buffer(n.value)
+    abi.check(abi.lib.trs_fusion_source(kid, buf, n.value, None))
+    src = buf.value.decode()
+    assert "v3 = v0 * v1" in src and "v4 = v3 + v2" in src
+    assert "trs::exp_value(v4)" in src and "__uint_as_float(0x3f800000u)" in src
+    assert "trs_fused_flat_v" in src and "trs_fused_tiled_v1" in src
+    ms = ctypes.c_double()
+    abi.check(abi.lib.trs_fusion_compile_ms(kid, ctypes.byref(ms)))
+    assert ms.value > 0
+    # Same IR -> same cached program.
+    rc2, kid2 = _compile(ir)
+    assert rc2 == 0 and kid2 == kid
+
+
+@pytest.mark.parametrize("ir,fragment", [
+    ("in f32\nadd %0 %1\nout %1\n", "bad operand"),
+    ("in f32\nfoo %0\nout %0\n", "unknown instruction"),
+    ("in f32\nrelu %0\n", "no 'out'"),
+    ("const 0x0\nout %0\n", "no inputs"),
+    ("in f64\nout %0\n", "in f32"),
+])
+def test_fusion_compiler_rejects_bad_programs(ir, fragment):
+    rc, _ = _compile(ir)
+    assert rc == -9
+    assert fragment in abi.lib.trs_last_error().decode()

@@ -1,0 +1,157 @@
+"""GPU parity of the reduction and backward entry points against the oracle.
+
+relu VJP, Multiply VJP (with and without broadcast), the add VJP
+(reduce-to-shape), accumulation and fills are bit-exact: the device kernels
+keep the reference's per-element expressions and its output-major
+accumulation order.  sum uses a fixed-order tree, checked within the float
+summation bound against the reference's sequential fold.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import gpu_util as U
+import oracle as O
+from helpers import assert_bitwise_equal, check_bits, f32_from_bits, golden
+from trs_backend import abi
+from trs_backend.abi import check, layout_of
+
+pytestmark = pytest.mark.gpu
+G = golden()
+
+
+def gpu_relu_backward(x, shape, strides, off, up):
+    dx, du = U.dev(x), U.dev(up)
+    n = int(np.prod(shape)) if shape else 1
+    do = U.out_buffer(n)
+    check(abi.lib.trs_relu_backward_f32(dx.ptr, ctypes.byref(layout_of(shape, strides, off)), du.ptr, do.ptr))
+    return do.to_numpy(count=n)
+
+
+def gpu_mul_backward(up, oshape, other, oth_shape, oth_strides, oth_off, self_shape):
+    du, dother = U.dev(up), U.dev(other)
+    n = int(np.prod(self_shape)) if self_shape else 1
+    do = U.out_buffer(n)
+    check(abi.lib.trs_mul_backward_f32(du.ptr, ctypes.byref(layout_of(oshape)), dother.ptr,
+                                       ctypes.byref(layout_of(oth_shape, oth_strides, oth_off)),
+                                       ctypes.byref(layout_of(self_shape)), do.ptr))
+    return do.to_numpy(count=n)
+
+
+def gpu_reduce(up, oshape, self_shape):
+    du = U.dev(up)
+    n = int(np.prod(self_shape)) if self_shape else 1
+    do = U.out_buffer(n)
+    check(abi.lib.trs_reduce_to_shape_f32(du.ptr, ctypes.byref(layout_of(oshape)), ctypes.byref(layout_of(self_shape)),
+                                          do.ptr))
+    return do.to_numpy(count=n)
+
+
+def gpu_sum(x, shape, strides=None, off=0):
+    dx = U.dev(x)
+    do = U.out_buffer(1)
+    check(abi.lib.trs_sum_f32(dx.ptr, ctypes.byref(layout_of(shape, strides, off)), do.ptr))
+    return do.to_numpy(count=1)[0]
+
+
+def test_relu_vjp_golden_bits():
+    g = G["autograd_relu_vjp"]
+    x = f32_from_bits(g["input_bits"])
+    w = f32_from_bits(g["weight_bits"])
+    n = x.size
+    up_relu = gpu_mul_backward(np.ones(n, np.float32), (n,), w, (n,), (1,), 0, (n,))
+    grad = gpu_relu_backward(x, (n,), (1,), 0, up_relu)
+    check_bits(grad, g["expected_gradient_bits"])
+
+
+@pytest.mark.parametrize("shape,strides,off", [((4096,), (1,), 0), ((64, 96), (1, 64), 0), ((300,), (2,), 1),
+                                               ((8, 16, 32), (1, 256, 8), 0), ((), (), 0)])
+def test_relu_vjp_layouts(shape, strides, off):
+    rng = np.random.default_rng(1)
+    need = O.storage_size(shape, strides, off)
+    x = U.special_mix(rng, max(need, 1))
+    n = int(np.prod(shape)) if shape else 1
+    up = U.special_mix(rng, n)
+    assert_bitwise_equal(gpu_relu_backward(x, shape, strides, off, up), O.relu_backward(x, shape, strides, off, up),
+                         nan_equal=False)
+
+
+MUL_CASES = [
+    # (out shape, other shape, other strides, self shape)
+    ((4096,), (4096,), (1,), (4096,)),
+    ((64, 96), (64, 96), (96, 1), (64, 96)),
+    ((64, 96), (96,), (1,), (64, 96)),          # other broadcast, self full: stored as is
+    ((64, 96), (64, 96), (96, 1), (96,)),       # self broadcast over rows
+    ((64, 96), (64, 96), (96, 1), (64, 1)),     # self broadcast over columns
+    ((2, 3), (1, 3), (3, 1), (2, 1)),           # autograd.rs:176-188
+    ((4, 5, 6), (4, 5, 6), (30, 6, 1), ()),     # rank-0 operand
+    ((4, 5, 6), (5, 1), (1, 1), (4, 1, 6)),
+    ((3, 2), (3, 2), (1, 3), ()),               # transposed other
+    ((0, 3), (0, 3), (3, 1), (3,)),             # empty output
+]
+
+
+@pytest.mark.parametrize("case", MUL_CASES, ids=[str(c) for c in MUL_CASES])
+def test_mul_vjp_bit_exact(case):
+    oshape, oth_shape, oth_strides, self_shape = case
+    rng = np.random.default_rng(len(oshape) * 31 + sum(oshape))
+    n = int(np.prod(oshape))
+    up = U.special_mix(rng, max(n, 1))[:n] if n else np.zeros(0, np.float32)
+    other = U.special_mix(rng, max(O.storage_size(oth_shape, oth_strides), 1))
+    want = O.mul_backward(up if n else np.zeros(1, np.float32), oshape, other, oth_shape, oth_strides, 0, self_shape)
+    got = gpu_mul_backward(up if n else np.zeros(1, np.float32), oshape, other, oth_shape, oth_strides, 0,
+                           self_shape)
+    assert_bitwise_equal(got, want)
+
+
+def test_mul_vjp_negative_zero_rules():
+    g = G["autograd_negative_zero"]
+    nb = g["no_broadcast"]
+    got = gpu_mul_backward(np.ones(1, np.float32), (1,), f32_from_bits(nb["right_bits"]), (1,), (1,), 0, (1,))
+    check_bits(got, nb["left_grad_bits"])
+    b = g["broadcast"]
+    got = gpu_mul_backward(np.ones(2, np.float32), (2,), f32_from_bits(b["right_bits"]), (2,), (1,), 0, ())
+    check_bits(got, b["left_grad_bits"])
+
+
+@pytest.mark.parametrize("oshape,self_shape", [((8192, 1024), (1024,)), ((64, 96), (64, 1)), ((4, 5, 6), (5, 1)),
+                                               ((4, 5, 6), ()), ((7, 9), (7, 9))])
+def test_add_vjp_reduce_to_shape_bit_exact(oshape, self_shape):
+    rng = np.random.default_rng(2)
+    up = rng.standard_normal(int(np.prod(oshape))).astype(np.float32)
+    assert_bitwise_equal(gpu_reduce(up, oshape, self_shape), O.reduce_to_shape(up, oshape, self_shape))
+
+
+@pytest.mark.parametrize("n", [1, 3, 1000, 1 << 20, (1 << 23) + 5])
+def test_sum_within_summation_bound(n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32)
+    got = gpu_sum(x, (n,))
+    want = O.sum_f32(x, (n,))
+    # Any two float orderings of an n-term sum differ by at most 2 * (n-1) * u * sum|x|.
+    bound = 2 * (n - 1) * 2.0 ** -24 * O.sum_abs(x)
+    assert abs(float(got) - float(want)) <= bound
+
+
+def test_sum_of_transposed_view_and_golden():
+    s = G["stride_aware_broadcast"]
+    got = gpu_sum(np.arange(24, dtype=np.float32), s["shape"], s["strides"])
+    assert int(np.float32(got).view(np.uint32)) == int(s["sum_bits"], 16)
+    assert gpu_sum(np.array(G["sum_small"]["input"], np.float32), (3,)) == G["sum_small"]["expected"]
+
+
+def test_accumulate_and_fill():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(10001).astype(np.float32)
+    b = rng.standard_normal(10001).astype(np.float32)
+    da, db = U.dev(a), U.dev(b)
+    check(abi.lib.trs_accumulate_f32(da.ptr, db.ptr, a.size))
+    want = a.copy()
+    O.lib().orc_accumulate_f32(want.ctypes.data, b.ctypes.data, a.size)
+    assert_bitwise_equal(da.to_numpy(count=a.size), want)
+    check(abi.lib.trs_fill_f32(da.ptr, 100, ctypes.c_float(-0.0)))
+    assert (da.to_numpy(count=100).view(np.uint32) == 0x80000000).all()
+    src = U.dev(np.array([2.5], np.float32))
+    check(abi.lib.trs_fill_from_device_f32(da.ptr, 77, src.ptr))
+    assert (da.to_numpy(count=77) == 2.5).all()

@@ -1,0 +1,98 @@
+"""GPU parity of the pointwise fusion compiler.
+
+A fused program performs the same IEEE operations as the eager chain, so
+it is bit-identical to the eager GPU chain (same device expf) and, except
+through exp, bit-identical to the CPU oracle; through exp the chain is
+within 2 ulp(exp(t)) absolute of the oracle (relu(exp(t) - 1) does not
+amplify absolute error).
+"""
+import numpy as np
+import pytest
+
+import gpu_util as U
+import oracle as O
+from helpers import assert_bitwise_equal, ulp_of
+from trs_backend.abi import layout_of
+
+pytestmark = pytest.mark.gpu
+
+CHAIN_IR = "in f32\nin f32\nin f32\nmul %0 %1\nadd %3 %2\nexp %4\nconst 0x3f800000\nsub %5 %6\nrelu %7\nout %8\n"
+BCAST_IR = "in f32\nin f32\nin f32\nadd %0 %1\nmul %3 %2\nout %4\n"
+
+
+def oracle_chain(x, y, z):
+    t = O.binary_contig(O.ADD, O.binary_contig(O.MUL, x, y), z)
+    e = O.unary_contig(O.EXP, t)
+    return O.unary_contig(O.RELU, O.scalar_contig(O.S_SUB, e, 1.0)), t
+
+
+def gpu_eager_chain(x, y, z):
+    n = x.size
+    t1 = U.binary(O.MUL, x, (n,), (1,), 0, y, (n,), (1,), 0, (n,), (1,))
+    t2 = U.binary(O.ADD, t1, (n,), (1,), 0, z, (n,), (1,), 0, (n,), (1,))
+    t3 = U.unary(O.EXP, t2, (n,), (1,), 0, (1,))
+    t4 = U.scalar(O.S_SUB, t3, (n,), (1,), 0, 1.0, (1,))
+    return U.unary(O.RELU, t4, (n,), (1,), 0, (1,))
+
+
+def gpu_fused(ir, arrays, layouts, oshape, ostr=None):
+    kid = U.fusion_compile(ir)
+    devs = [U.dev(a) for a in arrays]
+    n = int(np.prod(oshape))
+    out = U.out_buffer(n)
+    U.fusion_launch(kid, devs, layouts, out, layout_of(oshape, ostr))
+    return out.to_numpy(count=n)
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 100_003, 1 << 22])
+def test_fused_chain_matches_eager_bitwise_and_oracle_within_exp_bound(n):
+    rng = np.random.default_rng(n)
+    x, y, z = (rng.uniform(-4, 4, n).astype(np.float32) for _ in range(3))
+    lay = [layout_of((n,))] * 3
+    fused = gpu_fused(CHAIN_IR, [x, y, z], lay, (n,))
+    eager = gpu_eager_chain(x, y, z)
+    assert_bitwise_equal(fused, eager)
+    want, t = oracle_chain(x, y, z)
+    err = np.abs(fused.astype(np.float64) - want.astype(np.float64))
+    assert (err <= 2 * ulp_of(np.exp(t.astype(np.float64)).astype(np.float32))).all()
+
+
+def test_fused_broadcast_transposed_chain_bit_exact():
+    """(a + b) * c.mT on a mini config-3 shape: a [B,1,N], b [1,M,N], c [B,N,M]."""
+    rng = np.random.default_rng(2)
+    B, M, N = 4, 96, 160
+    a = rng.standard_normal(B * N).astype(np.float32)
+    b = rng.standard_normal(M * N).astype(np.float32)
+    c = rng.standard_normal(B * N * M).astype(np.float32)
+    la = layout_of((B, 1, N))
+    lb = layout_of((1, M, N))
+    lc = layout_of((B, M, N), (N * M, 1, M))  # c.mT
+    fused = gpu_fused(BCAST_IR, [a, b, c], [la, lb, lc], (B, M, N))
+    # oracle: the reference's two ops, add then mul
+    sh1, st1 = O.binary_output_layout((B, 1, N), (N, N, 1), (1, M, N), (M * N, N, 1))
+    s = O.binary(O.ADD, a, (B, 1, N), (N, N, 1), 0, b, (1, M, N), (M * N, N, 1), 0, sh1, st1)
+    sh2, st2 = O.binary_output_layout(sh1, st1, (B, M, N), (N * M, 1, M))
+    want = O.binary(O.MUL, s, sh1, st1, 0, c, (B, M, N), (N * M, 1, M), 0, sh2, st2)
+    assert st2 == (M * N, N, 1)
+    assert_bitwise_equal(fused, want)
+
+
+def test_fused_mask_apply_with_u8_input():
+    rng = np.random.default_rng(9)
+    n = 10_000
+    h = rng.standard_normal(n).astype(np.float32)
+    m = (rng.random(n) < 0.9).astype(np.uint8)
+    ir = f"in f32\nin u8\nmul %0 %1\nconst {np.float32(1 / 0.9).view(np.uint32):#010x}\nmul %2 %3\nout %4\n"
+    got = gpu_fused(ir, [h, m], [layout_of((n,)), layout_of((n,))], (n,))
+    assert_bitwise_equal(got, O.mask_apply(h, m, float(np.float32(1 / 0.9))))
+
+
+def test_fused_relu_bias_row_broadcast():
+    rng = np.random.default_rng(10)
+    R, C = 64, 1000
+    x = rng.standard_normal(R * C).astype(np.float32)
+    b = rng.standard_normal(C).astype(np.float32)
+    got = gpu_fused("in f32\nin f32\nadd %0 %1\nrelu %2\nout %3\n", [x, b], [layout_of((R, C)), layout_of((C,))],
+                    (R, C))
+    want = O.unary_contig(O.RELU, O.row_broadcast(O.ADD, x, b, R, C))
+    assert_bitwise_equal(got, want, nan_equal=False)

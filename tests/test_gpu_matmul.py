@@ -1,0 +1,138 @@
+"""GPU parity of trs_matmul_f32 (FP32 MFMA) against the oracle's sequential matmul.
+
+Bar (north_star): |C_gpu - C_ref| <= 1e-5 * sqrt(K) * (|A| |B|) elementwise,
+plus exact results on small integers (every partial sum exact) and the
+reference's known answers (tests/tensor_baseline.rs:1212-1218, 1889-1939).
+"""
+import numpy as np
+import pytest
+
+import gpu_util as U
+import oracle as O
+from helpers import golden
+
+pytestmark = pytest.mark.gpu
+G = golden()
+
+
+def _check_tol(got, want, bound, K):
+    tol = 1e-5 * np.sqrt(K) * bound
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bad = err > tol
+    assert not bad.any(), f"{bad.sum()} elements out of tolerance; worst {err.max()} vs {tol.ravel()[err.argmax()]}"
+
+
+def _abs_bound(a, b):
+    return np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+
+
+@pytest.mark.parametrize("key", ["matmul_known", "matmul_transposed", "matmul_indexed_transposed"])
+def test_known_answers(key):
+    g = G[key]
+    if key == "matmul_known":
+        a, b = np.array(g["left"], np.float32), np.array(g["right"], np.float32)
+        la = (g["left_shape"], O.contiguous_strides(g["left_shape"]), 0)
+        lb = (g["right_shape"], O.contiguous_strides(g["right_shape"]), 0)
+    else:
+        a = np.arange(g["left_storage_len"], dtype=np.float32)
+        b = np.arange(g["right_storage_len"], dtype=np.float32)
+        la = (g["left_shape"], g["left_strides"], g["left_offset"])
+        lb = (g["right_shape"], g["right_strides"], g["right_offset"])
+    got = U.matmul(a, *la, b, *lb)
+    assert got.ravel().tolist() == g["expected"]
+
+
+SHAPES = [(1, 1, 1), (5, 7, 3), (64, 64, 64), (128, 128, 128), (130, 70, 257), (256, 512, 384), (33, 1000, 65)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_small_integers_exact(m, k, n, ta, tb):
+    rng = np.random.default_rng(m + 3 * k + 7 * n + 11 * ta + 13 * tb)
+    a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+    b = rng.integers(-4, 5, size=(k, n)).astype(np.float32)
+    la = ((m, k), (1, m), 0) if ta else ((m, k), (k, 1), 0)
+    lb = ((k, n), (1, k), 0) if tb else ((k, n), (n, 1), 0)
+    sa = np.ascontiguousarray(a.T).ravel() if ta else a.ravel()
+    sb = np.ascontiguousarray(b.T).ravel() if tb else b.ravel()
+    got = U.matmul(sa, *la, sb, *lb)
+    assert np.array_equal(got, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("m,k,n", [(128, 256, 128), (200, 300, 100), (512, 512, 512)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True)])
+def test_normal_inputs_within_tolerance(m, k, n, ta, tb):
+    rng = np.random.default_rng(m * k + n)
+    a = (rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
+    b = (rng.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
+    sa = np.ascontiguousarray(a.T).ravel() if ta else a.ravel()
+    sb = np.ascontiguousarray(b.T).ravel() if tb else b.ravel()
+    la = ((m, k), (1, m), 0) if ta else ((m, k), (k, 1), 0)
+    lb = ((k, n), (1, k), 0) if tb else ((k, n), (n, 1), 0)
+    got = U.matmul(sa, *la, sb, *lb)
+    want = O.matmul(sa, *la, sb, *lb).reshape(m, n)
+    _check_tol(got, want, _abs_bound(a, b), k)
+
+
+def test_batched_against_per_matrix_reference():
+    rng = np.random.default_rng(3)
+    bt, m, k, n = 6, 96, 160, 72
+    a = rng.standard_normal((bt, m, k)).astype(np.float32)
+    b = rng.standard_normal((bt, k, n)).astype(np.float32)
+    got = U.matmul(a.ravel(), (bt, m, k), (m * k, k, 1), 0, b.ravel(), (bt, k, n), (k * n, n, 1), 0)
+    want = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0, batch=bt, bsa=m * k, bsb=k * n)
+    want = want.reshape(bt, m, n)
+    for t in range(bt):
+        _check_tol(got[t], want[t], _abs_bound(a[t], b[t]), k)
+
+
+def test_general_strides_use_the_strided_path():
+    rng = np.random.default_rng(4)
+    m, k, n = 20, 30, 10
+    buf_a = rng.standard_normal(m * k * 2).astype(np.float32)
+    buf_b = rng.standard_normal(k * n * 3).astype(np.float32)
+    la = ((m, k), (2 * k, 2), 1)   # no unit stride
+    lb = ((k, n), (3 * n, 3), 2)
+    got = U.matmul(buf_a, *la, buf_b, *lb)
+    want = O.matmul(buf_a, *la, buf_b, *lb).reshape(m, n)
+    # The strided fallback keeps the reference order (one rounding per op).
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_config4_full_size_sampled_rows():
+    """4096^3 with N(0, 1/64) inputs (seed 3); 24 sampled rows against the oracle."""
+    from trs_backend.configs import generate
+    A = generate("matmul", "A")
+    B = generate("matmul", "B")
+    K = 4096
+    got = U.matmul(A, (K, K), (K, 1), 0, B, (K, K), (K, 1), 0)
+    rows = np.random.default_rng(0).choice(K, 24, replace=False)
+    rows = np.concatenate([rows, [0, K - 1]])
+    want, bound = O.matmul_rows(A, (K, K), (K, 1), B, (K, K), (K, 1), rows)
+    _check_tol(got[rows], want, bound, K)
+
+
+def test_config4_batched_full():
+    from trs_backend.configs import generate
+    A = generate("matmul", "Ab")
+    B = generate("matmul", "Bb")
+    got = U.matmul(A, (32, 512, 512), (512 * 512, 512, 1), 0, B, (32, 512, 512), (512 * 512, 512, 1), 0)
+    for t in (0, 13, 31):
+        a = A[t * 512 * 512:(t + 1) * 512 * 512]
+        b = B[t * 512 * 512:(t + 1) * 512 * 512]
+        want = O.matmul(a, (512, 512), (512, 1), 0, b, (512, 512), (512, 1), 0).reshape(512, 512)
+        _check_tol(got[t], want, _abs_bound(a.reshape(512, 512), b.reshape(512, 512)), 512)
+
+
+def test_inner_mismatch_and_rank_errors():
+    import ctypes
+    from trs_backend import abi
+    a = U.dev(np.zeros(6, np.float32))
+    out = U.out_buffer(4)
+    rc = abi.lib.trs_matmul_f32(a.ptr, ctypes.byref(abi.layout_of((2, 3))), a.ptr, ctypes.byref(abi.layout_of((2, 3))),
+                                out.ptr, ctypes.byref(abi.layout_of((2, 3))))
+    assert rc == -5
+    assert "mat1 and mat2 shapes cannot be multiplied (2x3 and 2x3)" in abi.lib.trs_last_error().decode()
+    rc = abi.lib.trs_matmul_f32(a.ptr, ctypes.byref(abi.layout_of((6,))), a.ptr, ctypes.byref(abi.layout_of((6,))),
+                                out.ptr, ctypes.byref(abi.layout_of((1,))))
+    assert rc == -6

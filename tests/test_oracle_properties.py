@@ -1,0 +1,146 @@
+"""Pin the oracle where the reference tests leave it open, by mathematics.
+
+Each check is chosen so that a plausible mistake in the restatement (a
+dropped term, a transposed operand, a wrong accumulation order or start
+value, a fused multiply-add) fails it.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import assert_bitwise_equal, ulp_distance
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 2), (7, 4, 9), (16, 33, 5)])
+def test_matmul_exact_on_small_integers(m, k, n):
+    # Products and partial sums of small integers are exact in f32: any order,
+    # any operand mistake shows up as a wrong integer.
+    rng = _rng(m * 100 + k * 10 + n)
+    a = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
+    b = rng.integers(-8, 9, size=(k, n)).astype(np.float32)
+    got = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+    assert np.array_equal(got, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+    # transposed-view operands give the same result
+    got_t = O.matmul(np.ascontiguousarray(a.T).ravel(), (m, k), (1, m), 0,
+                     np.ascontiguousarray(b.T).ravel(), (k, n), (1, k), 0).reshape(m, n)
+    assert np.array_equal(got, got_t)
+
+
+def test_matmul_sequential_order_without_fma():
+    # The reference order is c = +0; c = c + a_k*b_k for k ascending, with the
+    # product rounded before the add.  Recompute that recurrence with numpy
+    # float32 scalars (which round each op) and demand bit equality.
+    rng = _rng(7)
+    m, k, n = 4, 37, 3
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    got = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+    want = np.zeros((m, n), np.float32)
+    for i in range(m):
+        for j in range(n):
+            c = np.float32(0.0)
+            for t in range(k):
+                c = np.float32(c + np.float32(a[i, t] * b[t, j]))
+            want[i, j] = c
+    assert_bitwise_equal(got, want)
+
+
+def test_matmul_rows_and_batch_agree_with_full():
+    rng = _rng(11)
+    a = rng.standard_normal((3, 6, 5)).astype(np.float32)
+    b = rng.standard_normal((3, 5, 4)).astype(np.float32)
+    full = O.matmul(a.ravel(), (6, 5), (5, 1), 0, b.ravel(), (5, 4), (4, 1), 0, batch=3, bsa=30, bsb=20)
+    full = full.reshape(3, 6, 4)
+    for t in range(3):
+        single = O.matmul(a[t].ravel(), (6, 5), (5, 1), 0, b[t].ravel(), (5, 4), (4, 1), 0).reshape(6, 4)
+        assert_bitwise_equal(full[t], single)
+    rows, bound = O.matmul_rows(a[1].ravel(), (6, 5), (5, 1), b[1].ravel(), (5, 4), (4, 1), [0, 5, 2])
+    assert_bitwise_equal(rows, full[1][[0, 5, 2]])
+    assert np.allclose(bound, np.abs(a[1][[0, 5, 2]]).astype(np.float64) @ np.abs(b[1]).astype(np.float64))
+
+
+def test_exp_is_within_one_ulp_of_correct_rounding():
+    # glibc expf is documented < 1 ulp; check against exp in float64 rounded.
+    rng = _rng(3)
+    x = np.concatenate([rng.uniform(-103.0, 88.7, 200_000), rng.uniform(-1, 1, 50_000)]).astype(np.float32)
+    got = O.unary_contig(O.EXP, x)
+    want = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert ulp_distance(got, want).max() <= 1
+
+
+def test_relu_exhaustive_sample_matches_closed_form():
+    # relu_value: exact zeros kept (incl. -0.0), NaN -> +0.0, else max(v, 0).
+    rng = _rng(5)
+    bits = rng.integers(0, 2**32, size=1_000_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    got = O.unary_contig(O.RELU, x)
+    want = np.where(x > 0, x, np.float32(0.0)).astype(np.float32)
+    zero = (bits & 0x7FFFFFFF) == 0
+    want[zero] = x[zero]
+    assert_bitwise_equal(got, want, nan_equal=False)
+
+
+def test_neg_flips_only_the_sign_bit():
+    bits = np.array([0, 0x80000000, 0x7FC00001, 0xFF800000, 1, 0x3F800000], dtype=np.uint32)
+    got = O.unary_contig(O.NEG, bits.view(np.float32)).view(np.uint32)
+    assert np.array_equal(got, bits ^ 0x80000000)
+
+
+def test_sum_sequential_left_fold():
+    rng = _rng(9)
+    x = rng.standard_normal(1000).astype(np.float32)
+    want = np.float32(-0.0)
+    for v in x:
+        want = np.float32(want + v)
+    assert O.sum_f32(x, (1000,)).view(np.uint32) == want.view(np.uint32)
+    # Logical order of a transposed view, not storage order.
+    y = rng.standard_normal((30, 40)).astype(np.float32)
+    want = np.float32(-0.0)
+    for v in y.T.ravel():
+        want = np.float32(want + v)
+    assert O.sum_f32(y.ravel(), (40, 30), (1, 40)).view(np.uint32) == want.view(np.uint32)
+
+
+def test_reduce_to_shape_is_mul_vjp_with_ones():
+    # The add VJP (new) is pinned to the reference's Multiply VJP by composition.
+    rng = _rng(13)
+    up = rng.standard_normal(4 * 5 * 6).astype(np.float32)
+    for self_shape in [(5, 1), (1, 6), (4, 1, 6), (6,), (), (4, 5, 6)]:
+        ones = np.ones(int(np.prod(self_shape)) if self_shape else 1, np.float32)
+        r = O.reduce_to_shape(up, (4, 5, 6), self_shape)
+        # mul VJP of operand `self` against an all-ones `other` of the output shape
+        m = O.mul_backward(up, (4, 5, 6), np.ones(120, np.float32), (4, 5, 6), (30, 6, 1), 0, self_shape)
+        assert_bitwise_equal(r, m)
+        del ones
+
+
+def test_mul_vjp_accumulation_order_is_output_major():
+    # Broadcast accumulation: grad[j] = ((0 + c0) + c1) + ... over output order.
+    rng = _rng(17)
+    up = rng.standard_normal(3 * 4).astype(np.float32)
+    other = rng.standard_normal(3 * 4).astype(np.float32)
+    got = O.mul_backward(up, (3, 4), other, (3, 4), (4, 1), 0, (4,))
+    want = np.zeros(4, np.float32)
+    for i in range(3):
+        for j in range(4):
+            want[j] = np.float32(want[j] + np.float32(up[i * 4 + j] * other[i * 4 + j]))
+    assert_bitwise_equal(got, want)
+
+
+def test_binary_broadcast_matches_numpy_elementwise():
+    # Each element is one IEEE op; numpy's float32 ops are IEEE too.
+    rng = _rng(19)
+    a = rng.standard_normal((4, 1, 6)).astype(np.float32)
+    b = rng.standard_normal((5, 1)).astype(np.float32)
+    shape, strides = O.binary_output_layout((4, 1, 6), (6, 6, 1), (5, 1), (1, 1))
+    for op, fn in [(O.ADD, np.add), (O.SUB, np.subtract), (O.MUL, np.multiply), (O.DIV, np.divide)]:
+        got = O.binary(op, a.ravel(), (4, 1, 6), (6, 6, 1), 0, b.ravel(), (5, 1), (1, 1), 0, shape, strides)
+        assert_bitwise_equal(got, fn(a, b).ravel())
+
+
+def test_libc_version_recorded():
+    assert O.libc_version()
