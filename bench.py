@@ -210,7 +210,7 @@ def cpu_baseline(x, y, z, n, log):
         t = O.unary_contig(O.RELU, t)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 12:
+        if el > 10.0 or reps >= 200:
             break
     gbs = 16 * sample * reps / el / 1e9
     log(f"cpu baseline: {gbs:.2f} GB/s over {reps} x 2^25 elements in {el:.1f}s")

@@ -137,7 +137,7 @@ DeviceState *device_state() {
     dev->index = g_device;
     dev->cu_count = prop.multiProcessorCount;
     dev->clock_khz = prop.clockRate;
-    std::snprintf(dev->name, sizeof dev->name, "%s", prop.name);
+    std::snprintf(dev->name, sizeof dev->name, "%s (%s)", prop.name[0] ? prop.name : "AMD GPU", prop.gcnArchName);
     dev->ready = true;
     return dev;
 }

@@ -95,7 +95,7 @@ def test_scalar_bit_exact(case, op):
 
 
 UNARY_CASES = {
-    "contiguous": ((1 << 16) + 3, None, 0),
+    "contiguous": (((1 << 16) + 3,), None, 0),
     "matrix": ((64, 1024), None, 0),
     "transposed": ((96, 80), (1, 96), 0),
     "permuted": ((8, 16, 32), (1, 256, 8), 0),
@@ -124,7 +124,8 @@ def test_exp_within_two_ulp(case):
     rng = np.random.default_rng(5)
     shape, strides, off = UNARY_CASES[case]
     x, shape, strides, off = _view(rng, shape, strides, off)
-    x = (x * 20).astype(np.float32)
+    with np.errstate(over="ignore"):
+        x = (x * 20).astype(np.float32)
     ostr = O.unary_output_strides(shape, strides)
     want = O.unary(O.EXP, x, shape, strides, off, ostr)
     got = U.unary(O.EXP, x, shape, strides, off, ostr)
