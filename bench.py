@@ -60,6 +60,8 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs, no CPU baseline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--workload", choices=("fused_chain", "copy"), default="fused_chain",
+                    help="copy: a plain 2^28-float copy kernel, the calibration run for rocprofv3 byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -83,6 +85,8 @@ def main() -> int:
     log(f"device {name.value.decode()} CUs={cus.value} clock={clk.value} kHz")
 
     n = 1 << 28
+    if args.workload == "copy":
+        return copy_calibration(n, args)
     t0 = time.time()
     x, y, z = (generate("fused_chain", k, threads=min(16, host_cores())) for k in ("x", "y", "z"))
     log(f"generated 3 x 2^28 inputs in {time.time() - t0:.1f}s")
@@ -176,6 +180,33 @@ def main() -> int:
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def copy_calibration(n: int, args) -> int:
+    """Plain contiguous copy of n floats (8 B/element moved): reference point for the PMC byte counters."""
+    import ctypes
+    import statistics
+
+    import numpy as np
+
+    from trs_backend import abi
+    from trs_backend.abi import DeviceArray, check, layout_of
+    from trs_backend.timing import time_launches
+
+    src = DeviceArray.from_numpy(np.arange(n, dtype=np.float32))
+    dst = DeviceArray(n * 4)
+    lay = layout_of((n,))
+
+    def step():
+        check(abi.lib.trs_unary_f32(3, src.ptr, ctypes.byref(lay), dst.ptr, ctypes.byref(lay)))
+
+    ev = time_launches(step, reps=max(10, args.steps), warmup=args.warmup)
+    ms = statistics.mean(ev)
+    gbs = 8 * n / (ms * 1e-3) / 1e9
+    log(f"copy: {ms * 1e3:.1f} us avg -> {gbs:.0f} GB/s")
+    print(json.dumps({"workload": "copy_calibration", "elements": n, "bytes_per_launch": 8 * n,
+                      "kernel_us_avg": ms * 1e3, "GBps": gbs}), flush=True)
     return 0
 
 

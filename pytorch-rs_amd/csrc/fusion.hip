@@ -156,6 +156,7 @@ int generate(const std::string &ir, Program *prog) {
         s << "extern \"C\" __global__ void __launch_bounds__(256) " << name
           << "(trs::PwGeom g, trs::PwPtrs p) { " << body << "(TrsFused{}, g, p); }\n";
     };
+    wrap("trs_fused_flat_c", "trs::pw_flat_contig_body<TrsFused, " + mask + ">");
     wrap("trs_fused_flat_v", "trs::pw_flat_body<TrsFused, " + mask + ", true>");
     wrap("trs_fused_flat_s", "trs::pw_flat_body<TrsFused, " + mask + ", false>");
     wrap("trs_fused_rows_v", "trs::pw_rows_body<TrsFused, " + mask + ", true>");
@@ -277,7 +278,9 @@ int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *input
     std::string name;
     switch (pl.variant) {
     case PwVariant::Empty: return TRS_OK;
-    case PwVariant::Flat: name = pl.vec ? "trs_fused_flat_v" : "trs_fused_flat_s"; break;
+    case PwVariant::Flat:
+        name = pl.contig ? "trs_fused_flat_c" : pl.vec ? "trs_fused_flat_v" : "trs_fused_flat_s";
+        break;
     case PwVariant::Rows: name = pl.vec ? "trs_fused_rows_v" : "trs_fused_rows_s"; break;
     case PwVariant::Tiled:
         name = std::string(pl.vec ? "trs_fused_tiled_v" : "trs_fused_tiled_s") + std::to_string(pl.ntransposed);

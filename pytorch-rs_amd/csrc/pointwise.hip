@@ -73,6 +73,8 @@ struct ReluBackwardF {
 
 template <class F, unsigned M, bool V>
 __global__ void __launch_bounds__(256) k_flat(F f, PwGeom g, PwPtrs p) { pw_flat_body<F, M, V>(f, g, p); }
+template <class F, unsigned M>
+__global__ void __launch_bounds__(256) k_flat_contig(F f, PwGeom g, PwPtrs p) { pw_flat_contig_body<F, M>(f, g, p); }
 template <class F, unsigned M, bool V>
 __global__ void __launch_bounds__(256) k_rows(F f, PwGeom g, PwPtrs p) { pw_rows_body<F, M, V>(f, g, p); }
 template <class F, unsigned M, bool V, int NT>
@@ -87,7 +89,8 @@ int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
     case PwVariant::Empty:
         return TRS_OK;
     case PwVariant::Flat:
-        if (pl.vec) hipLaunchKernelGGL((k_flat<F, M, true>), grid, block, 0, s, f, pl.g, pl.p);
+        if (pl.contig) hipLaunchKernelGGL((k_flat_contig<F, M>), grid, block, 0, s, f, pl.g, pl.p);
+        else if (pl.vec) hipLaunchKernelGGL((k_flat<F, M, true>), grid, block, 0, s, f, pl.g, pl.p);
         else hipLaunchKernelGGL((k_flat<F, M, false>), grid, block, 0, s, f, pl.g, pl.p);
         break;
     case PwVariant::Rows:

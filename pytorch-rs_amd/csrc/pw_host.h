@@ -24,6 +24,7 @@ enum class PwVariant { Empty, Flat, Rows, Tiled, Generic };
 struct PwPlan {
     PwVariant variant = PwVariant::Empty;
     bool vec = false;
+    bool contig = false;  // Flat + vec with every input unit-stride and read once
     int ntransposed = 0;
     int nin = 0;
     int64_t grid = 0;
@@ -177,7 +178,8 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
     const int inner = rank - 1;
     bool unit_or_bcast = os[inner] == 1;
     for (int i = 0; i < nin; i++) unit_or_bcast &= is[i][inner] == 0 || is[i][inner] == 1;
-    const int64_t want = (int64_t)cu_count * 16;
+    (void)cu_count;
+    const int64_t want = kMaxGrid;
 
     if (unit_or_bcast) {
         bool vec = aligned(out, lo->offset, os, inner, 4);
@@ -186,7 +188,10 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         if (rank == 1) {
             plan->variant = PwVariant::Flat;
             plan->vec = vec;
-            const int64_t work = vec ? (numel / 4) / 4 : numel;
+            bool all_unit = true;
+            for (int i = 0; i < nin; i++) all_unit &= is[i][0] == 1;
+            plan->contig = vec && all_unit;
+            const int64_t work = vec ? numel / 4 : numel;
             plan->grid = std::min<int64_t>(std::max<int64_t>(1, (work + 255) / 256), want);
         } else {
             plan->variant = PwVariant::Rows;
