@@ -71,9 +71,18 @@ int trs_set_device(int device);
 int trs_get_device(int *device);
 /* Device name, CU count and max engine clock (kHz) of the current device. */
 int trs_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz);
-/* Storage allocation (filled_storage, src/tensor.rs:4434-4442, without the fill). */
+/* Storage allocation (filled_storage, src/tensor.rs:4434-4442, without the
+ * fill).  Blocks come from a per-device cache (512 B granules below 1 MiB,
+ * 2 MiB above) and trs_free returns them to it without synchronising: the
+ * release is stream-ordered, so a block must not be used outside this
+ * library's stream after it is freed.  Pointers not from trs_alloc are
+ * released with a stream sync and hipFree. */
 int trs_alloc(size_t bytes, void **ptr);
 int trs_free(void *ptr);
+/* Return every cached block to HIP (after draining the device stream). */
+int trs_empty_cache(void);
+/* Bytes in live (allocated) and cached (freed, kept) blocks on the device. */
+int trs_memory_stats(size_t *live_bytes, size_t *cached_bytes);
 /* Host <-> device copies on the device stream; d2h blocks until done. */
 int trs_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int trs_memcpy_d2h(void *dst, const void *src, size_t bytes);

@@ -81,7 +81,7 @@ using MetaPtr = std::shared_ptr<AutogradMeta>;
 // backend adds for device tensors.
 enum class Node {
     Add, Alias, Clone, Multiply, Negate, Permute, Relu, ReflectedSubtract, Subtract, Sum, MatrixTranspose,
-    Transpose, View, Exp, Mm, Bmm, AddTensor, SubTensor
+    Transpose, View, Select, Exp, Mm, Bmm, AddTensor, SubTensor
 };
 const char *node_name(Node n);
 
@@ -94,7 +94,21 @@ struct SavedTensor {
     bool values_required = false;
 };
 
-enum class GradKind { Multiply, MultiplyScalar, Negate, Relu, Sum, Identity, Permute, AddTensor, SubTensor, Matmul, Exp };
+enum class GradKind {
+    Multiply, MultiplyScalar, Negate, Relu, Sum, Identity, Permute, Index, AddTensor, SubTensor, Matmul, Exp,
+    MaskApply
+};
+
+// One byte per element in HBM (a dropout keep-mask).
+struct ByteBuffer {
+    Device device;
+    Dims shape;
+    int64_t numel = 0;
+    uint8_t *dptr = nullptr;
+    ~ByteBuffer();
+    static std::shared_ptr<ByteBuffer> from_host(const uint8_t *data, const Dims &shape, Device device);
+};
+using BytePtr = std::shared_ptr<ByteBuffer>;
 
 struct GradFn {
     GradKind kind;
@@ -102,10 +116,11 @@ struct GradFn {
     std::vector<SavedTensor> inputs;
     float scalar = 0.0f;
     bool scalar_live = false;
-    Dims dims;          // permute: the permutation
-    Dims out_shape;     // output shape of the recorded op
-    SavedTensor output; // exp: its own output (values saved)
-    bool consumed = false;
+    Dims dims;            // permute: the permutation
+    int64_t index_start = 0;  // select: first input element of the output
+    Dims out_shape;       // output shape of the recorded op
+    SavedTensor output;   // exp: its own output (values saved)
+    BytePtr mask;         // mask-apply: the keep-mask
 };
 
 struct AutogradMeta {
@@ -173,6 +188,7 @@ public:
     Tensor sum() const;
     Tensor matmul(const Tensor &o) const;
     float item() const;
+    void require_cuda(const char *what) const;
 
     // autograd
     void backward() const;
@@ -184,8 +200,10 @@ private:
     Tensor scalar_op(int op, float s) const;
     Tensor unary_op(int op) const;
     Tensor alias_view(const Dims &shape, const Dims &strides, int64_t offset) const;
-    void require_cuda(const char *what) const;
 };
+
+// Dropout-apply with a precomputed keep-mask: (h * mask) * scale.
+Tensor mask_apply(const Tensor &h, const BytePtr &mask, float scale);
 
 // Thread-local no-grad depth (src/grad_mode.rs:5-38).
 void enter_no_grad();
@@ -201,7 +219,7 @@ struct FusedProgram {
     uint64_t id = 0;
     int nin = 0;
     static FusedProgram compile(const std::string &ir, int nin);
-    Tensor launch(const std::vector<Tensor> &inputs, const Dims &out_shape) const;
+    Tensor launch(const std::vector<Tensor> &inputs, const Dims &out_shape, const Dims &out_strides) const;
 };
 
 }  // namespace trs_engine

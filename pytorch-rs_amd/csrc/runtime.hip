@@ -20,7 +20,9 @@ thread_local std::string g_last_error;
 thread_local int g_device = 0;
 
 constexpr int kMaxDevices = 16;
-DeviceState g_devices[kMaxDevices];
+// Never destroyed: tensors released during interpreter shutdown may still
+// return blocks to the cache after static destructors would have run.
+DeviceState *const g_devices = new DeviceState[kMaxDevices];
 std::mutex g_init_mu;
 int g_device_count = -1;
 
@@ -45,6 +47,26 @@ int count_devices() {
         }
         g_device_count = n < kMaxDevices ? n : kMaxDevices;
     }
+    return TRS_OK;
+}
+
+// Block sizes: 512 B granules below 1 MiB, 2 MiB granules above (HBM pages).
+size_t round_block(size_t bytes) {
+    const size_t g = bytes < (1u << 20) ? 512 : (2u << 20);
+    return (bytes + g - 1) / g * g;
+}
+
+// Returns every cached block to HIP after the device stream has drained.
+int release_cache(DeviceState *dev) {
+    std::multimap<size_t, void *> blocks;
+    {
+        std::lock_guard<std::mutex> lock(dev->cache_mu);
+        blocks.swap(dev->free_blocks);
+        dev->cached_bytes = 0;
+    }
+    if (blocks.empty()) return TRS_OK;
+    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "cache release sync");
+    for (auto &kv : blocks) TRS_HIP_CHECK(hipFree(kv.second), "hipFree");
     return TRS_OK;
 }
 
@@ -207,13 +229,34 @@ int trs_alloc(size_t bytes, void **ptr) {
     DeviceState *dev = device_state();
     if (!dev) return TRS_E_NO_DEVICE;
     if (bytes == 0) return TRS_OK;
-    hipError_t e = hipMalloc(ptr, bytes);
+    const size_t rounded = round_block(bytes);
+    {
+        std::lock_guard<std::mutex> lock(dev->cache_mu);
+        auto it = dev->free_blocks.find(rounded);
+        if (it != dev->free_blocks.end()) {
+            *ptr = it->second;
+            dev->free_blocks.erase(it);
+            dev->cached_bytes -= rounded;
+            dev->live_blocks[*ptr] = rounded;
+            return TRS_OK;
+        }
+    }
+    hipError_t e = hipMalloc(ptr, rounded);
+    if (e != hipSuccess) {
+        // Out of memory with blocks parked in the cache: release them and retry once.
+        (void)hipGetLastError();
+        int rc = release_cache(dev);
+        if (rc) return rc;
+        e = hipMalloc(ptr, rounded);
+    }
     if (e != hipSuccess) {
         *ptr = nullptr;
         (void)hipGetLastError();
         return set_error(TRS_E_ALLOCATION_FAILED, "hipMalloc of %zu bytes failed: %s", bytes,
                          hipGetErrorString(e));
     }
+    std::lock_guard<std::mutex> lock(dev->cache_mu);
+    dev->live_blocks[*ptr] = rounded;
     return TRS_OK;
 }
 
@@ -221,9 +264,39 @@ int trs_free(void *ptr) {
     if (!ptr) return TRS_OK;
     DeviceState *dev = device_state();
     if (!dev) return TRS_E_NO_DEVICE;
-    // Memory may still be read by queued work: drain the stream first.
+    {
+        std::lock_guard<std::mutex> lock(dev->cache_mu);
+        auto it = dev->live_blocks.find(ptr);
+        if (it != dev->live_blocks.end()) {
+            // Stream-ordered release: work already queued on the device
+            // stream may still read the block; anything that reuses it is
+            // queued behind that work.
+            dev->free_blocks.emplace(it->second, ptr);
+            dev->cached_bytes += it->second;
+            dev->live_blocks.erase(it);
+            return TRS_OK;
+        }
+    }
+    // Not a block of this cache: drain queued readers, then hand it back.
     TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "free sync");
     TRS_HIP_CHECK(hipFree(ptr), "hipFree");
+    return TRS_OK;
+}
+
+int trs_empty_cache(void) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    return release_cache(dev);
+}
+
+int trs_memory_stats(size_t *live_bytes, size_t *cached_bytes) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    std::lock_guard<std::mutex> lock(dev->cache_mu);
+    size_t live = 0;
+    for (auto &kv : dev->live_blocks) live += kv.second;
+    if (live_bytes) *live_bytes = live;
+    if (cached_bytes) *cached_bytes = dev->cached_bytes;
     return TRS_OK;
 }
 

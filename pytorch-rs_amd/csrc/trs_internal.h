@@ -5,7 +5,9 @@
 
 #include <cstdarg>
 #include <cstdint>
+#include <map>
 #include <mutex>
+#include <unordered_map>
 
 #include "trs_hip.h"
 
@@ -25,6 +27,14 @@ struct DeviceState {
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
     std::mutex mu;
+    // Block cache behind trs_alloc/trs_free: freed blocks are kept by rounded
+    // size and handed out again without a hipFree/hipMalloc pair.  Reuse is
+    // safe without a sync because every kernel and copy of this library runs
+    // in order on `stream`.
+    std::mutex cache_mu;
+    std::multimap<size_t, void *> free_blocks;
+    std::unordered_map<void *, size_t> live_blocks;
+    size_t cached_bytes = 0;
 };
 
 // Returns the current device's state, initialising it on first use.

@@ -1,0 +1,268 @@
+"""torch_rs -- the pytorch-rs Python API for the MI355X device backend.
+
+Mirrors the hot-path surface of the reference package (python/torch_rs and
+the PyO3 module, src/python.rs:10558-10634): ``tensor``, ``relu``, ``exp``,
+``matmul``, ``mul``, ``no_grad``, the Tensor arithmetic and view methods,
+``backward`` / ``.grad``, ``nn.functional.relu/dropout`` and
+``get_float32_matmul_precision() == "highest"``.  Tensors created with
+``device="cuda"`` live in HBM and every op runs as a HIP kernel through
+libtrs_hip.so; ``"cpu"`` tensors are host staging for ``.to()`` only.
+
+Additions of this backend (absent from the reference, documented where
+they differ): device tensors record VJPs for matmul, tensor-tensor add/sub
+and exp; ``fuse`` compiles a pointwise function into one hipRTC kernel;
+``nn.functional.dropout`` accepts a precomputed uint8 keep-mask.
+"""
+from __future__ import annotations
+
+import builtins as _builtins
+import contextlib
+
+import numpy as _np
+
+from ._native import native as _C
+
+Tensor = _C.Tensor
+float32 = "torch_rs.float32"
+float = float32  # noqa: A001  (the reference exports torch_rs.float too)
+__version__ = "0.1.0+mi355x"
+
+_DEVICE_ALIASES = {"cuda", "cpu"}
+
+
+def _device_str(device) -> str:
+    if device is None:
+        return "cpu"
+    d = str(device)
+    if d in _DEVICE_ALIASES or d.startswith("cuda:"):
+        return d
+    raise RuntimeError(f"Expected one of cpu, cuda device type at start of device string: {d}")
+
+
+def _flatten(data):
+    """Nested sequences -> (flat list, shape), rejecting ragged input."""
+    if isinstance(data, (int, _builtins.float, _np.integer, _np.floating)):
+        return [data], ()
+    seq = list(data)
+    if not seq:
+        return [], (0,)
+    parts = [_flatten(x) for x in seq]
+    shape0 = parts[0][1]
+    for _, s in parts:
+        if s != shape0:
+            raise ValueError(f"expected sequence of length {shape0[0] if shape0 else 0} at dim 1")
+    flat = [v for p, _ in parts for v in p]
+    return flat, (len(seq),) + shape0
+
+
+def tensor(data, *, dtype=None, device=None, requires_grad=False) -> Tensor:
+    """torch_rs.tensor (src/python.rs:4139-4170): float32 values from a
+    number, a nested sequence, or any buffer/array (copied, row-major)."""
+    if dtype not in (None, float32):
+        raise TypeError("torch_rs supports only float32 tensors")
+    if isinstance(data, Tensor):
+        arr = data.numpy()
+    elif isinstance(data, (bytes, bytearray)):
+        raise TypeError("new(): invalid data type 'bytes'")
+    elif isinstance(data, (memoryview, _np.ndarray)):
+        arr = _np.asarray(data, dtype=_np.float32)
+    else:
+        flat, shape = _flatten(data)
+        arr = _np.asarray(flat, dtype=_np.float64).astype(_np.float32).reshape(shape)
+    t = _C.from_numpy(_np.ascontiguousarray(arr, dtype=_np.float32), _device_str(device))
+    return t.with_requires_grad(bool(requires_grad))
+
+
+def zeros(*shape, device=None, requires_grad=False) -> Tensor:
+    return full(shape, 0.0, device=device, requires_grad=requires_grad)
+
+
+def ones(*shape, device=None, requires_grad=False) -> Tensor:
+    return full(shape, 1.0, device=device, requires_grad=requires_grad)
+
+
+def full(shape, fill_value, *, device=None, requires_grad=False) -> Tensor:
+    if len(shape) == 1 and not isinstance(shape[0], int):
+        shape = tuple(shape[0])
+    return _C.full([int(d) for d in shape], _np.float32(fill_value), _device_str(device)).with_requires_grad(
+        bool(requires_grad))
+
+
+def is_tensor(obj) -> bool:
+    return isinstance(obj, Tensor)
+
+
+# ---- variable functions (src/python_variable_functions.rs:32-63) ----------
+
+def relu(input: Tensor) -> Tensor:
+    return input.relu()
+
+
+def exp(input: Tensor) -> Tensor:
+    return input.exp()
+
+
+def neg(input: Tensor) -> Tensor:
+    return input.neg()
+
+
+def add(input, other):
+    return input + other
+
+
+def sub(input, other):
+    return input - other
+
+
+def mul(input, other):
+    return input * other
+
+
+multiply = mul
+
+
+def div(input, other):
+    return input / other
+
+
+def matmul(input: Tensor, other: Tensor) -> Tensor:
+    return input.matmul(other)
+
+
+def sum(input: Tensor) -> Tensor:  # noqa: A001
+    return input.sum()
+
+
+def permute(input: Tensor, dims) -> Tensor:
+    return input.permute(tuple(dims))
+
+
+def transpose(input: Tensor, dim0: int, dim1: int) -> Tensor:
+    return input.transpose(dim0, dim1)
+
+
+def t(input: Tensor) -> Tensor:
+    return input.t()
+
+
+def clone(input: Tensor) -> Tensor:
+    return input.clone()
+
+
+def get_float32_matmul_precision() -> str:
+    """fp32 matmul runs on FP32 MFMA with fp32 accumulation: always "highest"
+    (python/torch_rs/__init__.py:81-85)."""
+    return "highest"
+
+
+def set_float32_matmul_precision(precision: str) -> None:
+    if precision != "highest":
+        raise RuntimeError("torch_rs runs fp32 matmul at 'highest' precision only")
+
+
+def get_num_threads() -> int:
+    return 1
+
+
+# ---- grad mode (src/grad_mode.rs) ---------------------------------------
+
+class no_grad(contextlib.ContextDecorator):
+    """Thread-local no-grad scope, usable as a context manager or decorator."""
+
+    def __enter__(self):
+        _C.enter_no_grad()
+        return self
+
+    def __exit__(self, *exc):
+        _C.exit_no_grad()
+        return False
+
+
+def is_grad_enabled() -> bool:
+    return _C.is_grad_enabled()
+
+
+# ---- Tensor conveniences (src/python.rs:3527-3919) ------------------------
+
+def _stride(self, dim=None):
+    s = self._strides()
+    if dim is None:
+        return s
+    r = max(len(s), 1)
+    if not -r <= dim < r:
+        raise IndexError(f"Dimension out of range (expected to be in range of [-{r}, {r - 1}], but got {dim})")
+    return s[dim]
+
+
+def _size(self, dim=None):
+    if dim is None:
+        return self.shape
+    return self.shape[dim]
+
+
+class _GradFn:
+    """Python-visible backward node (src/autograd_node.rs): named by class."""
+
+    _classes: dict = {}
+
+    @classmethod
+    def of(cls, name):
+        if name not in cls._classes:
+            cls._classes[name] = type(name, (cls,), {})
+        return cls._classes[name]()
+
+    def name(self):
+        return type(self).__name__
+
+    def __repr__(self):
+        return f"<{type(self).__name__} object>"
+
+
+def _grad_fn(self):
+    n = self._grad_fn_name
+    return None if n is None else _GradFn.of(n)
+
+
+def _grad(self):
+    return self._grad() if self._has_grad() else None
+
+
+def _repr(self):
+    body = _np.array2string(self.numpy(), precision=4, separator=", ")
+    extra = ""
+    if self.is_cuda:
+        extra += f", device='{self.device}'"
+    if self._grad_fn_name is not None:
+        extra += f", grad_fn=<{self._grad_fn_name}>"
+    elif self.requires_grad:
+        extra += ", requires_grad=True"
+    return f"tensor({body}{extra})"
+
+
+def _array(self, dtype=None, copy=None):
+    a = self.numpy()
+    return a if dtype is None else a.astype(dtype)
+
+
+def _len(self):
+    if not self.shape:
+        raise TypeError("len() of a 0-d tensor")
+    return self.shape[0]
+
+
+Tensor.stride = _stride
+Tensor.size = _size
+Tensor.grad_fn = property(_grad_fn)
+Tensor.grad = property(_grad)
+Tensor.dtype = property(lambda self: float32)
+Tensor.ndim = property(lambda self: self.dim())
+Tensor.cpu = lambda self: self.to("cpu")
+Tensor.cuda = lambda self, device=0: self.to(f"cuda:{device}")
+Tensor.tolist = lambda self: self.numpy().tolist()
+Tensor.__array__ = _array
+Tensor.__repr__ = _repr
+Tensor.__len__ = _len
+Tensor.multiply = Tensor.mul
+
+from . import autograd, cuda, nn  # noqa: E402,F401
+from .fusion import fuse  # noqa: E402,F401

@@ -142,10 +142,6 @@ def matmul(log, reps: int = 10) -> dict:
 
 def mlp(log, reps: int = 5) -> dict:
     """Config 4: 2-layer MLP forward+backward through the torch_rs API on the device."""
-    try:
-        import torch_rs  # noqa: F401
-    except Exception as exc:  # the host engine is optional for this report
-        return {"mlp": {"skipped": repr(exc)}}
     from . import mlp_bench
     return {"mlp": mlp_bench.run(log, reps)}
 

@@ -1,0 +1,264 @@
+"""Host-side checks of the C++ engine behind torch_rs (no GPU needed).
+
+The engine's output-layout planner is product code restated from
+src/tensor.rs; here it is pinned against the reference's golden stride
+fixtures and against the independent oracle restatement on random layouts.
+View metadata, graph recording on views, error messages and the fusion
+tracer are host logic and are checked on CPU tensors.
+"""
+import itertools
+import random
+
+import numpy as np
+import pytest
+
+import oracle as O
+import torch_rs
+from helpers import golden
+
+L = torch_rs._C.layout
+G = golden()
+
+
+# ---- golden output-stride fixtures (tests/tensor_baseline.rs) -------------------
+
+@pytest.mark.parametrize("case", G["output_strides"]["unary"], ids=lambda c: c["src"])
+def test_engine_unary_output_strides_golden(case):
+    n = int(np.prod(case["shape"], dtype=object)) if case["shape"] else 1
+    if "error" in case:
+        with pytest.raises(RuntimeError, match="Stride calculation overflowed"):
+            L.unary_output_strides(case["shape"], case["strides"], n)
+    else:
+        assert tuple(L.unary_output_strides(case["shape"], case["strides"], n)) == tuple(case["expected"])
+
+
+@pytest.mark.parametrize("case", G["output_strides"]["scalar"], ids=lambda c: c["src"])
+def test_engine_scalar_output_strides_golden(case):
+    assert tuple(L.scalar_output_strides(case["shape"], case["strides"])) == tuple(case["expected"])
+
+
+@pytest.mark.parametrize("case", G["output_strides"]["binary"], ids=lambda c: c["src"])
+def test_engine_binary_output_layout_golden(case):
+    args = (case["left_shape"], case["left_strides"], case["right_shape"], case["right_strides"])
+    if "error" in case:
+        msg = {"stride_overflow": "Stride calculation overflowed",
+               "shape_mismatch": "must match the size of tensor b"}[case["error"]]
+        with pytest.raises(RuntimeError, match=msg):
+            L.binary_output_layout(*args)
+    else:
+        shape, strides = L.binary_output_layout(*args)
+        assert shape == tuple(case["out_shape"])
+        assert strides == tuple(case["expected"])
+
+
+def test_shape_mismatch_message_matches_reference():
+    g = G["shape_mismatch_message"]
+    a = torch_rs.zeros(*g["left_shape"])
+    b = torch_rs.zeros(*g["right_shape"])
+    with pytest.raises(RuntimeError) as e:
+        a + b
+    assert str(e.value) == g["message"]
+
+
+# ---- engine planner == oracle planner on random layouts ---------------------------
+
+def _random_layout(rng, rank):
+    shape = [rng.choice([0, 1, 1, 2, 3, 4]) if rng.random() < 0.15 else rng.choice([1, 2, 3, 4, 5])
+             for _ in range(rank)]
+    kind = rng.random()
+    cs = list(O.contiguous_strides(shape))
+    if kind < 0.3:
+        strides = cs
+    elif kind < 0.6:  # permuted dense
+        perm = list(range(rank))
+        rng.shuffle(perm)
+        pshape = [shape[p] for p in perm]
+        pcs = O.contiguous_strides(pshape)
+        strides = [0] * rank
+        for i, p in enumerate(perm):
+            strides[p] = pcs[i]
+    elif kind < 0.8:  # sliced / strided
+        strides = [s * rng.choice([1, 2, 3]) for s in cs]
+    else:  # arbitrary, incl. zero strides
+        strides = [rng.choice([0, 1, 2, 3, 5, 7, 12]) for _ in range(rank)]
+    return shape, strides
+
+
+def _broadcast_partner(rng, shape):
+    rank = rng.randint(0, len(shape))
+    out = list(shape[len(shape) - rank:])
+    for i in range(len(out)):
+        if rng.random() < 0.3:
+            out[i] = 1
+    return out
+
+
+def test_engine_planner_matches_oracle_on_random_layouts():
+    rng = random.Random(0xC0FFEE)
+    checked = 0
+    for _ in range(3000):
+        rank = rng.randint(0, 5)
+        shape, strides = _random_layout(rng, rank)
+        n = int(np.prod(shape)) if shape else 1
+        assert L.is_contiguous(shape, strides, n) == O.is_contiguous(shape, strides)
+        assert L.is_non_overlapping_and_dense(shape, strides, n) == O.is_non_overlapping_and_dense(shape, strides)
+        assert tuple(L.unary_output_strides(shape, strides, n)) == O.unary_output_strides(shape, strides)
+        assert tuple(L.scalar_output_strides(shape, strides)) == O.scalar_output_strides(shape, strides)
+        rshape = _broadcast_partner(rng, shape) if rng.random() < 0.5 else list(shape)
+        _, rstrides = _random_layout(rng, len(rshape))
+        rstrides = rstrides if rshape == shape or rng.random() < 0.5 else list(O.contiguous_strides(rshape))
+        if rng.random() < 0.5:
+            shape, strides, rshape, rstrides = rshape, rstrides, shape, strides
+        want = O.binary_output_layout(shape, strides, rshape, rstrides)
+        got = L.binary_output_layout(shape, strides, rshape, rstrides)
+        assert got == want, (shape, strides, rshape, rstrides)
+        checked += 1
+    assert checked == 3000
+
+
+# ---- reshape / view strides ----------------------------------------------------------
+
+def _offsets(shape, strides):
+    return [sum(i * s for i, s in zip(idx, strides)) for idx in itertools.product(*[range(d) for d in shape])]
+
+
+def test_reshape_view_strides_are_sound_on_random_layouts():
+    rng = random.Random(7)
+    views = 0
+    for _ in range(2000):
+        rank = rng.randint(1, 4)
+        shape = [rng.choice([1, 2, 3, 4]) for _ in range(rank)]
+        _, strides = _random_layout(rng, rank)
+        n = int(np.prod(shape))
+        # a random factorisation of n as the new shape
+        new, rem = [], n
+        while rem > 1 and len(new) < 4:
+            f = rng.choice([d for d in range(1, rem + 1) if rem % d == 0])
+            new.append(f)
+            rem //= f
+        new.append(rem)
+        got = L.reshape_view_strides(shape, strides, new, n)
+        if got is not None:
+            views += 1
+            assert _offsets(new, got) == _offsets(shape, strides)
+    assert views > 500
+
+
+def test_view_of_transposed_matrix_is_rejected_and_reshape_copies_on_device_only():
+    x = torch_rs.zeros(2, 3)
+    with pytest.raises(RuntimeError, match="view size is not compatible"):
+        x.mT.view(6)
+    assert x.view(3, 2).stride() == (2, 1)
+    assert x.view(-1).shape == (6,)
+    with pytest.raises(RuntimeError, match="only one dimension can be inferred"):
+        x.view(-1, -1)
+    with pytest.raises(RuntimeError, match=r"shape '\[4, -1\]' is invalid for input of size 6"):
+        x.view(4, -1)
+
+
+# ---- view metadata and graph recording on host tensors ------------------------------
+
+def test_view_metadata_matches_reference_rules():
+    x = torch_rs.zeros(2, 3, 4)
+    p = x.permute(2, 0, 1)
+    assert p.shape == (4, 2, 3) and p.stride() == (1, 12, 4)
+    t = x.transpose(0, 2)
+    assert t.shape == (4, 3, 2) and t.stride() == (1, 4, 12)
+    assert x.mT.shape == (2, 4, 3) and x.mT.stride() == (12, 1, 4)
+    assert x.T.shape == (4, 3, 2)
+    s = x[1]
+    assert s.shape == (3, 4) and s.storage_offset() == 12
+    assert x[-1].storage_offset() == 12
+    with pytest.raises(IndexError, match="index 2 is out of bounds for dimension 0 with size 2"):
+        x[2]
+    with pytest.raises(RuntimeError, match="duplicate dims"):
+        x.permute(0, 0, 1)
+    with pytest.raises(IndexError, match=r"Dimension out of range \(expected to be in range of \[-3, 2\], but got 3\)"):
+        x.transpose(0, 3)
+    with pytest.raises(RuntimeError, match="tensor.mT is only supported on matrices"):
+        torch_rs.zeros(3).mT
+
+
+def test_views_record_transform_nodes_and_leafness():
+    x = torch_rs.zeros(2, 3, requires_grad=True)
+    assert x.is_leaf and x.requires_grad and x.grad_fn is None and x.grad is None
+    assert x.permute(1, 0).grad_fn.name() == "PermuteBackward0"
+    assert x.transpose(0, 1).grad_fn.name() == "TransposeBackward0"
+    assert x.t().grad_fn.name() == "TBackward0"
+    assert x.view(6).grad_fn.name() == "ViewBackward0"
+    assert x[0].grad_fn.name() == "SelectBackward0"
+    v = x.view(3, 2)
+    assert v.requires_grad and not v.is_leaf
+    with torch_rs.no_grad():
+        w = x.view(6)
+        assert w.requires_grad and w.grad_fn is None  # view_requires_grad without an edge
+        assert not torch_rs.is_grad_enabled()
+    assert torch_rs.is_grad_enabled()
+    d = x.detach()
+    assert not d.requires_grad and d.is_leaf
+
+
+def test_backward_errors_match_reference_messages():
+    x = torch_rs.zeros(2)
+    with pytest.raises(RuntimeError, match="element 0 of tensors does not require grad"):
+        x.backward()
+    y = torch_rs.zeros(2, requires_grad=True)
+    with pytest.raises(RuntimeError, match="grad can be implicitly created only for scalar outputs"):
+        y.backward()
+
+
+def test_host_tensors_do_not_compute():
+    x = torch_rs.tensor([1.0, 2.0])
+    with pytest.raises(RuntimeError, match="device tensors only"):
+        x * 2.0
+    with pytest.raises(RuntimeError, match="device tensors only"):
+        x.exp()
+    assert x.tolist() == [1.0, 2.0]
+    assert np.asarray(x).dtype == np.float32
+
+
+def test_tensor_constructor_and_scalar_conversion():
+    t = torch_rs.tensor([[1, 2], [3, 4.5]])
+    assert t.shape == (2, 2) and t.numpy().tolist() == [[1.0, 2.0], [3.0, 4.5]]
+    assert torch_rs.tensor(0.1).numpy() == np.float32(0.1)
+    assert torch_rs.tensor(np.arange(6, dtype=np.float64).reshape(2, 3)).stride() == (3, 1)
+    with pytest.raises(TypeError, match="invalid data type 'bytes'"):
+        torch_rs.tensor(b"ab")
+    with pytest.raises(ValueError):
+        torch_rs.tensor([[1.0], [2.0, 3.0]])
+    assert torch_rs.get_float32_matmul_precision() == "highest"
+
+
+def test_dropout_bridge_cases_on_host():
+    F = torch_rs.nn.functional
+    x = torch_rs.zeros(4)
+    assert F.dropout(x, 0.5, training=False) is x
+    assert F.dropout(x, 0.0) is x
+    with pytest.raises(RuntimeError, match="dropout probability has to be between 0 and 1, but got 1.5"):
+        F.dropout(x, 1.5)
+    with pytest.raises(NotImplementedError, match="does not support sampling"):
+        F.dropout(x, 0.5)
+    with pytest.raises(NotImplementedError, match="inplace=True"):
+        F.relu(x, inplace=True)
+
+
+# ---- fusion tracer --------------------------------------------------------------------------
+
+def test_fusion_tracer_emits_one_rounding_per_op_and_eager_layout():
+    f = torch_rs.fuse(lambda x, y, z: ((x * y + z).exp() - 1.0).relu())
+    x = torch_rs.zeros(8)
+    ir, shape, strides = f.trace(x, x, x)
+    assert ir == "in f32\nin f32\nin f32\nmul %0 %1\nadd %3 %2\nexp %4\nconst 0x3f800000\nsub %5 %6\nrelu %7\nout %8\n"
+    assert shape == (8,) and strides == (1,)
+    # (a + b) * c.mT: the planner's contiguous output for config 2's layouts
+    g = torch_rs.fuse(lambda a, b, c: (a + b) * c)
+    a, b = torch_rs.zeros(64, 1, 8), torch_rs.zeros(1, 16, 8)
+    c = torch_rs.zeros(64, 8, 16).mT
+    _, shape, strides = g.trace(a, b, c)
+    want_shape, want_strides = O.binary_output_layout((64, 16, 8), O.contiguous_strides((64, 16, 8)),
+                                                      c.shape, c.stride())
+    assert shape == want_shape == (64, 16, 8) and strides == want_strides
+    # scalar forms: s - x, s / x -> s * (1 / x), x * s
+    h = torch_rs.fuse(lambda x: (2.0 - x) + 3.0 / x + x * 0.5)
+    ir, _, _ = h.trace(x)
+    assert "sub %1 %0" in ir and "div %" in ir and "mul %0 %" in ir
