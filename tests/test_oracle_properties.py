@@ -144,3 +144,55 @@ def test_binary_broadcast_matches_numpy_elementwise():
 
 def test_libc_version_recorded():
     assert O.libc_version()
+
+
+def test_row_broadcast_matches_general_broadcast_and_numpy():
+    """orc_row_broadcast_f32 (the trailing-vector fast path, tensor.rs:3454-3543)
+    agrees with the oracle's general odometer path and with numpy's IEEE ops."""
+    rng = np.random.default_rng(21)
+    rows, cols = 37, 65
+    x = rng.standard_normal(rows * cols).astype(np.float32)
+    v = rng.standard_normal(cols).astype(np.float32)
+    for op, fn in ((O.ADD, np.add), (O.SUB, np.subtract), (O.MUL, np.multiply), (O.DIV, np.divide)):
+        fast = O.row_broadcast(op, x, v, rows, cols)
+        general = O.binary(op, x, (rows, cols), (cols, 1), 0, v, (cols,), (1,), 0, (rows, cols), (cols, 1))
+        assert np.array_equal(fast.view(np.uint32), general.view(np.uint32))
+        assert np.array_equal(fast, fn(x.reshape(rows, cols), v).ravel())
+
+
+def test_mask_apply_is_two_roundings_and_keeps_signed_zeros():
+    """(h * m) * s as the reference's mul then mul_scalar: two IEEE roundings,
+    -x * 0 -> -0.0 (not a select), NaN * 0 -> NaN."""
+    rng = np.random.default_rng(22)
+    h = rng.standard_normal(4096).astype(np.float32)
+    h[:4] = [-3.0, np.nan, np.inf, -0.0]
+    m = (rng.random(4096) < 0.9).astype(np.uint8)
+    m[:4] = 0
+    s = np.float32(1 / 0.9)
+    out = O.mask_apply(h, m, s)
+    with np.errstate(invalid="ignore"):
+        want = (h * m.astype(np.float32)) * s
+    assert np.array_equal(out.view(np.uint32)[4:], want.view(np.uint32)[4:])
+    assert out.view(np.uint32)[0] == 0x80000000  # -3 * 0 = -0.0
+    assert out.view(np.uint32)[3] == 0x80000000  # -0 * 0 = -0.0
+    assert np.isnan(out[1]) and np.isnan(out[2])  # NaN*0 and inf*0 are NaN
+
+
+def test_accumulate_is_elementwise_ieee_add():
+    rng = np.random.default_rng(23)
+    a = rng.standard_normal(1000).astype(np.float32)
+    b = rng.standard_normal(1000).astype(np.float32)
+    dst = a.copy()
+    O.lib().orc_accumulate_f32(dst.ctypes.data, b.ctypes.data, 1000)
+    assert np.array_equal(dst, a + b)
+
+
+def test_bound_helpers_are_absolute_value_products_in_double():
+    rng = np.random.default_rng(24)
+    a = rng.standard_normal((9, 13)).astype(np.float32)
+    b = rng.standard_normal((13, 7)).astype(np.float32)
+    rows = np.arange(9)
+    _, bound = O.matmul_rows(a.ravel(), (9, 13), (13, 1), b.ravel(), (13, 7), (7, 1), rows)
+    want = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    assert np.allclose(bound, want, rtol=1e-12, atol=0)
+    assert np.isclose(O.sum_abs(a.ravel()), np.abs(a.astype(np.float64)).sum(), rtol=1e-12)
