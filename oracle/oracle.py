@@ -7,7 +7,7 @@ and only as the checker (or the timed CPU baseline), never as a product path.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_uint64, c_void_p
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_uint32, c_uint64, c_void_p
 from pathlib import Path
 
 import numpy as np
@@ -86,6 +86,7 @@ def lib() -> ctypes.CDLL:
             "orc_reduce_to_shape_f32": ([c_void_p, _LP, _LP, c_void_p], None),
             "orc_permute_backward_f32": ([c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p], None),
             "orc_accumulate_f32": ([c_void_p, c_void_p, c_uint64], None),
+            "orc_exp_max_ulp": ([c_void_p, c_uint32, c_uint64, c_int, POINTER(c_uint64)], c_uint64),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -282,3 +283,11 @@ def permute_backward(up, out_shape, dims, in_shape):
     os_, d_, is_ = (np.asarray(v, dtype=np.int64) for v in (out_shape, dims, in_shape))
     lib().orc_permute_backward_f32(_p(up), len(out_shape), _p(os_), _p(d_), _p(is_), _p(out))
     return out[:n]
+
+
+def exp_max_ulp(got: np.ndarray, first_bits: int, threads: int = 8):
+    """(max ulp distance, index) of got[i] from glibc expf(bits first_bits + i)."""
+    got = np.ascontiguousarray(got, dtype=np.float32)
+    idx = c_uint64()
+    worst = lib().orc_exp_max_ulp(_p(got), first_bits, got.size, threads, ctypes.byref(idx))
+    return int(worst), int(idx.value)

@@ -23,6 +23,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <gnu/libc-version.h>
+#include <pthread.h>
 
 #define ORC_MAX_RANK 8
 
@@ -759,4 +760,77 @@ void orc_permute_backward_f32(const float *up, int rank, const int64_t *out_shap
  * storage.rs:85-100): dst[i] += src[i]. */
 void orc_accumulate_f32(float *dst, const float *src, uint64_t n) {
     for (uint64_t i = 0; i < n; i++) dst[i] += src[i];
+}
+
+/* ------------------------------------------------------------------------ */
+/* Exhaustive exp checker                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* Largest distance, in representable floats, between got[i] and glibc
+ * expf(x) for the n consecutive bit patterns x = first_bits + i (both NaN
+ * counts as 0).  Split over `threads` POSIX threads; each computes the same
+ * expf the reference calls (tensor.rs:2398-2400).  Checker only. */
+typedef struct {
+    const float *got;
+    uint32_t first;
+    uint64_t begin, end;
+    uint64_t worst;
+    uint64_t worst_index;
+} exp_chunk;
+
+static int64_t ordered_bits(float f) {
+    int32_t i;
+    memcpy(&i, &f, 4);
+    return i < 0 ? -(int64_t)(i & 0x7fffffff) : (int64_t)i;
+}
+
+static void *exp_check_worker(void *arg) {
+    exp_chunk *c = (exp_chunk *)arg;
+    for (uint64_t i = c->begin; i < c->end; i++) {
+        const float x = u2f((uint32_t)(c->first + i));
+        const float want = expf(x), got = c->got[i];
+        uint64_t d;
+        if (want != want || got != got) d = (want != want && got != got) ? 0 : UINT64_MAX;
+        else {
+            int64_t a = ordered_bits(got), b = ordered_bits(want);
+            d = (uint64_t)(a > b ? a - b : b - a);
+        }
+        if (d > c->worst) {
+            c->worst = d;
+            c->worst_index = i;
+        }
+    }
+    return NULL;
+}
+
+uint64_t orc_exp_max_ulp(const float *got, uint32_t first_bits, uint64_t n, int threads,
+                         uint64_t *worst_index) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t tid[64];
+    exp_chunk ch[64];
+    const uint64_t per = (n + (uint64_t)threads - 1) / (uint64_t)threads;
+    int started = 0;
+    for (int t = 0; t < threads; t++) {
+        ch[t].got = got;
+        ch[t].first = first_bits;
+        ch[t].begin = (uint64_t)t * per < n ? (uint64_t)t * per : n;
+        ch[t].end = ch[t].begin + per < n ? ch[t].begin + per : n;
+        ch[t].worst = 0;
+        ch[t].worst_index = 0;
+        if (pthread_create(&tid[t], NULL, exp_check_worker, &ch[t]) == 0) started = t + 1;
+        else {
+            exp_check_worker(&ch[t]);
+        }
+    }
+    uint64_t worst = 0, wi = 0;
+    for (int t = 0; t < threads; t++) {
+        if (t < started) pthread_join(tid[t], NULL);
+        if (ch[t].worst > worst) {
+            worst = ch[t].worst;
+            wi = ch[t].worst_index;
+        }
+    }
+    if (worst_index) *worst_index = wi;
+    return worst;
 }
