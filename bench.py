@@ -103,26 +103,35 @@ def main() -> int:
     def fused_step():
         check(abi.lib.trs_fusion_launch(kid, 3, ptrs, lays, dout.ptr, ctypes.byref(lay)))
 
+    from trs_backend.timing import Event, stream
+
     for _ in range(args.warmup):
         fused_step()
     check(abi.lib.trs_synchronize())
+    s = stream()
+    ev0, ev1 = Event(), Event()
     t0 = time.perf_counter()
+    ev0.record(s)
     for _ in range(args.steps):
         fused_step()
+    ev1.record(s)
     check(abi.lib.trs_synchronize())
     wall = time.perf_counter() - t0
     bytes_per_step = 16 * n
     value = bytes_per_step * args.steps / wall / 1e9
-    ev = time_launches(fused_step, reps=max(10, args.steps), warmup=0)
-    kern_ms = statistics.mean(ev)
+    # The dominant (only) kernel's average duration over the timed region,
+    # from HIP events on the stream it runs on.
+    kern_ms = ev0.elapsed_ms(ev1) / args.steps
     achieved = bytes_per_step / (kern_ms * 1e-3) / 1e9
+    ev = time_launches(fused_step, reps=max(10, args.steps), warmup=0)
     log(f"fused chain: {value:.0f} GB/s wall, kernel {kern_ms * 1e3:.1f} us avg -> {achieved:.0f} GB/s")
 
     # Checksum of a strided sample of the output (materialised result).
     out_sample = dout.to_numpy(count=n)[:: 4099]
     checksum = float(np.sum(out_sample, dtype=np.float64))
 
-    extra = {"fused_chain": {"kernel_us_median": statistics.median(ev) * 1e3,
+    extra = {"fused_chain": {"kernel_us_avg_timed_region": kern_ms * 1e3,
+                             "kernel_us_median_single_launch": statistics.median(ev) * 1e3,
                              "kernel_us_min": min(ev) * 1e3, "kernel_us_max": max(ev) * 1e3,
                              "hiprtc_compile_ms": compile_ms.value, "output_sample_checksum": checksum}}
 

@@ -7,8 +7,13 @@
 // python/torch_rs/__init__.py:81-85) but sums in MFMA order, so it is checked
 // against the reference within |dC| <= 1e-5*sqrt(K)*(|A||B|).
 //
-// Tiling: a 256-lane block (4 waves, 2x2) owns a BM x BN tile of C; each wave
-// owns (BM/2) x (BN/2) as a grid of 16x16 MFMA tiles held in accumulators.
+// Tiling: a block of WGM x WGN waves owns a BM x BN tile of C; each wave owns
+// (BM/WGM) x (BN/WGN) as a grid of 16x16 MFMA tiles held in accumulators.
+// Two shapes are used: 256x256x16 with 16 waves (one block per CU, 4 waves
+// per SIMD) when the output has at least one such tile per CU, else
+// 128x128x32 with 4 waves (two blocks per CU).  Measured on the MI355X at
+// 4096^3: 84-88% of the FP32 MFMA peak for the large shape in every operand
+// layout, against 71-80% for the small one.
 // K advances in BK slices staged through LDS, double-buffered: the next
 // slice's global loads are issued into registers before the MFMAs of the
 // current slice and written to the other LDS buffer afterwards, so one
@@ -47,19 +52,20 @@ constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
 // Load an R x C tile whose C dim is contiguous in memory (row stride ld),
-// starting at (r0, c0) of an Rv x Cv matrix, into registers.
-template <int R, int C, bool FULL>
+// starting at (r0, c0) of an Rv x Cv matrix, into registers: NT lanes, one
+// float4 each per step.
+template <int R, int C, int NT, bool FULL>
 struct TileLoader {
-    static constexpr int kVec = R * C / 4;           // float4 per tile
-    static constexpr int kPerThread = kVec / 256;    // float4 per lane
-    static_assert(kVec % 256 == 0, "tile must split evenly over 256 lanes");
+    static constexpr int kVec = R * C / 4;          // float4 per tile
+    static constexpr int kPerThread = kVec / NT;    // float4 per lane
+    static_assert(kVec % NT == 0 && kPerThread >= 1, "tile must split evenly over the block");
     vf4 v[kPerThread];
 
     __device__ __forceinline__ void load(const float *src, int64_t ld, int64_t r0, int64_t c0, int64_t Rv,
                                          int64_t Cv) {
 #pragma unroll
         for (int i = 0; i < kPerThread; i++) {
-            const int q = threadIdx.x + 256 * i;
+            const int q = threadIdx.x + NT * i;
             const int r = q / (C / 4);
             const int c = (q % (C / 4)) * 4;
             const int64_t gr = r0 + r, gc = c0 + c;
@@ -83,7 +89,7 @@ struct TileLoader {
     __device__ __forceinline__ void store(float *lds) const {
 #pragma unroll
         for (int i = 0; i < kPerThread; i++) {
-            const int q = threadIdx.x + 256 * i;
+            const int q = threadIdx.x + NT * i;
             const int r = q / (C / 4);
             const int c = (q % (C / 4)) * 4;
             *(vf4 *)(lds + r * PITCH + c) = v[i];
@@ -91,9 +97,10 @@ struct TileLoader {
     }
 };
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool FULL>
-__global__ void __launch_bounds__(256, 2) gemm_f32_mfma(GemmArgs args) {
-    constexpr int WM = BM / 2, WN = BN / 2;     // wave tile
+template <int BM, int BN, int BK, int WGM, int WGN, int MINB, bool TA, bool TB, bool FULL>
+__global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs args) {
+    constexpr int NT = WGM * WGN * 64;          // lanes per block
+    constexpr int WM = BM / WGM, WN = BN / WGN; // wave tile
     constexpr int TM = WM / 16, TN = WN / 16;   // MFMA tiles per wave
     // LDS tile shapes in memory order.
     constexpr int AR = TA ? BK : BM, AC = TA ? BM : BK;  // A: [m][k] or [k][m]
@@ -128,10 +135,10 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_mfma(GemmArgs args) {
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+    const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
 
-    TileLoader<AR, AC, FULL> la;
-    TileLoader<BR, BC, FULL> lb;
+    TileLoader<AR, AC, NT, FULL> la;
+    TileLoader<BR, BC, NT, FULL> lb;
 
     typedef float vf4acc __attribute__((ext_vector_type(4)));
     vf4acc acc[TM][TN];
@@ -224,15 +231,39 @@ __global__ void __launch_bounds__(256) gemm_f32_strided(const float *a, const fl
     }
 }
 
-template <int BM, int BN, int BK, bool TA, bool TB>
-int launch_tiled(const GemmArgs &g, bool full, hipStream_t s) {
+// A tile configuration: BM x BN x BK, a WGM x WGN grid of waves, MINB
+// blocks per CU requested from the compiler.
+template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int MINB_>
+struct Tiles {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, MINB = MINB_;
+    static constexpr int NT = WGM * WGN * 64;
+};
+using LargeTiles = Tiles<256, 256, 16, 4, 4, 1>;
+using SmallTiles = Tiles<128, 128, 32, 2, 2, 2>;
+
+template <class T, bool TA, bool TB>
+int launch_tiled(GemmArgs g, bool full, hipStream_t s) {
+    g.tiles_m = (int32_t)((g.M + T::BM - 1) / T::BM);
+    g.tiles_n = (int32_t)((g.N + T::BN - 1) / T::BN);
     const int64_t blocks = (int64_t)g.tiles_m * g.tiles_n * g.batch;
+    g.xcd_remap = blocks % kXcds == 0 ? 1 : 0;
+    const dim3 grid((unsigned)blocks), block(T::NT);
     if (full)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, TA, TB, true>), dim3((unsigned)blocks), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_f32_mfma<T::BM, T::BN, T::BK, T::WGM, T::WGN, T::MINB, TA, TB, true>), grid, block,
+                           0, s, g);
     else
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, TA, TB, false>), dim3((unsigned)blocks), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_f32_mfma<T::BM, T::BN, T::BK, T::WGM, T::WGN, T::MINB, TA, TB, false>), grid, block,
+                           0, s, g);
     TRS_LAUNCH_CHECK("gemm kernel launch");
     return TRS_OK;
+}
+
+template <class T>
+int launch_layout(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipStream_t s) {
+    if (a_plain && b_plain) return launch_tiled<T, false, false>(g, full, s);
+    if (a_plain) return launch_tiled<T, false, true>(g, full, s);
+    if (b_plain) return launch_tiled<T, true, false>(g, full, s);
+    return launch_tiled<T, true, true>(g, full, s);
 }
 
 }  // namespace
@@ -287,7 +318,6 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
         return TRS_OK;
     }
 
-    constexpr int BM = 128, BN = 128, BK = 32;
     GemmArgs g{};
     g.a = A;
     g.b = B;
@@ -302,15 +332,15 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
     g.bsb = bsb;
     g.bsc = M * N;
     g.batch = batch;
-    g.tiles_m = (int32_t)((M + BM - 1) / BM);
-    g.tiles_n = (int32_t)((N + BN - 1) / BN);
-    const int64_t blocks = (int64_t)g.tiles_m * g.tiles_n * batch;
-    g.xcd_remap = blocks % kXcds == 0 ? 1 : 0;
     auto al16 = [](const float *p) { return ((uintptr_t)p % 16) == 0; };
-    bool full = M % BM == 0 && N % BN == 0 && K % BK == 0 && al16(A) && al16(B) && al16(C) && g.lda % 4 == 0 &&
-                g.ldb % 4 == 0 && (batch == 1 || (bsa % 4 == 0 && bsb % 4 == 0));
-    if (a_plain && b_plain) return launch_tiled<BM, BN, BK, false, false>(g, full, dev->stream);
-    if (a_plain && !b_plain) return launch_tiled<BM, BN, BK, false, true>(g, full, dev->stream);
-    if (!a_plain && b_plain) return launch_tiled<BM, BN, BK, true, false>(g, full, dev->stream);
-    return launch_tiled<BM, BN, BK, true, true>(g, full, dev->stream);
+    const bool aligned = al16(A) && al16(B) && al16(C) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                         (batch == 1 || (bsa % 4 == 0 && bsb % 4 == 0));
+    // The large tile only when it divides the problem and still gives every
+    // CU a block; otherwise the small tile (full or edge-guarded).
+    const int64_t large_tiles = (M / LargeTiles::BM) * (N / LargeTiles::BN) * batch;
+    if (aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0 && K % LargeTiles::BK == 0 &&
+        large_tiles >= dev->cu_count)
+        return launch_layout<LargeTiles>(g, a_plain, b_plain, true, dev->stream);
+    const bool full = aligned && M % SmallTiles::BM == 0 && N % SmallTiles::BN == 0 && K % SmallTiles::BK == 0;
+    return launch_layout<SmallTiles>(g, a_plain, b_plain, full, dev->stream);
 }

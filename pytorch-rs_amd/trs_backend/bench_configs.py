@@ -7,14 +7,13 @@ several buffer sets so the GB/s figures reflect HBM.
 from __future__ import annotations
 
 import ctypes
-import statistics
 
 import numpy as np
 
 from . import abi
 from .abi import DeviceArray, check, layout_of
 from .configs import generate
-from .timing import time_launches
+from .timing import time_launches, time_region
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
@@ -60,8 +59,8 @@ def relu_bias(log, reps: int = 20, sets: int = 3) -> dict:
         i[0] += 1
         _fuse_launch(kid, [xs[k], db], [lx, lb], outs[k], lx)
 
-    e = statistics.median(time_launches(eager, reps))
-    f = statistics.median(time_launches(fused, reps))
+    e = time_region(eager, reps)
+    f = time_region(fused, reps)
     log(f"relu_bias: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us")
     return {"relu_bias": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
                           "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
@@ -99,8 +98,8 @@ def broadcast_strided(log, reps: int = 20, sets: int = 2) -> dict:
         i[0] += 1
         _fuse_launch(kid, [da, db, dcs[k]], [la, lb, lc], outs[k], lo)
 
-    e = statistics.median(time_launches(eager, reps))
-    f = statistics.median(time_launches(fused, reps))
+    e = time_region(eager, reps)
+    f = time_region(fused, reps)
     log(f"broadcast_strided: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us")
     return {"broadcast_strided": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
                                   "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
@@ -118,10 +117,11 @@ def matmul(log, reps: int = 10) -> dict:
     def mm():
         check(abi.lib.trs_matmul_f32(dA.ptr, ctypes.byref(l), dB.ptr, ctypes.byref(l), dC.ptr, ctypes.byref(l)))
 
+    med = time_region(mm, reps)
     t = time_launches(mm, reps)
-    med = statistics.median(t)
     tf = 2 * K ** 3 / (med * 1e-3) / 1e12
-    out["matmul_4096"] = {"ms_median": med, "ms_min": min(t), "TFLOPS": tf, "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS}
+    out["matmul_4096"] = {"ms_avg": med, "ms_min_single_launch": min(t), "TFLOPS": tf,
+                          "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS}
     log(f"matmul 4096^3: {med:.3f} ms, {tf:.1f} TFLOPS")
     Ab, Bb = generate("matmul", "Ab"), generate("matmul", "Bb")
     dAb, dBb, dCb = DeviceArray.from_numpy(Ab), DeviceArray.from_numpy(Bb), DeviceArray(32 * 512 * 512 * 4)
@@ -131,10 +131,10 @@ def matmul(log, reps: int = 10) -> dict:
         check(abi.lib.trs_matmul_f32(dAb.ptr, ctypes.byref(lb), dBb.ptr, ctypes.byref(lb), dCb.ptr,
                                      ctypes.byref(lb)))
 
+    med = time_region(bmm, reps * 3)
     t = time_launches(bmm, reps * 3)
-    med = statistics.median(t)
     tf = 2 * 32 * 512 ** 3 / (med * 1e-3) / 1e12
-    out["matmul_batched_32x512"] = {"ms_median": med, "ms_min": min(t), "TFLOPS": tf,
+    out["matmul_batched_32x512"] = {"ms_avg": med, "ms_min_single_launch": min(t), "TFLOPS": tf,
                                     "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS}
     log(f"batched matmul 32x512^3: {med:.3f} ms, {tf:.1f} TFLOPS")
     return out

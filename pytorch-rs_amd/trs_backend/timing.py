@@ -70,3 +70,19 @@ def time_launches(fn, reps: int, warmup: int = 3) -> list[float]:
         b.synchronize()
         times.append(a.elapsed_ms(b))
     return times
+
+
+def time_region(fn, reps: int, warmup: int = 3) -> float:
+    """Average device time (ms) per call of `fn` over `reps` back-to-back calls,
+    from one pair of events around the whole region on trs_stream."""
+    s = stream()
+    for _ in range(warmup):
+        fn()
+    check(lib.trs_synchronize())
+    a, b = Event(), Event()
+    a.record(s)
+    for _ in range(reps):
+        fn()
+    b.record(s)
+    b.synchronize()
+    return a.elapsed_ms(b) / reps

@@ -136,3 +136,18 @@ def test_inner_mismatch_and_rank_errors():
     rc = abi.lib.trs_matmul_f32(a.ptr, ctypes.byref(abi.layout_of((6,))), a.ptr, ctypes.byref(abi.layout_of((6,))),
                                 out.ptr, ctypes.byref(abi.layout_of((1,))))
     assert rc == -6
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_large_tile_all_layouts_exact_on_small_integers(ta, tb):
+    """4096 x 256 @ 256 x 4096 takes the 256x256 tile path in every operand
+    layout; small integers make every order of summation exact."""
+    rng = np.random.default_rng(31)
+    m, k, n = 4096, 256, 4096
+    a = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    b = rng.integers(-3, 4, (k, n)).astype(np.float32)
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    ast, aoff = (np.ascontiguousarray(a.T), (1, m)) if ta else (a, (k, 1))
+    bst, boff = (np.ascontiguousarray(b.T), (1, k)) if tb else (b, (n, 1))
+    got = U.matmul(ast.ravel(), (m, k), aoff, 0, bst.ravel(), (k, n), boff, 0)
+    assert np.array_equal(got, want)
