@@ -152,13 +152,13 @@ int generate(const std::string &ir, Program *prog) {
     }
     s << "    return v" << result << ";\n  }\n};\n";
     const std::string mask = std::to_string(u8mask) + "u";
-    auto wrap = [&](const char *name, const std::string &body) {
-        s << "extern \"C\" __global__ void __launch_bounds__(256) " << name
+    auto wrap = [&](const char *name, const std::string &body, const char *lanes = "256") {
+        s << "extern \"C\" __global__ void __launch_bounds__(" << lanes << ") " << name
           << "(trs::PwGeom g, trs::PwPtrs p) { " << body << "(TrsFused{}, g, p); }\n";
     };
-    wrap("trs_fused_flat_c", "trs::pw_flat_contig_body<TrsFused, " + mask + ">");
-    wrap("trs_fused_flat_v", "trs::pw_flat_body<TrsFused, " + mask + ", true>");
-    wrap("trs_fused_flat_s", "trs::pw_flat_body<TrsFused, " + mask + ", false>");
+    wrap("trs_fused_flat_c", "trs::pw_flat_contig_body<TrsFused, " + mask + ">", "trs::kFlatBlock");
+    wrap("trs_fused_flat_v", "trs::pw_flat_body<TrsFused, " + mask + ", true>", "trs::kFlatBlock");
+    wrap("trs_fused_flat_s", "trs::pw_flat_body<TrsFused, " + mask + ", false>", "trs::kFlatBlock");
     wrap("trs_fused_rows_v", "trs::pw_rows_body<TrsFused, " + mask + ", true>");
     wrap("trs_fused_rows_s", "trs::pw_rows_body<TrsFused, " + mask + ", false>");
     wrap("trs_fused_generic", "trs::pw_generic_body<TrsFused, " + mask + ">");
@@ -291,7 +291,8 @@ int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *input
     rc = get_function(prog, dev, name, &fn);
     if (rc) return rc;
     void *args[] = {(void *)&pl.g, (void *)&pl.p};
-    TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, 256, 1, 1, 0, dev->stream, args, nullptr),
+    TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, (unsigned)pl.block, 1, 1, 0, dev->stream, args,
+                                        nullptr),
                   "hipModuleLaunchKernel");
     return TRS_OK;
 }

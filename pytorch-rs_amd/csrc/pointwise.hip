@@ -72,9 +72,11 @@ struct ReluBackwardF {
 // ---- AOT wrappers -----------------------------------------------------------
 
 template <class F, unsigned M, bool V>
-__global__ void __launch_bounds__(256) k_flat(F f, PwGeom g, PwPtrs p) { pw_flat_body<F, M, V>(f, g, p); }
+__global__ void __launch_bounds__(kFlatBlock) k_flat(F f, PwGeom g, PwPtrs p) { pw_flat_body<F, M, V>(f, g, p); }
 template <class F, unsigned M>
-__global__ void __launch_bounds__(256) k_flat_contig(F f, PwGeom g, PwPtrs p) { pw_flat_contig_body<F, M>(f, g, p); }
+__global__ void __launch_bounds__(kFlatBlock) k_flat_contig(F f, PwGeom g, PwPtrs p) {
+    pw_flat_contig_body<F, M>(f, g, p);
+}
 template <class F, unsigned M, bool V>
 __global__ void __launch_bounds__(256) k_rows(F f, PwGeom g, PwPtrs p) { pw_rows_body<F, M, V>(f, g, p); }
 template <class F, unsigned M, bool V, int NT>
@@ -84,7 +86,7 @@ __global__ void __launch_bounds__(256) k_generic(F f, PwGeom g, PwPtrs p) { pw_g
 
 template <class F, unsigned M>
 int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
-    const dim3 grid((unsigned)pl.grid), block(256);
+    const dim3 grid((unsigned)pl.grid), block((unsigned)pl.block);
     switch (pl.variant) {
     case PwVariant::Empty:
         return TRS_OK;

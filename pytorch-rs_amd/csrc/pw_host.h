@@ -27,6 +27,7 @@ struct PwPlan {
     bool contig = false;  // Flat + vec with every input unit-stride and read once
     int ntransposed = 0;
     int nin = 0;
+    int block = 256;  // lanes per block (kFlatBlock for the flat variants)
     int64_t grid = 0;
     PwGeom g;
     PwPtrs p;
@@ -192,7 +193,8 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             for (int i = 0; i < nin; i++) all_unit &= is[i][0] == 1;
             plan->contig = vec && all_unit;
             const int64_t work = vec ? numel / 4 : numel;
-            plan->grid = std::min<int64_t>(std::max<int64_t>(1, (work + 255) / 256), want);
+            plan->block = kFlatBlock;
+            plan->grid = std::min<int64_t>(std::max<int64_t>(1, (work + kFlatBlock - 1) / kFlatBlock), want);
         } else {
             plan->variant = PwVariant::Rows;
             plan->vec = vec && size[inner] % 4 == 0;
