@@ -149,6 +149,12 @@ int trs_sum_f32(const float *x, const trs_layout *lx, float *out);
 int trs_fill_from_device_f32(float *out, size_t n, const float *value);
 /* out[0..n) = value. */
 int trs_fill_f32(float *out, size_t n, float value);
+/* grad = (up * scale) * f32(mask): the gradient of dropout-apply, as the
+ * reference's graph computes it for mul then mul_scalar -- the MultiplyScalar
+ * VJP (src/tensor.rs:3014-3021) followed by the Multiply VJP (:3031-3097) --
+ * in one pass, two roundings. */
+int trs_mask_backward_f32(const float *up, const trs_layout *lu, const uint8_t *mask,
+                          const trs_layout *lm, float scale, float *grad, const trs_layout *lg);
 /* grad (input-logical order) = relu'(input) * up; apply_relu_vjp
  * (src/tensor.rs:3161-3176) with relu_backward_value (:4422-4432).  `up` is
  * contiguous in the input's logical order. */

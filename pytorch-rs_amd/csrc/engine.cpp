@@ -571,8 +571,9 @@ std::vector<float> Tensor::to_host() const {
 }
 
 // Device transfer: copies the logical values into a fresh contiguous tensor
-// on `dev` (the same device returns this tensor).  Transfers are recorded as
-// identity transforms so gradients flow back to the source (CopyBackwards).
+// on `dev` (the same device returns this tensor).  A transfer of a tensor
+// that requires grad records a Transfer edge; backward through it raises,
+// because its gradient would have to be accumulated in host memory.
 Tensor Tensor::to(Device dev) const {
     if (dev == device()) return *this;
     const std::vector<float> host = to_host();
@@ -581,7 +582,7 @@ Tensor Tensor::to(Device dev) const {
         auto m = std::make_shared<AutogradMeta>();
         m->leaf = false;
         auto fn = std::make_unique<GradFn>();
-        fn->kind = GradKind::Identity;
+        fn->kind = GradKind::Transfer;
         fn->node = Node::Clone;
         SavedTensor s;
         s.shape = shape;
@@ -1162,7 +1163,12 @@ void consume(GradFn &fn) {
 }
 
 // Gradient of one node given its upstream (contiguous, node-output order).
-void apply_grad_fn(const GradFn &fn, const Grad &up, Device dev, std::map<GradKey, Grad> &grads) {
+// The caller hands `up` over: a VJP that passes the upstream through
+// unchanged gives its storage to the input instead of copying it.  `keep`
+// holds the storage until every kernel that reads it has been queued, so a
+// merge in add_gradient cannot return the block to the cache early.
+void apply_grad_fn(const GradFn &fn, Grad up, Device dev, std::map<GradKey, Grad> &grads) {
+    const StoragePtr keep = up.st;
     const trs_layout lup = abi_layout_of(up.shape, layout::contiguous_strides(up.shape), 0);
     const int64_t nup = layout::numel_of(up.shape);
     switch (fn.kind) {
@@ -1215,12 +1221,9 @@ void apply_grad_fn(const GradFn &fn, const Grad &up, Device dev, std::map<GradKe
     case GradKind::MaskApply: {  // (up * scale) * mask: the reverse of mul then mul_scalar
         const SavedTensor &in = fn.inputs[0];
         if (!in.autograd) return;
-        Grad t = new_grad(dev, in.shape), g = new_grad(dev, in.shape);
+        Grad g = new_grad(dev, in.shape);
         const trs_layout lg = abi_layout_of(in.shape, layout::contiguous_strides(in.shape), 0);
-        if (in.numel) {
-            check(trs_binary_scalar_f32(TRS_S_MUL, up.st->dptr, &lg, fn.scalar, t.st->dptr, &lg));
-            check(trs_mask_apply_f32(t.st->dptr, &lg, fn.mask->dptr, &lg, 1.0f, g.st->dptr, &lg));
-        }
+        if (in.numel) check(trs_mask_backward_f32(up.st->dptr, &lg, fn.mask->dptr, &lg, fn.scalar, g.st->dptr, &lg));
         add_gradient(grads, in.autograd, in.output_nr, std::move(g));
         return;
     }
@@ -1239,9 +1242,17 @@ void apply_grad_fn(const GradFn &fn, const Grad &up, Device dev, std::map<GradKe
     }
     case GradKind::AddTensor:
     case GradKind::SubTensor: {  // db = sum over broadcast dims of up
+        bool up_given = false;
         for (int side = 0; side < 2; side++) {
             const SavedTensor &self = fn.inputs[side];
             if (!self.autograd) continue;
+            const bool negate = side == 1 && fn.kind == GradKind::SubTensor;
+            if (!negate && !up_given && self.numel == nup) {
+                // Not broadcast: the gradient is the upstream itself.
+                add_gradient(grads, self.autograd, self.output_nr, Grad{up.st, self.shape});
+                up_given = true;
+                continue;
+            }
             Grad g = new_grad(dev, self.shape);
             const trs_layout ls = abi_layout_of(self.shape, layout::contiguous_strides(self.shape), 0);
             if (self.numel) {
@@ -1278,12 +1289,13 @@ void apply_grad_fn(const GradFn &fn, const Grad &up, Device dev, std::map<GradKe
         }
         return;
     }
-    case GradKind::Identity: {  // TransformMapping::Identity: a copy
+    case GradKind::Transfer:
+        throw TensorError("backward through a device transfer is not supported: create the leaf tensor on the device "
+                          "(device=\"cuda\") so its gradient stays in HBM");
+    case GradKind::Identity: {  // TransformMapping::Identity: the same values in logical order
         const SavedTensor &in = fn.inputs[0];
         if (!in.autograd) return;
-        Grad g = new_grad(dev, in.shape);
-        if (in.numel) check(trs_memcpy_d2d(g.st->dptr, up.st->dptr, (size_t)in.numel * sizeof(float)));
-        add_gradient(grads, in.autograd, in.output_nr, std::move(g));
+        add_gradient(grads, in.autograd, in.output_nr, Grad{up.st, in.shape});
         return;
     }
     case GradKind::Permute: {  // transform_backward Permute (src/tensor.rs:3246-3298)
@@ -1379,7 +1391,7 @@ void Tensor::backward() const {
             leaf_grads.emplace_back(it->meta, std::move(up));
             continue;
         }
-        apply_grad_fn(*it->fn, up, dev, grads);
+        apply_grad_fn(*it->fn, std::move(up), dev, grads);
     }
     // Free value-dependent saved state only after every gradient succeeded.
     for (auto &e : topo)

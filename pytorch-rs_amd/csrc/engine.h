@@ -96,7 +96,7 @@ struct SavedTensor {
 
 enum class GradKind {
     Multiply, MultiplyScalar, Negate, Relu, Sum, Identity, Permute, Index, AddTensor, SubTensor, Matmul, Exp,
-    MaskApply
+    MaskApply, Transfer
 };
 
 // One byte per element in HBM (a dropout keep-mask).

@@ -62,6 +62,18 @@ struct MaskApplyF {
     }
 };
 
+// Backward of dropout-apply (h * mask) * scale, in the order the reference's
+// graph runs it: the MultiplyScalar VJP (up * scale) and then the Multiply VJP
+// (* mask) -- two roundings, one pass.
+struct MaskBackwardF {
+    static constexpr int NIN = 2;  // (upstream, mask as u8)
+    float scale;
+    __device__ __forceinline__ float operator()(const float *a) const {
+        const float t = a[0] * scale;
+        return t * a[1];
+    }
+};
+
 struct ReluBackwardF {
     static constexpr int NIN = 2;  // (saved input, upstream)
     __device__ __forceinline__ float operator()(const float *a) const {
@@ -376,6 +388,14 @@ int trs_mask_apply_f32(const float *h, const trs_layout *lh, const uint8_t *mask
     const trs_layout *ls[2] = {lh, lm};
     const int eb[2] = {4, 1};
     return run_pointwise<MaskApplyF, 2u>(MaskApplyF{scale}, lo, out, 2, bases, ls, eb);
+}
+
+int trs_mask_backward_f32(const float *up, const trs_layout *lu, const uint8_t *mask, const trs_layout *lm,
+                          float scale, float *grad, const trs_layout *lg) {
+    const void *bases[2] = {up, mask};
+    const trs_layout *ls[2] = {lu, lm};
+    const int eb[2] = {4, 1};
+    return run_pointwise<MaskBackwardF, 2u>(MaskBackwardF{scale}, lg, grad, 2, bases, ls, eb);
 }
 
 int trs_relu_backward_f32(const float *input, const trs_layout *li, const float *up, float *grad) {

@@ -100,6 +100,7 @@ _SIGNATURES = {
     "trs_sum_f32": ([c_void_p, _LP, c_void_p], c_int),
     "trs_fill_from_device_f32": ([c_void_p, c_size_t, c_void_p], c_int),
     "trs_fill_f32": ([c_void_p, c_size_t, c_float], c_int),
+    "trs_mask_backward_f32": ([c_void_p, _LP, c_void_p, _LP, c_float, c_void_p, _LP], c_int),
     "trs_relu_backward_f32": ([c_void_p, _LP, c_void_p, c_void_p], c_int),
     "trs_mul_backward_f32": ([c_void_p, _LP, c_void_p, _LP, _LP, c_void_p], c_int),
     "trs_reduce_to_shape_f32": ([c_void_p, _LP, _LP, c_void_p], c_int),

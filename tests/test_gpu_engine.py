@@ -409,3 +409,41 @@ def test_host_device_round_trip_preserves_bits_and_views():
     assert_bitwise_equal(t.mT.cpu().numpy().ravel(), a.T.ravel())
     back = t.mT.cpu().cuda()
     assert back.is_contiguous() and back.shape == (5, 6)
+
+
+def test_backward_through_a_host_to_device_transfer_raises_before_consuming():
+    x = torch_rs.tensor([1.0, 2.0], requires_grad=True)  # a host leaf
+    y = x.to("cuda")
+    assert y.requires_grad and not y.is_leaf
+    loss = (y * y).sum()
+    with pytest.raises(RuntimeError, match="backward through a device transfer is not supported"):
+        loss.backward()
+    assert x.grad is None
+
+
+def test_pass_through_gradients_accumulate_without_aliasing():
+    # x feeds two identity edges and one add: every contribution must land once.
+    x = cuda([1.0, 2.0, 3.0], requires_grad=True)
+    y = x.view(3) + 1.0          # identity edges (view, add_scalar)
+    z = x.reshape(1, 3).view(3)  # identity edges
+    w = y + z                    # add: upstream handed to one side, copied to the other
+    (w * 2.0).sum().backward()
+    assert vals(x.grad).tolist() == [4.0, 4.0, 4.0]
+    b = cuda([[1.0, 2.0], [3.0, 4.0]], requires_grad=True)
+    c = cuda([10.0, 20.0], requires_grad=True)
+    ((b + c) * cuda([[1.0, 2.0], [3.0, 4.0]])).sum().backward()
+    assert vals(b.grad).tolist() == [1.0, 2.0, 3.0, 4.0]
+    assert vals(c.grad).tolist() == [4.0, 6.0]
+
+
+def test_dropout_backward_is_scale_then_mask_in_one_pass():
+    rng = np.random.default_rng(15)
+    h = cuda(rng.standard_normal(5000), True)
+    mask = (rng.random(5000) < 0.9).astype(np.uint8)
+    mask[:3] = [0, 1, 3]  # a non-0/1 byte keeps the two-rounding order observable
+    up = rng.standard_normal(5000).astype(np.float32)
+    up[0] = -np.inf
+    with np.errstate(invalid="ignore"):
+        want = (np.float32(1 / 0.9) * up) * mask.astype(np.float32)
+    (F.dropout(h, 0.1, mask=mask) * cuda(up)).sum().backward()
+    assert_bitwise_equal(vals(h.grad), want)
