@@ -9,11 +9,12 @@
 //
 // Tiling: a block of WGM x WGN waves owns a BM x BN tile of C; each wave owns
 // (BM/WGM) x (BN/WGN) as a grid of 16x16 MFMA tiles held in accumulators.
-// Two shapes are used: 256x256x16 with 16 waves (one block per CU, 4 waves
-// per SIMD) when the output has at least one such tile per CU, else
-// 128x128x32 with 4 waves (two blocks per CU).  Measured on the MI355X at
-// 4096^3: 84-88% of the FP32 MFMA peak for the large shape in every operand
-// layout, against 71-80% for the small one.
+// Three shapes are used: 256x256x16 with 16 waves (one block per CU, 4 waves
+// per SIMD) when the output has at least one such tile per CU; else
+// 128x128x32 with 4 waves (two blocks per CU), or 64x128x32 when 128x128
+// would give fewer than two blocks per CU.  Measured on the MI355X at 4096^3:
+// 84-88% of the FP32 MFMA peak for the large shape in every operand layout,
+// against 71-80% for the small one.
 // K advances in BK slices staged through LDS, double-buffered: the next
 // slice's global loads are issued into registers before the MFMAs of the
 // current slice and written to the other LDS buffer afterwards, so one
@@ -240,6 +241,7 @@ struct Tiles {
 };
 using LargeTiles = Tiles<256, 256, 16, 4, 4, 1>;
 using SmallTiles = Tiles<128, 128, 32, 2, 2, 2>;
+using MediumTiles = Tiles<64, 128, 32, 2, 2, 2>;  // halves M per block when 128x128 leaves CUs idle
 
 template <class T, bool TA, bool TB>
 int launch_tiled(GemmArgs g, bool full, hipStream_t s) {
@@ -342,5 +344,11 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
         large_tiles >= dev->cu_count)
         return launch_layout<LargeTiles>(g, a_plain, b_plain, true, dev->stream);
     const bool full = aligned && M % SmallTiles::BM == 0 && N % SmallTiles::BN == 0 && K % SmallTiles::BK == 0;
+    // Fewer than two 128x128 blocks per CU (e.g. a 4096x1024 weight gradient
+    // with K = 8192): 64x128 blocks double the count (76% against 69% of peak
+    // measured for that shape).
+    const int64_t small_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+    if (full && small_tiles < 2 * (int64_t)dev->cu_count)
+        return launch_layout<MediumTiles>(g, a_plain, b_plain, true, dev->stream);
     return launch_layout<SmallTiles>(g, a_plain, b_plain, full, dev->stream);
 }

@@ -48,7 +48,7 @@ def run(log, reps: int = 5) -> dict:
     def timed():
         holder["last"] = step()
 
-    med = time_region(timed, reps=reps, warmup=2)
+    med = time_region(timed, reps=reps, warmup=4)  # ~30 ms: steady MFMA clocks
     t = time_launches(timed, reps=reps, warmup=0)
     tf = GEMM_FLOP / (med * 1e-3) / 1e12
     loss = holder["last"][0].item()
