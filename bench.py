@@ -60,6 +60,8 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs, no CPU baseline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="time the reference's CPU path (oracle, one thread) on every BASELINE config and exit")
     ap.add_argument("--workload", choices=("fused_chain", "copy"), default="fused_chain",
                     help="copy: a plain 2^28-float copy kernel, the calibration run for rocprofv3 byte counters")
     args = ap.parse_args()
@@ -69,6 +71,8 @@ def main() -> int:
         return 2
 
     ensure_built()
+    if args.cpu_configs:
+        return cpu_configs()
     import ctypes
 
     import numpy as np
@@ -189,6 +193,105 @@ def main() -> int:
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_configs() -> int:
+    """The reference's single-threaded CPU path (oracle restatement) on every
+    BASELINE config, each on a bounded sample scaled to the full size.  The
+    matmuls use the reference's 4-row blocked loop (src/tensor.rs:3919-3966);
+    the MLP runs at batch 64 and is scaled by 8192/64 (every GEMM is linear in
+    the batch), plus the once-per-step .contiguous() of W1^T and W2^T."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+    from trs_backend.configs import generate
+
+    res = {}
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        out = fn()
+        return time.perf_counter() - t0, out
+
+    x, b = generate("relu_bias", "x"), generate("relu_bias", "b")
+    t, _ = timed(lambda: O.unary_contig(O.RELU, O.row_broadcast(O.ADD, x, b, 4096, 4096)))
+    res["relu_bias"] = {"seconds": t, "sample": "full [4096,4096]"}
+    log(f"cpu relu_bias: {t:.3f} s")
+
+    n = 1 << 25
+    xs = [generate("fused_chain", k, count=n) for k in ("x", "y", "z")]
+    t, _ = timed(lambda: O.unary_contig(O.RELU, O.scalar_contig(O.S_SUB, O.unary_contig(
+        O.EXP, O.binary_contig(O.ADD, O.binary_contig(O.MUL, xs[0], xs[1]), xs[2])), 1.0)))
+    res["fused_chain"] = {"seconds": t * 8, "sample": "2^25 of 2^28 elements, x8"}
+    log(f"cpu fused_chain: {t * 8:.3f} s (scaled)")
+
+    a = generate("broadcast_strided", "a")
+    bb = generate("broadcast_strided", "b")
+    c = generate("broadcast_strided", "c")
+    osh = (64, 512, 1024)
+    ocs = O.contiguous_strides(osh)
+
+    def cfg2():
+        s_ = O.binary(O.ADD, a, (64, 1, 1024), (1024, 1024, 1), 0, bb, (1, 512, 1024), (524288, 1024, 1), 0, osh, ocs)
+        return O.binary(O.MUL, s_, osh, ocs, 0, c, osh, (524288, 1, 512), 0, osh, ocs)
+
+    t, _ = timed(cfg2)
+    res["broadcast_strided"] = {"seconds": t, "sample": "full [64,512,1024]"}
+    log(f"cpu broadcast_strided: {t:.3f} s")
+
+    A, B = generate("matmul", "A").reshape(4096, 4096), generate("matmul", "B").reshape(4096, 4096)
+    t, _ = timed(lambda: O.matmul_row_blocked(A[:64], B))
+    res["matmul_4096"] = {"seconds": t * 64, "sample": "64 of 4096 rows, x64",
+                          "GFLOPS": 2 * 64 * 4096 * 4096 / t / 1e9}
+    log(f"cpu matmul 4096^3: {t * 64:.1f} s (scaled)")
+    Ab, Bb = generate("matmul", "Ab").reshape(32, 512, 512), generate("matmul", "Bb").reshape(32, 512, 512)
+    t, _ = timed(lambda: [O.matmul_row_blocked(Ab[i], Bb[i]) for i in range(32)])
+    res["matmul_batched_32x512"] = {"seconds": t, "sample": "full, 32 rank-2 calls"}
+    log(f"cpu batched matmul: {t:.3f} s")
+
+    bs = 64
+    X = generate("mlp", "X", count=bs * 4096).reshape(bs, 4096)
+    W1, W2 = generate("mlp", "W1").reshape(4096, 4096), generate("mlp", "W2").reshape(4096, 1024)
+    mask = generate("mlp", "mask", count=bs * 4096).reshape(bs, 4096)
+    s_ = np.float32(1 / 0.9)
+    z1b, z2b = np.zeros(4096, np.float32), np.zeros(1024, np.float32)
+
+    def transposes():
+        w1t = O.unary(O.COPY, W1.ravel(), (4096, 4096), (1, 4096), 0, (4096, 1)).reshape(4096, 4096)
+        w2t = O.unary(O.COPY, W2.ravel(), (1024, 4096), (1, 1024), 0, (4096, 1)).reshape(1024, 4096)
+        return w1t, w2t
+
+    t_tr, (w1t, w2t) = timed(transposes)
+
+    def step():
+        z1 = O.row_broadcast(O.ADD, O.matmul_row_blocked(X, W1).ravel(), z1b, bs, 4096)
+        h = O.unary_contig(O.RELU, z1)
+        d = O.mask_apply(h, mask.ravel(), s_).reshape(bs, 4096)
+        out = O.row_broadcast(O.ADD, O.matmul_row_blocked(d, W2).ravel(), z2b, bs, 1024)
+        O.sum_f32(out, (bs * 1024,))
+        ones = np.ones((bs, 1024), np.float32)
+        dd = O.matmul_row_blocked(ones, w2t)
+        dt = O.unary(O.COPY, d.ravel(), (4096, bs), (1, 4096), 0, (bs, 1)).reshape(4096, bs)
+        O.matmul_row_blocked(dt, ones)
+        dh = O.mask_apply(O.scalar_contig(O.S_MUL, dd.ravel(), s_), mask.ravel(), np.float32(1.0))
+        dz1 = O.relu_backward(z1, (bs, 4096), (4096, 1), 0, dh).reshape(bs, 4096)
+        xt = O.unary(O.COPY, X.ravel(), (4096, bs), (1, 4096), 0, (bs, 1)).reshape(4096, bs)
+        O.matmul_row_blocked(xt, dz1)
+        O.matmul_row_blocked(dz1, w1t)
+
+    t, _ = timed(step)
+    res["mlp"] = {"seconds": t * (8192 // bs) + t_tr, "sample": f"batch {bs} of 8192, x{8192 // bs}, "
+                  f"plus the W1^T/W2^T .contiguous() once ({t_tr:.2f} s)"}
+    log(f"cpu mlp step: {res['mlp']['seconds']:.1f} s (scaled)")
+    cpu = ""
+    try:
+        cpu = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
+    except Exception:
+        pass
+    print(json.dumps({"cpu_configs": res, "threads": 1, "host_cpu": cpu, "host_cores": host_cores(),
+                      "libc": O.libc_version()}), flush=True)
     return 0
 
 

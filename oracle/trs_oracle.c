@@ -627,6 +627,43 @@ int orc_matmul_f32(const float *a, const orc_layout *la, const float *b, const o
 
 /* Selected rows of a contiguous-output matmul (same order as above): the
  * full-size parity check evaluates a sample of rows. */
+/* contiguous_matmul_row_blocked (tensor.rs:3919-3966): contiguous operands,
+ * rows taken four at a time with depth outermost, so each right-hand row is
+ * streamed once per 4-row block; leftover rows one at a time.  Per output
+ * element the additions run in the same order as orc_matmul_f32 (k
+ * ascending from +0.0), so the two are bit-identical; this one exists for
+ * timing the reference's CPU path at its own speed (CONTIGUOUS_MATMUL_ROW_BLOCK
+ * = 4, tensor.rs:17-19). */
+void orc_matmul_row_blocked_f32(const float *left, const float *right, float *out, uint64_t rows,
+                                uint64_t inner, uint64_t cols) {
+    for (uint64_t i = 0; i < rows * cols; i++) out[i] = 0.0f;
+    const uint64_t blocked = rows / 4 * 4;
+    for (uint64_t r = 0; r < blocked; r += 4) {
+        const float *l0 = left + r * inner, *l1 = l0 + inner, *l2 = l1 + inner, *l3 = l2 + inner;
+        float *o0 = out + r * cols, *o1 = o0 + cols, *o2 = o1 + cols, *o3 = o2 + cols;
+        for (uint64_t d = 0; d < inner; d++) {
+            const float a0 = l0[d], a1 = l1[d], a2 = l2[d], a3 = l3[d];
+            const float *rr = right + d * cols;
+            for (uint64_t c = 0; c < cols; c++) {
+                const float b = rr[c];
+                o0[c] += a0 * b;
+                o1[c] += a1 * b;
+                o2[c] += a2 * b;
+                o3[c] += a3 * b;
+            }
+        }
+    }
+    for (uint64_t r = blocked; r < rows; r++) {
+        const float *l = left + r * inner;
+        float *o = out + r * cols;
+        for (uint64_t d = 0; d < inner; d++) {
+            const float a = l[d];
+            const float *rr = right + d * cols;
+            for (uint64_t c = 0; c < cols; c++) o[c] += a * rr[c];
+        }
+    }
+}
+
 int orc_matmul_rows_f32(const float *a, const orc_layout *la, const float *b, const orc_layout *lb,
                         const int64_t *rows, int64_t nrows, float *out_rows) {
     uint64_t K = la->shape[1], N = lb->shape[1];

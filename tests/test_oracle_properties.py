@@ -196,3 +196,15 @@ def test_bound_helpers_are_absolute_value_products_in_double():
     want = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
     assert np.allclose(bound, want, rtol=1e-12, atol=0)
     assert np.isclose(O.sum_abs(a.ravel()), np.abs(a.astype(np.float64)).sum(), rtol=1e-12)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 3, 5), (4, 8, 8), (7, 33, 9), (13, 64, 70)])
+def test_row_blocked_matmul_is_bit_identical_to_the_plain_loop(m, k, n):
+    """The 4-row blocked loop (tensor.rs:3919-3966) keeps every output's
+    addition order, so it must equal the plain sequential loop bit for bit."""
+    rng = _rng(40 + m)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    plain = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+    blocked = O.matmul_row_blocked(a, b)
+    assert_bitwise_equal(blocked, plain)
