@@ -87,10 +87,16 @@ static void select_device(const Device &d) {
 
 // ---- storage (src/storage.rs:7-18) ------------------------------------------
 
+// Destructors must not throw: select the device without error checks.
+static void select_device_quietly(const Device &d) {
+    int cur = -1;
+    if (d.is_cuda() && trs_get_device(&cur) == TRS_OK && cur != d.index) (void)trs_set_device(d.index);
+}
+
 Storage::~Storage() {
     if (dptr) {
-        select_device(device);
-        trs_free(dptr);  // stream-ordered return to the library's block cache
+        select_device_quietly(device);
+        (void)trs_free(dptr);  // stream-ordered return to the library's block cache
     }
 }
 
@@ -1433,7 +1439,10 @@ Tensor Tensor::grad() const {
 // ---- byte buffers (dropout masks) ----------------------------------------------------
 
 ByteBuffer::~ByteBuffer() {
-    if (dptr) trs_free(dptr);
+    if (dptr) {
+        select_device_quietly(device);
+        (void)trs_free(dptr);
+    }
 }
 
 std::shared_ptr<ByteBuffer> ByteBuffer::from_host(const uint8_t *data, const Dims &shape, Device device) {

@@ -491,11 +491,14 @@ int trs_sum_f32(const float *x, const trs_layout *lx, float *out) {
         if (lx->shape[d] > (int64_t)UINT32_MAX) g.wide = 1;
         g.fd[d] = make_fast_div(lx->shape[d] > (int64_t)UINT32_MAX ? 1u : (uint32_t)lx->shape[d]);
     }
-    rc = ensure_scratch(dev, kSumBlocks * sizeof(float));
+    // Block partials in a buffer of this call's own: the block cache returns
+    // it in stream order, so concurrent callers on one device never share it.
+    void *partial_buf = nullptr;
+    rc = trs_alloc(kSumBlocks * sizeof(float), &partial_buf);
     if (rc) return rc;
     const int64_t chunk = (n + kSumBlocks - 1) / kSumBlocks;
     const int blocks = (int)((n + chunk - 1) / chunk);
-    float *partial = (float *)dev->scratch;
+    float *partial = (float *)partial_buf;
     if (layout_is_contiguous(lx))
         hipLaunchKernelGGL(sum_pass1<true>, dim3(blocks), dim3(256), 0, dev->stream, x, g, chunk, partial);
     else
@@ -503,7 +506,7 @@ int trs_sum_f32(const float *x, const trs_layout *lx, float *out) {
     TRS_LAUNCH_CHECK("sum pass 1");
     hipLaunchKernelGGL(sum_pass2, dim3(1), dim3(256), 0, dev->stream, partial, blocks, out);
     TRS_LAUNCH_CHECK("sum pass 2");
-    return TRS_OK;
+    return trs_free(partial_buf);
 }
 
 }  // extern "C"

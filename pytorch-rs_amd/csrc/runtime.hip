@@ -164,21 +164,6 @@ DeviceState *device_state() {
     return dev;
 }
 
-int ensure_scratch(DeviceState *dev, size_t bytes) {
-    std::lock_guard<std::mutex> lock(dev->mu);
-    if (dev->scratch_bytes >= bytes) return TRS_OK;
-    if (dev->scratch) {
-        // Stream-ordered reuse: wait for queued users before replacing it.
-        TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "scratch sync");
-        TRS_HIP_CHECK(hipFree(dev->scratch), "scratch free");
-        dev->scratch = nullptr;
-        dev->scratch_bytes = 0;
-    }
-    TRS_HIP_CHECK(hipMalloc(&dev->scratch, bytes), "scratch alloc");
-    dev->scratch_bytes = bytes;
-    return TRS_OK;
-}
-
 }  // namespace trs
 
 using namespace trs;

@@ -22,10 +22,6 @@ struct DeviceState {
     int cu_count = 0;
     int clock_khz = 0;
     char name[256] = {0};
-    // Stream-ordered scratch for multi-pass kernels (partial sums).  Reused in
-    // stream order; guarded by `mu` only for (re)allocation.
-    void *scratch = nullptr;
-    size_t scratch_bytes = 0;
     std::mutex mu;
     // Block cache behind trs_alloc/trs_free: freed blocks are kept by rounded
     // size and handed out again without a hipFree/hipMalloc pair.  Reuse is
@@ -41,8 +37,6 @@ struct DeviceState {
 // On failure returns nullptr with the error recorded.
 DeviceState *device_state();
 
-// Ensures dev->scratch holds at least `bytes`; returns TRS_OK or an error.
-int ensure_scratch(DeviceState *dev, size_t bytes);
 
 // Records a thread-local error message and returns `code`.
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));

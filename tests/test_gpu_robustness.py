@@ -1,0 +1,84 @@
+"""Concurrency and large-size robustness of the C ABI on the GPU.
+
+ctypes releases the GIL for foreign calls, so the threads below really do
+call into libtrs_hip.so at the same time; every call's work still lands in
+order on the device stream and must give the same results as a lone call.
+The large-size case drives the flat kernels past 2^32 elements (64-bit
+offsets and the grid-stride continuation beyond the one-shot grid).
+"""
+import ctypes
+import threading
+
+import numpy as np
+import pytest
+
+import gpu_util as U
+import oracle as O
+from trs_backend import abi
+from trs_backend.abi import DeviceArray, check, layout_of
+
+pytestmark = pytest.mark.gpu
+
+
+def test_concurrent_sums_and_ops_from_threads_match_serial_results():
+    rng = np.random.default_rng(41)
+    arrays = [rng.standard_normal(1 << 20).astype(np.float32) * (i + 1) for i in range(8)]
+    devs = [DeviceArray.from_numpy(a) for a in arrays]
+    lay = layout_of((1 << 20,))
+    outs = [DeviceArray(4) for _ in arrays]
+
+    def serial(i):
+        check(abi.lib.trs_sum_f32(devs[i].ptr, ctypes.byref(lay), outs[i].ptr))
+        return outs[i].to_numpy(count=1)[0]
+
+    want = [serial(i) for i in range(8)]
+    errors, got = [], {}
+    barrier = threading.Barrier(8)
+
+    def worker(i):
+        try:
+            barrier.wait()
+            res = []
+            scratch = DeviceArray((1 << 20) * 4)
+            for _ in range(50):
+                # interleave a pointwise op with the two-pass sum
+                check(abi.lib.trs_unary_f32(3, devs[i].ptr, ctypes.byref(lay), scratch.ptr, ctypes.byref(lay)))
+                check(abi.lib.trs_sum_f32(scratch.ptr, ctypes.byref(lay), outs[i].ptr))
+                res.append(outs[i].to_numpy(count=1)[0])
+            got[i] = res
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors
+    for i in range(8):
+        assert all(np.float32(v).view(np.uint32) == np.float32(want[i]).view(np.uint32) for v in got[i]), i
+
+
+def test_flat_kernels_beyond_two_to_the_32_elements():
+    n = (1 << 32) + 7
+    period = 65521
+    step = 1 << 28
+    base = (np.arange(step + period, dtype=np.int64) % period).astype(np.float32)  # x[i] = i mod 65521
+    x = np.empty(n, dtype=np.float32)
+    for s in range(0, n, step):
+        e = min(n, s + step)
+        x[s:e] = base[s % period: s % period + (e - s)]
+    dx = DeviceArray.from_numpy(x)
+    del x
+    dout = DeviceArray(n * 4)
+    lay = layout_of((n,))
+    check(abi.lib.trs_binary_scalar_f32(2, dx.ptr, ctypes.byref(lay), ctypes.c_float(0.5), dout.ptr,
+                                        ctypes.byref(lay)))
+    del dx
+    out = dout.to_numpy(count=n)
+    half = O.scalar_contig(O.S_MUL, base, 0.5)  # the oracle's (i mod 65521) * 0.5
+    for s in range(0, n, step):
+        e = min(n, s + step)
+        assert np.array_equal(out[s:e], half[s % period: s % period + (e - s)]), s
+    del dout
+    check(abi.lib.trs_empty_cache())  # hand the 32 GiB back to HIP for the tests that follow
