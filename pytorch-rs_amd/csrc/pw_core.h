@@ -46,11 +46,11 @@ constexpr int kTile = 64;        // pw_tiled tile edge
 // Largest grid a launch uses (256-lane blocks).  Launches are one-shot --
 // one tile per block -- up to this many blocks; beyond it the bodies loop.
 constexpr int64_t kMaxGrid = 1 << 20;
-// Lanes per block of the flat kernels (the others use 256).  On gfx950 the
-// three-input chain measured 128 and 256 within 2% of each other (their
-// order changes from board to board, ~79-82% of HBM peak), 512 and 1024
-// 2-3% slower.
-constexpr int kFlatBlock = 128;
+// Lanes per block of the flat kernels.  On gfx950 the 4 GiB three-input
+// chain measured 64, 128 and 256 within 2% of each other (their order changes
+// from board to board, ~79-82% of HBM peak) and 512/1024 2-3% slower, while
+// at 128 MiB (an MLP activation) 128 was ~4% slower than 64 or 256.
+constexpr int kFlatBlock = 256;
 
 // Unsigned 32-bit division by a runtime-invariant divisor (Granlund-Montgomery
 // round-up method): q = (umulhi(n, mul) + n) >> shift, exact for all n < 2^32.
