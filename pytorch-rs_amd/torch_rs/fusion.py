@@ -30,21 +30,51 @@ def _f32_bits(v) -> str:
 
 
 class _Trace:
+    """Instructions in definition order: ("in", i), ("const", bits), (op, a[, b])."""
+
     def __init__(self):
-        self.lines: list[str] = []
-        self.count = 0
+        self.ins: list[tuple] = []
         self.consts: dict[str, int] = {}
 
-    def emit(self, line: str) -> int:
-        self.lines.append(line)
-        self.count += 1
-        return self.count - 1
+    def emit(self, *instr) -> int:
+        self.ins.append(instr)
+        return len(self.ins) - 1
 
     def const(self, v) -> int:
         bits = _f32_bits(v)
         if bits not in self.consts:
-            self.consts[bits] = self.emit(f"const {bits}")
+            self.consts[bits] = self.emit("const", bits)
         return self.consts[bits]
+
+    def finish(self, out: int):
+        """IR text of the instructions `out` depends on, renumbered, and the
+        argument positions of the inputs it reads (dead code and unused
+        inputs are dropped, so they are neither loaded nor required to
+        broadcast to the output shape)."""
+        live = set()
+        stack = [out]
+        while stack:
+            v = stack.pop()
+            if v in live:
+                continue
+            live.add(v)
+            ins = self.ins[v]
+            if ins[0] not in ("in", "const"):
+                stack.extend(ins[1:])
+        new_id, lines, used_inputs = {}, [], []
+        for v, ins in enumerate(self.ins):
+            if v not in live:
+                continue
+            new_id[v] = len(lines)
+            if ins[0] == "in":
+                used_inputs.append(ins[1])
+                lines.append("in f32")
+            elif ins[0] == "const":
+                lines.append(f"const {ins[1]}")
+            else:
+                lines.append(ins[0] + "".join(f" %{new_id[a]}" for a in ins[1:]))
+        lines.append(f"out %{new_id[out]}")
+        return "\n".join(lines) + "\n", used_inputs
 
 
 def _scalar(v):
@@ -73,7 +103,7 @@ class _Proxy:
         if isinstance(other, _Proxy):
             l, r = (other, self) if reverse else (self, other)
             shape, strides = _L.binary_output_layout(list(l.shape), list(l.strides), list(r.shape), list(r.strides))
-            return _Proxy(self.tr, self.tr.emit(f"{op} %{l.vid} %{r.vid}"), shape, strides)
+            return _Proxy(self.tr, self.tr.emit(op, l.vid, r.vid), shape, strides)
         s = _scalar(other)
         if s is None:
             return NotImplemented
@@ -86,16 +116,16 @@ class _Proxy:
             ustr = _L.unary_output_strides(list(self.shape), list(self.strides), self._numel())
             strides = _L.elementwise_output_strides(list(self.shape), [(list(self.shape), list(ustr))])
             one = self.tr.const(1.0)
-            rec = self.tr.emit(f"div %{one} %{self.vid}")
-            return _Proxy(self.tr, self.tr.emit(f"mul %{c} %{rec}"), self.shape, strides)
+            rec = self.tr.emit("div", one, self.vid)
+            return _Proxy(self.tr, self.tr.emit("mul", c, rec), self.shape, strides)
         a, b = (c, self.vid) if reverse else (self.vid, c)
         if op in ("add", "mul") and reverse:
             a, b = self.vid, c  # v + s and v * s, as add_scalar / mul_scalar compute them
-        return _Proxy(self.tr, self.tr.emit(f"{op} %{a} %{b}"), self.shape, strides)
+        return _Proxy(self.tr, self.tr.emit(op, a, b), self.shape, strides)
 
     def _unary(self, op):
         strides = _L.unary_output_strides(list(self.shape), list(self.strides), self._numel())
-        return _Proxy(self.tr, self.tr.emit(f"{op} %{self.vid}"), self.shape, strides)
+        return _Proxy(self.tr, self.tr.emit(op, self.vid), self.shape, strides)
 
     __add__ = lambda self, o: self._binary(o, "add")
     __radd__ = lambda self, o: self._binary(o, "add", True)
@@ -128,24 +158,26 @@ class Fused:
         functools.update_wrapper(self, fn)
 
     def trace(self, *inputs):
-        """(IR text, output shape, output strides) for inputs of these layouts."""
+        """(IR text, output shape, output strides, positions of the inputs the
+        output reads) for inputs of these layouts."""
         tr = _Trace()
         proxies = []
-        for t in inputs:
-            vid = tr.emit("in f32")
-            proxies.append(_Proxy(tr, vid, t.shape, t.stride()))
+        for i, t in enumerate(inputs):
+            proxies.append(_Proxy(tr, tr.emit("in", i), t.shape, t.stride()))
         out = self.fn(*proxies)
         if not isinstance(out, _Proxy):
             raise TypeError("a fused function must return a traced tensor expression")
-        tr.lines.append(f"out %{out.vid}")
-        return "\n".join(tr.lines) + "\n", out.shape, out.strides
+        if tr.ins[out.vid][0] == "in":
+            raise TypeError("a fused function must compute something from its inputs")
+        ir, used = tr.finish(out.vid)
+        return ir, out.shape, out.strides, used
 
     def program(self, *inputs):
         key = tuple((t.shape, t.stride()) for t in inputs)
         hit = self._cache.get(key)
         if hit is None:
-            ir, shape, strides = self.trace(*inputs)
-            hit = (_C.FusedProgram.compile(ir, len(inputs)), list(shape), list(strides), ir)
+            ir, shape, strides, used = self.trace(*inputs)
+            hit = (_C.FusedProgram.compile(ir, len(used)), list(shape), list(strides), used, ir)
             self._cache[key] = hit
         return hit
 
@@ -154,8 +186,8 @@ class Fused:
             raise TypeError("fused functions take tensors only (bind scalars in the function body)")
         if _C.is_grad_enabled() and any(t.requires_grad for t in inputs):
             return self.fn(*inputs)
-        prog, shape, strides, _ = self.program(*inputs)
-        return prog.launch(list(inputs), shape, strides)
+        prog, shape, strides, used, _ = self.program(*inputs)
+        return prog.launch([inputs[i] for i in used], shape, strides)
 
 
 def fuse(fn):

@@ -247,18 +247,29 @@ def test_dropout_bridge_cases_on_host():
 def test_fusion_tracer_emits_one_rounding_per_op_and_eager_layout():
     f = torch_rs.fuse(lambda x, y, z: ((x * y + z).exp() - 1.0).relu())
     x = torch_rs.zeros(8)
-    ir, shape, strides = f.trace(x, x, x)
+    ir, shape, strides, used = f.trace(x, x, x)
     assert ir == "in f32\nin f32\nin f32\nmul %0 %1\nadd %3 %2\nexp %4\nconst 0x3f800000\nsub %5 %6\nrelu %7\nout %8\n"
-    assert shape == (8,) and strides == (1,)
+    assert shape == (8,) and strides == (1,) and used == [0, 1, 2]
     # (a + b) * c.mT: the planner's contiguous output for config 2's layouts
     g = torch_rs.fuse(lambda a, b, c: (a + b) * c)
     a, b = torch_rs.zeros(64, 1, 8), torch_rs.zeros(1, 16, 8)
     c = torch_rs.zeros(64, 8, 16).mT
-    _, shape, strides = g.trace(a, b, c)
+    _, shape, strides, _ = g.trace(a, b, c)
     want_shape, want_strides = O.binary_output_layout((64, 16, 8), O.contiguous_strides((64, 16, 8)),
                                                       c.shape, c.stride())
     assert shape == want_shape == (64, 16, 8) and strides == want_strides
     # scalar forms: s - x, s / x -> s * (1 / x), x * s
     h = torch_rs.fuse(lambda x: (2.0 - x) + 3.0 / x + x * 0.5)
-    ir, _, _ = h.trace(x)
+    ir, _, _, _ = h.trace(x)
     assert "sub %1 %0" in ir and "div %" in ir and "mul %0 %" in ir
+
+
+def test_fusion_tracer_drops_dead_code_and_unused_inputs():
+    f = torch_rs.fuse(lambda x, y, z: (y * 2.0).relu())  # x and z unused
+    x, y, z = torch_rs.zeros(5, 7), torch_rs.zeros(3), torch_rs.zeros(9)
+    ir, shape, _, used = f.trace(x, y, z)
+    assert used == [1] and shape == (3,)
+    assert ir == "in f32\nconst 0x40000000\nmul %0 %1\nrelu %2\nout %3\n"
+    g = torch_rs.fuse(lambda x, y: ((x + 1.0) * 3.0, y - x)[1])
+    ir, _, _, used = g.trace(torch_rs.zeros(4), torch_rs.zeros(4))
+    assert used == [0, 1] and "add" not in ir

@@ -96,3 +96,98 @@ def test_fused_relu_bias_row_broadcast():
                     (R, C))
     want = O.unary_contig(O.RELU, O.row_broadcast(O.ADD, x, b, R, C))
     assert_bitwise_equal(got, want, nan_equal=False)
+
+
+def _random_program(rng, nin):
+    """A random straight-line program over nin inputs: a list of (op, args)."""
+    prog = []
+    nvals = nin
+    for _ in range(int(rng.integers(2, 9))):
+        kind = rng.integers(0, 10)
+        a = int(rng.integers(0, nvals))
+        if kind < 4:
+            b = int(rng.integers(0, nvals))
+            prog.append((["add", "sub", "mul", "div"][kind], a, b))
+        elif kind < 8:
+            s = float(rng.choice([0.5, -1.25, 3.0, 1e-3, 2.0]))
+            prog.append((["sadd", "ssub", "smul", "rsub"][kind - 4], a, s))
+        elif kind == 8:
+            prog.append(("relu", a))
+        else:
+            prog.append(("neg", a))
+        nvals += 1
+    return prog
+
+
+def _run_program(prog, args):
+    vals = list(args)
+    for ins in prog:
+        op = ins[0]
+        if op in ("add", "sub", "mul", "div"):
+            x, y = vals[ins[1]], vals[ins[2]]
+            if op == "add":
+                vals.append(x + y)
+            elif op == "sub":
+                vals.append(x - y)
+            elif op == "mul":
+                vals.append(x * y)
+            else:
+                vals.append(x / y)
+        elif op in ("sadd", "ssub", "smul", "rsub"):
+            x, s = vals[ins[1]], ins[2]
+            if op == "sadd":
+                vals.append(x + s)
+            elif op == "ssub":
+                vals.append(x - s)
+            elif op == "smul":
+                vals.append(x * s)
+            else:
+                vals.append(s - x)
+        elif op == "relu":
+            vals.append(vals[ins[1]].relu())
+        else:
+            vals.append(-vals[ins[1]])
+    return vals[-1]
+
+
+def _random_operand(rng, oshape):
+    """A device tensor broadcastable to oshape: a suffix of its shape with some
+    dims set to 1, laid out contiguously, transposed in its last two dims, or
+    as every other column of a wider tensor (stride 2 innermost)."""
+    import torch_rs
+    r = len(oshape)
+    k = int(rng.integers(0, r + 1))
+    shape = [1 if rng.random() < 0.25 else d for d in oshape[r - k:]]
+    n = int(np.prod(shape)) if shape else 1
+    kind = rng.integers(0, 3)
+    if kind == 1 and len(shape) >= 2:
+        base = rng.standard_normal(n).astype(np.float32).reshape(shape[:-2] + [shape[-1], shape[-2]])
+        return torch_rs.tensor(base, device="cuda").mT
+    if kind == 2 and len(shape) >= 1:
+        base = rng.standard_normal(2 * n).astype(np.float32).reshape(shape[:-1] + [shape[-1], 2])
+        t = torch_rs.tensor(base, device="cuda")
+        last = len(shape)
+        return t.permute(*([last] + list(range(last))))[0]  # select column 0 of each pair
+    return torch_rs.tensor(rng.standard_normal(n).astype(np.float32).reshape(shape), device="cuda")
+
+
+def test_random_programs_fused_equal_eager_bit_for_bit():
+    import torch_rs
+    rng = np.random.default_rng(77)
+    for case in range(40):
+        rank = int(rng.integers(1, 4))
+        oshape = [int(rng.integers(1, 70)) for _ in range(rank)]
+        nin = int(rng.integers(1, 6))
+        args = [_random_operand(rng, oshape) for _ in range(nin)]
+        # make sure the broadcast result has the full output shape
+        args[0] = torch_rs.tensor(rng.standard_normal(int(np.prod(oshape))).astype(np.float32).reshape(oshape),
+                                  device="cuda") if rng.random() < 0.5 else \
+            torch_rs.tensor(rng.standard_normal(int(np.prod(oshape))).astype(np.float32).reshape(oshape[::-1]),
+                            device="cuda").permute(*range(rank - 1, -1, -1))
+        prog = _random_program(rng, nin)
+        fn = lambda *xs, prog=prog: _run_program(prog, xs)
+        eager = fn(*args)
+        fused = torch_rs.fuse(fn)(*args)
+        assert fused.shape == eager.shape, (case, prog)
+        assert fused.stride() == eager.stride(), (case, prog, fused.stride(), eager.stride())
+        assert_bitwise_equal(fused.numpy().ravel(), eager.numpy().ravel())
