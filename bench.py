@@ -62,8 +62,9 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-configs", action="store_true",
                     help="time the reference's CPU path (oracle, one thread) on every BASELINE config and exit")
-    ap.add_argument("--workload", choices=("fused_chain", "copy"), default="fused_chain",
-                    help="copy: a plain 2^28-float copy kernel, the calibration run for rocprofv3 byte counters")
+    ap.add_argument("--workload", choices=("fused_chain", "copy", "transfer"), default="fused_chain",
+                    help="copy: a plain 2^28-float copy kernel, the calibration run for rocprofv3 byte counters; "
+                         "transfer: host<->device copy rates (pageable and page-locked host memory)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -91,6 +92,8 @@ def main() -> int:
     n = 1 << 28
     if args.workload == "copy":
         return copy_calibration(n, args)
+    if args.workload == "transfer":
+        return transfer_rates()
     t0 = time.time()
     x, y, z = (generate("fused_chain", k, threads=min(16, host_cores())) for k in ("x", "y", "z"))
     log(f"generated 3 x 2^28 inputs in {time.time() - t0:.1f}s")
@@ -319,6 +322,61 @@ def copy_calibration(n: int, args) -> int:
     log(f"copy: {ms * 1e3:.1f} us avg -> {gbs:.0f} GB/s")
     print(json.dumps({"workload": "copy_calibration", "elements": n, "bytes_per_launch": 8 * n,
                       "kernel_us_avg": ms * 1e3, "GBps": gbs}), flush=True)
+    return 0
+
+
+def transfer_rates() -> int:
+    """Host <-> device copy rates through trs_memcpy_h2d/d2h, for pageable numpy
+    buffers (staged through the library's page-locked chunks above a few MiB)
+    and for page-locked ones from trs_host_alloc (one DMA).  Median of five
+    timed batches of back-to-back copies per size; every copy is checked."""
+    import ctypes
+
+    import numpy as np
+
+    from trs_backend import abi
+    from trs_backend.abi import DeviceArray, check
+
+    def rate(fn, nbytes):
+        fn()
+        fn()
+        reps = max(3, int(5e9 / nbytes))  # about 0.1 s per batch at 50 GB/s
+        res = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            res.append(nbytes * reps / (time.perf_counter() - t0) / 1e9)
+        return sorted(res)[2]
+
+    rows = []
+    for mib in (4, 16, 64, 256, 1024):
+        nb = mib << 20
+        src = np.random.default_rng(mib).integers(0, 256, nb, dtype=np.uint8)
+        dev = DeviceArray(nb)
+        out = np.empty(nb, np.uint8)
+        h2d = rate(lambda: check(abi.lib.trs_memcpy_h2d(dev.ptr, ctypes.c_void_p(src.ctypes.data), nb)), nb)
+        d2h = rate(lambda: check(abi.lib.trs_memcpy_d2h(ctypes.c_void_p(out.ctypes.data), dev.ptr, nb)), nb)
+        if not np.array_equal(out, src):
+            raise SystemExit(f"transfer of {mib} MiB through pageable memory changed the bytes")
+        p = ctypes.c_void_p()
+        check(abi.lib.trs_host_alloc(nb, ctypes.byref(p)))
+        try:
+            pin = np.ctypeslib.as_array((ctypes.c_uint8 * nb).from_address(p.value))
+            pin[:] = src
+            ph2d = rate(lambda: check(abi.lib.trs_memcpy_h2d(dev.ptr, p, nb)), nb)
+            pin[:] = 0
+            pd2h = rate(lambda: check(abi.lib.trs_memcpy_d2h(p, dev.ptr, nb)), nb)
+            if not np.array_equal(pin, src):
+                raise SystemExit(f"transfer of {mib} MiB through page-locked memory changed the bytes")
+            del pin
+        finally:
+            check(abi.lib.trs_host_free(p))
+        log(f"{mib:5d} MiB: pageable h2d {h2d:5.1f} d2h {d2h:5.1f} GB/s | page-locked h2d {ph2d:5.1f} "
+            f"d2h {pd2h:5.1f} GB/s")
+        rows.append({"MiB": mib, "pageable_h2d_GBps": round(h2d, 1), "pageable_d2h_GBps": round(d2h, 1),
+                     "pinned_h2d_GBps": round(ph2d, 1), "pinned_d2h_GBps": round(pd2h, 1)})
+    print(json.dumps({"workload": "host_transfer", "unit": "GB/s", "rows": rows}), flush=True)
     return 0
 
 

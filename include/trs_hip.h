@@ -83,7 +83,18 @@ int trs_free(void *ptr);
 int trs_empty_cache(void);
 /* Bytes in live (allocated) and cached (freed, kept) blocks on the device. */
 int trs_memory_stats(size_t *live_bytes, size_t *cached_bytes);
-/* Host <-> device copies on the device stream; d2h blocks until done. */
+/* Page-locked host memory (hipHostMalloc).  Copies to and from it run as one
+ * DMA.  Ingest and egress of whole buffers replace the reference's per-element
+ * buffer conversion (src/python.rs:10329-10403) and Python-list egress
+ * (src/python.rs:3744-3756, 4031-4052).  trs_host_free waits for the device
+ * stream before releasing the buffer. */
+int trs_host_alloc(size_t bytes, void **ptr);
+int trs_host_free(void *ptr);
+/* Host <-> device copies, ordered on the device stream.  h2d and d2h return
+ * once the copy is complete, so the host buffer may be reused at once.
+ * Pageable host memory of 16 MiB or more (h2d) or 4 MiB or more (d2h) is
+ * pipelined through two page-locked chunks per device with a host copy pool;
+ * smaller or page-locked buffers go as one DMA.  d2d does not block. */
 int trs_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int trs_memcpy_d2h(void *dst, const void *src, size_t bytes);
 int trs_memcpy_d2d(void *dst, const void *src, size_t bytes);

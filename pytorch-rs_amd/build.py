@@ -37,7 +37,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}", f"-I{GEN}",
 ]
-HIP_SOURCES = ["runtime.hip", "pointwise.hip", "gemm.hip", "fusion.hip"]
+HIP_SOURCES = ["runtime.hip", "transfer.hip", "pointwise.hip", "gemm.hip", "fusion.hip"]
 ENGINE_SOURCES = ["engine.cpp", "py_module.cpp"]
 
 

@@ -544,19 +544,18 @@ Tensor Tensor::detach() const {
     return t;
 }
 
-// Logical row-major values on the host.
-std::vector<float> Tensor::to_host() const {
-    std::vector<float> out((size_t)numel);
-    if (numel == 0) return out;
+// Logical row-major values written to `out` (numel floats of host memory).
+void Tensor::copy_to_host(float *out) const {
+    if (numel == 0) return;
     if (device().is_cuda()) {
         select_device(device());
         if (is_contiguous()) {
-            check(trs_memcpy_d2h(out.data(), storage->dptr + offset, (size_t)numel * sizeof(float)));
+            check(trs_memcpy_d2h(out, storage->dptr + offset, (size_t)numel * sizeof(float)));
         } else {
             Tensor c = contiguous();
-            check(trs_memcpy_d2h(out.data(), c.storage->dptr + c.offset, (size_t)numel * sizeof(float)));
+            check(trs_memcpy_d2h(out, c.storage->dptr + c.offset, (size_t)numel * sizeof(float)));
         }
-        return out;
+        return;
     }
     // host odometer over the strided view
     const int rank = (int)shape.size();
@@ -573,6 +572,11 @@ std::vector<float> Tensor::to_host() const {
             idx[a] = 0;
         }
     }
+}
+
+std::vector<float> Tensor::to_host() const {
+    std::vector<float> out((size_t)numel);
+    copy_to_host(out.data());
     return out;
 }
 

@@ -159,6 +159,7 @@ public:
     Tensor detach() const;
     Tensor to(Device device) const;
     std::vector<float> to_host() const;  // logical row-major values
+    void copy_to_host(float *out) const;  // the same, into numel floats at `out`
 
     // views (src/tensor.rs:1082-1215, 2032-2189)
     Tensor permute(const Dims &dims, Node node = Node::Permute) const;

@@ -20,6 +20,12 @@ using namespace trs_engine;
 
 namespace {
 
+std::string to_str(const Dims &d) {
+    std::string s = "[";
+    for (size_t i = 0; i < d.size(); i++) s += (i ? ", " : "") + std::to_string(d[i]);
+    return s + "]";
+}
+
 py::tuple to_tuple(const Dims &d) {
     py::tuple t(d.size());
     for (size_t i = 0; i < d.size(); i++) t[i] = py::int_(d[i]);
@@ -81,16 +87,50 @@ py::object binary_operation(const Tensor &self, const py::object &other, BinOp o
 
 // Logical values as a numpy array of the tensor's shape (a copy).
 py::array_t<float> to_numpy(const Tensor &t) {
-    std::vector<float> v = t.to_host();
     std::vector<py::ssize_t> shape(t.shape.begin(), t.shape.end());
     py::array_t<float> a(shape);
-    if (!v.empty()) std::memcpy(a.mutable_data(), v.data(), v.size() * sizeof(float));
+    t.copy_to_host(a.mutable_data());
     return a;
 }
 
 Tensor from_numpy(py::array_t<float, py::array::c_style | py::array::forcecast> arr, const std::string &device) {
     Dims shape(arr.shape(), arr.shape() + arr.ndim());
     return Tensor::from_host(arr.data(), shape, Device::parse(device));
+}
+
+// A numpy array in page-locked host memory (trs_host_alloc), released when
+// the array is collected.  Copies between it and the device run as one DMA.
+py::array empty_pinned(const std::vector<int64_t> &shape, const std::string &dtype) {
+    py::dtype dt(dtype);
+    if (!dt.is(py::dtype::of<float>()) && !dt.is(py::dtype::of<uint8_t>()))
+        throw TensorError("empty_pinned supports float32 and uint8, got " + dtype);
+    int64_t n = 1;
+    for (int64_t d : shape) {
+        if (d < 0) throw TensorError("empty_pinned: negative dimension");
+        n *= d;
+    }
+    void *p = nullptr;
+    const size_t bytes = (size_t)n * (size_t)dt.itemsize();
+    if (trs_host_alloc(bytes, &p) != TRS_OK) throw TensorError(trs_last_error());
+    static char empty_byte;
+    if (!p) p = &empty_byte;  // zero bytes: nothing was allocated
+    py::capsule owner(p, [](void *q) {
+        if (q != &empty_byte) (void)trs_host_free(q);
+    });
+    std::vector<py::ssize_t> dims(shape.begin(), shape.end());
+    return py::array(dt, dims, p, owner);
+}
+
+// Logical values of `t` written into a C-contiguous float32 array of its
+// shape (for example one from empty_pinned), without an intermediate buffer.
+void copy_into(const Tensor &t, py::array out) {
+    if (!out.dtype().is(py::dtype::of<float>())) throw TensorError("copy_to_host: out must be float32");
+    if (!(out.flags() & py::array::c_style) || !out.writeable())
+        throw TensorError("copy_to_host: out must be a writeable C-contiguous array");
+    Dims shape(out.shape(), out.shape() + out.ndim());
+    if (shape != t.shape)
+        throw TensorError("copy_to_host: out has shape " + to_str(shape) + ", tensor has " + to_str(t.shape));
+    t.copy_to_host(static_cast<float *>(out.mutable_data()));
 }
 
 std::vector<int64_t> dims_arg(const py::args &args) {
@@ -118,6 +158,8 @@ PYBIND11_MODULE(_trs_native, m) {
         .def_property_readonly("shape", [](const ByteBuffer &b) { return to_tuple(b.shape); })
         .def_property_readonly("device", [](const ByteBuffer &b) { return b.device.str(); });
 
+    m.def("empty_pinned", &empty_pinned, py::arg("shape"), py::arg("dtype") = "float32");
+    m.def("copy_into", &copy_into, py::arg("tensor"), py::arg("out"));
     m.def("bytes_from_numpy",
           [](py::array_t<uint8_t, py::array::c_style | py::array::forcecast> arr, const std::string &device) {
               Dims shape(arr.shape(), arr.shape() + arr.ndim());

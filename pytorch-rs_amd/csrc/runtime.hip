@@ -285,28 +285,6 @@ int trs_memory_stats(size_t *live_bytes, size_t *cached_bytes) {
     return TRS_OK;
 }
 
-int trs_memcpy_h2d(void *dst, const void *src, size_t bytes) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    if (bytes == 0) return TRS_OK;
-    if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in h2d copy");
-    // Pageable host memory: the runtime stages the copy; returning after
-    // hipMemcpyAsync means `src` has been consumed.
-    TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream), "h2d copy");
-    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "h2d sync");
-    return TRS_OK;
-}
-
-int trs_memcpy_d2h(void *dst, const void *src, size_t bytes) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    if (bytes == 0) return TRS_OK;
-    if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in d2h copy");
-    TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream), "d2h copy");
-    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "d2h sync");
-    return TRS_OK;
-}
-
 int trs_memcpy_d2d(void *dst, const void *src, size_t bytes) {
     DeviceState *dev = device_state();
     if (!dev) return TRS_E_NO_DEVICE;

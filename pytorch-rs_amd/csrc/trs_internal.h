@@ -31,6 +31,11 @@ struct DeviceState {
     std::multimap<size_t, void *> free_blocks;
     std::unordered_map<void *, size_t> live_blocks;
     size_t cached_bytes = 0;
+    // Two page-locked chunks that pipeline copies from or to pageable host
+    // memory, each with the event of the last DMA that used it.
+    std::mutex stage_mu;
+    void *stage[2] = {nullptr, nullptr};
+    hipEvent_t stage_done[2] = {nullptr, nullptr};
 };
 
 // Returns the current device's state, initialising it on first use.
@@ -52,6 +57,13 @@ bool layout_is_contiguous(const trs_layout *l);
     do {                                          \
         hipError_t trs_e_ = (expr);               \
         if (trs_e_ != hipSuccess) return ::trs::hip_fail(trs_e_, what); \
+    } while (0)
+
+// Returns a non-OK status of a call of this library to the caller.
+#define TRS_CHECK(expr)               \
+    do {                              \
+        const int trs_rc_ = (expr);   \
+        if (trs_rc_ != TRS_OK) return trs_rc_; \
     } while (0)
 
 // A launch's error surfaces from hipGetLastError right after the launch.

@@ -19,3 +19,20 @@ def synchronize() -> None:
 
 def current_device() -> int:
     return 0
+
+
+def empty_pinned(shape, dtype="float32"):
+    """A numpy array (float32 or uint8) in page-locked host memory.  Passing it
+    to ``torch_rs.tensor(..., device="cuda")`` or ``copy_to_host`` moves the
+    data as one DMA at the PCIe rate; pageable arrays are pipelined through
+    the library's own page-locked chunks instead."""
+    if isinstance(shape, int):
+        shape = (shape,)
+    import numpy as np
+    return _C.empty_pinned([int(d) for d in shape], np.dtype(dtype).name)
+
+
+def copy_to_host(tensor, out) -> None:
+    """Writes ``tensor``'s logical values into ``out``, a writeable C-contiguous
+    float32 array of the same shape, with no intermediate buffer."""
+    _C.copy_into(tensor, out)

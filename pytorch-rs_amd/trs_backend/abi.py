@@ -85,6 +85,8 @@ _SIGNATURES = {
     "trs_alloc": ([c_size_t, POINTER(c_void_p)], c_int),
     "trs_free": ([c_void_p], c_int),
     "trs_empty_cache": ([], c_int),
+    "trs_host_alloc": ([c_size_t, POINTER(c_void_p)], c_int),
+    "trs_host_free": ([c_void_p], c_int),
     "trs_memory_stats": ([POINTER(c_size_t), POINTER(c_size_t)], c_int),
     "trs_memcpy_h2d": ([c_void_p, c_void_p, c_size_t], c_int),
     "trs_memcpy_d2h": ([c_void_p, c_void_p, c_size_t], c_int),
