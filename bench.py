@@ -62,9 +62,10 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-configs", action="store_true",
                     help="time the reference's CPU path (oracle, one thread) on every BASELINE config and exit")
-    ap.add_argument("--workload", choices=("fused_chain", "copy", "transfer"), default="fused_chain",
+    ap.add_argument("--workload", choices=("fused_chain", "copy", "transfer", "matmul"), default="fused_chain",
                     help="copy: a plain 2^28-float copy kernel, the calibration run for rocprofv3 byte counters; "
-                         "transfer: host<->device copy rates (pageable and page-locked host memory)")
+                         "transfer: host<->device copy rates (pageable and page-locked host memory); "
+                         "matmul: the 4096^3 fp32 GEMM alone, for rocprofv3 MFMA counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -94,6 +95,8 @@ def main() -> int:
         return copy_calibration(n, args)
     if args.workload == "transfer":
         return transfer_rates()
+    if args.workload == "matmul":
+        return matmul_only(args)
     t0 = time.time()
     x, y, z = (generate("fused_chain", k, threads=min(16, host_cores())) for k in ("x", "y", "z"))
     log(f"generated 3 x 2^28 inputs in {time.time() - t0:.1f}s")
@@ -137,7 +140,13 @@ def main() -> int:
     out_sample = dout.to_numpy(count=n)[:: 4099]
     checksum = float(np.sum(out_sample, dtype=np.float64))
 
-    extra = {"fused_chain": {"kernel_us_avg_timed_region": kern_ms * 1e3,
+    # Peaks: the published figures, and the FP32 MFMA rate re-derived from this
+    # device's CU count and engine clock (256 FLOP per clock per CU).
+    derived_tflops = cus.value * clk.value * 1e3 * 256 / 1e12
+    extra = {"peaks": {"hbm_GBps_published": HBM_PEAK_GBS, "fp32_mfma_TFLOPS_published": FP32_MFMA_PEAK_TFLOPS,
+                       "fp32_mfma_TFLOPS_derived": round(derived_tflops, 1), "cu_count": cus.value,
+                       "engine_clock_khz": clk.value},
+             "fused_chain": {"kernel_us_avg_timed_region": kern_ms * 1e3,
                              "kernel_us_median_single_launch": statistics.median(ev) * 1e3,
                              "kernel_us_min": min(ev) * 1e3, "kernel_us_max": max(ev) * 1e3,
                              "hiprtc_compile_ms": compile_ms.value, "output_sample_checksum": checksum}}
@@ -322,6 +331,32 @@ def copy_calibration(n: int, args) -> int:
     log(f"copy: {ms * 1e3:.1f} us avg -> {gbs:.0f} GB/s")
     print(json.dumps({"workload": "copy_calibration", "elements": n, "bytes_per_launch": 8 * n,
                       "kernel_us_avg": ms * 1e3, "GBps": gbs}), flush=True)
+    return 0
+
+
+def matmul_only(args) -> int:
+    """The 4096^3 GEMM of the matmul config alone: `warmup` untimed launches,
+    then `steps` launches between two HIP events on the library stream."""
+    import ctypes
+
+    from trs_backend import abi
+    from trs_backend.abi import DeviceArray, check, layout_of
+    from trs_backend.configs import generate
+    from trs_backend.timing import time_region
+
+    K = 4096
+    dA, dB = DeviceArray.from_numpy(generate("matmul", "A")), DeviceArray.from_numpy(generate("matmul", "B"))
+    dC = DeviceArray(K * K * 4)
+    lay = layout_of((K, K))
+
+    def mm():
+        check(abi.lib.trs_matmul_f32(dA.ptr, ctypes.byref(lay), dB.ptr, ctypes.byref(lay), dC.ptr, ctypes.byref(lay)))
+
+    ms = time_region(mm, reps=args.steps, warmup=args.warmup)
+    tf = 2 * K ** 3 / (ms * 1e-3) / 1e12
+    log(f"matmul 4096^3: {ms:.3f} ms avg over {args.steps} launches -> {tf:.1f} TFLOPS")
+    print(json.dumps({"workload": "matmul_4096", "flop_per_launch": 2 * K ** 3, "ms_avg": ms, "TFLOPS": tf,
+                      "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS}), flush=True)
     return 0
 
 

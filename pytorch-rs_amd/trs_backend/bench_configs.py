@@ -1,8 +1,11 @@
 """Secondary benchmark configurations reported under bench.py's "extra".
 
 Each returns device-time figures measured with HIP events on the library
-stream.  Working sets that fit the 256 MB Infinity Cache are rotated over
-several buffer sets so the GB/s figures reflect HBM.
+stream: the average over a region of back-to-back launches (the rate used
+for GB/s and TFLOPS) and the median, min and max of single launches (the
+dispersion).  Working sets that fit the 256 MB Infinity Cache are rotated
+over several buffer sets so the GB/s figures reflect HBM.  Every output is
+read back and summed in float64 as a checksum of the materialised result.
 """
 from __future__ import annotations
 
@@ -17,6 +20,17 @@ from .timing import time_launches, time_region
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def _spread(times_ms: list[float], scale: float = 1e3, unit: str = "us") -> dict:
+    """Median, min and max of single-launch times (ms in), in `unit`."""
+    t = sorted(times_ms)
+    return {f"{unit}_median_single_launch": t[len(t) // 2] * scale, f"{unit}_min": t[0] * scale,
+            f"{unit}_max": t[-1] * scale, "launches": len(t)}
+
+
+def _checksum(d: DeviceArray, count: int) -> float:
+    return float(np.sum(d.to_numpy(count=count), dtype=np.float64))
 
 
 def _fusion(ir: str) -> int:
@@ -61,10 +75,12 @@ def relu_bias(log, reps: int = 20, sets: int = 3) -> dict:
 
     e = time_region(eager, reps)
     f = time_region(fused, reps)
+    spread = _spread(time_launches(fused, reps))
     log(f"relu_bias: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us")
     return {"relu_bias": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
                           "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
-                          "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+                          "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS, "fused_spread": spread,
+                          "output_checksum": _checksum(outs[(i[0] - 1) % sets], R * C)}}
 
 
 def broadcast_strided(log, reps: int = 20, sets: int = 2) -> dict:
@@ -100,10 +116,12 @@ def broadcast_strided(log, reps: int = 20, sets: int = 2) -> dict:
 
     e = time_region(eager, reps)
     f = time_region(fused, reps)
+    spread = _spread(time_launches(fused, reps))
     log(f"broadcast_strided: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us")
     return {"broadcast_strided": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
                                   "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
-                                  "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+                                  "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS, "fused_spread": spread,
+                                  "output_checksum": _checksum(outs[(i[0] - 1) % sets], B * M * N)}}
 
 
 # MFMA-bound kernels reach steady clocks only after ~25 ms of sustained
@@ -127,7 +145,8 @@ def matmul(log, reps: int = 20) -> dict:
     t = time_launches(mm, reps)
     tf = 2 * K ** 3 / (med * 1e-3) / 1e12
     out["matmul_4096"] = {"ms_avg": med, "ms_min_single_launch": min(t), "TFLOPS": tf,
-                          "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS}
+                          "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS, "spread": _spread(t, 1.0, "ms"),
+                          "output_checksum": _checksum(dC, K * K)}
     log(f"matmul 4096^3: {med:.3f} ms, {tf:.1f} TFLOPS")
     Ab, Bb = generate("matmul", "Ab"), generate("matmul", "Bb")
     dAb, dBb, dCb = DeviceArray.from_numpy(Ab), DeviceArray.from_numpy(Bb), DeviceArray(32 * 512 * 512 * 4)
@@ -141,12 +160,13 @@ def matmul(log, reps: int = 20) -> dict:
     t = time_launches(bmm, reps * 3)
     tf = 2 * 32 * 512 ** 3 / (med * 1e-3) / 1e12
     out["matmul_batched_32x512"] = {"ms_avg": med, "ms_min_single_launch": min(t), "TFLOPS": tf,
-                                    "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS}
+                                    "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS, "spread": _spread(t, 1.0, "ms"),
+                                    "output_checksum": _checksum(dCb, 32 * 512 * 512)}
     log(f"batched matmul 32x512^3: {med:.3f} ms, {tf:.1f} TFLOPS")
     return out
 
 
-def mlp(log, reps: int = 5) -> dict:
+def mlp(log, reps: int = 20) -> dict:
     """Config 4: 2-layer MLP forward+backward through the torch_rs API on the device."""
     from . import mlp_bench
     return {"mlp": mlp_bench.run(log, reps)}

@@ -8,6 +8,7 @@ stream.  Work: six GEMMs, 1,030,792,151,040 FLOP per step.
 """
 from __future__ import annotations
 
+import numpy as np
 
 from .configs import generate
 from .timing import time_launches, time_region
@@ -41,7 +42,7 @@ def build(device: str = "cuda"):
     return step
 
 
-def run(log, reps: int = 5) -> dict:
+def run(log, reps: int = 20) -> dict:
     step = build()
     holder = {}
 
@@ -53,5 +54,10 @@ def run(log, reps: int = 5) -> dict:
     tf = GEMM_FLOP / (med * 1e-3) / 1e12
     loss = holder["last"][0].item()
     log(f"mlp fwd+bwd: {med:.3f} ms/step, {tf:.1f} TFLOPS on the GEMM work, loss {loss:.4f}")
-    return {"ms_avg": med, "ms_min_single_step": min(t), "gemm_flop_per_step": GEMM_FLOP, "TFLOPS": tf,
-            "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS, "loss": loss}
+    t = sorted(t)
+    _, x, w1, w2 = holder["last"]
+    grad_sums = {name: float(np.sum(v.grad.numpy(), dtype=np.float64)) for name, v in
+                 (("dX", x), ("dW1", w1), ("dW2", w2))}
+    return {"ms_avg": med, "ms_min_single_step": t[0], "ms_median_single_step": t[len(t) // 2],
+            "ms_max_single_step": t[-1], "gemm_flop_per_step": GEMM_FLOP, "TFLOPS": tf,
+            "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS, "loss": loss, "grad_checksums": grad_sums}
