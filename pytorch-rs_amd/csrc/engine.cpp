@@ -407,7 +407,7 @@ const char *node_name(Node n) {
     case Node::Permute: return "PermuteBackward0";
     case Node::Relu: return "ReluBackward0";
     case Node::ReflectedSubtract: return "RsubBackward1";
-    case Node::Subtract: return "SubBackward1";
+    case Node::Subtract: return "SubBackward0";
     case Node::Sum: return "SumBackward0";
     case Node::MatrixTranspose: return "TBackward0";
     case Node::Transpose: return "TransposeBackward0";
@@ -418,6 +418,9 @@ const char *node_name(Node n) {
     case Node::Bmm: return "BmmBackward0";
     case Node::AddTensor: return "AddBackward0";
     case Node::SubTensor: return "SubBackward0";
+    case Node::Squeeze: return "SqueezeBackward0";
+    case Node::SqueezeDimension: return "SqueezeBackward1";
+    case Node::SqueezeDimensions: return "SqueezeBackward2";
     }
     return "UnknownBackward";
 }
@@ -695,6 +698,45 @@ Tensor Tensor::transpose(int64_t d0, int64_t d1) const {
     for (size_t i = 0; i < dims.size(); i++) dims[i] = (int64_t)i;
     if (!dims.empty()) std::swap(dims[a0], dims[a1]);
     return permute(dims, Node::Transpose);
+}
+
+// squeeze / squeeze_dim / squeeze_dims (src/tensor.rs:1305-1390): drop the
+// selected size-1 dims; storage, offset and the logical order are unchanged,
+// so the gradient maps back as Identity.
+Tensor Tensor::squeeze_selected(const std::vector<bool> &selected, Node node) const {
+    Dims s, st;
+    for (size_t a = 0; a < shape.size(); a++) {
+        if (selected[a] && shape[a] == 1) continue;
+        s.push_back(shape[a]);
+        st.push_back(strides[a]);
+    }
+    Tensor out = alias_view(s, st, offset);
+    record_transform(*this, out, GradKind::Identity, node);
+    return out;
+}
+
+Tensor Tensor::squeeze() const {
+    return squeeze_selected(std::vector<bool>(shape.size(), true), Node::Squeeze);
+}
+
+Tensor Tensor::squeeze_dim(int64_t dim) const {
+    const int64_t a = normalize_dim(dim, shape.size());
+    std::vector<bool> sel(shape.size(), false);
+    if (!sel.empty()) sel[a] = true;
+    return squeeze_selected(sel, Node::SqueezeDimension);
+}
+
+Tensor Tensor::squeeze_dims(const std::vector<int64_t> &dims) const {
+    if (shape.size() > 64) throw TensorError("only tensors with up to 64 dims are supported");
+    std::vector<bool> sel(shape.size(), false);
+    std::vector<bool> seen(std::max<size_t>(shape.size(), 1), false);
+    for (int64_t d : dims) {
+        const int64_t a = normalize_dim(d, shape.size());
+        if (seen[a]) throw TensorError("dim " + std::to_string(a) + " appears multiple times in the list of dims");
+        seen[a] = true;
+        if (!sel.empty()) sel[a] = true;
+    }
+    return squeeze_selected(sel, Node::SqueezeDimensions);
 }
 
 // matrix_transpose = .mT (src/tensor.rs:1209-1215).

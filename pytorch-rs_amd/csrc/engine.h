@@ -81,7 +81,7 @@ using MetaPtr = std::shared_ptr<AutogradMeta>;
 // backend adds for device tensors.
 enum class Node {
     Add, Alias, Clone, Multiply, Negate, Permute, Relu, ReflectedSubtract, Subtract, Sum, MatrixTranspose,
-    Transpose, View, Select, Exp, Mm, Bmm, AddTensor, SubTensor
+    Transpose, View, Select, Exp, Mm, Bmm, AddTensor, SubTensor, Squeeze, SqueezeDimension, SqueezeDimensions
 };
 const char *node_name(Node n);
 
@@ -164,6 +164,9 @@ public:
     // views (src/tensor.rs:1082-1215, 2032-2189)
     Tensor permute(const Dims &dims, Node node = Node::Permute) const;
     Tensor transpose(int64_t d0, int64_t d1) const;
+    Tensor squeeze() const;                                    // every size-1 dim
+    Tensor squeeze_dim(int64_t dim) const;                     // that dim, if size 1
+    Tensor squeeze_dims(const std::vector<int64_t> &dims) const;  // those dims that have size 1
     Tensor matrix_transpose() const;
     Tensor reverse_dims() const;
     Tensor reshape(const std::vector<int64_t> &req) const;
@@ -201,6 +204,7 @@ private:
     Tensor scalar_op(int op, float s) const;
     Tensor unary_op(int op) const;
     Tensor alias_view(const Dims &shape, const Dims &strides, int64_t offset) const;
+    Tensor squeeze_selected(const std::vector<bool> &selected, Node node) const;
 };
 
 // Dropout-apply with a precomputed keep-mask: (h * mask) * scale.

@@ -447,7 +447,8 @@ int trs_mul_backward_f32(const float *up, const trs_layout *lout, const float *o
     int rc = check_layout(lout, "output");
     if (!rc) rc = check_layout(lself, "operand");
     if (rc) return rc;
-    if (!other) return set_error(TRS_E_INVALID_ARGUMENT, "null other operand");
+    // An empty output reads nothing (an empty operand's storage may be null).
+    if (!other && layout_numel(lout) != 0) return set_error(TRS_E_INVALID_ARGUMENT, "null other operand");
     if (layout_numel(lself) == layout_numel(lout)) {
         // No broadcast: one contribution per element, stored as is.
         const trs_layout lc = contiguous_like(lout);

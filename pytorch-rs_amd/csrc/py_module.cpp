@@ -201,6 +201,17 @@ PYBIND11_MODULE(_trs_native, m) {
         .def("item", &Tensor::item)
         .def("permute", [](const Tensor &t, const py::args &a) { return t.permute(dims_arg(a)); })
         .def("transpose", &Tensor::transpose)
+        // swapdims / swapaxes are transpose under another name (src/python.rs:3634-3672)
+        .def("swapdims", &Tensor::transpose, py::arg("dim0"), py::arg("dim1"))
+        .def("swapaxes", &Tensor::transpose, py::arg("axis0"), py::arg("axis1"))
+        // squeeze(), squeeze(dim), squeeze((d0, d1, ...)) (src/python.rs:6112-6121)
+        .def("squeeze",
+             [](const Tensor &t, const py::object &dim) {
+                 if (dim.is_none()) return t.squeeze();
+                 if (py::isinstance<py::int_>(dim)) return t.squeeze_dim(dim.cast<int64_t>());
+                 return t.squeeze_dims(dim.cast<std::vector<int64_t>>());
+             },
+             py::arg("dim") = py::none())
         .def_property_readonly("mT", &Tensor::matrix_transpose)
         .def_property_readonly("T", &Tensor::reverse_dims)
         .def("t", &Tensor::reverse_dims)

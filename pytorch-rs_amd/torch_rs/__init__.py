@@ -69,7 +69,8 @@ def tensor(data, *, dtype=None, device=None, requires_grad=False) -> Tensor:
     else:
         flat, shape = _flatten(data)
         arr = _np.asarray(flat, dtype=_np.float64).astype(_np.float32).reshape(shape)
-    t = _C.from_numpy(_np.ascontiguousarray(arr, dtype=_np.float32), _device_str(device))
+    # asarray(order="C") keeps 0-d arrays 0-d (ascontiguousarray would make them [1]).
+    t = _C.from_numpy(_np.asarray(arr, dtype=_np.float32, order="C"), _device_str(device))
     return t.with_requires_grad(bool(requires_grad))
 
 

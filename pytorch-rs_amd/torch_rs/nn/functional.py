@@ -43,5 +43,5 @@ def dropout(input, p: float = 0.5, training: bool = True, inplace: bool = False,
 
 def keep_mask(mask, device="cuda"):
     """Upload a uint8 keep-mask (1 = keep) to the device once, for reuse across steps."""
-    arr = _np.ascontiguousarray(_np.asarray(mask), dtype=_np.uint8)
+    arr = _np.asarray(mask, dtype=_np.uint8, order="C")
     return _C.bytes_from_numpy(arr, str(device))

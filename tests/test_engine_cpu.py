@@ -179,6 +179,34 @@ def test_view_metadata_matches_reference_rules():
         torch_rs.zeros(3).mT
 
 
+def test_squeeze_and_swapdims_views_follow_reference_rules():
+    # squeeze / squeeze_dim / squeeze_dims (src/tensor.rs:1305-1390): size-1
+    # dims dropped, other strides and the offset kept; swapdims/swapaxes are
+    # transpose (src/python.rs:3634-3672).
+    x = torch_rs.zeros(2, 1, 3, 1, requires_grad=True)
+    s = x.squeeze()
+    assert s.shape == (2, 3) and s.stride() == (3, 1) and s.grad_fn.name() == "SqueezeBackward0"
+    s1 = x.squeeze(1)
+    assert s1.shape == (2, 3, 1) and s1.stride() == (3, 1, 1) and s1.grad_fn.name() == "SqueezeBackward1"
+    assert x.squeeze(0).shape == (2, 1, 3, 1)  # size 2: unchanged metadata
+    assert x.squeeze(-1).shape == (2, 1, 3)
+    s2 = x.squeeze((1, -1))
+    assert s2.shape == (2, 3) and s2.grad_fn.name() == "SqueezeBackward2"
+    assert x.squeeze(()).shape == (2, 1, 3, 1)
+    with pytest.raises(RuntimeError, match="dim 1 appears multiple times in the list of dims"):
+        x.squeeze((1, -3))
+    with pytest.raises(IndexError, match=r"Dimension out of range \(expected to be in range of \[-4, 3\]"):
+        x.squeeze(4)
+    o = torch_rs.zeros(2, 3, 4)[1].squeeze()
+    assert o.storage_offset() == 12 and o.stride() == (4, 1)
+    sc = torch_rs.zeros(())
+    assert sc.squeeze().shape == () and sc.squeeze(0).shape == () and sc.squeeze(-1).shape == ()
+    w = torch_rs.zeros(2, 3, 4, requires_grad=True).swapdims(0, -1)
+    assert w.shape == (4, 3, 2) and w.stride() == (1, 4, 12) and w.grad_fn.name() == "TransposeBackward0"
+    assert torch_rs.zeros(2, 3).swapaxes(1, 0).stride() == (1, 3)
+    assert sc.swapdims(0, -1).shape == ()
+
+
 def test_views_record_transform_nodes_and_leafness():
     x = torch_rs.zeros(2, 3, requires_grad=True)
     assert x.is_leaf and x.requires_grad and x.grad_fn is None and x.grad is None
@@ -222,6 +250,11 @@ def test_tensor_constructor_and_scalar_conversion():
     assert t.shape == (2, 2) and t.numpy().tolist() == [[1.0, 2.0], [3.0, 4.5]]
     assert torch_rs.tensor(0.1).numpy() == np.float32(0.1)
     assert torch_rs.tensor(np.arange(6, dtype=np.float64).reshape(2, 3)).stride() == (3, 1)
+    # 0-d arrays and numpy scalars stay scalars; transposed arrays are copied row-major.
+    assert torch_rs.tensor(np.array(0.5, np.float32)).shape == ()
+    assert torch_rs.tensor(np.float32(0.5)).shape == ()
+    assert torch_rs.tensor(np.arange(6, dtype=np.float32).reshape(2, 3).T).numpy().tolist() == [[0, 3], [1, 4], [2, 5]]
+    assert torch_rs.tensor(np.zeros((2, 0, 3), np.float32)).shape == (2, 0, 3)
     with pytest.raises(TypeError, match="invalid data type 'bytes'"):
         torch_rs.tensor(b"ab")
     with pytest.raises(ValueError):
