@@ -228,16 +228,30 @@ def _grad(self):
     return self._grad() if self._has_grad() else None
 
 
+_EXP_LOW, _EXP_HIGH = _np.float32(1e-4), _np.float32(1e16)
+
+
+def _rust_f32_debug(v) -> str:
+    """One f32 as Rust's `{:?}` prints it: the shortest digits that round-trip,
+    in positional form with at least one fractional digit, or in exponent form
+    (`1e-5`, `1.5e16`) when 0 < |v| < 1e-4 or |v| >= 1e16; `NaN`, `inf`, `-inf`."""
+    v = _np.float32(v)
+    if _np.isnan(v):
+        return "NaN"
+    if _np.isinf(v):
+        return "inf" if v > 0 else "-inf"
+    a = abs(v)
+    if a != 0 and (a < _EXP_LOW or a >= _EXP_HIGH):
+        return _np.format_float_scientific(v, unique=True, trim="-", exp_digits=1).replace("e+", "e")
+    return _np.format_float_positional(v, unique=True, trim="0")
+
+
 def _repr(self):
-    body = _np.array2string(self.numpy(), precision=4, separator=", ")
-    extra = ""
-    if self.is_cuda:
-        extra += f", device='{self.device}'"
-    if self._grad_fn_name is not None:
-        extra += f", grad_fn=<{self._grad_fn_name}>"
-    elif self.requires_grad:
-        extra += ", requires_grad=True"
-    return f"tensor({body}{extra})"
+    """`tensor({values:?}, shape={shape:?})`: every logical value in row-major
+    order and the shape, as the reference's Tensor.__repr__ (src/python.rs:3933-3942)."""
+    values = ", ".join(_rust_f32_debug(v) for v in self.numpy().reshape(-1))
+    shape = ", ".join(str(d) for d in self.shape)
+    return f"tensor([{values}], shape=[{shape}])"
 
 
 def _array(self, dtype=None, copy=None):

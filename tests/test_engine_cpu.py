@@ -207,6 +207,33 @@ def test_squeeze_and_swapdims_views_follow_reference_rules():
     assert sc.swapdims(0, -1).shape == ()
 
 
+def test_repr_matches_reference_known_answers():
+    # Tensor.__repr__ prints every logical value with Rust's f32 `{:?}` and the
+    # shape (src/python.rs:3933-3942).  Known answers: tests/test_tensor_t.py:216-219
+    # and tests/test_squeeze.py:81 (a (3, 2) view with strides (4, 12), offset 1).
+    source = torch_rs.tensor(np.arange(24, dtype=np.float32).reshape(2, 3, 4))
+    assert repr(source.T) == (
+        "tensor([0.0, 12.0, 4.0, 16.0, 8.0, 20.0, 1.0, 13.0, 5.0, 17.0, 9.0, 21.0, 2.0, 14.0, 6.0, 18.0, "
+        "10.0, 22.0, 3.0, 15.0, 7.0, 19.0, 11.0, 23.0], shape=[4, 3, 2])")
+    view = source.T[1]
+    assert view.stride() == (4, 12) and view.storage_offset() == 1
+    assert repr(view) == "tensor([1.0, 13.0, 5.0, 17.0, 9.0, 21.0], shape=[3, 2])"
+    assert repr(torch_rs.tensor(2.5)) == "tensor([2.5], shape=[])"
+    assert repr(torch_rs.zeros(2, 0, 3)) == "tensor([], shape=[2, 0, 3])"
+
+
+@pytest.mark.parametrize("value,text", [
+    (0.1, "0.1"), (1.0, "1.0"), (-0.0, "-0.0"), (100.0, "100.0"), (123456789.0, "123456790.0"),
+    (1e15, "1000000000000000.0"), (1e16, "1e16"), (1.5e16, "1.5e16"), (1e-4, "0.0001"), (9.99e-5, "9.99e-5"),
+    (1e-5, "1e-5"), (3.4028235e38, "3.4028235e38"), (1.1754944e-38, "1.1754944e-38"), (1e-45, "1e-45"),
+    (float("nan"), "NaN"), (float("inf"), "inf"), (float("-inf"), "-inf"),
+])
+def test_f32_debug_format_follows_rust(value, text):
+    # Rust's Debug for f32: shortest round-trip digits; exponent form when
+    # 0 < |v| < 1e-4 or |v| >= 1e16, else positional with a fractional digit.
+    assert torch_rs._rust_f32_debug(np.float32(value)) == text
+
+
 def test_views_record_transform_nodes_and_leafness():
     x = torch_rs.zeros(2, 3, requires_grad=True)
     assert x.is_leaf and x.requires_grad and x.grad_fn is None and x.grad is None
