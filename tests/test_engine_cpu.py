@@ -289,12 +289,69 @@ def test_tensor_constructor_and_scalar_conversion():
     assert torch_rs.get_float32_matmul_precision() == "highest"
 
 
+def test_dropout_argument_checks_follow_the_reference_order_and_messages():
+    # python/torch_rs/nn/functional.py:14-31 (range check, ValueError, before
+    # anything else) and src/python_nn_functional.rs:103-200 (type checks, then
+    # a RuntimeError with `.6g` formatting for what passes the Python check);
+    # cases after tests/test_nn_functional_dropout.py:335-560.
+    F = torch_rs.nn.functional
+    src = torch_rs.tensor([1.0, 2.0])
+    for p, shown in ((-0.1, "-0.1"), (1.1, "1.1"), (float("inf"), "inf"), (2, "2")):
+        with pytest.raises(ValueError) as e:
+            F.dropout(None, p=p, training="invalid", inplace=True)
+        assert str(e.value) == f"dropout probability has to be between 0 and 1, but got {shown}"
+    for p in (float("nan"), np.float32(np.nan)):
+        with pytest.raises(RuntimeError, match="^dropout probability has to be between 0 and 1, but got nan$"):
+            F.dropout(src, p=p, training=False)
+    with pytest.raises(RuntimeError, match="^dropout probability has to be between 0 and 1, but got -nan$"):
+        F.dropout(src, p=-float("nan"), training=False)
+
+    class Sneaky(float):  # defeats the Python-level comparisons
+        def __lt__(self, other):
+            return False
+
+        def __gt__(self, other):
+            return False
+
+    for value, shown in ((2, "2"), (1.0000000000001, "1"), (1.23456789, "1.23457"), (999999.9, "1e+06"),
+                         (-1.23456789e-7, "-1.23457e-07"), (-5e-324, "-4.94066e-324")):
+        with pytest.raises(RuntimeError) as e:
+            F.dropout(src, p=Sneaky(value), training=False)
+        assert str(e.value) == f"dropout probability has to be between 0 and 1, but got {shown}"
+    # scalar-tensor probabilities: 0-d shows the value, others the tensor with its autograd state
+    for value in (-0.1, 1.1, float("inf")):
+        prob = torch_rs.tensor(value)
+        with pytest.raises(ValueError) as e:
+            F.dropout(None, p=prob, training=False)
+        assert str(e.value) == f"dropout probability has to be between 0 and 1, but got {prob.item()}"
+    leaf = torch_rs.tensor([2.0], requires_grad=True)
+    for prob, shown in ((torch_rs.tensor([2.0]), "tensor([2.])"), (leaf, "tensor([2.], requires_grad=True)"),
+                        (leaf.reshape(1, 1), "tensor([[2.]], grad_fn=<ViewBackward0>)")):
+        with pytest.raises(ValueError) as e:
+            F.dropout(src, p=prob)
+        assert str(e.value) == f"dropout probability has to be between 0 and 1, but got {shown}"
+    with pytest.raises(RuntimeError, match="Boolean value of Tensor with more than one value is ambiguous"):
+        F.dropout(src, p=torch_rs.tensor([0.1, 0.2]))
+    with pytest.raises(TypeError, match=r"^dropout\(\): argument 'input' \(position 1\) must be Tensor, not NoneType$"):
+        F.dropout(None, p=0)
+    with pytest.raises(TypeError, match=r"^dropout_\(\): argument 'input' \(position 1\) must be Tensor, not NoneType$"):
+        F.dropout(None, p=0, inplace=True)
+    with pytest.raises(TypeError, match="'<' not supported between instances of 'NoneType' and 'float'"):
+        F.dropout(src, p=None, training=False)
+    with pytest.raises(TypeError, match=r"^dropout\(\): argument 'train' \(position 3\) must be bool, not int$"):
+        F.dropout(src, p=0, training=1)
+    with pytest.raises(TypeError, match=r"^dropout\(\): argument 'train' \(position 3\) must be bool, not numpy.bool$"):
+        F.dropout(src, p=0, training=np.bool_(False))
+    assert F.dropout(src, p=torch_rs.tensor(0.0)) is src
+    assert F.dropout(torch_rs.zeros(0), p=0.5) is not None
+
+
 def test_dropout_bridge_cases_on_host():
     F = torch_rs.nn.functional
     x = torch_rs.zeros(4)
     assert F.dropout(x, 0.5, training=False) is x
     assert F.dropout(x, 0.0) is x
-    with pytest.raises(RuntimeError, match="dropout probability has to be between 0 and 1, but got 1.5"):
+    with pytest.raises(ValueError, match="^dropout probability has to be between 0 and 1, but got 1.5$"):
         F.dropout(x, 1.5)
     with pytest.raises(NotImplementedError, match="does not support sampling"):
         F.dropout(x, 0.5)
