@@ -1062,13 +1062,13 @@ Tensor Tensor::sum() const {
 
 // matmul (src/tensor.rs:2453-2533) for rank-2 operands, plus equal-batch
 // rank-3 operands; on the device it records dA = dC @ B^T, dB = A^T @ dC.
+// matmul (src/tensor.rs:2453-2533): shapes are validated first, with the
+// reference's messages (src/tensor_error.rs:120, 243), then the device.
+// Device tensors also take two rank-3 operands with equal batch (bmm).
 Tensor Tensor::matmul(const Tensor &o) const {
-    require_cuda("matmul");
-    if (!(o.device() == device()))
-        throw TensorError("Expected all tensors to be on the same device, but found at least two devices, " +
-                          device().str() + " and " + o.device().str() + "!");
     const size_t r = shape.size();
-    if (r != o.shape.size() || (r != 2 && r != 3))
+    const bool batched_ok = device().is_cuda() && o.device().is_cuda();
+    if (r != o.shape.size() || (r != 2 && !(r == 3 && batched_ok)))
         throw TensorError("matmul currently requires two rank-2 tensors, got " + dims_str(shape) + " and " +
                           dims_str(o.shape));
     if (r == 3 && shape[0] != o.shape[0])
@@ -1080,6 +1080,10 @@ Tensor Tensor::matmul(const Tensor &o) const {
                               std::to_string(o.shape[1]) + ")");
         throw TensorError("matmul inner dimensions differ for " + dims_str(shape) + " and " + dims_str(o.shape));
     }
+    require_cuda("matmul");
+    if (!(o.device() == device()))
+        throw TensorError("Expected all tensors to be on the same device, but found at least two devices, " +
+                          device().str() + " and " + o.device().str() + "!");
     Dims oshape = shape;
     oshape[r - 1] = o.shape[r - 1];
     Tensor out = empty_like_layout(device(), oshape, layout::contiguous_strides(oshape));

@@ -126,8 +126,24 @@ def div(input, other):
     return input / other
 
 
-def matmul(input: Tensor, other: Tensor) -> Tensor:
-    return input.matmul(other)
+def matmul(*args, **kwargs) -> Tensor:
+    """torch_rs.matmul(input, other) -- also as matmul(input=, other=) or
+    matmul(x1=, x2=), the keyword spellings the reference accepts."""
+    left, right = _two_operands("matmul", args, kwargs, (("input", "other"), ("x1", "x2")))
+    return left.matmul(right)
+
+
+def _two_operands(name, args, kwargs, spellings):
+    if "out" in kwargs:
+        raise TypeError(f"{name}() got an unexpected keyword argument 'out'")
+    if len(args) == 2 and not kwargs:
+        return args
+    for first, second in spellings:
+        if len(args) == 1 and set(kwargs) == {second}:
+            return args[0], kwargs[second]
+        if not args and set(kwargs) == {first, second}:
+            return kwargs[first], kwargs[second]
+    raise TypeError(f"{name}() received an invalid combination of arguments")
 
 
 def sum(input: Tensor) -> Tensor:  # noqa: A001
@@ -274,6 +290,21 @@ Tensor.ndim = property(lambda self: self.dim())
 Tensor.cpu = lambda self: self.to("cpu")
 Tensor.cuda = lambda self, device=0: self.to(f"cuda:{device}")
 Tensor.tolist = lambda self: self.numpy().tolist()
+_native_matmul = Tensor.matmul
+
+
+def _matmul_method(self, *args, **kwargs):
+    """Tensor.matmul(other), also as matmul(other=) or matmul(x2=)."""
+    if len(args) == 1 and not kwargs:
+        return _native_matmul(self, args[0])
+    if not args and len(kwargs) == 1:
+        (key, value), = kwargs.items()
+        if key in ("other", "x2"):
+            return _native_matmul(self, value)
+    raise TypeError("matmul() received an invalid combination of arguments")
+
+
+Tensor.matmul = _matmul_method
 Tensor.__array__ = _array
 Tensor.__repr__ = _repr
 Tensor.__len__ = _len

@@ -289,6 +289,32 @@ def test_tensor_constructor_and_scalar_conversion():
     assert torch_rs.get_float32_matmul_precision() == "highest"
 
 
+def test_matmul_shape_and_rank_errors_come_before_the_device_check():
+    # tests/test_matmul.py:326-361 and 492-539: every spelling reports the
+    # reference's shape message (src/tensor_error.rs:243); other ranks report
+    # src/tensor_error.rs:120.  Host tensors are never computed on, but they
+    # fail with the same message as the reference first.
+    for ls, rs in (((2, 3), (4, 2)), ((0, 3), (4, 0))):
+        l, r = torch_rs.zeros(ls), torch_rs.zeros(rs)
+        msg = f"^mat1 and mat2 shapes cannot be multiplied \\({ls[0]}x{ls[1]} and {rs[0]}x{rs[1]}\\)$"
+        for call in (lambda: l.matmul(r), lambda: l @ r, lambda: l.matmul(other=r), lambda: l.matmul(x2=r),
+                     lambda: torch_rs.matmul(l, r), lambda: torch_rs.matmul(input=l, other=r),
+                     lambda: torch_rs.matmul(x1=l, x2=r)):
+            with pytest.raises(RuntimeError, match=msg):
+                call()
+    for l, r in ((torch_rs.tensor(1.0), torch_rs.ones((1, 1))), (torch_rs.ones((2,)), torch_rs.ones((2, 2))),
+                 (torch_rs.ones((1, 2, 2)), torch_rs.ones((2, 2))), (torch_rs.ones((2, 2, 2)), torch_rs.ones((2, 2, 2)))):
+        with pytest.raises(RuntimeError) as a:
+            l.matmul(r)
+        with pytest.raises(RuntimeError) as b:
+            l @ r
+        assert str(a.value) == str(b.value) and "requires two rank-2 tensors" in str(a.value)
+    with pytest.raises(TypeError, match="^matmul\\(\\) got an unexpected keyword argument 'out'$"):
+        torch_rs.matmul(torch_rs.ones((1, 1)), torch_rs.ones((1, 1)), out=torch_rs.zeros((1, 1)))
+    with pytest.raises(RuntimeError, match="device tensors only"):
+        torch_rs.ones((2, 3)) @ torch_rs.ones((3, 2))
+
+
 def test_dropout_argument_checks_follow_the_reference_order_and_messages():
     # python/torch_rs/nn/functional.py:14-31 (range check, ValueError, before
     # anything else) and src/python_nn_functional.rs:103-200 (type checks, then
