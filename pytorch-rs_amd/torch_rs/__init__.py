@@ -99,11 +99,29 @@ def relu(input: Tensor) -> Tensor:
     return input.relu()
 
 
-def exp(input: Tensor) -> Tensor:
+def _unary_out(name, input, out, autograd_error=None):
+    """Top-level unary with the reference's `out` and autograd guards
+    (apply_top_level_unary_out, src/python.rs:1784-1820, 2673-2694).  The
+    autograd guard applies to host tensors; device tensors record the VJP."""
+    if out is not None:
+        raise RuntimeError(f"{name}(): the 'out' argument is not supported")
+    if (autograd_error and isinstance(input, Tensor) and not input.is_cuda and input.requires_grad
+            and is_grad_enabled()):
+        raise RuntimeError(autograd_error)
+
+
+def exp(input: Tensor, *, out=None) -> Tensor:
+    _unary_out("exp", input, out, "exp(): autograd recording is not supported")
     return input.exp()
 
 
-def neg(input: Tensor) -> Tensor:
+def neg(input: Tensor, *, out=None) -> Tensor:
+    _unary_out("neg", input, out)
+    return input.neg()
+
+
+def negative(input: Tensor, *, out=None) -> Tensor:
+    _unary_out("negative", input, out)
     return input.neg()
 
 

@@ -289,6 +289,21 @@ def test_tensor_constructor_and_scalar_conversion():
     assert torch_rs.get_float32_matmul_precision() == "highest"
 
 
+def test_top_level_unary_guards_follow_the_reference():
+    # apply_top_level_unary_out (src/python.rs:2673-2694, 1784-1820): `out` is
+    # rejected first; torch.exp refuses to record on a grad-requiring input
+    # (tests/test_top_level_exp.py:108-137).  Host tensors keep that refusal.
+    x = torch_rs.tensor([[-2.0, 0.0, 1.0], [2.0, 4.0, 6.0]], requires_grad=True).transpose(0, 1)[1]
+    with pytest.raises(RuntimeError, match=r"^exp\(\): autograd recording is not supported$"):
+        torch_rs.exp(x)
+    for fn, name in ((torch_rs.exp, "exp"), (torch_rs.neg, "neg"), (torch_rs.negative, "negative")):
+        with pytest.raises(RuntimeError, match=f"^{name}\\(\\): the 'out' argument is not supported$"):
+            fn(x, out=torch_rs.zeros(2))
+    with torch_rs.no_grad():
+        with pytest.raises(RuntimeError, match="device tensors only"):
+            torch_rs.exp(x)  # past the guard; host tensors do not compute
+
+
 def test_matmul_shape_and_rank_errors_come_before_the_device_check():
     # tests/test_matmul.py:326-361 and 492-539: every spelling reports the
     # reference's shape message (src/tensor_error.rs:243); other ranks report
