@@ -202,7 +202,10 @@ int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const t
 /* ---- pointwise fusion compiler (new; no counterpart in the reference) */
 
 /* Compile a pointwise IR program to a gfx950 kernel with hipRTC (-O3,
- * -ffp-contract=off), cached by IR text.  IR grammar, one instruction per
+ * -ffp-contract=off), cached by IR text in the process and on disk: the code
+ * object is kept under TRS_FUSION_CACHE_DIR (empty disables), else
+ * $XDG_CACHE_HOME/trs_hip/fusion or $HOME/.cache/trs_hip/fusion, keyed by the
+ * hipRTC version, options and full source.  IR grammar, one instruction per
  * line, values numbered from 0 in order of definition:
  *     in f32 | in u8           -- next kernel input
  *     const <hex f32 bits>     -- scalar constant
@@ -217,8 +220,11 @@ int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *input
                       const trs_layout *in_layouts, float *out, const trs_layout *lo);
 /* Generated HIP C++ source of a compiled program (for inspection). */
 int trs_fusion_source(uint64_t kernel_id, char *buf, size_t buf_len, size_t *needed);
-/* Milliseconds spent in hipRTC for this program (reported apart from timings). */
+/* Milliseconds spent producing this program's code object: the hipRTC
+ * compile, or the load from the disk cache (reported apart from timings). */
 int trs_fusion_compile_ms(uint64_t kernel_id, double *ms);
+/* *hit = 1 when the code object came from the disk cache, else 0. */
+int trs_fusion_from_disk_cache(uint64_t kernel_id, int *hit);
 
 #ifdef __cplusplus
 }

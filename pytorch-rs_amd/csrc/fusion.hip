@@ -11,10 +11,17 @@
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cerrno>
 #include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <fstream>
 #include <map>
+#include <thread>
 #include <memory>
 #include <mutex>
 #include <sstream>
@@ -39,6 +46,7 @@ struct Program {
     int nin = 0;
     unsigned u8mask = 0;
     double compile_ms = 0.0;
+    bool from_disk = false;
     std::vector<char> code;
     hipModule_t module[16] = {};
     std::map<std::string, hipFunction_t> functions[16];
@@ -174,15 +182,117 @@ int generate(const std::string &ir, Program *prog) {
     return TRS_OK;
 }
 
+const char *const kRtcOpts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-std=c++20", "-DTRS_RTC",
+                                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-w"};
+
+// ---- on-disk code-object cache ------------------------------------------------
+// A compiled program is stored as <dir>/<fnv1a64(key)>.co holding a magic line,
+// the full key (hipRTC version, options, complete source) and the code
+// object; a hit requires the stored key to equal the current one, so a hash
+// collision or a stale file is a miss.  Files are written to a temporary name
+// and renamed, so concurrent processes never read a partial file.  Any I/O
+// failure falls back to compiling.  The directory is TRS_FUSION_CACHE_DIR
+// when set (empty disables the cache), else $XDG_CACHE_HOME/trs_hip/fusion
+// or $HOME/.cache/trs_hip/fusion.
+
+constexpr char kCacheMagic[] = "TRS-FUSION-CO-1\n";
+
+std::string cache_dir() {
+    if (const char *d = std::getenv("TRS_FUSION_CACHE_DIR")) return d;
+    if (const char *x = std::getenv("XDG_CACHE_HOME"); x && *x) return std::string(x) + "/trs_hip/fusion";
+    if (const char *h = std::getenv("HOME"); h && *h) return std::string(h) + "/.cache/trs_hip/fusion";
+    return "";
+}
+
+bool make_dirs(const std::string &dir) {
+    for (size_t i = 1; i <= dir.size(); i++) {
+        if (i == dir.size() || dir[i] == '/') {
+            const std::string part = dir.substr(0, i);
+            if (mkdir(part.c_str(), 0755) != 0 && errno != EEXIST) return false;
+        }
+    }
+    return true;
+}
+
+uint64_t fnv1a64(const std::string &s) {
+    uint64_t h = 1469598103934665603ull;
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+std::string cache_key(const std::string &full_source) {
+    int major = 0, minor = 0;
+    hiprtcVersion(&major, &minor);
+    std::string key = "hiprtc " + std::to_string(major) + "." + std::to_string(minor) + "\n";
+    for (const char *o : kRtcOpts) key += std::string(o) + "\n";
+    return key + full_source;
+}
+
+std::string cache_path(const std::string &dir, const std::string &key) {
+    char name[32];
+    std::snprintf(name, sizeof name, "%016llx.co", (unsigned long long)fnv1a64(key));
+    return dir + "/" + name;
+}
+
+bool cache_load(const std::string &path, const std::string &key, std::vector<char> *code) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return false;
+    char magic[sizeof kCacheMagic - 1];
+    uint64_t klen = 0, clen = 0;
+    if (!f.read(magic, sizeof magic) || std::memcmp(magic, kCacheMagic, sizeof magic) != 0) return false;
+    if (!f.read((char *)&klen, sizeof klen) || klen != key.size()) return false;
+    std::string stored(klen, '\0');
+    if (!f.read(&stored[0], (std::streamsize)klen) || stored != key) return false;
+    if (!f.read((char *)&clen, sizeof clen) || clen == 0 || clen > (1ull << 30)) return false;
+    code->resize(clen);
+    return (bool)f.read(code->data(), (std::streamsize)clen);
+}
+
+void cache_store(const std::string &dir, const std::string &path, const std::string &key,
+                 const std::vector<char> &code) {
+    if (!make_dirs(dir)) return;
+    std::ostringstream tmp_name;
+    tmp_name << path << ".tmp." << getpid() << "." << std::this_thread::get_id();
+    const std::string tmp = tmp_name.str();
+    {
+        std::ofstream f(tmp, std::ios::binary | std::ios::trunc);
+        if (!f) return;
+        const uint64_t klen = key.size(), clen = code.size();
+        f.write(kCacheMagic, sizeof kCacheMagic - 1);
+        f.write((const char *)&klen, sizeof klen);
+        f.write(key.data(), (std::streamsize)klen);
+        f.write((const char *)&clen, sizeof clen);
+        f.write(code.data(), (std::streamsize)clen);
+        if (!f) {
+            f.close();
+            std::remove(tmp.c_str());
+            return;
+        }
+    }
+    if (std::rename(tmp.c_str(), path.c_str()) != 0) std::remove(tmp.c_str());
+}
+
 int compile(Program *prog) {
     std::string full = std::string(kPwCoreSource) + "\n" + prog->source;
+    const auto t0 = std::chrono::steady_clock::now();
+    const std::string dir = cache_dir();
+    std::string key, path;
+    if (!dir.empty()) {
+        key = cache_key(full);
+        path = cache_path(dir, key);
+        if (cache_load(path, key, &prog->code)) {
+            prog->from_disk = true;
+            prog->compile_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+            return TRS_OK;
+        }
+    }
     hiprtcProgram rp;
     hiprtcResult r = hiprtcCreateProgram(&rp, full.c_str(), "trs_fused.hip", 0, nullptr, nullptr);
     if (r != HIPRTC_SUCCESS) return set_error(TRS_E_FUSION, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
-    const char *opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-std=c++20", "-DTRS_RTC",
-                          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-w"};
-    const auto t0 = std::chrono::steady_clock::now();
-    r = hiprtcCompileProgram(rp, (int)(sizeof opts / sizeof opts[0]), opts);
+    r = hiprtcCompileProgram(rp, (int)(sizeof kRtcOpts / sizeof kRtcOpts[0]), kRtcOpts);
     prog->compile_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     if (r != HIPRTC_SUCCESS) {
         size_t n = 0;
@@ -197,6 +307,7 @@ int compile(Program *prog) {
     prog->code.resize(n);
     hiprtcGetCode(rp, prog->code.data());
     hiprtcDestroyProgram(&rp);
+    if (!dir.empty()) cache_store(dir, path, key, prog->code);
     return TRS_OK;
 }
 
@@ -313,6 +424,13 @@ int trs_fusion_compile_ms(uint64_t kernel_id, double *ms) {
     Program *prog = lookup(kernel_id);
     if (!prog || !ms) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id");
     *ms = prog->compile_ms;
+    return TRS_OK;
+}
+
+int trs_fusion_from_disk_cache(uint64_t kernel_id, int *hit) {
+    Program *prog = lookup(kernel_id);
+    if (!prog || !hit) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id");
+    *hit = prog->from_disk ? 1 : 0;
     return TRS_OK;
 }
 

@@ -112,6 +112,7 @@ _SIGNATURES = {
     "trs_fusion_launch": ([c_uint64, c_int, POINTER(c_void_p), _LP, c_void_p, _LP], c_int),
     "trs_fusion_source": ([c_uint64, ctypes.c_char_p, c_size_t, POINTER(c_size_t)], c_int),
     "trs_fusion_compile_ms": ([c_uint64, POINTER(c_double)], c_int),
+    "trs_fusion_from_disk_cache": ([c_uint64, POINTER(c_int)], c_int),
 }
 
 

@@ -101,3 +101,54 @@ def test_fusion_compiler_rejects_bad_programs(ir, fragment):
     rc, _ = _compile(ir)
     assert rc == -9
     assert fragment in abi.lib.trs_last_error().decode()
+
+
+_CACHE_CHILD = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+from trs_backend import abi
+ir = sys.argv[2]
+kid = ctypes.c_uint64()
+abi.check(abi.lib.trs_fusion_compile(ir.encode(), len(ir), ctypes.byref(kid)))
+hit, ms = ctypes.c_int(), ctypes.c_double()
+abi.check(abi.lib.trs_fusion_from_disk_cache(kid, ctypes.byref(hit)))
+abi.check(abi.lib.trs_fusion_compile_ms(kid, ctypes.byref(ms)))
+print(hit.value, ms.value)
+"""
+
+
+def _compile_in_child(ir: str, cache_dir: str):
+    import os
+    import subprocess
+    import sys
+    env = dict(os.environ, TRS_FUSION_CACHE_DIR=cache_dir)
+    pkg = str(Path(__file__).resolve().parent.parent / "pytorch-rs_amd")
+    out = subprocess.run([sys.executable, "-c", _CACHE_CHILD, pkg, ir], env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    hit, ms = out.stdout.split()
+    return int(hit), float(ms)
+
+
+def test_fusion_disk_cache_persists_across_processes_and_rejects_bad_files(tmp_path):
+    ir = "in f32\nconst 0x40490fdb\nmul %0 %1\nneg %2\nout %3\n"
+    cache = tmp_path / "fusion"
+    hit, compile_ms = _compile_in_child(ir, str(cache))
+    assert hit == 0
+    files = list(cache.glob("*.co"))
+    assert len(files) == 1 and not list(cache.glob("*.tmp.*"))
+    hit, load_ms = _compile_in_child(ir, str(cache))
+    assert hit == 1 and load_ms < compile_ms
+    # A damaged file (wrong key bytes) is a miss and is replaced by a good one.
+    data = bytearray(files[0].read_bytes())
+    data[40] ^= 0xFF
+    files[0].write_bytes(bytes(data))
+    assert _compile_in_child(ir, str(cache))[0] == 0
+    assert _compile_in_child(ir, str(cache))[0] == 1
+    # A truncated file is a miss as well.
+    files[0].write_bytes(files[0].read_bytes()[:-100])
+    assert _compile_in_child(ir, str(cache))[0] == 0
+    # An empty directory setting disables the cache.
+    before = sorted(p.name for p in tmp_path.rglob("*"))
+    assert _compile_in_child(ir, "")[0] == 0
+    assert sorted(p.name for p in tmp_path.rglob("*")) == before

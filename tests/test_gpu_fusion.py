@@ -191,3 +191,53 @@ def test_random_programs_fused_equal_eager_bit_for_bit():
         assert fused.shape == eager.shape, (case, prog)
         assert fused.stride() == eager.stride(), (case, prog, fused.stride(), eager.stride())
         assert_bitwise_equal(fused.numpy().ravel(), eager.numpy().ravel())
+
+
+_DISK_CHILD = r"""
+import ctypes, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from trs_backend import abi
+from trs_backend.abi import DeviceArray, check, layout_of
+ir = sys.argv[2]
+kid = ctypes.c_uint64()
+check(abi.lib.trs_fusion_compile(ir.encode(), len(ir), ctypes.byref(kid)))
+hit = ctypes.c_int()
+check(abi.lib.trs_fusion_from_disk_cache(kid, ctypes.byref(hit)))
+if sys.argv[3] == "launch":
+    check(abi.lib.trs_init())
+    n = (1 << 20) + 3
+    x = np.random.default_rng(5).standard_normal(n).astype(np.float32)
+    dx, fused, t1, eager = DeviceArray.from_numpy(x), DeviceArray(n * 4), DeviceArray(n * 4), DeviceArray(n * 4)
+    lay = layout_of((n,))
+    check(abi.lib.trs_fusion_launch(kid, 1, (ctypes.c_void_p * 1)(dx.addr), (abi.Layout * 1)(lay), fused.ptr,
+                                    ctypes.byref(lay)))
+    check(abi.lib.trs_binary_scalar_f32(2, dx.ptr, ctypes.byref(lay), ctypes.c_float(np.float32(3.14159274)),
+                                        t1.ptr, ctypes.byref(lay)))
+    check(abi.lib.trs_unary_f32(2, t1.ptr, ctypes.byref(lay), eager.ptr, ctypes.byref(lay)))
+    same = np.array_equal(fused.to_numpy().view(np.uint32), eager.to_numpy().view(np.uint32))
+    print(hit.value, int(same))
+else:
+    print(hit.value, 1)
+"""
+
+
+def test_program_loaded_from_the_disk_cache_runs_bit_exact(tmp_path):
+    """A code object written by one process and loaded by another computes
+    the same bits as the eager ops: x * f32(pi), then neg."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    ir = "in f32\nconst 0x40490fdb\nmul %0 %1\nneg %2\nout %3\n"
+    env = dict(os.environ, TRS_FUSION_CACHE_DIR=str(tmp_path / "fusion"))
+    pkg = str(Path(__file__).resolve().parent.parent / "pytorch-rs_amd")
+
+    def child(mode):
+        out = subprocess.run([sys.executable, "-c", _DISK_CHILD, pkg, ir, mode], env=env, capture_output=True,
+                             text=True, timeout=120)
+        assert out.returncode == 0, out.stderr
+        return tuple(int(v) for v in out.stdout.split())
+
+    assert child("compile") == (0, 1)
+    assert child("launch") == (1, 1)
