@@ -144,11 +144,13 @@ int run_pointwise(const F &f, const trs_layout *lo, float *out, int nin, const v
 // ---- reductions -------------------------------------------------------------
 
 constexpr int kSumBlocks = 1024;
+constexpr int64_t kSumOneBlock = 32768;  // at most 128 elements per lane in one block
 
 // Fixed-order two-level sum.  Pass 1: block b sums the contiguous element
 // range [b*chunk, (b+1)*chunk) -- lane l adds elements l, l+256, ... in order,
 // then a fixed shuffle/LDS tree over the 256 lanes.  Pass 2 sums the block
-// partials in the same way.  The order depends only on the element count.
+// partials in the same way.  Up to kSumOneBlock elements, pass 1 runs as one
+// block over the whole range.  The order depends only on the element count.
 template <bool CONTIG>
 __global__ void __launch_bounds__(256) sum_pass1(const float *x, PwGeom g, int64_t chunk, float *partial) {
     __shared__ float red[256];
@@ -491,6 +493,16 @@ int trs_sum_f32(const float *x, const trs_layout *lx, float *out) {
         g.istride[0][d] = lx->stride[d];
         if (lx->shape[d] > (int64_t)UINT32_MAX) g.wide = 1;
         g.fd[d] = make_fast_div(lx->shape[d] > (int64_t)UINT32_MAX ? 1u : (uint32_t)lx->shape[d]);
+    }
+    // Up to kSumOneBlock elements: pass 1 alone, one block writing the result
+    // (one launch and no partials buffer; the order is still fixed by n).
+    if (n <= kSumOneBlock) {
+        if (layout_is_contiguous(lx))
+            hipLaunchKernelGGL(sum_pass1<true>, dim3(1), dim3(256), 0, dev->stream, x, g, n, out);
+        else
+            hipLaunchKernelGGL(sum_pass1<false>, dim3(1), dim3(256), 0, dev->stream, x, g, n, out);
+        TRS_LAUNCH_CHECK("sum one pass");
+        return TRS_OK;
     }
     // Block partials in a buffer of this call's own: the block cache returns
     // it in stream order, so concurrent callers on one device never share it.

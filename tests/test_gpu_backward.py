@@ -123,7 +123,7 @@ def test_add_vjp_reduce_to_shape_bit_exact(oshape, self_shape):
     assert_bitwise_equal(gpu_reduce(up, oshape, self_shape), O.reduce_to_shape(up, oshape, self_shape))
 
 
-@pytest.mark.parametrize("n", [1, 3, 1000, 1 << 20, (1 << 23) + 5])
+@pytest.mark.parametrize("n", [1, 3, 1000, 32768, 32769, 1 << 20, (1 << 23) + 5])
 def test_sum_within_summation_bound(n):
     rng = np.random.default_rng(n)
     x = rng.standard_normal(n).astype(np.float32)
@@ -132,6 +132,17 @@ def test_sum_within_summation_bound(n):
     # Any two float orderings of an n-term sum differ by at most 2 * (n-1) * u * sum|x|.
     bound = 2 * (n - 1) * 2.0 ** -24 * O.sum_abs(x)
     assert abs(float(got) - float(want)) <= bound
+
+
+@pytest.mark.parametrize("n", [257, 32768, 32769, 100003])
+def test_sum_of_small_integers_is_exact_on_both_paths(n):
+    # Integers below 2^24 in total sum exactly in any order: the one-block
+    # path (n <= 32768) and the two-pass path must both equal the fold.
+    x = (np.arange(n) % 7 - 3).astype(np.float32)
+    assert float(gpu_sum(x, (n,))) == float(O.sum_f32(x, (n,)))
+    xt = x[: (n // 3) * 3].reshape(3, -1)
+    got = gpu_sum(np.ascontiguousarray(xt), (xt.shape[1], 3), (1, xt.shape[1]))  # a transposed view
+    assert float(got) == float(xt.sum())
 
 
 def test_sum_of_transposed_view_and_golden():
