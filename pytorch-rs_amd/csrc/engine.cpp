@@ -421,6 +421,7 @@ const char *node_name(Node n) {
     case Node::Squeeze: return "SqueezeBackward0";
     case Node::SqueezeDimension: return "SqueezeBackward1";
     case Node::SqueezeDimensions: return "SqueezeBackward2";
+    case Node::Unsqueeze: return "UnsqueezeBackward0";
     }
     return "UnknownBackward";
 }
@@ -737,6 +738,18 @@ Tensor Tensor::squeeze_dims(const std::vector<int64_t> &dims) const {
         if (!sel.empty()) sel[a] = true;
     }
     return squeeze_selected(sel, Node::SqueezeDimensions);
+}
+
+// unsqueeze_front (src/tensor.rs:1218-1268): a leading size-1 dim whose
+// stride is stride[0] * shape[0] (1 for a scalar); Identity mapping.
+Tensor Tensor::unsqueeze_front() const {
+    Dims s{1}, st;
+    st.push_back(shape.empty() ? 1 : (int64_t)((uint64_t)strides[0] * (uint64_t)shape[0]));
+    s.insert(s.end(), shape.begin(), shape.end());
+    st.insert(st.end(), strides.begin(), strides.end());
+    Tensor out = alias_view(s, st, offset);
+    record_transform(*this, out, GradKind::Identity, Node::Unsqueeze);
+    return out;
 }
 
 // matrix_transpose = .mT (src/tensor.rs:1209-1215).

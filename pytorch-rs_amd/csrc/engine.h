@@ -81,7 +81,8 @@ using MetaPtr = std::shared_ptr<AutogradMeta>;
 // backend adds for device tensors.
 enum class Node {
     Add, Alias, Clone, Multiply, Negate, Permute, Relu, ReflectedSubtract, Subtract, Sum, MatrixTranspose,
-    Transpose, View, Select, Exp, Mm, Bmm, AddTensor, SubTensor, Squeeze, SqueezeDimension, SqueezeDimensions
+    Transpose, View, Select, Exp, Mm, Bmm, AddTensor, SubTensor, Squeeze, SqueezeDimension, SqueezeDimensions,
+    Unsqueeze
 };
 const char *node_name(Node n);
 
@@ -167,6 +168,7 @@ public:
     Tensor squeeze() const;                                    // every size-1 dim
     Tensor squeeze_dim(int64_t dim) const;                     // that dim, if size 1
     Tensor squeeze_dims(const std::vector<int64_t> &dims) const;  // those dims that have size 1
+    Tensor unsqueeze_front() const;                            // a leading size-1 dim
     Tensor matrix_transpose() const;
     Tensor reverse_dims() const;
     Tensor reshape(const std::vector<int64_t> &req) const;

@@ -204,6 +204,7 @@ PYBIND11_MODULE(_trs_native, m) {
         // swapdims / swapaxes are transpose under another name (src/python.rs:3634-3672)
         .def("swapdims", &Tensor::transpose, py::arg("dim0"), py::arg("dim1"))
         .def("swapaxes", &Tensor::transpose, py::arg("axis0"), py::arg("axis1"))
+        .def("_unsqueeze_front", &Tensor::unsqueeze_front)
         // squeeze(), squeeze(dim), squeeze((d0, d1, ...)) (src/python.rs:6112-6121)
         .def("squeeze",
              [](const Tensor &t, const py::object &dim) {

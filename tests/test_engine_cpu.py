@@ -387,6 +387,70 @@ def test_dropout_argument_checks_follow_the_reference_order_and_messages():
     assert F.dropout(torch_rs.zeros(0), p=0.5) is not None
 
 
+def test_dropout_family_deterministic_cases_follow_the_reference():
+    # src/python_nn_functional.rs:13-62 (kinds) and :117-200 (bridge);
+    # messages after tests/test_nn_functional_dropout1d.py:297-580 and the
+    # dropout2d/alpha tests.
+    import warnings as _w
+    F = torch_rs.nn.functional
+    x3 = torch_rs.zeros((1, 2, 3), requires_grad=True)
+    x2 = torch_rs.zeros((2, 3), requires_grad=True)
+    # identities return the input itself, except unbatched dropout1d
+    for fn, x in ((F.dropout1d, x3), (F.dropout3d, torch_rs.zeros((1, 1, 1, 1, 2)))):
+        assert fn(x, p=0.75, training=False) is x
+    y = F.dropout1d(x2, p=0.75, training=False)
+    assert y is not x2 and y.shape == (2, 3) and y.stride() == x2.stride()
+    assert y.grad_fn.name() == "SqueezeBackward1"
+    assert F.alpha_dropout(x3, p=0.5) is x3  # training defaults to False
+    assert F.feature_alpha_dropout(x3, p=0.5) is x3
+    with pytest.raises(AttributeError, match="^'NoneType' object has no attribute 'dim'$"):
+        F.dropout1d(None, p=0)
+    with pytest.raises(NotImplementedError, match="^torch_rs.nn.functional.dropout1d does not support inplace=True "
+                                                  "for rank-2 inputs$"):
+        F.dropout1d(x2, p=0.5, inplace=True)
+    with pytest.raises(NotImplementedError, match="^torch_rs.nn.functional.dropout1d only supports rank-2 or "
+                                                  "rank-3 inputs$"):
+        F.dropout1d(torch_rs.zeros(4), p=0.5)
+    with pytest.raises(NotImplementedError, match="^torch_rs.nn.functional.dropout2d only supports rank-3 or "
+                                                  "rank-4 inputs$"):
+        F.dropout2d(x2, p=0.5, training=False)
+    with pytest.raises(NotImplementedError, match="^torch_rs.nn.functional.dropout3d only supports rank-5 inputs$"):
+        F.dropout3d(x3, p=0.5, training=False)
+    with _w.catch_warnings(record=True) as caught:
+        _w.simplefilter("always")
+        assert F.dropout2d(x3, p=0.5, training=False) is x3
+    assert any("Received a 3D input to dropout2d" in str(w.message) for w in caught)
+    for fn in (F.dropout1d, F.dropout2d, F.feature_alpha_dropout, F.alpha_dropout):
+        with pytest.raises(NotImplementedError, match=f"^torch_rs.nn.functional.{fn.__name__} does not support "
+                                                      "sampling$"):
+            fn(x3, p=0.5, training=True)
+    # p == 1 is input * 0.0 only where the kind allows it (dropout2d does not)
+    with pytest.raises(NotImplementedError, match="dropout2d does not support sampling"):
+        F.dropout2d(x3, p=1.0, training=True)
+    with pytest.raises(RuntimeError, match="device tensors only"):  # the multiply itself needs the device
+        F.dropout3d(torch_rs.zeros((1, 1, 1, 1, 2)), p=1.0, training=True)
+    # probability arguments
+    with pytest.raises(TypeError, match=r"^alpha_dropout\(\): argument 'p' \(position 2\) must be float, not Tensor$"):
+        F.alpha_dropout(x3, p=torch_rs.tensor(0.5))
+    with pytest.raises(TypeError, match=r"^feature_dropout_\(\): argument 'p' \(position 2\) must be float, "
+                                        r"not Tensor$"):
+        F.dropout2d(x3, p=torch_rs.tensor([0.5]), inplace=True)
+    with pytest.raises(TypeError, match=r"^dropout\(\): argument 'p' \(position 2\) must be float, not Tensor$"):
+        F.dropout(x3, p=torch_rs.tensor(0.5, requires_grad=True))
+    assert F.dropout(x3, p=np.float32(0.0)) is x3 and F.dropout(x3, p=np.bool_(False)) is x3
+    with pytest.raises(TypeError, match=r"^dropout\(\): argument 'p' \(position 2\) must be float, not "
+                                        r"test_engine_cpu.SneakyStr$"):
+        F.dropout(x3, p=SneakyStr("0.5"))
+
+
+class SneakyStr(str):  # passes the Python-level range check; not float-like
+    def __lt__(self, other):
+        return False
+
+    def __gt__(self, other):
+        return False
+
+
 def test_dropout_bridge_cases_on_host():
     F = torch_rs.nn.functional
     x = torch_rs.zeros(4)
