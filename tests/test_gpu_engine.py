@@ -447,3 +447,16 @@ def test_dropout_backward_is_scale_then_mask_in_one_pass():
         want = (np.float32(1 / 0.9) * up) * mask.astype(np.float32)
     (F.dropout(h, 0.1, mask=mask) * cuda(up)).sum().backward()
     assert_bitwise_equal(vals(h.grad), want)
+
+
+def test_unbatched_dropout1d_identity_view_passes_gradients_through():
+    # unsqueeze(0) then squeeze(0) (src/python_nn_functional.rs:168-178): a new
+    # view whose SqueezeBackward1 and UnsqueezeBackward0 edges reach the leaf.
+    x = cuda(np.arange(6, dtype=np.float32).reshape(2, 3), requires_grad=True)
+    y = F.dropout1d(x, p=0.5, training=False)
+    assert y is not x and y.grad_fn.name() == "SqueezeBackward1"
+    w = cuda(np.float32([[1, -2, 3], [-4, 5, -6]]))
+    (y * w).sum().backward()
+    assert x.grad.numpy().tolist() == [[1, -2, 3], [-4, 5, -6]]
+    z = cuda(np.ones((1, 1, 1, 1, 2), np.float32))
+    assert F.dropout3d(z, p=1.0, training=True).numpy().reshape(-1).tolist() == [0.0, 0.0]
