@@ -1,12 +1,49 @@
-"""torch_rs.autograd -- single-root backward (python/torch_rs/autograd/__init__.py:44-127)."""
+"""torch_rs.autograd -- single-root backward with the reference's option
+checks (python/torch_rs/autograd/__init__.py:22-127)."""
 from __future__ import annotations
 
+import operator as _operator
 
-def backward(tensors, grad_tensors=None) -> None:
-    if isinstance(tensors, (list, tuple)):
-        if len(tensors) != 1:
-            raise NotImplementedError("torch_rs.autograd.backward supports a single root tensor")
-        tensors = tensors[0]
+from ._native import native as _C
+
+
+def _require_default(name, value, *, allow_none):
+    if value is None and allow_none:
+        return
+    if _operator.index(value):
+        raise NotImplementedError(f"torch_rs.autograd.backward does not support {name}=True")
+
+
+def _single_root(tensors):
+    if type(tensors) is _C.Tensor:
+        return tensors
+    if type(tensors) in (tuple, list) and len(tensors) == 1 and type(tensors[0]) is _C.Tensor:
+        return tensors[0]
+    raise TypeError("torch_rs.autograd.backward only supports an exact native Tensor, "
+                    "directly or in an exact one-element tuple or list")
+
+
+def backward(tensors, grad_tensors=None, retain_graph=None, create_graph=False, grad_variables=None,
+             inputs=None) -> None:
+    """Reverse pass from one scalar root, in the reference's order of checks."""
+    root = _single_root(tensors)
     if grad_tensors is not None:
-        raise NotImplementedError("torch_rs.autograd.backward does not support grad_tensors")
-    tensors.backward()
+        raise NotImplementedError("torch_rs.autograd.backward does not support explicit gradients")
+    _require_default("retain_graph", retain_graph, allow_none=True)
+    _require_default("create_graph", create_graph, allow_none=False)
+    if grad_variables is not None:
+        raise NotImplementedError("torch_rs.autograd.backward does not support grad_variables")
+    if inputs is not None:
+        raise NotImplementedError("torch_rs.autograd.backward does not support inputs")
+    root.backward()
+
+
+def __getattr__(name):
+    # no_grad lives in the package root; re-exported here as the reference does.
+    if name == "no_grad":
+        from . import no_grad
+        return no_grad
+    raise AttributeError(name)
+
+
+__all__ = ["backward", "no_grad"]

@@ -253,6 +253,28 @@ def test_views_record_transform_nodes_and_leafness():
     assert not d.requires_grad and d.is_leaf
 
 
+def test_autograd_backward_option_checks_follow_the_reference():
+    # python/torch_rs/autograd/__init__.py:22-127
+    A = torch_rs.autograd
+    x = torch_rs.zeros(2, requires_grad=True)
+    with pytest.raises(TypeError, match="only supports an exact native Tensor"):
+        A.backward([x, x])
+    with pytest.raises(TypeError, match="only supports an exact native Tensor"):
+        A.backward(None)
+    for kwargs, msg in (({"grad_tensors": x}, "does not support explicit gradients"),
+                        ({"retain_graph": True}, "does not support retain_graph=True"),
+                        ({"create_graph": 1}, "does not support create_graph=True"),
+                        ({"grad_variables": [x]}, "does not support grad_variables"),
+                        ({"inputs": [x]}, "does not support inputs")):
+        with pytest.raises(NotImplementedError, match=msg):
+            A.backward((x,), **kwargs)
+    with pytest.raises(TypeError):
+        A.backward(x, create_graph=None)  # operator.index(None)
+    with pytest.raises(RuntimeError, match="grad can be implicitly created only for scalar outputs"):
+        A.backward([x], retain_graph=False)
+    assert A.no_grad is torch_rs.no_grad
+
+
 def test_backward_errors_match_reference_messages():
     x = torch_rs.zeros(2)
     with pytest.raises(RuntimeError, match="element 0 of tensors does not require grad"):
