@@ -22,6 +22,11 @@
  *   - The caller allocates every output (trs_alloc) and computes its layout;
  *     the output layout of the reference's planner (elementwise_output_strides,
  *     src/tensor.rs:4249-4312) is a host-side property.
+ *   - An output must not overlap itself, and may share memory with an input
+ *     only as the very same view (same address, shape and strides: in place,
+ *     element for element).  A matmul output shares no memory with A or B.
+ *     Other overlaps are rejected with TRS_E_INVALID_ARGUMENT before any
+ *     launch.
  *   - All work is queued in order on one HIP stream per device (trs_stream);
  *     only trs_memcpy_d2h and trs_synchronize block the host.
  *   - Callable from any thread; the allocator and the fusion cache are

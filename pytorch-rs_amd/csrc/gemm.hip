@@ -354,6 +354,12 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
     if (!layout_is_contiguous(lc)) return set_error(TRS_E_INVALID_ARGUMENT, "matmul output must be contiguous");
     if (M == 0 || N == 0 || batch == 0) return TRS_OK;
     if (!a || !b || !c) return set_error(TRS_E_INVALID_ARGUMENT, "null matmul operand");
+    {
+        // C is written while A and B are still being read: no shared memory.
+        const ByteRange out_bytes = byte_range(c, lc, 4);
+        if (K > 0 && (ranges_overlap(out_bytes, byte_range(a, la, 4)) || ranges_overlap(out_bytes, byte_range(b, lb, 4))))
+            return set_error(TRS_E_INVALID_ARGUMENT, "matmul output overlaps an operand");
+    }
     float *C = c + lc->offset;
     if (K == 0) return trs_memset_zero(C, (size_t)(M * N * batch) * sizeof(float));
 

@@ -83,6 +83,19 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
     if (out == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "null output pointer");
     for (int i = 0; i < nin; i++)
         if (bases[i] == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "null input pointer %d", i);
+    // An input may share memory with the output only as the very same view
+    // (element-wise in place: every lane reads and writes its own elements);
+    // any other overlap would race across lanes.
+    {
+        const ByteRange ro = byte_range(out, lo, 4);
+        for (int i = 0; i < nin; i++) {
+            if (layout_numel(lins[i]) == 0) continue;
+            const ByteRange ri = byte_range(bases[i], lins[i], elem_bytes[i]);
+            if (!ranges_overlap(ro, ri)) continue;
+            if (elem_bytes[i] == 4 && ri.begin == ro.begin && same_view_shape(lins[i], lo)) continue;
+            return set_error(TRS_E_INVALID_ARGUMENT, "output overlaps input %d other than as the same view", i);
+        }
+    }
 
     // 1-2. align, drop singleton dims.
     int rank = 0;
@@ -114,7 +127,6 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         return set_error(TRS_E_INVALID_ARGUMENT, "output layout overlaps itself");
     // Merge dims that are contiguous for every operand.
     {
-        int w = rank - 1;  // merge outward into the innermost kept dim
         int64_t nsize[kMaxRank], nos[kMaxRank], nis[kMaxIn][kMaxRank];
         int nr = 0;
         // Walk from innermost to outermost, building reversed list.
@@ -133,7 +145,6 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             for (int i = 0; i < nin; i++) nis[i][nr] = is[i][d];
             nr++;
         }
-        (void)w;
         rank = nr;
         for (int d = 0; d < rank; d++) {
             size[d] = nsize[rank - 1 - d];

@@ -53,6 +53,25 @@ int check_layout(const trs_layout *l, const char *what);
 int64_t layout_numel(const trs_layout *l);
 bool layout_is_contiguous(const trs_layout *l);
 
+// The bytes a non-empty view can touch: [begin, end) from its base pointer.
+struct ByteRange {
+    uintptr_t begin = 0, end = 0;
+};
+inline ByteRange byte_range(const void *base, const trs_layout *l, int elem_bytes) {
+    int64_t last = l->offset;
+    for (int d = 0; d < l->rank; d++) last += (l->shape[d] - 1) * l->stride[d];
+    const uintptr_t b = (uintptr_t)base;
+    return ByteRange{b + (uintptr_t)(l->offset * elem_bytes), b + (uintptr_t)((last + 1) * elem_bytes)};
+}
+inline bool ranges_overlap(const ByteRange &a, const ByteRange &b) { return a.begin < b.end && b.begin < a.end; }
+// Same rank, shape and strides (the offsets are compared as byte addresses).
+inline bool same_view_shape(const trs_layout *a, const trs_layout *b) {
+    if (a->rank != b->rank) return false;
+    for (int d = 0; d < a->rank; d++)
+        if (a->shape[d] != b->shape[d] || a->stride[d] != b->stride[d]) return false;
+    return true;
+}
+
 #define TRS_HIP_CHECK(expr, what)                 \
     do {                                          \
         hipError_t trs_e_ = (expr);               \

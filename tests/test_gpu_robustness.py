@@ -82,3 +82,35 @@ def test_flat_kernels_beyond_two_to_the_32_elements():
         assert np.array_equal(out[s:e], half[s % period: s % period + (e - s)]), s
     del dout
     check(abi.lib.trs_empty_cache())  # hand the 32 GiB back to HIP for the tests that follow
+
+
+def test_outputs_may_alias_inputs_only_as_the_same_view():
+    """In place is allowed element for element; any other overlap with an
+    input (shifted, transposed, broadcast) or with a matmul operand is
+    rejected on the host before anything is launched."""
+    rng = np.random.default_rng(9)
+    a = rng.standard_normal(64 * 64).astype(np.float32)
+    b = rng.standard_normal(64 * 64).astype(np.float32)
+    da, db = DeviceArray.from_numpy(a), DeviceArray.from_numpy(b)
+    sq = layout_of((64, 64))
+    # a = a + b in place: the same view
+    check(abi.lib.trs_binary_f32(0, da.ptr, ctypes.byref(sq), db.ptr, ctypes.byref(sq), da.ptr, ctypes.byref(sq)))
+    assert np.array_equal(da.to_numpy(), a + b)
+    # accumulate is in place by construction
+    check(abi.lib.trs_accumulate_f32(da.ptr, db.ptr, a.size))
+    assert np.array_equal(da.to_numpy(), (a + b) + b)
+    shifted = layout_of((64, 63), (64, 1), 1)
+    first = layout_of((64, 63))
+    rc = abi.lib.trs_binary_f32(0, da.ptr, ctypes.byref(first), db.ptr, ctypes.byref(first), da.ptr,
+                                ctypes.byref(shifted))
+    assert rc == abi.TRS_E_INVALID_ARGUMENT and b"overlaps input 0" in abi.lib.trs_last_error()
+    transposed = layout_of((64, 64), (1, 64))
+    rc = abi.lib.trs_unary_f32(3, da.ptr, ctypes.byref(transposed), da.ptr, ctypes.byref(sq))
+    assert rc == abi.TRS_E_INVALID_ARGUMENT
+    row = layout_of((64,))
+    rc = abi.lib.trs_binary_f32(0, db.ptr, ctypes.byref(sq), da.ptr, ctypes.byref(row), da.ptr, ctypes.byref(sq))
+    assert rc == abi.TRS_E_INVALID_ARGUMENT  # a broadcast row of the output's own memory
+    rc = abi.lib.trs_matmul_f32(da.ptr, ctypes.byref(sq), db.ptr, ctypes.byref(sq), da.ptr, ctypes.byref(sq))
+    assert rc == abi.TRS_E_INVALID_ARGUMENT and b"overlaps an operand" in abi.lib.trs_last_error()
+    # the rejected calls changed nothing
+    assert np.array_equal(da.to_numpy(), (a + b) + b)
