@@ -27,6 +27,8 @@
  *     element for element).  A matmul output shares no memory with A or B.
  *     Other overlaps are rejected with TRS_E_INVALID_ARGUMENT before any
  *     launch.
+ *   - A non-empty view whose element count, last element offset or last byte
+ *     offset leaves 64 bits is rejected with TRS_E_INDEX_OVERFLOW.
  *   - All work is queued in order on one HIP stream per device (trs_stream);
  *     only trs_memcpy_d2h and trs_synchronize block the host.
  *   - Callable from any thread; the allocator and the fusion cache are

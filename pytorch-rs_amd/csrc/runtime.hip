@@ -91,10 +91,23 @@ int check_layout(const trs_layout *l, const char *what) {
     if (l->rank < 0 || l->rank > TRS_MAX_RANK)
         return set_error(TRS_E_INVALID_ARGUMENT, "%s rank %d outside [0, 8]", what, l->rank);
     if (l->offset < 0) return set_error(TRS_E_INVALID_ARGUMENT, "%s offset is negative", what);
+    int64_t numel = 1;
     for (int d = 0; d < l->rank; d++) {
         if (l->shape[d] < 0 || l->stride[d] < 0)
             return set_error(TRS_E_INVALID_ARGUMENT, "%s dim %d has a negative size or stride", what, d);
+        if (__builtin_mul_overflow(numel, l->shape[d], &numel))
+            return set_error(TRS_E_INDEX_OVERFLOW, "%s element count overflows 64 bits", what);
     }
+    if (numel == 0) return TRS_OK;  // nothing is addressed
+    // The last element's offset, and its byte offset, must fit in 64 bits
+    // (IndexCalculationOverflow, src/tensor.rs:3815-3841).
+    int64_t last = l->offset;
+    for (int d = 0; d < l->rank; d++) {
+        int64_t step;
+        if (__builtin_mul_overflow(l->shape[d] - 1, l->stride[d], &step) || __builtin_add_overflow(last, step, &last))
+            return set_error(TRS_E_INDEX_OVERFLOW, "%s offsets overflow 64 bits", what);
+    }
+    if (last > (INT64_MAX >> 3)) return set_error(TRS_E_INDEX_OVERFLOW, "%s byte offsets overflow 64 bits", what);
     return TRS_OK;
 }
 

@@ -114,3 +114,22 @@ def test_outputs_may_alias_inputs_only_as_the_same_view():
     assert rc == abi.TRS_E_INVALID_ARGUMENT and b"overlaps an operand" in abi.lib.trs_last_error()
     # the rejected calls changed nothing
     assert np.array_equal(da.to_numpy(), (a + b) + b)
+
+
+def test_layouts_whose_offsets_overflow_are_rejected_before_launch():
+    """IndexCalculationOverflow (src/tensor.rs:3815-3841): a view whose last
+    offset, byte offset or element count leaves 64 bits is refused; a
+    zero-element view addresses nothing and is accepted."""
+    d = DeviceArray(4096)
+    huge_stride = layout_of((4,), (1 << 62,))
+    rc = abi.lib.trs_unary_f32(1, d.ptr, ctypes.byref(huge_stride), d.ptr, ctypes.byref(layout_of((4,))))
+    assert rc == -2 and b"overflow" in abi.lib.trs_last_error()
+    byte_overflow = layout_of((2,), (1 << 61,))
+    out = DeviceArray(64)
+    rc = abi.lib.trs_unary_f32(1, d.ptr, ctypes.byref(byte_overflow), out.ptr, ctypes.byref(layout_of((2,))))
+    assert rc == -2
+    many = layout_of((1 << 32, 1 << 32), (0, 0))
+    rc = abi.lib.trs_sum_f32(d.ptr, ctypes.byref(many), out.ptr)
+    assert rc == -2 and b"element count" in abi.lib.trs_last_error()
+    empty = layout_of((0, (1 << 62), 3), ((1 << 62), 3, 1))
+    check(abi.lib.trs_unary_f32(1, d.ptr, ctypes.byref(empty), out.ptr, ctypes.byref(empty)))
