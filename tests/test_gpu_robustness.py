@@ -133,3 +133,46 @@ def test_layouts_whose_offsets_overflow_are_rejected_before_launch():
     assert rc == -2 and b"element count" in abi.lib.trs_last_error()
     empty = layout_of((0, (1 << 62), 3), ((1 << 62), 3, 1))
     check(abi.lib.trs_unary_f32(1, d.ptr, ctypes.byref(empty), out.ptr, ctypes.byref(empty)))
+
+
+def test_allocation_failure_is_reported_and_the_library_keeps_working():
+    """AllocationFailed (src/tensor.rs:5540-5580 forces it with elements =
+    usize::MAX): an impossible request fails with the allocation code, after
+    the block cache has been released and the allocation retried, and later
+    work is unaffected."""
+    import torch_rs
+    p = ctypes.c_void_p()
+    rc = abi.lib.trs_alloc(1 << 52, ctypes.byref(p))
+    assert rc == -1 and not p.value
+    assert abi.lib.trs_last_error()
+    with pytest.raises(RuntimeError):
+        torch_rs.zeros((1 << 40,), device="cuda")
+    x = torch_rs.tensor(np.arange(8, dtype=np.float32), device="cuda")
+    assert (x * 2.0).numpy().tolist() == [float(2 * i) for i in range(8)]
+
+
+def test_square_sum_backward_smoke_matches_closed_form_and_is_fast():
+    """The reference's only timing test (tests/test_autograd.py:1843-1867):
+    (v*v).sum().backward() on 16,384 values, median of 7 timed runs after 3
+    warm-ups, with a checksum of the gradients.  Here the gradient 2v is exact,
+    so the checksum sum((2v)^2) is checked against float64, and the median is
+    held to 2 ms (a device step measures about 30 us)."""
+    import statistics
+    import time
+    import torch_rs
+    values = np.linspace(-2.0, 2.0, 16_384, dtype=np.float32)
+    inputs = [torch_rs.tensor(values, device="cuda", requires_grad=True) for _ in range(10)]
+    samples, checksum = [], 0.0
+    for i, v in enumerate(inputs):
+        t0 = time.perf_counter()
+        (v * v).sum().backward()
+        torch_rs.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        g = v.grad.numpy().astype(np.float64)
+        assert np.array_equal(g, 2.0 * values.astype(np.float64))
+        checksum += float((g * g).sum())
+        if i >= 3:
+            samples.append(elapsed)
+    want = 10 * float(((2.0 * values.astype(np.float64)) ** 2).sum())
+    assert abs(checksum - want) <= 1e-9 * want
+    assert statistics.median(samples) < 2e-3
