@@ -293,6 +293,16 @@ def _array(self, dtype=None, copy=None):
     return a if dtype is None else a.astype(dtype)
 
 
+def _bool(self):
+    """truth_value (src/python.rs:4015-4029): one element -> value != 0."""
+    n = self.numel()
+    if n == 0:
+        raise RuntimeError("Boolean value of Tensor with no values is ambiguous")
+    if n != 1:
+        raise RuntimeError("Boolean value of Tensor with more than one value is ambiguous")
+    return self.item() != 0.0
+
+
 def _len(self):
     if not self.shape:
         raise TypeError("len() of a 0-d tensor")
@@ -326,6 +336,7 @@ Tensor.matmul = _matmul_method
 Tensor.__array__ = _array
 Tensor.__repr__ = _repr
 Tensor.__len__ = _len
+Tensor.__bool__ = _bool
 Tensor.multiply = Tensor.mul
 
 from . import autograd, cuda, nn  # noqa: E402,F401

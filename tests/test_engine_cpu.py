@@ -294,6 +294,18 @@ def test_host_tensors_do_not_compute():
     assert np.asarray(x).dtype == np.float32
 
 
+def test_truth_value_follows_the_reference():
+    # src/python.rs:4015-4029: one element -> value != 0; otherwise an error.
+    assert bool(torch_rs.tensor(2.0)) and not bool(torch_rs.tensor(0.0)) and not bool(torch_rs.tensor(-0.0))
+    assert bool(torch_rs.tensor([[3.0]])) and bool(torch_rs.tensor(float("nan")))
+    with pytest.raises(RuntimeError, match="^Boolean value of Tensor with more than one value is ambiguous$"):
+        bool(torch_rs.zeros(2))
+    with pytest.raises(RuntimeError, match="^Boolean value of Tensor with no values is ambiguous$"):
+        bool(torch_rs.zeros(0))
+    with pytest.raises(TypeError, match="len\\(\\) of a 0-d tensor"):
+        len(torch_rs.tensor(1.0))
+
+
 def test_tensor_constructor_and_scalar_conversion():
     t = torch_rs.tensor([[1, 2], [3, 4.5]])
     assert t.shape == (2, 2) and t.numpy().tolist() == [[1.0, 2.0], [3.0, 4.5]]
