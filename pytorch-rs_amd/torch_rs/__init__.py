@@ -289,6 +289,10 @@ def _repr(self):
 
 
 def _array(self, dtype=None, copy=None):
+    """__array__ (src/python.rs:3744-3756, 4031-4052): always a copy of the
+    logical values, float32 unless `dtype` is given."""
+    if copy is False:
+        raise ValueError("cannot create a non-copying NumPy view of tensor storage")
     a = self.numpy()
     return a if dtype is None else a.astype(dtype)
 

@@ -294,6 +294,15 @@ def test_host_tensors_do_not_compute():
     assert np.asarray(x).dtype == np.float32
 
 
+def test_array_protocol_copies_and_refuses_views():
+    x = torch_rs.tensor(np.arange(6, dtype=np.float32).reshape(2, 3))
+    a = np.asarray(x)
+    assert a.dtype == np.float32 and a.shape == (2, 3) and a.tolist() == [[0, 1, 2], [3, 4, 5]]
+    assert np.asarray(x, dtype=np.float64).dtype == np.float64
+    with pytest.raises(ValueError, match="^cannot create a non-copying NumPy view of tensor storage$"):
+        np.array(x, copy=False)
+
+
 def test_truth_value_follows_the_reference():
     # src/python.rs:4015-4029: one element -> value != 0; otherwise an error.
     assert bool(torch_rs.tensor(2.0)) and not bool(torch_rs.tensor(0.0)) and not bool(torch_rs.tensor(-0.0))
