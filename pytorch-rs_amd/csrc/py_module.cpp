@@ -32,28 +32,63 @@ py::tuple to_tuple(const Dims &d) {
     return t;
 }
 
-// parse_arithmetic_scalar + into_f32 (src/python.rs:10070-10093, 10296-10320).
-bool scalar_of(const py::handle &h, float *out, bool *is_bool) {
-    *is_bool = false;
-    if (py::isinstance<py::bool_>(h)) {
-        *is_bool = true;
-        *out = h.cast<bool>() ? 1.0f : 0.0f;
-        return true;
+// Logical values as a numpy array of the tensor's shape (a copy).
+py::array_t<float> to_numpy(const Tensor &t) {
+    std::vector<py::ssize_t> shape(t.shape.begin(), t.shape.end());
+    py::array_t<float> a(shape);
+    t.copy_to_host(a.mutable_data());
+    return a;
+}
+
+// parse_arithmetic_scalar + into_f32 (src/python.rs:10070-10184, 10258-10320).
+enum class Scalar { None, Bool, Number, WideNumpyUnsigned, Overflow };
+
+Scalar scalar_of(const py::handle &h, float *out) {
+    if (Py_TYPE(h.ptr()) == &PyBool_Type) {  // exactly bool: the only "bool tensor" operand
+        *out = h.ptr() == Py_True ? 1.0f : 0.0f;
+        return Scalar::Bool;
     }
-    if (py::isinstance<py::int_>(h)) {
-        *out = (float)h.cast<int64_t>();
-        return true;
+    if (PyLong_Check(h.ptr())) {
+        int overflow = 0;
+        const long long v = PyLong_AsLongLongAndOverflow(h.ptr(), &overflow);
+        if (overflow == 0) {
+            *out = (float)(int64_t)v;  // i64 as f32: round to nearest
+            return Scalar::Number;
+        }
+        const unsigned long long u = overflow > 0 ? PyLong_AsUnsignedLongLong(h.ptr()) : 0;
+        if (overflow < 0 || PyErr_Occurred()) {  // beyond both i64 and u64
+            PyErr_Clear();
+            return Scalar::Overflow;
+        }
+        *out = (float)(uint64_t)u;
+        return Scalar::Number;
     }
-    if (py::isinstance<py::float_>(h)) {
-        *out = (float)h.cast<double>();
-        return true;
+    if (PyFloat_Check(h.ptr())) {
+        *out = (float)PyFloat_AsDouble(h.ptr());  // f64 as f32: round to nearest, +-inf beyond range
+        return Scalar::Number;
     }
     py::module_ np = py::module_::import("numpy");
-    if (py::isinstance(h, np.attr("generic"))) {
-        *out = (float)h.attr("__float__")().cast<double>();
-        return true;
+    if (!py::isinstance(h, np.attr("generic"))) return Scalar::None;
+    if (py::isinstance(h, np.attr("bool_"))) {
+        *out = h.cast<bool>() ? 1.0f : 0.0f;
+        return Scalar::Number;
     }
-    return false;
+    if (py::isinstance(h, np.attr("integer"))) {
+        py::int_ v = py::reinterpret_steal<py::int_>(PyNumber_Long(h.ptr()));
+        if (!v) throw py::error_already_set();
+        int overflow = 0;
+        const long long i = PyLong_AsLongLongAndOverflow(v.ptr(), &overflow);
+        if (overflow == 0) {
+            *out = (float)(int64_t)i;
+            return Scalar::Number;
+        }
+        return Scalar::WideNumpyUnsigned;
+    }
+    if (py::isinstance(h, np.attr("floating"))) {
+        *out = (float)h.attr("__float__")().cast<double>();
+        return Scalar::Number;
+    }
+    return Scalar::None;
 }
 
 enum class BinOp { Add, Sub, Mul, Div };
@@ -70,10 +105,20 @@ py::object binary_operation(const Tensor &self, const py::object &other, BinOp o
         case BinOp::Div: return py::cast(l.div(r));
         }
     }
-    float s;
-    bool is_bool;
-    if (!scalar_of(other, &s, &is_bool)) return py::reinterpret_borrow<py::object>(Py_NotImplemented);
-    if (op == BinOp::Sub && is_bool)
+    float s = 0.0f;
+    const Scalar kind = scalar_of(other, &s);
+    if (kind == Scalar::Overflow) {
+        PyErr_SetString(PyExc_OverflowError, "Python integer is outside the supported scalar range");
+        throw py::error_already_set();
+    }
+    if (kind == Scalar::None) return py::reinterpret_borrow<py::object>(Py_NotImplemented);
+    if (kind == Scalar::WideNumpyUnsigned) {
+        // numpy_reflected_divide (src/python.rs:4054-4065): numpy divides.
+        if (reverse && op == BinOp::Div)
+            return py::module_::import("numpy").attr("true_divide")(other, to_numpy(self));
+        return py::reinterpret_borrow<py::object>(Py_NotImplemented);
+    }
+    if (op == BinOp::Sub && kind == Scalar::Bool)
         throw TensorError("Subtraction, the `-` operator, with a bool tensor is not supported. If you are trying to "
                           "invert a mask, use the `~` or `logical_not()` operator instead.");
     switch (op) {
@@ -83,14 +128,6 @@ py::object binary_operation(const Tensor &self, const py::object &other, BinOp o
     case BinOp::Div: return py::cast(reverse ? self.scalar_div(s) : self.div_scalar(s));
     }
     return py::none();
-}
-
-// Logical values as a numpy array of the tensor's shape (a copy).
-py::array_t<float> to_numpy(const Tensor &t) {
-    std::vector<py::ssize_t> shape(t.shape.begin(), t.shape.end());
-    py::array_t<float> a(shape);
-    t.copy_to_host(a.mutable_data());
-    return a;
 }
 
 Tensor from_numpy(py::array_t<float, py::array::c_style | py::array::forcecast> arr, const std::string &device) {

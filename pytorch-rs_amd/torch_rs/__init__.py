@@ -340,6 +340,7 @@ Tensor.matmul = _matmul_method
 Tensor.__array__ = _array
 Tensor.__repr__ = _repr
 Tensor.__len__ = _len
+Tensor.__array_priority__ = 1000.0  # numpy operands defer to the tensor's reflected ops (src/python.rs:3465)
 Tensor.__bool__ = _bool
 Tensor.multiply = Tensor.mul
 

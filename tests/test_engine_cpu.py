@@ -294,6 +294,28 @@ def test_host_tensors_do_not_compute():
     assert np.asarray(x).dtype == np.float32
 
 
+def test_scalar_operands_are_parsed_as_the_reference_does():
+    # parse_arithmetic_scalar (src/python.rs:10070-10184) and binary_operation
+    # (:4067-4133).  Host tensors stop at the device check once parsing passed.
+    x = torch_rs.zeros(2)
+    with pytest.raises(RuntimeError, match="^Subtraction, the `-` operator, with a bool tensor is not supported"):
+        x - True
+    with pytest.raises(RuntimeError, match="device tensors only"):
+        x - np.bool_(True)  # a NumPy bool is a number, not a bool operand
+    for big in (2 ** 70, -(2 ** 64)):
+        with pytest.raises(OverflowError, match="^Python integer is outside the supported scalar range$"):
+            x + big
+    with pytest.raises(RuntimeError, match="device tensors only"):
+        x + 2 ** 63  # fits u64
+    with pytest.raises(RuntimeError, match="device tensors only"):
+        np.float32(2) / x  # __array_priority__: NumPy defers to Tensor.__rtruediv__
+    wide = np.uint64(2 ** 63 + 5)
+    r = wide / x  # numpy_reflected_divide: NumPy divides by the tensor's values
+    assert isinstance(r, np.ndarray) and np.isinf(r).all()
+    with pytest.raises(TypeError, match="unsupported operand"):
+        x + "a"
+
+
 def test_array_protocol_copies_and_refuses_views():
     x = torch_rs.tensor(np.arange(6, dtype=np.float32).reshape(2, 3))
     a = np.asarray(x)

@@ -460,3 +460,14 @@ def test_unbatched_dropout1d_identity_view_passes_gradients_through():
     assert x.grad.numpy().tolist() == [[1, -2, 3], [-4, 5, -6]]
     z = cuda(np.ones((1, 1, 1, 1, 2), np.float32))
     assert F.dropout3d(z, p=1.0, training=True).numpy().reshape(-1).tolist() == [0.0, 0.0]
+
+
+def test_scalar_operands_convert_to_f32_as_the_reference_does():
+    # into_arithmetic_f32 (src/python.rs:10258-10277): Python and NumPy numbers
+    # are rounded to f32 once, then the op rounds once.
+    x = cuda([1.0, -3.0])
+    assert (x + 2 ** 63).numpy().tolist() == [np.float32(2.0 ** 63) + np.float32(1), np.float32(2.0 ** 63) - 3]
+    assert (x * np.float64(0.1)).numpy().tolist() == (np.float32([1.0, -3.0]) * np.float32(0.1)).tolist()
+    assert (x - np.bool_(True)).numpy().tolist() == [0.0, -4.0]
+    assert (np.float32(2) / x).numpy().tolist() == (np.float32(2) / np.float32([1.0, -3.0])).tolist()
+    assert (x + np.int64(-7)).numpy().tolist() == [-6.0, -10.0]
