@@ -218,6 +218,8 @@ int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const t
  *     const <hex f32 bits>     -- scalar constant
  *     add|sub|mul|div %a %b    -- binary32 op, one rounding
  *     exp|relu|neg %a          -- unary op with the reference semantics
+ *     relub %x %g              -- relu's VJP: g where x is NaN or > 0, else +0
+ *                                 (relu_backward_value, src/tensor.rs:4422-4432)
  *     out %a                   -- the (single) output
  * Each instruction rounds exactly as the eager op it mirrors, so a fused
  * chain is bit-identical to the eager chain except through exp. */

@@ -422,6 +422,7 @@ const char *node_name(Node n) {
     case Node::SqueezeDimension: return "SqueezeBackward1";
     case Node::SqueezeDimensions: return "SqueezeBackward2";
     case Node::Unsqueeze: return "UnsqueezeBackward0";
+    case Node::Fused: return "FusedBackward0";
     }
     return "UnknownBackward";
 }
@@ -1209,6 +1210,13 @@ void validate(const GradFn &fn) {
     case GradKind::MaskApply:
         if (!fn.mask) throw TensorError(kGraphFreed);
         break;
+    case GradKind::Fused:
+        for (size_t k = 0; k < fn.inputs.size(); k++) {
+            if (!fn.inputs[k].autograd || fn.fused[k].program == 0) continue;
+            for (int a : fn.fused[k].args)
+                if (a >= 0 && !fn.inputs[a].values) throw TensorError(kGraphFreed);
+        }
+        break;
     default:
         break;
     }
@@ -1227,6 +1235,9 @@ void consume(GradFn &fn) {
     case GradKind::Relu: fn.inputs[0].values.reset(); break;
     case GradKind::Exp: fn.output.values.reset(); break;
     case GradKind::MaskApply: fn.mask.reset(); break;
+    case GradKind::Fused:
+        for (auto &in : fn.inputs) in.values.reset();
+        break;
     default: break;
     }
 }
@@ -1285,6 +1296,39 @@ void apply_grad_fn(const GradFn &fn, Grad up, Device dev, std::map<GradKey, Grad
         const trs_layout lg = abi_layout_of(in.shape, layout::contiguous_strides(in.shape), 0);
         if (in.numel) check(trs_binary_f32(TRS_MUL, up.st->dptr, &lg, fn.output.values->dptr, &lo, g.st->dptr, &lg));
         add_gradient(grads, in.autograd, in.output_nr, std::move(g));
+        return;
+    }
+    case GradKind::Fused: {  // per input: its gradient program over the output shape, then unbroadcast
+        const Dims ostr = layout::contiguous_strides(up.shape);
+        const Tensor upt = make_tensor(up.st, up.shape, ostr, 0);
+        for (size_t k = 0; k < fn.inputs.size(); k++) {
+            const SavedTensor &in = fn.inputs[k];
+            const FusedVjp &vjp = fn.fused[k];
+            if (!in.autograd || vjp.program == 0) continue;
+            std::vector<Tensor> args;
+            for (int a : vjp.args) {
+                if (a < 0) {
+                    args.push_back(upt);
+                } else {
+                    const SavedTensor &sv = fn.inputs[a];
+                    args.push_back(make_tensor(sv.values, sv.shape, sv.strides, sv.offset));
+                }
+            }
+            FusedProgram prog;
+            prog.id = vjp.program;
+            prog.nin = (int)args.size();
+            Tensor full = prog.launch(args, up.shape, ostr);
+            if (in.shape == up.shape) {
+                add_gradient(grads, in.autograd, in.output_nr, Grad{full.storage, up.shape});
+                continue;
+            }
+            // A broadcast input: the reference's accumulation (from +0.0 in
+            // output row-major order), as the eager VJPs reduce.
+            Grad g = new_grad(dev, in.shape);
+            const trs_layout lin = abi_layout_of(in.shape, layout::contiguous_strides(in.shape), 0);
+            check(trs_reduce_to_shape_f32(full.storage->dptr, &lup, &lin, g.st->dptr));
+            add_gradient(grads, in.autograd, in.output_nr, std::move(g));
+        }
         return;
     }
     case GradKind::MaskApply: {  // (up * scale) * mask: the reverse of mul then mul_scalar
@@ -1553,6 +1597,27 @@ Tensor FusedProgram::launch(const std::vector<Tensor> &inputs, const Dims &out_s
     }
     const trs_layout lo = out.abi_layout();
     check(trs_fusion_launch(id, nin, ptrs.data(), lays.data(), out.storage->dptr, &lo));
+    return out;
+}
+
+Tensor FusedProgram::launch_with_grad(const std::vector<Tensor> &inputs, const Dims &out_shape,
+                                      const Dims &out_strides, const std::vector<FusedVjp> &vjps) const {
+    if (vjps.size() != inputs.size())
+        throw TensorError("fused gradient programs: expected " + std::to_string(inputs.size()) + ", got " +
+                          std::to_string(vjps.size()));
+    for (const auto &v : vjps)
+        for (int a : v.args)
+            if (a < -1 || a >= (int)inputs.size()) throw TensorError("fused gradient program argument out of range");
+    Tensor out = launch(inputs, out_shape, out_strides);
+    bool any = false;
+    for (size_t k = 0; k < inputs.size(); k++) any = any || (vjps[k].program != 0 && inputs[k].requires_grad());
+    if (!any || !is_grad_enabled()) return out;
+    auto fn = std::make_unique<GradFn>();
+    fn->kind = GradKind::Fused;
+    fn->node = Node::Fused;
+    for (const auto &t : inputs) fn->inputs.push_back(save(t, true));
+    fn->fused = vjps;
+    attach(out, std::move(fn));
     return out;
 }
 

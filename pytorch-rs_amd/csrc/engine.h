@@ -82,7 +82,7 @@ using MetaPtr = std::shared_ptr<AutogradMeta>;
 enum class Node {
     Add, Alias, Clone, Multiply, Negate, Permute, Relu, ReflectedSubtract, Subtract, Sum, MatrixTranspose,
     Transpose, View, Select, Exp, Mm, Bmm, AddTensor, SubTensor, Squeeze, SqueezeDimension, SqueezeDimensions,
-    Unsqueeze
+    Unsqueeze, Fused
 };
 const char *node_name(Node n);
 
@@ -97,7 +97,15 @@ struct SavedTensor {
 
 enum class GradKind {
     Multiply, MultiplyScalar, Negate, Relu, Sum, Identity, Permute, Index, AddTensor, SubTensor, Matmul, Exp,
-    MaskApply, Transfer
+    MaskApply, Transfer, Fused
+};
+
+// One input's gradient program of a fused node: a compiled pointwise
+// program whose arguments are saved forward inputs (index into
+// GradFn::inputs) or the upstream gradient (-1); program 0 = no gradient.
+struct FusedVjp {
+    uint64_t program = 0;
+    std::vector<int> args;
 };
 
 // One byte per element in HBM (a dropout keep-mask).
@@ -122,6 +130,7 @@ struct GradFn {
     Dims out_shape;       // output shape of the recorded op
     SavedTensor output;   // exp: its own output (values saved)
     BytePtr mask;         // mask-apply: the keep-mask
+    std::vector<FusedVjp> fused;  // fused: per-input gradient programs
 };
 
 struct AutogradMeta {
@@ -227,6 +236,10 @@ struct FusedProgram {
     int nin = 0;
     static FusedProgram compile(const std::string &ir, int nin);
     Tensor launch(const std::vector<Tensor> &inputs, const Dims &out_shape, const Dims &out_strides) const;
+    // The forward launch recorded as one graph node whose backward runs the
+    // per-input gradient programs `vjps` (one per input, in order).
+    Tensor launch_with_grad(const std::vector<Tensor> &inputs, const Dims &out_shape, const Dims &out_strides,
+                            const std::vector<FusedVjp> &vjps) const;
 };
 
 }  // namespace trs_engine

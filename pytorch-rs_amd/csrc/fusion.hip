@@ -108,7 +108,7 @@ int generate(const std::string &ir, Program *prog) {
             ins.bits = (uint32_t)v;
             code.push_back(ins);
             defined++;
-        } else if (op == "add" || op == "sub" || op == "mul" || op == "div") {
+        } else if (op == "add" || op == "sub" || op == "mul" || op == "div" || op == "relub") {
             if (toks.size() != 2) return set_error(TRS_E_FUSION, "line %d: '%s' takes two values", lineno, op.c_str());
             for (auto &tk : toks) {
                 int v;
@@ -156,6 +156,7 @@ int generate(const std::string &ir, Program *prog) {
         else if (c.op == "exp") s << "trs::exp_value(v" << c.args[0] << ")";
         else if (c.op == "relu") s << "trs::relu_value(v" << c.args[0] << ")";
         else if (c.op == "neg") s << "trs::negate_value(v" << c.args[0] << ")";
+        else if (c.op == "relub") s << "trs::relu_backward_value(v" << c.args[0] << ", v" << c.args[1] << ")";
         s << ";\n";
     }
     s << "    return v" << result << ";\n  }\n};\n";

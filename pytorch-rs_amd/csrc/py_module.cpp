@@ -299,7 +299,14 @@ PYBIND11_MODULE(_trs_native, m) {
         .def_static("compile", &FusedProgram::compile)
         .def_property_readonly("id", [](const FusedProgram &p) { return p.id; })
         .def_property_readonly("nin", [](const FusedProgram &p) { return p.nin; })
-        .def("launch", &FusedProgram::launch);
+        .def("launch", &FusedProgram::launch)
+        .def("launch_with_grad",
+             [](const FusedProgram &p, const std::vector<Tensor> &inputs, const Dims &shape, const Dims &strides,
+                const std::vector<std::pair<uint64_t, std::vector<int>>> &vjps) {
+                 std::vector<FusedVjp> v;
+                 for (const auto &e : vjps) v.push_back(FusedVjp{e.first, e.second});
+                 return p.launch_with_grad(inputs, shape, strides, v);
+             });
 
     // The restated layout planner, exposed for the CPU parity tests.
     py::module_ L = m.def_submodule("layout", "output-layout planning restated from src/tensor.rs");

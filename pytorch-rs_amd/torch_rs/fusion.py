@@ -10,8 +10,19 @@ would produce: the tracer runs the same output-stride planner
 (elementwise_output_strides and friends, src/tensor.rs:4249-4312) op by op.
 
 The reference has no fusion (torch.jit.strict_fusion is a warning-only
-no-op, README.md:178); this component is new.  Calls whose inputs need
-gradients run ``fn`` eagerly instead, so autograd records as usual.
+no-op, README.md:178); this component is new.
+
+Calls whose inputs need gradients record the fused launch as one graph node
+(FusedBackward0).  Its backward is generated from the same IR by reverse
+mode: one fused program per input that needs a gradient, recomputing the
+forward values and applying, per element, exactly the roundings of the
+eager VJPs (up * other for mul, up * exp(x) for exp, relu' for relu, sign
+flips for neg and reflected sub; division records nothing, as in the
+reference).  Broadcast inputs are then reduced in the reference's order.
+That reproduces eager autograd bit for bit when every intermediate has the
+output's shape, no value feeds more than two gradient-carrying uses (two
+contributions add commutatively) and each input feeds exactly one; other
+programs run ``fn`` eagerly so autograd records op by op.
 """
 from __future__ import annotations
 
@@ -30,27 +41,28 @@ def _f32_bits(v) -> str:
 
 
 class _Trace:
-    """Instructions in definition order: ("in", i), ("const", bits), (op, a[, b])."""
+    """Instructions in definition order: ("in", i), ("const", bits), (op, a[, b]);
+    `shapes` holds the eager shape of every traced (non-constant) value."""
 
     def __init__(self):
         self.ins: list[tuple] = []
         self.consts: dict[str, int] = {}
+        self.shapes: dict[int, tuple] = {}
 
     def emit(self, *instr) -> int:
         self.ins.append(instr)
         return len(self.ins) - 1
 
     def const(self, v) -> int:
-        bits = _f32_bits(v)
+        return self.const_bits(_f32_bits(v))
+
+    def const_bits(self, bits: str) -> int:
         if bits not in self.consts:
             self.consts[bits] = self.emit("const", bits)
         return self.consts[bits]
 
-    def finish(self, out: int):
-        """IR text of the instructions `out` depends on, renumbered, and the
-        argument positions of the inputs it reads (dead code and unused
-        inputs are dropped, so they are neither loaded nor required to
-        broadcast to the output shape)."""
+    def live(self, out: int) -> set:
+        """The values `out` depends on."""
         live = set()
         stack = [out]
         while stack:
@@ -61,6 +73,14 @@ class _Trace:
             ins = self.ins[v]
             if ins[0] not in ("in", "const"):
                 stack.extend(ins[1:])
+        return live
+
+    def finish(self, out: int):
+        """IR text of the instructions `out` depends on, renumbered, and the
+        argument positions of the inputs it reads (dead code and unused
+        inputs are dropped, so they are neither loaded nor required to
+        broadcast to the output shape)."""
+        live = self.live(out)
         new_id, lines, used_inputs = {}, [], []
         for v, ins in enumerate(self.ins):
             if v not in live:
@@ -92,6 +112,7 @@ class _Proxy:
 
     def __init__(self, tr, vid, shape, strides):
         self.tr, self.vid, self.shape, self.strides = tr, vid, tuple(shape), tuple(strides)
+        tr.shapes[vid] = self.shape
 
     def _numel(self):
         n = 1
@@ -149,6 +170,97 @@ class _Proxy:
         return self._unary("relu")
 
 
+_NO_GRAD = "no-grad"
+
+
+def _gradient_programs(tr, out, requires, out_shape):
+    """Backward IR for each input of a traced program, or None when the
+    program needs the eager path for bit-exact gradients, or _NO_GRAD when
+    the output records nothing (every path to it goes through a division).
+
+    `requires[i]`: input i requires grad.  Returns {input position: (IR text,
+    argument list)} where an argument is an input position or -1 for the
+    upstream gradient."""
+    ins = tr.ins
+    live = sorted(tr.live(out))
+    rg = {}
+    for v in live:
+        op = ins[v][0]
+        if op == "in":
+            rg[v] = bool(requires[ins[v][1]])
+        elif op in ("const", "div"):
+            rg[v] = False
+        elif op in ("add", "sub", "mul"):
+            rg[v] = rg[ins[v][1]] or rg[ins[v][2]]
+        else:  # exp, relu, neg
+            rg[v] = rg[ins[v][1]]
+    if not rg[out]:
+        return _NO_GRAD
+    uses: dict[int, int] = {}
+    for v in live:
+        if ins[v][0] in ("in", "const", "div") or not rg[v]:
+            continue
+        for a in ins[v][1:]:
+            if rg[a]:
+                uses[a] = uses.get(a, 0) + 1
+    for v in live:
+        if not rg[v]:
+            continue
+        if ins[v][0] == "in":
+            if uses.get(v, 0) > 1:
+                return None
+        elif tr.shapes.get(v) != tuple(out_shape) or uses.get(v, 0) > 2:
+            return None
+
+    n_in = len(requires)  # the upstream gradient's argument slot
+    programs = {}
+    for v in live:
+        if ins[v][0] != "in" or not rg[v] or uses.get(v, 0) == 0:
+            continue  # no gradient-carrying path (only through a division)
+        bt = _Trace()
+        fwd = {}
+        for u in live:  # the forward values, recomputed
+            i = ins[u]
+            if i[0] == "in":
+                fwd[u] = bt.emit("in", i[1])
+            elif i[0] == "const":
+                fwd[u] = bt.const_bits(i[1])
+            else:
+                fwd[u] = bt.emit(i[0], *(fwd[a] for a in i[1:]))
+        adj = {out: bt.emit("in", n_in)}  # the upstream gradient
+
+        def contribute(x, val):
+            if not rg[x]:
+                return
+            adj[x] = bt.emit("add", adj[x], val) if x in adj else val
+
+        for u in reversed(live):
+            if u not in adj or ins[u][0] in ("in", "const"):
+                continue
+            g, (op, *args) = adj[u], ins[u]
+            if op == "add":
+                contribute(args[0], g)
+                contribute(args[1], g)
+            elif op == "sub":
+                contribute(args[0], g)
+                if rg[args[1]]:
+                    contribute(args[1], bt.emit("neg", g))
+            elif op == "mul":
+                if rg[args[0]]:
+                    contribute(args[0], bt.emit("mul", g, fwd[args[1]]))
+                if rg[args[1]]:
+                    contribute(args[1], bt.emit("mul", g, fwd[args[0]]))
+            elif op == "exp":
+                contribute(args[0], bt.emit("mul", g, fwd[u]))
+            elif op == "relu":
+                contribute(args[0], bt.emit("relub", fwd[args[0]], g))
+            elif op == "neg":
+                contribute(args[0], bt.emit("neg", g))
+        ir, used = bt.finish(adj[v])
+        programs[ins[v][1]] = (ir, [-1 if i == n_in else i for i in used])
+    return programs
+
+
 class Fused:
     """A traced-and-compiled pointwise function (see the module docstring)."""
 
@@ -157,9 +269,7 @@ class Fused:
         self._cache: dict = {}
         functools.update_wrapper(self, fn)
 
-    def trace(self, *inputs):
-        """(IR text, output shape, output strides, positions of the inputs the
-        output reads) for inputs of these layouts."""
+    def _trace(self, inputs):
         tr = _Trace()
         proxies = []
         for i, t in enumerate(inputs):
@@ -169,6 +279,12 @@ class Fused:
             raise TypeError("a fused function must return a traced tensor expression")
         if tr.ins[out.vid][0] == "in":
             raise TypeError("a fused function must compute something from its inputs")
+        return tr, out
+
+    def trace(self, *inputs):
+        """(IR text, output shape, output strides, positions of the inputs the
+        output reads) for inputs of these layouts."""
+        tr, out = self._trace(inputs)
         ir, used = tr.finish(out.vid)
         return ir, out.shape, out.strides, used
 
@@ -181,13 +297,41 @@ class Fused:
             self._cache[key] = hit
         return hit
 
+    def grad_plan(self, *inputs):
+        """None (eager autograd), _NO_GRAD, or the per-input gradient programs
+        as (compiled program, argument positions among the forward's inputs)."""
+        requires = tuple(bool(t.requires_grad) for t in inputs)
+        key = (tuple((t.shape, t.stride()) for t in inputs), requires)
+        if key in self._cache:
+            return self._cache[key]
+        tr, out = self._trace(inputs)
+        plan = _gradient_programs(tr, out.vid, requires, out.shape)
+        if isinstance(plan, dict):
+            _, _, _, used, _ = self.program(*inputs)
+            pos = {orig: p for p, orig in enumerate(used)}
+            vjps = []
+            for orig in used:
+                if orig in plan:
+                    ir, args = plan[orig]
+                    vjps.append((_C.FusedProgram.compile(ir, len(args)).id, [-1 if a < 0 else pos[a] for a in args]))
+                else:
+                    vjps.append((0, []))
+            plan = vjps
+        self._cache[key] = plan
+        return plan
+
     def __call__(self, *inputs):
         if not inputs or not all(isinstance(t, _C.Tensor) for t in inputs):
             raise TypeError("fused functions take tensors only (bind scalars in the function body)")
-        if _C.is_grad_enabled() and any(t.requires_grad for t in inputs):
-            return self.fn(*inputs)
         prog, shape, strides, used, _ = self.program(*inputs)
-        return prog.launch([inputs[i] for i in used], shape, strides)
+        args = [inputs[i] for i in used]
+        if _C.is_grad_enabled() and any(t.requires_grad for t in inputs):
+            plan = self.grad_plan(*inputs)
+            if plan is None:
+                return self.fn(*inputs)
+            if plan != _NO_GRAD:
+                return prog.launch_with_grad(args, shape, strides, plan)
+        return prog.launch(args, shape, strides)
 
 
 def fuse(fn):

@@ -241,3 +241,83 @@ def test_program_loaded_from_the_disk_cache_runs_bit_exact(tmp_path):
 
     assert child("compile") == (0, 1)
     assert child("launch") == (1, 1)
+
+
+def _random_program_with_exp(rng, nin):
+    """_random_program's ops plus exp of a damped value (x * 0.25, then exp)."""
+    prog = []
+    nvals = nin
+    for _ in range(int(rng.integers(2, 9))):
+        a = int(rng.integers(0, nvals))
+        if rng.random() < 0.2:
+            prog.append(("smul", a, 0.25))
+            prog.append(("exp", nvals))
+            nvals += 2
+            continue
+        one = _random_program(np.random.default_rng(int(rng.integers(0, 1 << 30))), nvals)[:1]
+        op = one[0][0]
+        if op in ("add", "sub", "mul", "div"):
+            prog.append((op, a, int(rng.integers(0, nvals))))
+        elif op in ("sadd", "ssub", "smul", "rsub"):
+            prog.append((op, a, one[0][2]))
+        else:
+            prog.append((op, a))
+        nvals += 1
+    return prog
+
+
+def test_fused_backward_equals_eager_autograd_bit_for_bit():
+    """Random programs (add/sub/mul/div, scalar ops, relu, neg, exp) over
+    broadcast, transposed and strided operands, with random subsets of the
+    inputs requiring grad: the fused node's gradients equal eager autograd's
+    bit for bit, its output equals the eager output, and inputs with no
+    gradient path stay without a gradient."""
+    import torch_rs
+    rng = np.random.default_rng(91)
+    fused_nodes = 0
+    for case in range(40):
+        rank = int(rng.integers(1, 4))
+        oshape = [int(rng.integers(1, 40)) for _ in range(rank)]
+        nin = int(rng.integers(1, 5))
+        base = [_random_operand(rng, oshape) for _ in range(nin)]
+        base[0] = torch_rs.tensor(rng.standard_normal(int(np.prod(oshape))).astype(np.float32).reshape(oshape),
+                                  device="cuda")
+        requires = [bool(rng.random() < 0.7) for _ in range(nin)]
+        requires[int(rng.integers(0, nin))] = True
+        prog = _random_program_with_exp(rng, nin)
+        fn = lambda *xs, prog=prog: _eval(prog, xs)
+        w = torch_rs.tensor(rng.standard_normal(int(np.prod(oshape))).astype(np.float32).reshape(oshape),
+                            device="cuda")
+
+        def leaves():
+            return [b.detach().with_requires_grad(r) for b, r in zip(base, requires)]
+
+        le, lf = leaves(), leaves()
+        out_e = fn(*le)
+        out_f = torch_rs.fuse(fn)(*lf)
+        assert_bitwise_equal(out_f.numpy().ravel(), out_e.numpy().ravel())
+        assert out_f.requires_grad == out_e.requires_grad, (case, prog)
+        if not out_e.requires_grad:
+            continue
+        fused_nodes += out_f.grad_fn is not None and out_f.grad_fn.name() == "FusedBackward0"
+        if tuple(out_e.shape) != tuple(oshape):
+            continue  # w would not match; the output is a broadcast of fewer dims
+        (out_e * w).sum().backward()
+        (out_f * w).sum().backward()
+        for i in range(nin):
+            ge, gf = le[i].grad, lf[i].grad
+            assert (ge is None) == (gf is None), (case, i, prog)
+            if ge is not None:
+                assert ge.shape == gf.shape, (case, i)
+                assert_bitwise_equal(gf.numpy().ravel(), ge.numpy().ravel())
+    assert fused_nodes >= 12, fused_nodes  # many programs take the fused backward
+
+
+def _eval(prog, xs):
+    vals = list(xs)
+    for ins in prog:
+        if ins[0] == "exp":
+            vals.append(vals[ins[1]].exp())
+        else:
+            vals.append(_run_program([ins], vals))
+    return vals[-1]
