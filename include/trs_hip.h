@@ -220,13 +220,22 @@ int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const t
  *     exp|relu|neg %a          -- unary op with the reference semantics
  *     relub %x %g              -- relu's VJP: g where x is NaN or > 0, else +0
  *                                 (relu_backward_value, src/tensor.rs:4422-4432)
- *     out %a                   -- the (single) output
+ *     out %a                   -- an output; the `out` lines end the program,
+ *                                 at most 8 of them, in output order
  * Each instruction rounds exactly as the eager op it mirrors, so a fused
  * chain is bit-identical to the eager chain except through exp. */
 int trs_fusion_compile(const char *ir, size_t ir_len, uint64_t *kernel_id);
-/* Launch a compiled program: inputs broadcast to lo's shape. */
+/* Launch a compiled one-output program: inputs broadcast to lo's shape. */
 int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *inputs,
                       const trs_layout *in_layouts, float *out, const trs_layout *lo);
+/* Launch a program with n_outputs outputs in one kernel; every output has the
+ * layout lo.  Outputs share no memory with each other; an output may share
+ * memory with an input only as the very same view. */
+int trs_fusion_launch_multi(uint64_t kernel_id, int n_inputs, const void *const *inputs,
+                            const trs_layout *in_layouts, int n_outputs, float *const *outputs,
+                            const trs_layout *lo);
+/* Number of outputs of a compiled program. */
+int trs_fusion_outputs(uint64_t kernel_id, int *n_outputs);
 /* Generated HIP C++ source of a compiled program (for inspection). */
 int trs_fusion_source(uint64_t kernel_id, char *buf, size_t buf_len, size_t *needed);
 /* Milliseconds spent producing this program's code object: the hipRTC

@@ -1211,11 +1211,8 @@ void validate(const GradFn &fn) {
         if (!fn.mask) throw TensorError(kGraphFreed);
         break;
     case GradKind::Fused:
-        for (size_t k = 0; k < fn.inputs.size(); k++) {
-            if (!fn.inputs[k].autograd || fn.fused[k].program == 0) continue;
-            for (int a : fn.fused[k].args)
-                if (a >= 0 && !fn.inputs[a].values) throw TensorError(kGraphFreed);
-        }
+        for (int a : fn.fused.args)
+            if (a >= 0 && !fn.inputs[a].values) throw TensorError(kGraphFreed);
         break;
     default:
         break;
@@ -1298,35 +1295,41 @@ void apply_grad_fn(const GradFn &fn, Grad up, Device dev, std::map<GradKey, Grad
         add_gradient(grads, in.autograd, in.output_nr, std::move(g));
         return;
     }
-    case GradKind::Fused: {  // per input: its gradient program over the output shape, then unbroadcast
-        const Dims ostr = layout::contiguous_strides(up.shape);
-        const Tensor upt = make_tensor(up.st, up.shape, ostr, 0);
-        for (size_t k = 0; k < fn.inputs.size(); k++) {
-            const SavedTensor &in = fn.inputs[k];
-            const FusedVjp &vjp = fn.fused[k];
-            if (!in.autograd || vjp.program == 0) continue;
-            std::vector<Tensor> args;
-            for (int a : vjp.args) {
-                if (a < 0) {
-                    args.push_back(upt);
-                } else {
-                    const SavedTensor &sv = fn.inputs[a];
-                    args.push_back(make_tensor(sv.values, sv.shape, sv.strides, sv.offset));
-                }
+    case GradKind::Fused: {  // every input gradient in one kernel over the output shape, then unbroadcast
+        const FusedBackward &bwd = fn.fused;
+        std::vector<const void *> ptrs;
+        std::vector<trs_layout> lays;
+        for (int a : bwd.args) {
+            if (a < 0) {
+                ptrs.push_back(up.st->dptr);
+                lays.push_back(lup);
+            } else {
+                const SavedTensor &sv = fn.inputs[a];
+                ptrs.push_back(sv.values->dptr);
+                lays.push_back(saved_layout(sv));
             }
-            FusedProgram prog;
-            prog.id = vjp.program;
-            prog.nin = (int)args.size();
-            Tensor full = prog.launch(args, up.shape, ostr);
+        }
+        std::vector<std::shared_ptr<Storage>> full;
+        std::vector<float *> outs;
+        for (size_t o = 0; o < bwd.targets.size(); o++) {
+            full.push_back(new_grad(dev, up.shape).st);
+            outs.push_back(full.back()->dptr);
+        }
+        if (layout::numel_of(up.shape) > 0)
+            check(trs_fusion_launch_multi(bwd.program, (int)ptrs.size(), ptrs.data(), lays.data(), (int)outs.size(),
+                                          outs.data(), &lup));
+        for (size_t o = 0; o < bwd.targets.size(); o++) {
+            const SavedTensor &in = fn.inputs[bwd.targets[o]];
+            if (!in.autograd) continue;
             if (in.shape == up.shape) {
-                add_gradient(grads, in.autograd, in.output_nr, Grad{full.storage, up.shape});
+                add_gradient(grads, in.autograd, in.output_nr, Grad{full[o], up.shape});
                 continue;
             }
             // A broadcast input: the reference's accumulation (from +0.0 in
             // output row-major order), as the eager VJPs reduce.
             Grad g = new_grad(dev, in.shape);
             const trs_layout lin = abi_layout_of(in.shape, layout::contiguous_strides(in.shape), 0);
-            check(trs_reduce_to_shape_f32(full.storage->dptr, &lup, &lin, g.st->dptr));
+            check(trs_reduce_to_shape_f32(full[o]->dptr, &lup, &lin, g.st->dptr));
             add_gradient(grads, in.autograd, in.output_nr, std::move(g));
         }
         return;
@@ -1601,22 +1604,28 @@ Tensor FusedProgram::launch(const std::vector<Tensor> &inputs, const Dims &out_s
 }
 
 Tensor FusedProgram::launch_with_grad(const std::vector<Tensor> &inputs, const Dims &out_shape,
-                                      const Dims &out_strides, const std::vector<FusedVjp> &vjps) const {
-    if (vjps.size() != inputs.size())
-        throw TensorError("fused gradient programs: expected " + std::to_string(inputs.size()) + ", got " +
-                          std::to_string(vjps.size()));
-    for (const auto &v : vjps)
-        for (int a : v.args)
-            if (a < -1 || a >= (int)inputs.size()) throw TensorError("fused gradient program argument out of range");
+                                      const Dims &out_strides, const FusedBackward &bwd) const {
+    for (int a : bwd.args)
+        if (a < -1 || a >= (int)inputs.size()) throw TensorError("fused gradient program argument out of range");
+    std::vector<bool> seen(inputs.size(), false);
+    for (int t : bwd.targets) {
+        if (t < 0 || t >= (int)inputs.size() || seen[t]) throw TensorError("fused gradient program target invalid");
+        seen[t] = true;
+    }
+    int nout = 0;
+    check(trs_fusion_outputs(bwd.program, &nout));
+    if (nout != (int)bwd.targets.size())
+        throw TensorError("fused gradient program has " + std::to_string(nout) + " outputs for " +
+                          std::to_string(bwd.targets.size()) + " targets");
     Tensor out = launch(inputs, out_shape, out_strides);
     bool any = false;
-    for (size_t k = 0; k < inputs.size(); k++) any = any || (vjps[k].program != 0 && inputs[k].requires_grad());
+    for (int t : bwd.targets) any = any || inputs[t].requires_grad();
     if (!any || !is_grad_enabled()) return out;
     auto fn = std::make_unique<GradFn>();
     fn->kind = GradKind::Fused;
     fn->node = Node::Fused;
     for (const auto &t : inputs) fn->inputs.push_back(save(t, true));
-    fn->fused = vjps;
+    fn->fused = bwd;
     attach(out, std::move(fn));
     return out;
 }

@@ -100,12 +100,14 @@ enum class GradKind {
     MaskApply, Transfer, Fused
 };
 
-// One input's gradient program of a fused node: a compiled pointwise
-// program whose arguments are saved forward inputs (index into
-// GradFn::inputs) or the upstream gradient (-1); program 0 = no gradient.
-struct FusedVjp {
+// The backward of a fused node: one compiled pointwise program whose
+// arguments are saved forward inputs (index into GradFn::inputs) or the
+// upstream gradient (-1), and whose output o, over the node's output shape,
+// is the gradient of input targets[o].
+struct FusedBackward {
     uint64_t program = 0;
     std::vector<int> args;
+    std::vector<int> targets;
 };
 
 // One byte per element in HBM (a dropout keep-mask).
@@ -130,7 +132,7 @@ struct GradFn {
     Dims out_shape;       // output shape of the recorded op
     SavedTensor output;   // exp: its own output (values saved)
     BytePtr mask;         // mask-apply: the keep-mask
-    std::vector<FusedVjp> fused;  // fused: per-input gradient programs
+    FusedBackward fused;  // fused: the gradient program
 };
 
 struct AutogradMeta {
@@ -237,9 +239,9 @@ struct FusedProgram {
     static FusedProgram compile(const std::string &ir, int nin);
     Tensor launch(const std::vector<Tensor> &inputs, const Dims &out_shape, const Dims &out_strides) const;
     // The forward launch recorded as one graph node whose backward runs the
-    // per-input gradient programs `vjps` (one per input, in order).
+    // gradient program `bwd` (all input gradients in one kernel).
     Tensor launch_with_grad(const std::vector<Tensor> &inputs, const Dims &out_shape, const Dims &out_strides,
-                            const std::vector<FusedVjp> &vjps) const;
+                            const FusedBackward &bwd) const;
 };
 
 }  // namespace trs_engine

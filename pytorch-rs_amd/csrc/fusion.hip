@@ -44,6 +44,7 @@ struct Program {
     std::string ir;
     std::string source;
     int nin = 0;
+    int nout = 1;
     unsigned u8mask = 0;
     double compile_ms = 0.0;
     bool from_disk = false;
@@ -76,7 +77,8 @@ int generate(const std::string &ir, Program *prog) {
     std::istringstream in(ir);
     std::string line;
     std::vector<Instr> code;
-    int defined = 0, nin = 0, result = -1, lineno = 0;
+    std::vector<int> results;
+    int defined = 0, nin = 0, lineno = 0;
     unsigned u8mask = 0;
     while (std::getline(in, line)) {
         lineno++;
@@ -85,7 +87,8 @@ int generate(const std::string &ir, Program *prog) {
         std::istringstream ls(line);
         std::string op;
         if (!(ls >> op)) continue;
-        if (result >= 0) return set_error(TRS_E_FUSION, "line %d: instruction after 'out'", lineno);
+        if (!results.empty() && op != "out")
+            return set_error(TRS_E_FUSION, "line %d: instruction after 'out'", lineno);
         Instr ins;
         ins.op = op;
         std::vector<std::string> toks;
@@ -129,18 +132,26 @@ int generate(const std::string &ir, Program *prog) {
             int v;
             if (toks.size() != 1 || parse_value(toks[0], defined, &v))
                 return set_error(TRS_E_FUSION, "line %d: 'out' takes one value", lineno);
-            result = v;
+            if ((int)results.size() >= kMaxOut)
+                return set_error(TRS_E_FUSION, "line %d: more than %d outputs", lineno, kMaxOut);
+            results.push_back(v);
         } else {
             return set_error(TRS_E_FUSION, "line %d: unknown instruction '%s'", lineno, op.c_str());
         }
     }
-    if (result < 0) return set_error(TRS_E_FUSION, "program has no 'out'");
+    if (results.empty()) return set_error(TRS_E_FUSION, "program has no 'out'");
     if (nin == 0) return set_error(TRS_E_FUSION, "program has no inputs");
+    const int nout = (int)results.size();
 
     std::ostringstream s;
     s << "// generated by libtrs_hip fusion compiler\n";
     s << "struct TrsFused {\n  static constexpr int NIN = " << nin << ";\n";
-    s << "  __device__ __forceinline__ float operator()(const float *a) const {\n";
+    if (nout == 1) {
+        s << "  __device__ __forceinline__ float operator()(const float *a) const {\n";
+    } else {
+        s << "  static constexpr int NOUT = " << nout << ";\n";
+        s << "  __device__ __forceinline__ void operator()(const float *a, float *r) const {\n";
+    }
     for (size_t i = 0; i < code.size(); i++) {
         const Instr &c = code[i];
         s << "    const float v" << i << " = ";
@@ -159,7 +170,12 @@ int generate(const std::string &ir, Program *prog) {
         else if (c.op == "relub") s << "trs::relu_backward_value(v" << c.args[0] << ", v" << c.args[1] << ")";
         s << ";\n";
     }
-    s << "    return v" << result << ";\n  }\n};\n";
+    if (nout == 1) {
+        s << "    return v" << results[0] << ";\n";
+    } else {
+        for (int o = 0; o < nout; o++) s << "    r[" << o << "] = v" << results[o] << ";\n";
+    }
+    s << "  }\n};\n";
     const std::string mask = std::to_string(u8mask) + "u";
     auto wrap = [&](const char *name, const std::string &body, const char *lanes = "256") {
         s << "extern \"C\" __global__ void __launch_bounds__(" << lanes << ") " << name
@@ -178,6 +194,7 @@ int generate(const std::string &ir, Program *prog) {
         wrap(sc.c_str(), "trs::pw_tiled_body<TrsFused, " + mask + ", false, " + std::to_string(nt) + ">");
     }
     prog->nin = nin;
+    prog->nout = nout;
     prog->u8mask = u8mask;
     prog->source = s.str();
     return TRS_OK;
@@ -371,11 +388,19 @@ int trs_fusion_compile(const char *ir, size_t ir_len, uint64_t *kernel_id) {
 
 int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *inputs, const trs_layout *in_layouts,
                       float *out, const trs_layout *lo) {
+    return trs_fusion_launch_multi(kernel_id, n_inputs, inputs, in_layouts, 1, &out, lo);
+}
+
+int trs_fusion_launch_multi(uint64_t kernel_id, int n_inputs, const void *const *inputs,
+                            const trs_layout *in_layouts, int n_outputs, float *const *outputs,
+                            const trs_layout *lo) {
     Program *prog = lookup(kernel_id);
     if (!prog) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id %llu", (unsigned long long)kernel_id);
     if (n_inputs != prog->nin)
         return set_error(TRS_E_INVALID_ARGUMENT, "program takes %d inputs, got %d", prog->nin, n_inputs);
-    if (!inputs || !in_layouts) return set_error(TRS_E_INVALID_ARGUMENT, "null inputs");
+    if (n_outputs != prog->nout)
+        return set_error(TRS_E_INVALID_ARGUMENT, "program has %d outputs, got %d", prog->nout, n_outputs);
+    if (!inputs || !in_layouts || !outputs) return set_error(TRS_E_INVALID_ARGUMENT, "null inputs or outputs");
     DeviceState *dev = device_state();
     if (!dev) return TRS_E_NO_DEVICE;
     const trs_layout *ls[kMaxIn];
@@ -385,7 +410,7 @@ int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *input
         eb[i] = ((prog->u8mask >> i) & 1u) ? 1 : 4;
     }
     PwPlan pl;
-    int rc = plan_pointwise(lo, out, n_inputs, inputs, ls, eb, dev->cu_count, &pl);
+    int rc = plan_pointwise(lo, outputs[0], n_inputs, inputs, ls, eb, dev->cu_count, &pl, n_outputs, outputs + 1);
     if (rc) return rc;
     std::string name;
     switch (pl.variant) {
@@ -406,6 +431,13 @@ int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *input
     TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, (unsigned)pl.block, 1, 1, 0, dev->stream, args,
                                         nullptr),
                   "hipModuleLaunchKernel");
+    return TRS_OK;
+}
+
+int trs_fusion_outputs(uint64_t kernel_id, int *n_outputs) {
+    Program *prog = lookup(kernel_id);
+    if (!prog || !n_outputs) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id");
+    *n_outputs = prog->nout;
     return TRS_OK;
 }
 

@@ -41,6 +41,7 @@ namespace trs {
 
 constexpr int kMaxRank = 8;
 constexpr int kMaxIn = 8;
+constexpr int kMaxOut = 8;  // outputs of one program (all share one layout)
 constexpr int kRowChunk = 1024;  // columns per pw_rows tile (256 lanes x 4)
 constexpr int kTile = 64;        // pw_tiled tile edge
 // Largest grid a launch uses (256-lane blocks).  Launches are one-shot --
@@ -88,9 +89,12 @@ struct PwGeom {
 typedef float vf4 __attribute__((ext_vector_type(4)));
 typedef uint8_t vu8x4 __attribute__((ext_vector_type(4)));
 
+// Output 0 and the inputs; `more` holds outputs 1.. of a multi-output
+// program.  Every output has the output layout (same offset and strides).
 struct PwPtrs {
     float *out;
     const void *in[kMaxIn];
+    float *more[kMaxOut - 1];
 };
 
 // ---- element loads --------------------------------------------------------
@@ -139,6 +143,63 @@ __device__ __forceinline__ void static_for(Fn &&fn) {
     }
 }
 
+// ---- functor outputs --------------------------------------------------------
+// A functor computes one value (float operator()(const float *args)) or, when
+// it declares `static constexpr int NOUT` > 1, NOUT values
+// (void operator()(const float *args, float *results)).
+
+template <class F>
+constexpr int nout_of() {
+    if constexpr (requires { F::NOUT; }) {
+        return F::NOUT;
+    } else {
+        return 1;
+    }
+}
+
+template <class F>
+__device__ __forceinline__ void eval1(const F &f, const float *a, float *r) {
+    if constexpr (nout_of<F>() == 1) {
+        r[0] = f(a);
+    } else {
+        f(a, r);
+    }
+}
+
+// r[o][k]: output o of element k of a four-element group v[input][k].
+template <class F, int NI, int NO>
+__device__ __forceinline__ void eval4(const F &f, const float (&v)[NI][4], float (&r)[NO][4]) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float a[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) a[i] = v[i][k];
+        float o[NO];
+        eval1(f, a, o);
+#pragma unroll
+        for (int q = 0; q < NO; q++) r[q][k] = o[q];
+    }
+}
+
+template <int O>
+__device__ __forceinline__ float *out_base(const PwPtrs &p) {
+    if constexpr (O == 0) {
+        return p.out;
+    } else {
+        return p.more[O - 1];
+    }
+}
+
+template <int NO>
+__device__ __forceinline__ void store4(const PwPtrs &p, int64_t off, const float (&r)[NO][4]) {
+    static_for<NO>([&]<int O>() { st4(out_base<O>(p) + off, r[O]); });
+}
+
+template <int NO>
+__device__ __forceinline__ void store1(const PwPtrs &p, int64_t off, const float *o) {
+    static_for<NO>([&]<int O>() { out_base<O>(p)[off] = o[O]; });
+}
+
 // Offsets of output and inputs for a logical index tuple given by the first
 // `ndims` dims of the decomposition of `outer` (row-major over dims
 // [0, ndims)).  Uses 32-bit magic division when `outer` fits in 32 bits.
@@ -179,12 +240,12 @@ __device__ __forceinline__ void decode_outer(const PwGeom &g, int ndims, int64_t
 template <class F, unsigned U8MASK, bool VEC>
 __device__ __forceinline__ void pw_flat_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
+    constexpr int NOUT = nout_of<F>();
     const int64_t n = g.numel;
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
     bool unit[NIN > 0 ? NIN : 1];
     for (int i = 0; i < NIN; i++) unit[i] = g.istride[i][0] != 0;
-    float *out = p.out + g.ooff;
     int64_t tail_start = 0;
     if constexpr (VEC) {
         // One float4 group per lane.  The host sizes the grid to cover every
@@ -199,22 +260,18 @@ __device__ __forceinline__ void pw_flat_body(const F &f, const PwGeom &g, const 
             static_for<NIN>([&]<int I>() {
                 ld4<U8MASK, I>(p, g.ioff[I] + (unit[I] ? e : 0), unit[I], v[I], (g.streamed >> I) & 1u);
             });
-            float r[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                float a[NIN > 0 ? NIN : 1];
-#pragma unroll
-                for (int i = 0; i < NIN; i++) a[i] = v[i][k];
-                r[k] = f(a);
-            }
-            st4(out + e, r);
+            float r[NOUT][4];
+            eval4(f, v, r);
+            store4(p, g.ooff + e, r);
         }
         tail_start = groups << 2;
     }
     for (int64_t e = tail_start + tid; e < n; e += nthreads) {
         float a[NIN > 0 ? NIN : 1];
         static_for<NIN>([&]<int I>() { a[I] = ld1<U8MASK, I>(p, g.ioff[I] + (unit[I] ? e : 0)); });
-        out[e] = f(a);
+        float o[NOUT];
+        eval1(f, a, o);
+        store1<NOUT>(p, g.ooff + e, o);
     }
 }
 
@@ -237,29 +294,25 @@ __device__ __forceinline__ void ld4_stream(const PwPtrs &p, int64_t off, float *
 template <class F, unsigned U8MASK>
 __device__ __forceinline__ void pw_flat_contig_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
+    constexpr int NOUT = nout_of<F>();
     const int64_t n = g.numel;
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
-    float *out = p.out + g.ooff;
     const int64_t groups = n >> 2;
     for (int64_t gi = tid; gi < groups; gi += nthreads) {
         const int64_t e = gi << 2;
         float v[NIN > 0 ? NIN : 1][4];
         static_for<NIN>([&]<int I>() { ld4_stream<U8MASK, I>(p, g.ioff[I] + e, v[I]); });
-        float r[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float a[NIN > 0 ? NIN : 1];
-#pragma unroll
-            for (int i = 0; i < NIN; i++) a[i] = v[i][k];
-            r[k] = f(a);
-        }
-        st4(out + e, r);
+        float r[NOUT][4];
+        eval4(f, v, r);
+        store4(p, g.ooff + e, r);
     }
     for (int64_t e = (groups << 2) + tid; e < n; e += nthreads) {
         float a[NIN > 0 ? NIN : 1];
         static_for<NIN>([&]<int I>() { a[I] = ld1<U8MASK, I>(p, g.ioff[I] + e); });
-        out[e] = f(a);
+        float o[NOUT];
+        eval1(f, a, o);
+        store1<NOUT>(p, g.ooff + e, o);
     }
 }
 
@@ -270,6 +323,7 @@ __device__ __forceinline__ void pw_flat_contig_body(const F &f, const PwGeom &g,
 template <class F, unsigned U8MASK, bool VEC>
 __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
+    constexpr int NOUT = nout_of<F>();
     const int inner = g.rank - 1;
     const int64_t cols = g.size[inner];
     const int64_t ntiles = g.rows * g.chunks;
@@ -289,15 +343,9 @@ __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const 
                 static_for<NIN>([&]<int I>() {
                     ld4<U8MASK, I>(p, io[I] + (unit[I] ? c : 0), unit[I], v[I], (g.streamed >> I) & 1u);
                 });
-                float r[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    float a[NIN > 0 ? NIN : 1];
-#pragma unroll
-                    for (int i = 0; i < NIN; i++) a[i] = v[i][k];
-                    r[k] = f(a);
-                }
-                st4(p.out + oo + c, r);
+                float r[NOUT][4];
+                eval4(f, v, r);
+                store4(p, oo + c, r);
             }
         } else {
             for (int k = 0; k < 4; k++) {
@@ -307,7 +355,9 @@ __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const 
                     static_for<NIN>([&]<int I>() {
                         a[I] = ld1<U8MASK, I>(p, io[I] + (unit[I] ? c : 0));
                     });
-                    p.out[oo + c] = f(a);
+                    float o[NOUT];
+                    eval1(f, a, o);
+                    store1<NOUT>(p, oo + c, o);
                 }
             }
         }
@@ -325,6 +375,7 @@ __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const 
 template <class F, unsigned U8MASK, bool VEC, int NT>
 __device__ __forceinline__ void pw_tiled_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
+    constexpr int NOUT = nout_of<F>();
     __shared__ float lds[NT > 0 ? NT : 1][kTile][kTile + 1];
     const int xd = g.rank - 1;
     const int td = g.tdim;
@@ -408,19 +459,18 @@ __device__ __forceinline__ void pw_tiled_body(const F &f, const PwGeom &g, const
                         }
                     }
                 });
-                float r[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    float a[NIN > 0 ? NIN : 1];
-#pragma unroll
-                    for (int i = 0; i < NIN; i++) a[i] = v[i][k];
-                    r[k] = f(a);
-                }
+                float r[NOUT][4];
+                eval4(f, v, r);
                 if (full) {
-                    st4(p.out + ob, r);
+                    store4(p, ob, r);
                 } else {
-                    for (int k = 0; k < 4; k++)
-                        if (x + k < xs) p.out[ob + k] = r[k];
+                    for (int k = 0; k < 4; k++) {
+                        if (x + k < xs) {
+                            float o[NOUT];
+                            for (int q = 0; q < NOUT; q++) o[q] = r[q][k];
+                            store1<NOUT>(p, ob + k, o);
+                        }
+                    }
                 }
             }
         }
@@ -432,13 +482,16 @@ __device__ __forceinline__ void pw_tiled_body(const F &f, const PwGeom &g, const
 template <class F, unsigned U8MASK>
 __device__ __forceinline__ void pw_generic_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
+    constexpr int NOUT = nout_of<F>();
     const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < g.numel; e += nthreads) {
         int64_t oo, io[NIN > 0 ? NIN : 1];
         decode_outer<NIN>(g, g.rank, e, oo, io);
         float a[NIN > 0 ? NIN : 1];
         static_for<NIN>([&]<int I>() { a[I] = ld1<U8MASK, I>(p, io[I]); });
-        p.out[oo] = f(a);
+        float o[NOUT];
+        eval1(f, a, o);
+        store1<NOUT>(p, oo, o);
     }
 }
 

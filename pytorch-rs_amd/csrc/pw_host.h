@@ -45,13 +45,17 @@ inline FastDiv make_fast_div(uint32_t d) {
     return f;
 }
 
-// `elem_bytes[i]` is 4 for f32 inputs and 1 for u8 inputs.
+// `elem_bytes[i]` is 4 for f32 inputs and 1 for u8 inputs.  A program with
+// several outputs passes outputs 1.. in `more` (nout - 1 of them); they share
+// the output layout `lo`.
 inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void *const *bases,
                           const trs_layout *const *lins, const int *elem_bytes, int cu_count,
-                          PwPlan *plan) {
+                          PwPlan *plan, int nout = 1, float *const *more = nullptr) {
     int rc = check_layout(lo, "output");
     if (rc) return rc;
     if (nin > kMaxIn) return set_error(TRS_E_INVALID_ARGUMENT, "too many pointwise inputs (%d)", nin);
+    if (nout < 1 || nout > kMaxOut || (nout > 1 && more == nullptr))
+        return set_error(TRS_E_INVALID_ARGUMENT, "bad pointwise output count (%d)", nout);
     for (int i = 0; i < nin; i++) {
         rc = check_layout(lins[i], "input");
         if (rc) return rc;
@@ -74,6 +78,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
     std::memset(&g, 0, sizeof(g));
     plan->p.out = out;
     for (int i = 0; i < nin; i++) plan->p.in[i] = bases[i];
+    for (int o = 1; o < nout; o++) plan->p.more[o - 1] = more[o - 1];
 
     int64_t numel = layout_numel(lo);
     if (numel == 0) {
@@ -81,19 +86,27 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         return TRS_OK;
     }
     if (out == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "null output pointer");
+    for (int o = 1; o < nout; o++)
+        if (more[o - 1] == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "null output pointer %d", o);
     for (int i = 0; i < nin; i++)
         if (bases[i] == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "null input pointer %d", i);
-    // An input may share memory with the output only as the very same view
+    // An input may share memory with an output only as the very same view
     // (element-wise in place: every lane reads and writes its own elements);
-    // any other overlap would race across lanes.
-    {
-        const ByteRange ro = byte_range(out, lo, 4);
+    // any other overlap would race across lanes.  Outputs never share memory.
+    for (int o = 0; o < nout; o++) {
+        float *const base = o == 0 ? out : more[o - 1];
+        const ByteRange ro = byte_range(base, lo, 4);
         for (int i = 0; i < nin; i++) {
             if (layout_numel(lins[i]) == 0) continue;
             const ByteRange ri = byte_range(bases[i], lins[i], elem_bytes[i]);
             if (!ranges_overlap(ro, ri)) continue;
             if (elem_bytes[i] == 4 && ri.begin == ro.begin && same_view_shape(lins[i], lo)) continue;
-            return set_error(TRS_E_INVALID_ARGUMENT, "output overlaps input %d other than as the same view", i);
+            return set_error(TRS_E_INVALID_ARGUMENT, "output %d overlaps input %d other than as the same view", o,
+                             i);
+        }
+        for (int q = 0; q < o; q++) {
+            if (ranges_overlap(ro, byte_range(q == 0 ? out : more[q - 1], lo, 4)))
+                return set_error(TRS_E_INVALID_ARGUMENT, "outputs %d and %d overlap", q, o);
         }
     }
 
@@ -188,13 +201,18 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
     };
 
     const int inner = rank - 1;
+    auto outputs_aligned = [&]() {
+        bool ok = aligned(out, lo->offset, os, inner, 4);
+        for (int o = 1; o < nout; o++) ok = ok && aligned(more[o - 1], lo->offset, os, inner, 4);
+        return ok;
+    };
     bool unit_or_bcast = os[inner] == 1;
     for (int i = 0; i < nin; i++) unit_or_bcast &= is[i][inner] == 0 || is[i][inner] == 1;
     (void)cu_count;
     const int64_t want = kMaxGrid;
 
     if (unit_or_bcast) {
-        bool vec = aligned(out, lo->offset, os, inner, 4);
+        bool vec = outputs_aligned();
         for (int i = 0; i < nin; i++)
             if (is[i][inner] == 1) vec &= aligned(bases[i], g.ioff[i], is[i], inner, elem_bytes[i]);
         if (rank == 1) {
@@ -236,7 +254,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             plan->ntransposed = nt;
             g.tdim = tdim;
             g.transposed = tmask;
-            bool vec = aligned(out, lo->offset, os, inner, 4);
+            bool vec = outputs_aligned();
             for (int i = 0; i < nin; i++) {
                 if ((tmask >> i) & 1u) {
                     vec &= aligned(bases[i], g.ioff[i], is[i], tdim, elem_bytes[i]);

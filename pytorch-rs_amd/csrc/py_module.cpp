@@ -302,10 +302,8 @@ PYBIND11_MODULE(_trs_native, m) {
         .def("launch", &FusedProgram::launch)
         .def("launch_with_grad",
              [](const FusedProgram &p, const std::vector<Tensor> &inputs, const Dims &shape, const Dims &strides,
-                const std::vector<std::pair<uint64_t, std::vector<int>>> &vjps) {
-                 std::vector<FusedVjp> v;
-                 for (const auto &e : vjps) v.push_back(FusedVjp{e.first, e.second});
-                 return p.launch_with_grad(inputs, shape, strides, v);
+                uint64_t program, const std::vector<int> &args, const std::vector<int> &targets) {
+                 return p.launch_with_grad(inputs, shape, strides, FusedBackward{program, args, targets});
              });
 
     // The restated layout planner, exposed for the CPU parity tests.

@@ -14,15 +14,16 @@ no-op, README.md:178); this component is new.
 
 Calls whose inputs need gradients record the fused launch as one graph node
 (FusedBackward0).  Its backward is generated from the same IR by reverse
-mode: one fused program per input that needs a gradient, recomputing the
-forward values and applying, per element, exactly the roundings of the
-eager VJPs (up * other for mul, up * exp(x) for exp, relu' for relu, sign
-flips for neg and reflected sub; division records nothing, as in the
-reference).  Broadcast inputs are then reduced in the reference's order.
-That reproduces eager autograd bit for bit when every intermediate has the
-output's shape, no value feeds more than two gradient-carrying uses (two
-contributions add commutatively) and each input feeds exactly one; other
-programs run ``fn`` eagerly so autograd records op by op.
+mode: ONE fused program with an output per input that needs a gradient,
+recomputing the forward values and applying, per element, exactly the
+roundings of the eager VJPs (up * other for mul, up * exp(x) for exp, relu'
+for relu, sign flips for neg and reflected sub; division records nothing, as
+in the reference).  Broadcast inputs are then reduced in the reference's
+order.  That reproduces eager autograd bit for bit when every value the
+gradient reaches has the output's shape, no such value feeds more than two
+gradient-carrying uses (two contributions add commutatively) and each input
+feeds exactly one; other programs run ``fn`` eagerly so autograd records op
+by op.
 """
 from __future__ import annotations
 
@@ -61,10 +62,10 @@ class _Trace:
             self.consts[bits] = self.emit("const", bits)
         return self.consts[bits]
 
-    def live(self, out: int) -> set:
-        """The values `out` depends on."""
+    def live(self, outs) -> set:
+        """The values the output(s) `outs` depend on."""
         live = set()
-        stack = [out]
+        stack = [outs] if isinstance(outs, int) else list(outs)
         while stack:
             v = stack.pop()
             if v in live:
@@ -75,12 +76,13 @@ class _Trace:
                 stack.extend(ins[1:])
         return live
 
-    def finish(self, out: int):
-        """IR text of the instructions `out` depends on, renumbered, and the
-        argument positions of the inputs it reads (dead code and unused
-        inputs are dropped, so they are neither loaded nor required to
-        broadcast to the output shape)."""
-        live = self.live(out)
+    def finish(self, outs):
+        """IR text of the instructions the output(s) `outs` depend on,
+        renumbered, and the argument positions of the inputs it reads (dead
+        code and unused inputs are dropped, so they are neither loaded nor
+        required to broadcast to the output shape)."""
+        outs = [outs] if isinstance(outs, int) else list(outs)
+        live = self.live(outs)
         new_id, lines, used_inputs = {}, [], []
         for v, ins in enumerate(self.ins):
             if v not in live:
@@ -93,7 +95,7 @@ class _Trace:
                 lines.append(f"const {ins[1]}")
             else:
                 lines.append(ins[0] + "".join(f" %{new_id[a]}" for a in ins[1:]))
-        lines.append(f"out %{new_id[out]}")
+        lines.extend(f"out %{new_id[o]}" for o in outs)
         return "\n".join(lines) + "\n", used_inputs
 
 
@@ -173,14 +175,14 @@ class _Proxy:
 _NO_GRAD = "no-grad"
 
 
-def _gradient_programs(tr, out, requires, out_shape):
-    """Backward IR for each input of a traced program, or None when the
-    program needs the eager path for bit-exact gradients, or _NO_GRAD when
-    the output records nothing (every path to it goes through a division).
+def _gradient_program(tr, out, requires, out_shape):
+    """The backward IR of a traced program, or None when the program needs the
+    eager path for bit-exact gradients, or _NO_GRAD when the output records
+    nothing (every path to it goes through a division).
 
-    `requires[i]`: input i requires grad.  Returns {input position: (IR text,
-    argument list)} where an argument is an input position or -1 for the
-    upstream gradient."""
+    `requires[i]`: input i requires grad.  Returns (IR text, argument list,
+    targets): an argument is an input position or -1 for the upstream
+    gradient; output o of the program is the gradient of input targets[o]."""
     ins = tr.ins
     live = sorted(tr.live(out))
     rg = {}
@@ -196,16 +198,18 @@ def _gradient_programs(tr, out, requires, out_shape):
             rg[v] = rg[ins[v][1]]
     if not rg[out]:
         return _NO_GRAD
+    # The values a gradient reaches from the output (never through a
+    # division, which records nothing), and their gradient-carrying uses.
+    reach = {out}
     uses: dict[int, int] = {}
-    for v in live:
-        if ins[v][0] in ("in", "const", "div") or not rg[v]:
+    for u in reversed(live):
+        if u not in reach or ins[u][0] in ("in", "const"):
             continue
-        for a in ins[v][1:]:
+        for a in ins[u][1:]:
             if rg[a]:
+                reach.add(a)
                 uses[a] = uses.get(a, 0) + 1
-    for v in live:
-        if not rg[v]:
-            continue
+    for v in reach:
         if ins[v][0] == "in":
             if uses.get(v, 0) > 1:
                 return None
@@ -213,52 +217,48 @@ def _gradient_programs(tr, out, requires, out_shape):
             return None
 
     n_in = len(requires)  # the upstream gradient's argument slot
-    programs = {}
-    for v in live:
-        if ins[v][0] != "in" or not rg[v] or uses.get(v, 0) == 0:
-            continue  # no gradient-carrying path (only through a division)
-        bt = _Trace()
-        fwd = {}
-        for u in live:  # the forward values, recomputed
-            i = ins[u]
-            if i[0] == "in":
-                fwd[u] = bt.emit("in", i[1])
-            elif i[0] == "const":
-                fwd[u] = bt.const_bits(i[1])
-            else:
-                fwd[u] = bt.emit(i[0], *(fwd[a] for a in i[1:]))
-        adj = {out: bt.emit("in", n_in)}  # the upstream gradient
+    bt = _Trace()
+    fwd = {}
+    for u in live:  # the forward values, recomputed
+        i = ins[u]
+        if i[0] == "in":
+            fwd[u] = bt.emit("in", i[1])
+        elif i[0] == "const":
+            fwd[u] = bt.const_bits(i[1])
+        else:
+            fwd[u] = bt.emit(i[0], *(fwd[a] for a in i[1:]))
+    adj = {out: bt.emit("in", n_in)}  # the upstream gradient
 
-        def contribute(x, val):
-            if not rg[x]:
-                return
-            adj[x] = bt.emit("add", adj[x], val) if x in adj else val
+    def contribute(x, val):
+        if not rg[x]:
+            return
+        adj[x] = bt.emit("add", adj[x], val) if x in adj else val
 
-        for u in reversed(live):
-            if u not in adj or ins[u][0] in ("in", "const"):
-                continue
-            g, (op, *args) = adj[u], ins[u]
-            if op == "add":
-                contribute(args[0], g)
-                contribute(args[1], g)
-            elif op == "sub":
-                contribute(args[0], g)
-                if rg[args[1]]:
-                    contribute(args[1], bt.emit("neg", g))
-            elif op == "mul":
-                if rg[args[0]]:
-                    contribute(args[0], bt.emit("mul", g, fwd[args[1]]))
-                if rg[args[1]]:
-                    contribute(args[1], bt.emit("mul", g, fwd[args[0]]))
-            elif op == "exp":
-                contribute(args[0], bt.emit("mul", g, fwd[u]))
-            elif op == "relu":
-                contribute(args[0], bt.emit("relub", fwd[args[0]], g))
-            elif op == "neg":
-                contribute(args[0], bt.emit("neg", g))
-        ir, used = bt.finish(adj[v])
-        programs[ins[v][1]] = (ir, [-1 if i == n_in else i for i in used])
-    return programs
+    for u in reversed(live):
+        if u not in adj or ins[u][0] in ("in", "const"):
+            continue
+        g, (op, *args) = adj[u], ins[u]
+        if op == "add":
+            contribute(args[0], g)
+            contribute(args[1], g)
+        elif op == "sub":
+            contribute(args[0], g)
+            if rg[args[1]]:
+                contribute(args[1], bt.emit("neg", g))
+        elif op == "mul":
+            if rg[args[0]]:
+                contribute(args[0], bt.emit("mul", g, fwd[args[1]]))
+            if rg[args[1]]:
+                contribute(args[1], bt.emit("mul", g, fwd[args[0]]))
+        elif op == "exp":
+            contribute(args[0], bt.emit("mul", g, fwd[u]))
+        elif op == "relu":
+            contribute(args[0], bt.emit("relub", fwd[args[0]], g))
+        elif op == "neg":
+            contribute(args[0], bt.emit("neg", g))
+    inputs = [v for v in live if ins[v][0] == "in" and v in reach]
+    ir, used = bt.finish([adj[v] for v in inputs])
+    return ir, [-1 if i == n_in else i for i in used], [ins[v][1] for v in inputs]
 
 
 class Fused:
@@ -298,25 +298,21 @@ class Fused:
         return hit
 
     def grad_plan(self, *inputs):
-        """None (eager autograd), _NO_GRAD, or the per-input gradient programs
-        as (compiled program, argument positions among the forward's inputs)."""
+        """None (eager autograd), _NO_GRAD, or the gradient program as
+        (compiled program id, argument positions among the forward's inputs
+        or -1 for the upstream, the forward input position of each output)."""
         requires = tuple(bool(t.requires_grad) for t in inputs)
         key = (tuple((t.shape, t.stride()) for t in inputs), requires)
         if key in self._cache:
             return self._cache[key]
         tr, out = self._trace(inputs)
-        plan = _gradient_programs(tr, out.vid, requires, out.shape)
-        if isinstance(plan, dict):
+        plan = _gradient_program(tr, out.vid, requires, out.shape)
+        if isinstance(plan, tuple):
+            ir, args, targets = plan
             _, _, _, used, _ = self.program(*inputs)
             pos = {orig: p for p, orig in enumerate(used)}
-            vjps = []
-            for orig in used:
-                if orig in plan:
-                    ir, args = plan[orig]
-                    vjps.append((_C.FusedProgram.compile(ir, len(args)).id, [-1 if a < 0 else pos[a] for a in args]))
-                else:
-                    vjps.append((0, []))
-            plan = vjps
+            plan = (_C.FusedProgram.compile(ir, len(args)).id, [-1 if a < 0 else pos[a] for a in args],
+                    [pos[t] for t in targets])
         self._cache[key] = plan
         return plan
 
@@ -330,7 +326,7 @@ class Fused:
             if plan is None:
                 return self.fn(*inputs)
             if plan != _NO_GRAD:
-                return prog.launch_with_grad(args, shape, strides, plan)
+                return prog.launch_with_grad(args, shape, strides, *plan)
         return prog.launch(args, shape, strides)
 
 

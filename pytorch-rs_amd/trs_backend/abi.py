@@ -111,6 +111,8 @@ _SIGNATURES = {
     "trs_matmul_f32": ([c_void_p, _LP, c_void_p, _LP, c_void_p, _LP], c_int),
     "trs_fusion_compile": ([c_char_p, c_size_t, POINTER(c_uint64)], c_int),
     "trs_fusion_launch": ([c_uint64, c_int, POINTER(c_void_p), _LP, c_void_p, _LP], c_int),
+    "trs_fusion_launch_multi": ([c_uint64, c_int, POINTER(c_void_p), _LP, c_int, POINTER(c_void_p), _LP], c_int),
+    "trs_fusion_outputs": ([c_uint64, POINTER(c_int)], c_int),
     "trs_fusion_source": ([c_uint64, ctypes.c_char_p, c_size_t, POINTER(c_size_t)], c_int),
     "trs_fusion_compile_ms": ([c_uint64, POINTER(c_double)], c_int),
     "trs_fusion_from_disk_cache": ([c_uint64, POINTER(c_int)], c_int),

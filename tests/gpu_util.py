@@ -79,6 +79,15 @@ def fusion_launch(kid: int, inputs, layouts, out: DeviceArray, olayout) -> None:
     check(abi.lib.trs_fusion_launch(kid, n, ptrs, lays, out.ptr, ctypes.byref(olayout)))
 
 
+def fusion_launch_multi(kid: int, inputs, layouts, outs, olayout) -> int:
+    """trs_fusion_launch_multi; returns the status code (not checked)."""
+    n, m = len(inputs), len(outs)
+    ptrs = (ctypes.c_void_p * n)(*[x.addr for x in inputs])
+    lays = (abi.Layout * n)(*layouts)
+    optrs = (ctypes.c_void_p * m)(*[o.addr for o in outs])
+    return abi.lib.trs_fusion_launch_multi(kid, n, ptrs, lays, m, optrs, ctypes.byref(olayout))
+
+
 def special_mix(rng, n: int) -> np.ndarray:
     """Normals with IEEE specials sprinkled in (signed zeros, infs, NaNs, subnormals)."""
     x = rng.standard_normal(n).astype(np.float32)

@@ -90,7 +90,29 @@ def test_fusion_compiler_generates_and_compiles_on_the_host():
     assert rc2 == 0 and kid2 == kid
 
 
+def test_fusion_compiler_multi_output_program():
+    ir = "in f32\nin f32\nmul %0 %1\nexp %2\nrelub %0 %1\nout %2\nout %3\nout %4\nout %2\n"
+    rc, kid = _compile(ir)
+    abi.check(rc)
+    n = ctypes.c_int()
+    abi.check(abi.lib.trs_fusion_outputs(kid, ctypes.byref(n)))
+    assert n.value == 4
+    size = ctypes.c_size_t()
+    abi.check(abi.lib.trs_fusion_source(kid, None, 0, ctypes.byref(size)))
+    buf = ctypes.create_string_buffer(size.value)
+    abi.check(abi.lib.trs_fusion_source(kid, buf, size.value, None))
+    src = buf.value.decode()
+    assert "static constexpr int NOUT = 4;" in src
+    assert "r[0] = v2;" in src and "r[2] = v4;" in src and "r[3] = v2;" in src
+    rc, one = _compile("in f32\nneg %0\nout %1\n")
+    abi.check(rc)
+    abi.check(abi.lib.trs_fusion_outputs(one, ctypes.byref(n)))
+    assert n.value == 1
+
+
 @pytest.mark.parametrize("ir,fragment", [
+    ("in f32\nout %0\nrelu %0\n", "instruction after 'out'"),
+    ("in f32\n" + "out %0\n" * 9, "more than 8 outputs"),
     ("in f32\nadd %0 %1\nout %1\n", "bad operand"),
     ("in f32\nfoo %0\nout %0\n", "unknown instruction"),
     ("in f32\nrelu %0\n", "no 'out'"),

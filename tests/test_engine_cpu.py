@@ -551,6 +551,38 @@ def test_fusion_tracer_emits_one_rounding_per_op_and_eager_layout():
     assert "sub %1 %0" in ir and "div %" in ir and "mul %0 %" in ir
 
 
+def test_fusion_backward_program_is_the_reverse_mode_of_the_ir():
+    """The fused node's backward: one program with one output per input that
+    needs a gradient, each the eager VJP's expression (mul: up * other; add:
+    up); a division passes no gradient; an input used twice falls back to
+    eager autograd (None)."""
+    from torch_rs import fusion as F
+    x = torch_rs.zeros(4)
+
+    def plan(fn, requires):
+        tr, out = torch_rs.fuse(fn)._trace(tuple(x for _ in requires))
+        return F._gradient_program(tr, out.vid, requires, out.shape)
+
+    # x*y + z: dx = up*y, dy = up*x, dz = up; arguments x, y, upstream
+    assert plan(lambda x, y, z: x * y + z, (True, True, True)) == (
+        "in f32\nin f32\nin f32\nmul %2 %1\nmul %2 %0\nout %3\nout %4\nout %2\n", [0, 1, -1], [0, 1, 2])
+    assert plan(lambda x, y, z: x * y + z, (False, True, False)) == ("in f32\nin f32\nmul %1 %0\nout %2\n",
+                                                                    [0, -1], [1])
+    # x reaches the output only through a division: no gradient for x
+    assert plan(lambda x, y, z, t: (x * y) / z + t, (True, False, False, True)) == ("in f32\nout %0\n", [-1], [3])
+    assert plan(lambda x, y, z, t: (x * y) / z + t, (True, False, False, False)) == F._NO_GRAD
+    # an input with two gradient-carrying uses: eager
+    assert plan(lambda x, y: (x * y).exp() - x.relu(), (True, True)) is None
+
+    def two_uses(x, y):
+        s = x * y
+        return s.relu() * s.exp()
+
+    ir, args, targets = plan(two_uses, (True, False))
+    assert targets == [0] and args == [0, 1, -1]
+    assert "relub" in ir and ir.count("\nout ") == 1
+
+
 def test_fusion_tracer_drops_dead_code_and_unused_inputs():
     f = torch_rs.fuse(lambda x, y, z: (y * 2.0).relu())  # x and z unused
     x, y, z = torch_rs.zeros(5, 7), torch_rs.zeros(3), torch_rs.zeros(9)

@@ -377,7 +377,7 @@ def test_fused_broadcast_strided_chain_is_bit_exact_with_eager():
     assert_bitwise_equal(got.numpy().ravel(), want.numpy().ravel())
 
 
-def test_fused_call_with_grad_inputs_runs_eagerly_and_records():
+def test_fused_call_with_grad_inputs_records_and_backpropagates():
     x = cuda([1.0, -2.0, 3.0], True)
     y = torch_rs.fuse(lambda x: (x * 2.0).relu())(x)
     assert y.grad_fn is not None

@@ -321,3 +321,105 @@ def _eval(prog, xs):
         else:
             vals.append(_run_program([ins], vals))
     return vals[-1]
+
+
+# ---- multi-output programs ----------------------------------------------------
+
+_MULTI_BODY = ("in f32\nin f32\nin f32\nadd %0 %1\nmul %3 %2\nconst 0x3e800000\nmul %4 %5\nexp %6\n"
+               "relub %0 %4\n")
+_MULTI_OUTS = [4, 7, 8, 3]
+
+
+def _multi_cases():
+    """(name, arrays, input layouts, output shape, output strides): one case
+    per kernel variant of the pointwise engine."""
+    rng = np.random.default_rng(77)
+    n = 100_003
+    flat = [rng.standard_normal(n).astype(np.float32) for _ in range(3)]
+    yield "flat_contig", flat, [layout_of((n,))] * 3, (n,), None
+    shifted = [np.concatenate([[0.0], a]).astype(np.float32) for a in flat]
+    yield "flat_unaligned", shifted, [layout_of((n,), (1,), 1)] * 3, (n,), None
+    R, C = 64, 1000
+    rows = [rng.standard_normal(R * C).astype(np.float32), rng.standard_normal(C).astype(np.float32),
+            rng.standard_normal(R * C).astype(np.float32)]
+    yield "rows", rows, [layout_of((R, C)), layout_of((C,)), layout_of((R, C))], (R, C), None
+    B, M, N = 3, 70, 130
+    tiled = [rng.standard_normal(B * N).astype(np.float32), rng.standard_normal(M * N).astype(np.float32),
+             rng.standard_normal(B * N * M).astype(np.float32)]
+    yield ("tiled", tiled, [layout_of((B, 1, N)), layout_of((1, M, N)), layout_of((B, M, N), (N * M, 1, M))],
+           (B, M, N), None)
+    A, D = 9, 11
+    gen = [rng.standard_normal(A * D * 3).astype(np.float32) for _ in range(3)]
+    lays = [layout_of((A, D), (1, A * 3)), layout_of((A, D), (D * 3, 3)), layout_of((A, D), (3, A * 3), 1)]
+    yield "generic", gen, lays, (A, D), (1, A)
+
+
+@pytest.mark.parametrize("case", list(_multi_cases()), ids=lambda c: c[0])
+def test_multi_output_program_equals_single_output_programs(case):
+    """A four-output program writes, in one launch, exactly what the four
+    one-output programs over the same instructions write, on every kernel
+    variant (flat, unaligned flat, row broadcast, LDS-tiled transpose,
+    generic strides)."""
+    _, arrays, lays, oshape, ostr = case
+    n = int(np.prod(oshape))
+    kid = U.fusion_compile(_MULTI_BODY + "".join(f"out %{o}\n" for o in _MULTI_OUTS))
+    devs = [U.dev(a) for a in arrays]
+    outs = [U.out_buffer(n) for _ in _MULTI_OUTS]
+    assert U.fusion_launch_multi(kid, devs, lays, outs, layout_of(oshape, ostr)) == 0
+    for o, buf in zip(_MULTI_OUTS, outs):
+        single = gpu_fused(_MULTI_BODY + f"out %{o}\n", arrays, lays, oshape, ostr)
+        assert_bitwise_equal(buf.to_numpy(count=n), single)
+
+
+def test_multi_output_launch_rejects_bad_outputs():
+    from trs_backend.abi import TRS_E_INVALID_ARGUMENT
+    n = 4096
+    rng = np.random.default_rng(5)
+    arrays = [rng.standard_normal(n).astype(np.float32) for _ in range(3)]
+    devs = [U.dev(a) for a in arrays]
+    lays = [layout_of((n,))] * 3
+    kid = U.fusion_compile(_MULTI_BODY + "out %4\nout %7\n")
+    a, b = U.out_buffer(n), U.out_buffer(n)
+    lo = layout_of((n,))
+    # output count must match the program
+    assert U.fusion_launch_multi(kid, devs, lays, [a], lo) == TRS_E_INVALID_ARGUMENT
+    assert U.fusion_launch_multi(kid, devs, lays, [a, b, U.out_buffer(n)], lo) == TRS_E_INVALID_ARGUMENT
+    ptrs = (U.ctypes.c_void_p * 3)(*[d.addr for d in devs])
+    larr = (U.abi.Layout * 3)(*lays)
+    assert U.abi.lib.trs_fusion_launch(kid, 3, ptrs, larr, a.ptr, U.ctypes.byref(lo)) == TRS_E_INVALID_ARGUMENT
+    # outputs may not share memory with each other
+    assert U.fusion_launch_multi(kid, devs, lays, [a, a], lo) == TRS_E_INVALID_ARGUMENT
+    # an output may share memory with an input only as the same view
+    assert U.fusion_launch_multi(kid, devs, lays, [a, devs[2]], lo) == 0
+    half = layout_of((n // 2,))
+    assert U.fusion_launch_multi(kid, devs, [layout_of((n // 2,), (1,), 1)] * 3, [a, devs[0]],
+                                 half) == TRS_E_INVALID_ARGUMENT
+    # the in-place launch above computed from the inputs as they were
+    want_7 = gpu_fused(_MULTI_BODY + "out %7\n", arrays, lays, (n,))
+    assert_bitwise_equal(devs[2].to_numpy(count=n), want_7)
+
+
+def test_fused_backward_input_reaching_output_only_through_division():
+    """x reaches the output only through a division (which records nothing):
+    x gets no gradient, t gets the upstream, as eager autograd gives."""
+    import torch_rs
+    rng = np.random.default_rng(13)
+    shape = (37, 5)
+    vals = [rng.standard_normal(shape).astype(np.float32) for _ in range(4)]
+    fn = lambda x, y, z, t: (x * y) / z + t
+
+    def run(f):
+        x = torch_rs.tensor(vals[0], device="cuda").with_requires_grad(True)
+        y = torch_rs.tensor(vals[1], device="cuda")
+        z = torch_rs.tensor(vals[2], device="cuda")
+        t = torch_rs.tensor(vals[3], device="cuda").with_requires_grad(True)
+        out = f(x, y, z, t)
+        out.sum().backward()
+        return out, x, t
+
+    out_e, xe, te = run(fn)
+    out_f, xf, tf = run(torch_rs.fuse(fn))
+    assert_bitwise_equal(out_f.numpy().ravel(), out_e.numpy().ravel())
+    assert out_f._grad_fn_name == "FusedBackward0"
+    assert xe.grad is None and xf.grad is None
+    assert_bitwise_equal(tf.grad.numpy().ravel(), te.grad.numpy().ravel())
