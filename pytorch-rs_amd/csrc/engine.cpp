@@ -78,6 +78,14 @@ int device_count() {
 
 void synchronize() { check(trs_synchronize()); }
 
+int current_device() {
+    int d = 0;
+    check(trs_get_device(&d));
+    return d;
+}
+
+void set_device(int index) { check(trs_set_device(index)); }
+
 static void select_device(const Device &d) {
     if (!d.is_cuda()) return;
     int cur = -1;

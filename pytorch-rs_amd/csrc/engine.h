@@ -231,6 +231,8 @@ bool is_grad_enabled();
 // Device helpers
 int device_count();
 void synchronize();
+int current_device();
+void set_device(int index);
 
 // Fused pointwise program (compiled once, cached by IR text).
 struct FusedProgram {

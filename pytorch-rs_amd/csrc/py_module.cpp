@@ -212,7 +212,7 @@ PYBIND11_MODULE(_trs_native, m) {
         .def("is_contiguous", &Tensor::is_contiguous)
         .def("is_non_overlapping_and_dense",
              [](const Tensor &t) { return layout::is_non_overlapping_and_dense(t.shape, t.strides, t.numel); })
-        .def_property_readonly("device", [](const Tensor &t) { return t.device().str(); })
+        .def_property_readonly("_device_str", [](const Tensor &t) { return t.device().str(); })
         .def_property_readonly("is_cuda", [](const Tensor &t) { return t.device().is_cuda(); })
         .def_property_readonly("requires_grad", &Tensor::requires_grad)
         .def_property_readonly("is_leaf", &Tensor::is_leaf)
@@ -294,6 +294,8 @@ PYBIND11_MODULE(_trs_native, m) {
     m.def("is_grad_enabled", &is_grad_enabled);
     m.def("device_count", &device_count);
     m.def("synchronize", &synchronize);
+    m.def("current_device", &current_device);
+    m.def("set_device", &set_device);
 
     py::class_<FusedProgram>(m, "FusedProgram")
         .def_static("compile", &FusedProgram::compile)

@@ -11,7 +11,8 @@ libtrs_hip.so; ``"cpu"`` tensors are host staging for ``.to()`` only.
 Additions of this backend (absent from the reference, documented where
 they differ): device tensors record VJPs for matmul, tensor-tensor add/sub
 and exp; ``fuse`` compiles a pointwise function into one hipRTC kernel;
-``nn.functional.dropout`` accepts a precomputed uint8 keep-mask.
+``nn.functional.dropout`` accepts a precomputed uint8 keep-mask; ``device``
+and ``accelerator`` know the "cuda" device type besides "cpu".
 """
 from __future__ import annotations
 
@@ -20,6 +21,7 @@ import contextlib
 
 import numpy as _np
 
+from ._device import device, parse_device as _parse_device
 from ._native import native as _C
 
 Tensor = _C.Tensor
@@ -27,16 +29,19 @@ float32 = "torch_rs.float32"
 float = float32  # noqa: A001  (the reference exports torch_rs.float too)
 __version__ = "0.1.0+mi355x"
 
-_DEVICE_ALIASES = {"cuda", "cpu"}
-
-
-def _device_str(device) -> str:
+def _device_str(device, function: str = "tensor") -> str:
+    """The engine's device string for a factory's ``device`` argument: None
+    is the CPU, an indexed CPU descriptor is the CPU (the reference keeps CPU
+    storage unindexed), an unindexed "cuda" is the current GPU."""
     if device is None:
         return "cpu"
-    d = str(device)
-    if d in _DEVICE_ALIASES or d.startswith("cuda:"):
-        return d
-    raise RuntimeError(f"Expected one of cpu, cuda device type at start of device string: {d}")
+    d = _parse_device(function, device)
+    if d.type == "cpu":
+        return "cpu"
+    index = d.index if d.index is not None else _C.current_device()
+    if index < 0:
+        raise RuntimeError(f"{function}(): invalid device ordinal {index}")
+    return f"cuda:{index}"
 
 
 def _flatten(data):
@@ -70,23 +75,27 @@ def tensor(data, *, dtype=None, device=None, requires_grad=False) -> Tensor:
         flat, shape = _flatten(data)
         arr = _np.asarray(flat, dtype=_np.float64).astype(_np.float32).reshape(shape)
     # asarray(order="C") keeps 0-d arrays 0-d (ascontiguousarray would make them [1]).
-    t = _C.from_numpy(_np.asarray(arr, dtype=_np.float32, order="C"), _device_str(device))
+    t = _C.from_numpy(_np.asarray(arr, dtype=_np.float32, order="C"), _device_str(device, "tensor"))
     return t.with_requires_grad(bool(requires_grad))
 
 
 def zeros(*shape, device=None, requires_grad=False) -> Tensor:
-    return full(shape, 0.0, device=device, requires_grad=requires_grad)
+    return _full("zeros", shape, 0.0, device, requires_grad)
 
 
 def ones(*shape, device=None, requires_grad=False) -> Tensor:
-    return full(shape, 1.0, device=device, requires_grad=requires_grad)
+    return _full("ones", shape, 1.0, device, requires_grad)
 
 
 def full(shape, fill_value, *, device=None, requires_grad=False) -> Tensor:
+    return _full("full", shape, fill_value, device, requires_grad)
+
+
+def _full(function, shape, fill_value, device, requires_grad) -> Tensor:
     if len(shape) == 1 and not isinstance(shape[0], int):
         shape = tuple(shape[0])
-    return _C.full([int(d) for d in shape], _np.float32(fill_value), _device_str(device)).with_requires_grad(
-        bool(requires_grad))
+    return _C.full([int(d) for d in shape], _np.float32(fill_value),
+                   _device_str(device, function)).with_requires_grad(bool(requires_grad))
 
 
 def is_tensor(obj) -> bool:
@@ -319,8 +328,43 @@ Tensor.grad_fn = property(_grad_fn)
 Tensor.grad = property(_grad)
 Tensor.dtype = property(lambda self: float32)
 Tensor.ndim = property(lambda self: self.dim())
-Tensor.cpu = lambda self: self.to("cpu")
-Tensor.cuda = lambda self, device=0: self.to(f"cuda:{device}")
+_native_to = Tensor.to
+
+
+def _tensor_device(self) -> device:
+    """device(type='cpu') for host tensors, device(type='cuda', index=i) on GPU i."""
+    s = self._device_str
+    if s == "cpu":
+        return device("cpu")
+    return device("cuda", int(s.split(":")[1]))
+
+
+def _to(self, *args, **kwargs):
+    """Tensor.to(device): a copy on that device (the same tensor if already there)."""
+    if len(args) + len(kwargs) != 1 or (kwargs and "device" not in kwargs):
+        raise TypeError("to() supports only a device argument: to(device) or to(device=...)")
+    return _native_to(self, _device_str(args[0] if args else kwargs["device"], "to"))
+
+
+def _cuda(self, device=None):
+    """Tensor.cuda(device=None): to the current GPU, or GPU `device` (an index,
+    a device or a device string)."""
+    if device is None:
+        return _native_to(self, f"cuda:{_C.current_device()}")
+    if isinstance(device, int) and not isinstance(device, bool):
+        return _native_to(self, f"cuda:{device}")
+    d = _parse_device("cuda", device)
+    if d.type != "cuda":
+        raise RuntimeError(f"Invalid device, must be cuda device: {d}")
+    return _native_to(self, _device_str(d, "cuda"))
+
+
+Tensor.device = property(_tensor_device)
+Tensor.is_cpu = property(lambda self: not self.is_cuda)
+Tensor.get_device = lambda self: -1 if not self.is_cuda else int(self._device_str.split(":")[1])
+Tensor.to = _to
+Tensor.cpu = lambda self: _native_to(self, "cpu")
+Tensor.cuda = _cuda
 Tensor.tolist = lambda self: self.numpy().tolist()
 _native_matmul = Tensor.matmul
 
@@ -344,5 +388,5 @@ Tensor.__array_priority__ = 1000.0  # numpy operands defer to the tensor's refle
 Tensor.__bool__ = _bool
 Tensor.multiply = Tensor.mul
 
-from . import autograd, cuda, nn  # noqa: E402,F401
+from . import accelerator, autograd, cuda, nn  # noqa: E402,F401
 from .fusion import fuse  # noqa: E402,F401

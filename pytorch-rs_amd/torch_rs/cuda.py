@@ -18,7 +18,19 @@ def synchronize() -> None:
 
 
 def current_device() -> int:
-    return 0
+    """Index of the GPU that unindexed "cuda" means (hipGetDevice)."""
+    return _C.current_device()
+
+
+def set_device(device) -> None:
+    """Make GPU `device` (an index, or a "cuda:i" device) the current one."""
+    if not isinstance(device, int):
+        from ._device import parse_device
+        d = parse_device("set_device", device)
+        if d.type != "cuda" or d.index is None:
+            raise ValueError(f"Expected a cuda device with an index, but got: {d}")
+        device = d.index
+    _C.set_device(device)
 
 
 def empty_pinned(shape, dtype="float32"):

@@ -190,5 +190,6 @@ def feature_alpha_dropout(input, p: float = 0.5, training: bool = False, inplace
 
 def keep_mask(mask, device="cuda"):
     """Upload a uint8 keep-mask (1 = keep) to the device once, for reuse across steps."""
+    from .. import _device_str
     arr = _np.asarray(mask, dtype=_np.uint8, order="C")
-    return _C.bytes_from_numpy(arr, str(device))
+    return _C.bytes_from_numpy(arr, _device_str(device, "keep_mask"))

@@ -405,10 +405,29 @@ def test_host_device_round_trip_preserves_bits_and_views():
     rng = np.random.default_rng(14)
     a = rng.standard_normal((6, 5)).astype(np.float32)
     t = cuda(a)
-    assert t.device == "cuda:0" and t.is_cuda
+    assert t.device == torch_rs.device("cuda", 0) and str(t.device) == "cuda:0" and t.is_cuda
     assert_bitwise_equal(t.mT.cpu().numpy().ravel(), a.T.ravel())
     back = t.mT.cpu().cuda()
     assert back.is_contiguous() and back.shape == (5, 6)
+
+
+def test_device_objects_select_the_gpu_and_accelerator_reports_it():
+    dev = torch_rs.device("cuda")
+    assert torch_rs.cuda.current_device() == 0
+    t = torch_rs.tensor([1.5, -2.0], device=dev)
+    assert t.device == torch_rs.device("cuda", 0) and t.get_device() == 0 and not t.is_cpu
+    u = torch_rs.zeros(3, device=torch_rs.device("cuda", 0))
+    assert u.device == t.device
+    h = t.to(torch_rs.device("cpu"))
+    assert h.device == torch_rs.device("cpu") and h.get_device() == -1
+    for back in (h.to(dev), h.to(device="cuda:0"), h.cuda(), h.cuda(0), h.cuda(torch_rs.device("cuda", 0))):
+        assert back.device == torch_rs.device("cuda", 0)
+        assert vals(back).tolist() == [1.5, -2.0]
+    with pytest.raises(RuntimeError, match="must be cuda device"):
+        h.cuda("cpu")
+    acc = torch_rs.accelerator
+    assert acc.is_available() and acc.device_count() >= 1
+    assert acc.current_accelerator(check_available=True) == torch_rs.device("cuda")
 
 
 def test_backward_through_a_host_to_device_transfer_raises_before_consuming():
