@@ -76,22 +76,39 @@ class _Trace:
                 stack.extend(ins[1:])
         return live
 
+    def _numel(self, v) -> int:
+        n = 1
+        for d in self.shapes.get(v, ()):
+            n *= d
+        return n
+
     def finish(self, outs):
         """IR text of the instructions the output(s) `outs` depend on,
         renumbered, and the argument positions of the inputs it reads (dead
         code and unused inputs are dropped, so they are neither loaded nor
-        required to broadcast to the output shape)."""
+        required to broadcast to the output shape).
+
+        Inputs smaller than the output (broadcast, re-read from cache) are
+        declared before the full-size ones: a kernel issues its loads in
+        input order, and issuing the cached loads before the streaming ones
+        measured 2-3% faster on a row-broadcast add.  The instructions still
+        take their operands in traced order, so the arithmetic is unchanged."""
         outs = [outs] if isinstance(outs, int) else list(outs)
         live = self.live(outs)
+        full = max(self._numel(o) for o in outs)
+        inputs = [v for v, ins in enumerate(self.ins) if v in live and ins[0] == "in"]
+        if all(v in self.shapes for v in inputs):
+            inputs.sort(key=lambda v: self._numel(v) >= full)  # stable: broadcast first
         new_id, lines, used_inputs = {}, [], []
+        for v in inputs:
+            new_id[v] = len(lines)
+            used_inputs.append(self.ins[v][1])
+            lines.append("in f32")
         for v, ins in enumerate(self.ins):
-            if v not in live:
+            if v not in live or ins[0] == "in":
                 continue
             new_id[v] = len(lines)
-            if ins[0] == "in":
-                used_inputs.append(ins[1])
-                lines.append("in f32")
-            elif ins[0] == "const":
+            if ins[0] == "const":
                 lines.append(f"const {ins[1]}")
             else:
                 lines.append(ins[0] + "".join(f" %{new_id[a]}" for a in ins[1:]))

@@ -66,12 +66,15 @@ def relu_bias(log, reps: int = 20, sets: int = 3) -> dict:
                                      ctypes.byref(lx)))
         check(abi.lib.trs_unary_f32(1, tmp[k].ptr, ctypes.byref(lx), outs[k].ptr, ctypes.byref(lx)))
 
-    kid = _fusion("in f32\nin f32\nadd %0 %1\nrelu %2\nout %3\n")
+    # The IR torch_rs.fuse emits for relu(x + b) at these layouts: the
+    # broadcast row b is declared first (loaded before the streamed x), and
+    # the add still computes x + b.
+    kid = _fusion("in f32\nin f32\nadd %1 %0\nrelu %2\nout %3\n")
 
     def fused():
         k = i[0] % sets
         i[0] += 1
-        _fuse_launch(kid, [xs[k], db], [lx, lb], outs[k], lx)
+        _fuse_launch(kid, [db, xs[k]], [lb, lx], outs[k], lx)
 
     e = time_region(eager, reps)
     f = time_region(fused, reps)

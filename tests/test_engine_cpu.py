@@ -583,6 +583,18 @@ def test_fusion_backward_program_is_the_reverse_mode_of_the_ir():
     assert "relub" in ir and ir.count("\nout ") == 1
 
 
+def test_fusion_tracer_declares_broadcast_inputs_first():
+    """relu(x + b) with b a row broadcast: b's `in` comes first so kernels load
+    it before streaming x; the add still takes x, then b.  This is the IR the
+    bench launches for the row-broadcast config."""
+    f = torch_rs.fuse(lambda x, b: (x + b).relu())
+    ir, shape, _, used = f.trace(torch_rs.zeros(4096, 4096), torch_rs.zeros(4096))
+    assert ir == "in f32\nin f32\nadd %1 %0\nrelu %2\nout %3\n" and used == [1, 0] and shape == (4096, 4096)
+    g = torch_rs.fuse(lambda a, b, c: (a + b) * c)
+    ir, _, _, used = g.trace(torch_rs.zeros(2, 3), torch_rs.zeros(3), torch_rs.zeros(1, 1))
+    assert used == [1, 2, 0] and ir == "in f32\nin f32\nin f32\nadd %2 %0\nmul %3 %1\nout %4\n"
+
+
 def test_fusion_tracer_drops_dead_code_and_unused_inputs():
     f = torch_rs.fuse(lambda x, y, z: (y * 2.0).relu())  # x and z unused
     x, y, z = torch_rs.zeros(5, 7), torch_rs.zeros(3), torch_rs.zeros(9)
