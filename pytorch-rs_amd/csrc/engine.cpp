@@ -1219,8 +1219,11 @@ void validate(const GradFn &fn) {
         if (!fn.mask) throw TensorError(kGraphFreed);
         break;
     case GradKind::Fused:
-        for (int a : fn.fused.args)
-            if (a >= 0 && !fn.inputs[a].values) throw TensorError(kGraphFreed);
+        for (int a : fn.fused.args) {
+            if (a < 0) continue;
+            const bool bytes = (size_t)a < fn.fused_bytes.size() && fn.fused_bytes[a];
+            if (!bytes && !fn.inputs[a].values) throw TensorError(kGraphFreed);
+        }
         break;
     default:
         break;
@@ -1242,6 +1245,7 @@ void consume(GradFn &fn) {
     case GradKind::MaskApply: fn.mask.reset(); break;
     case GradKind::Fused:
         for (auto &in : fn.inputs) in.values.reset();
+        for (auto &b : fn.fused_bytes) b.reset();
         break;
     default: break;
     }
@@ -1313,7 +1317,8 @@ void apply_grad_fn(const GradFn &fn, Grad up, Device dev, std::map<GradKey, Grad
                 lays.push_back(lup);
             } else {
                 const SavedTensor &sv = fn.inputs[a];
-                ptrs.push_back(sv.values->dptr);
+                const bool bytes = (size_t)a < fn.fused_bytes.size() && fn.fused_bytes[a];
+                ptrs.push_back(bytes ? (const void *)fn.fused_bytes[a]->dptr : (const void *)sv.values->dptr);
                 lays.push_back(saved_layout(sv));
             }
         }
@@ -1589,35 +1594,55 @@ FusedProgram FusedProgram::compile(const std::string &ir, int nin) {
     return p;
 }
 
-Tensor FusedProgram::launch(const std::vector<Tensor> &inputs, const Dims &out_shape, const Dims &out_strides) const {
+namespace {
+
+Device fused_arg_device(const FusedArg &a) { return a.bytes ? a.bytes->device : a.tensor.device(); }
+
+trs_layout fused_arg_layout(const FusedArg &a) {
+    if (!a.bytes) return a.tensor.abi_layout();
+    return abi_layout_of(a.bytes->shape, layout::contiguous_strides(a.bytes->shape), 0);
+}
+
+const void *fused_arg_ptr(const FusedArg &a) {
+    return a.bytes ? (const void *)a.bytes->dptr : (const void *)a.tensor.storage->dptr;
+}
+
+}  // namespace
+
+Tensor FusedProgram::launch(const std::vector<FusedArg> &inputs, const Dims &out_shape, const Dims &out_strides) const {
     if ((int)inputs.size() != nin)
         throw TensorError("fused program takes " + std::to_string(nin) + " inputs, got " + std::to_string(inputs.size()));
     if (inputs.empty()) throw TensorError("fused program has no inputs");
-    const Device dev = inputs[0].device();
-    for (auto &t : inputs) {
-        t.require_cuda("fused program");
-        if (!(t.device() == dev)) throw TensorError("fused program inputs are on different devices");
+    const Device dev = fused_arg_device(inputs[0]);
+    for (auto &a : inputs) {
+        if (a.bytes) {
+            if (!a.bytes->device.is_cuda()) throw TensorError("fused program: byte buffer is not on a device");
+        } else {
+            a.tensor.require_cuda("fused program");
+        }
+        if (!(fused_arg_device(a) == dev)) throw TensorError("fused program inputs are on different devices");
     }
     Tensor out = empty_like_layout(dev, out_shape, out_strides);
     if (out.numel == 0) return out;
     std::vector<trs_layout> lays;
     std::vector<const void *> ptrs;
-    for (auto &t : inputs) {
-        lays.push_back(t.abi_layout());
-        ptrs.push_back(t.storage->dptr);
+    for (auto &a : inputs) {
+        lays.push_back(fused_arg_layout(a));
+        ptrs.push_back(fused_arg_ptr(a));
     }
     const trs_layout lo = out.abi_layout();
     check(trs_fusion_launch(id, nin, ptrs.data(), lays.data(), out.storage->dptr, &lo));
     return out;
 }
 
-Tensor FusedProgram::launch_with_grad(const std::vector<Tensor> &inputs, const Dims &out_shape,
+Tensor FusedProgram::launch_with_grad(const std::vector<FusedArg> &inputs, const Dims &out_shape,
                                       const Dims &out_strides, const FusedBackward &bwd) const {
     for (int a : bwd.args)
         if (a < -1 || a >= (int)inputs.size()) throw TensorError("fused gradient program argument out of range");
     std::vector<bool> seen(inputs.size(), false);
     for (int t : bwd.targets) {
-        if (t < 0 || t >= (int)inputs.size() || seen[t]) throw TensorError("fused gradient program target invalid");
+        if (t < 0 || t >= (int)inputs.size() || seen[t] || inputs[t].bytes)
+            throw TensorError("fused gradient program target invalid");
         seen[t] = true;
     }
     int nout = 0;
@@ -1627,12 +1652,23 @@ Tensor FusedProgram::launch_with_grad(const std::vector<Tensor> &inputs, const D
                           std::to_string(bwd.targets.size()) + " targets");
     Tensor out = launch(inputs, out_shape, out_strides);
     bool any = false;
-    for (int t : bwd.targets) any = any || inputs[t].requires_grad();
+    for (int t : bwd.targets) any = any || inputs[t].tensor.requires_grad();
     if (!any || !is_grad_enabled()) return out;
     auto fn = std::make_unique<GradFn>();
     fn->kind = GradKind::Fused;
     fn->node = Node::Fused;
-    for (const auto &t : inputs) fn->inputs.push_back(save(t, true));
+    for (const auto &a : inputs) {
+        if (a.bytes) {
+            SavedTensor sv;
+            sv.shape = a.bytes->shape;
+            sv.strides = layout::contiguous_strides(a.bytes->shape);
+            sv.numel = a.bytes->numel;
+            fn->inputs.push_back(sv);
+        } else {
+            fn->inputs.push_back(save(a.tensor, true));
+        }
+        fn->fused_bytes.push_back(a.bytes);
+    }
     fn->fused = bwd;
     attach(out, std::move(fn));
     return out;

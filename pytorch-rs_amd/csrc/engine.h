@@ -133,6 +133,7 @@ struct GradFn {
     SavedTensor output;   // exp: its own output (values saved)
     BytePtr mask;         // mask-apply: the keep-mask
     FusedBackward fused;  // fused: the gradient program
+    std::vector<BytePtr> fused_bytes;  // fused: byte-buffer inputs by position (null for tensors)
 };
 
 struct AutogradMeta {
@@ -234,15 +235,22 @@ void synchronize();
 int current_device();
 void set_device(int index);
 
+// One argument of a fused program: a tensor, or (bytes set) a byte buffer
+// read as an `in u8` operand, such as a dropout keep-mask.
+struct FusedArg {
+    Tensor tensor;
+    BytePtr bytes;
+};
+
 // Fused pointwise program (compiled once, cached by IR text).
 struct FusedProgram {
     uint64_t id = 0;
     int nin = 0;
     static FusedProgram compile(const std::string &ir, int nin);
-    Tensor launch(const std::vector<Tensor> &inputs, const Dims &out_shape, const Dims &out_strides) const;
+    Tensor launch(const std::vector<FusedArg> &inputs, const Dims &out_shape, const Dims &out_strides) const;
     // The forward launch recorded as one graph node whose backward runs the
     // gradient program `bwd` (all input gradients in one kernel).
-    Tensor launch_with_grad(const std::vector<Tensor> &inputs, const Dims &out_shape, const Dims &out_strides,
+    Tensor launch_with_grad(const std::vector<FusedArg> &inputs, const Dims &out_shape, const Dims &out_strides,
                             const FusedBackward &bwd) const;
 };
 

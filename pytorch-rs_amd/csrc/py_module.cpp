@@ -178,6 +178,21 @@ std::vector<int64_t> dims_arg(const py::args &args) {
 
 }  // namespace
 
+// A fused program's arguments: tensors, or byte buffers for `in u8` operands.
+static std::vector<FusedArg> fused_args(const py::sequence &inputs) {
+    std::vector<FusedArg> out;
+    for (const py::handle &h : inputs) {
+        if (py::isinstance<Tensor>(h)) {
+            out.push_back(FusedArg{h.cast<Tensor>(), nullptr});
+        } else if (py::isinstance<ByteBuffer>(h)) {
+            out.push_back(FusedArg{Tensor{}, h.cast<BytePtr>()});
+        } else {
+            throw py::type_error("fused program arguments must be Tensors or ByteBuffers");
+        }
+    }
+    return out;
+}
+
 PYBIND11_MODULE(_trs_native, m) {
     m.doc() = "C++ host engine of the MI355X pytorch-rs backend (tensors, views, autograd) over libtrs_hip.so";
 
@@ -301,11 +316,14 @@ PYBIND11_MODULE(_trs_native, m) {
         .def_static("compile", &FusedProgram::compile)
         .def_property_readonly("id", [](const FusedProgram &p) { return p.id; })
         .def_property_readonly("nin", [](const FusedProgram &p) { return p.nin; })
-        .def("launch", &FusedProgram::launch)
+        .def("launch",
+             [](const FusedProgram &p, const py::sequence &inputs, const Dims &shape, const Dims &strides) {
+                 return p.launch(fused_args(inputs), shape, strides);
+             })
         .def("launch_with_grad",
-             [](const FusedProgram &p, const std::vector<Tensor> &inputs, const Dims &shape, const Dims &strides,
+             [](const FusedProgram &p, const py::sequence &inputs, const Dims &shape, const Dims &strides,
                 uint64_t program, const std::vector<int> &args, const std::vector<int> &targets) {
-                 return p.launch_with_grad(inputs, shape, strides, FusedBackward{program, args, targets});
+                 return p.launch_with_grad(fused_args(inputs), shape, strides, FusedBackward{program, args, targets});
              });
 
     // The restated layout planner, exposed for the CPU parity tests.

@@ -1,7 +1,9 @@
 """torch_rs.fuse -- the pointwise fusion front end.
 
 ``fuse(fn)`` traces ``fn`` (a function of tensors built from + - * /, scalar
-operands, exp, relu and neg) into the pointwise IR of libtrs_hip.so's
+operands, exp, relu and neg; a device byte buffer such as a dropout keep-mask
+may stand in for a tensor and is read as 0/1 floats) into the pointwise IR of
+libtrs_hip.so's
 fusion compiler, which emits HIP C++ and compiles it with hipRTC for gfx950
 into ONE kernel.  Every IR instruction rounds exactly as the eager op it
 stands for, so the fused result is the eager chain's result (bit for bit
@@ -45,10 +47,11 @@ class _Trace:
     """Instructions in definition order: ("in", i), ("const", bits), (op, a[, b]);
     `shapes` holds the eager shape of every traced (non-constant) value."""
 
-    def __init__(self):
+    def __init__(self, u8=()):
         self.ins: list[tuple] = []
         self.consts: dict[str, int] = {}
         self.shapes: dict[int, tuple] = {}
+        self.u8 = set(u8)  # input positions read as bytes ("in u8")
 
     def emit(self, *instr) -> int:
         self.ins.append(instr)
@@ -103,7 +106,7 @@ class _Trace:
         for v in inputs:
             new_id[v] = len(lines)
             used_inputs.append(self.ins[v][1])
-            lines.append("in f32")
+            lines.append("in u8" if self.ins[v][1] in self.u8 else "in f32")
         for v, ins in enumerate(self.ins):
             if v not in live or ins[0] == "in":
                 continue
@@ -234,7 +237,7 @@ def _gradient_program(tr, out, requires, out_shape):
             return None
 
     n_in = len(requires)  # the upstream gradient's argument slot
-    bt = _Trace()
+    bt = _Trace(tr.u8)
     fwd = {}
     for u in live:  # the forward values, recomputed
         i = ins[u]
@@ -287,10 +290,10 @@ class Fused:
         functools.update_wrapper(self, fn)
 
     def _trace(self, inputs):
-        tr = _Trace()
+        tr = _Trace(i for i, t in enumerate(inputs) if isinstance(t, _C.ByteBuffer))
         proxies = []
         for i, t in enumerate(inputs):
-            proxies.append(_Proxy(tr, tr.emit("in", i), t.shape, t.stride()))
+            proxies.append(_Proxy(tr, tr.emit("in", i), t.shape, _strides(t)))
         out = self.fn(*proxies)
         if not isinstance(out, _Proxy):
             raise TypeError("a fused function must return a traced tensor expression")
@@ -306,7 +309,7 @@ class Fused:
         return ir, out.shape, out.strides, used
 
     def program(self, *inputs):
-        key = tuple((t.shape, t.stride()) for t in inputs)
+        key = _layout_key(inputs)
         hit = self._cache.get(key)
         if hit is None:
             ir, shape, strides, used = self.trace(*inputs)
@@ -318,8 +321,8 @@ class Fused:
         """None (eager autograd), _NO_GRAD, or the gradient program as
         (compiled program id, argument positions among the forward's inputs
         or -1 for the upstream, the forward input position of each output)."""
-        requires = tuple(bool(t.requires_grad) for t in inputs)
-        key = (tuple((t.shape, t.stride()) for t in inputs), requires)
+        requires = tuple(bool(getattr(t, "requires_grad", False)) for t in inputs)
+        key = (_layout_key(inputs), requires)
         if key in self._cache:
             return self._cache[key]
         tr, out = self._trace(inputs)
@@ -334,17 +337,29 @@ class Fused:
         return plan
 
     def __call__(self, *inputs):
-        if not inputs or not all(isinstance(t, _C.Tensor) for t in inputs):
-            raise TypeError("fused functions take tensors only (bind scalars in the function body)")
+        if not inputs or not all(isinstance(t, (_C.Tensor, _C.ByteBuffer)) for t in inputs):
+            raise TypeError("fused functions take tensors (or device byte buffers) only; bind scalars in the "
+                            "function body")
         prog, shape, strides, used, _ = self.program(*inputs)
         args = [inputs[i] for i in used]
-        if _C.is_grad_enabled() and any(t.requires_grad for t in inputs):
+        if _C.is_grad_enabled() and any(getattr(t, "requires_grad", False) for t in inputs):
             plan = self.grad_plan(*inputs)
             if plan is None:
                 return self.fn(*inputs)
             if plan != _NO_GRAD:
                 return prog.launch_with_grad(args, shape, strides, *plan)
         return prog.launch(args, shape, strides)
+
+
+def _strides(t) -> tuple:
+    if isinstance(t, _C.ByteBuffer):
+        return tuple(_L.contiguous_strides(list(t.shape)))
+    return t.stride()
+
+
+def _layout_key(inputs) -> tuple:
+    return tuple(("u8" if isinstance(t, _C.ByteBuffer) else "f32", tuple(t.shape), tuple(_strides(t)))
+                 for t in inputs)
 
 
 def fuse(fn):

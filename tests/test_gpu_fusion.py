@@ -423,3 +423,38 @@ def test_fused_backward_input_reaching_output_only_through_division():
     assert out_f._grad_fn_name == "FusedBackward0"
     assert xe.grad is None and xf.grad is None
     assert_bitwise_equal(tf.grad.numpy().ravel(), te.grad.numpy().ravel())
+
+
+def test_fused_dropout_activation_with_byte_mask_equals_eager_under_autograd():
+    """The MLP's activation, relu(z + b) then dropout-apply with a uint8
+    keep-mask, as one fused node reading the mask as bytes: output and
+    gradients equal eager F.dropout(relu(z + b), mask=...) bit for bit (the
+    backward is (up * f32(1/0.9)) * mask, then relu', as the eager VJPs)."""
+    import torch_rs
+    F = torch_rs.nn.functional
+    rng = np.random.default_rng(31)
+    R, C = 96, 257
+    zv = rng.standard_normal((R, C)).astype(np.float32)
+    zv[0, :4] = [0.0, -0.0, np.nan, np.inf]
+    bv = rng.standard_normal(C).astype(np.float32)
+    mv = (rng.random((R, C)) < 0.9).astype(np.uint8)
+    mask = F.keep_mask(mv, "cuda")
+    act = torch_rs.fuse(lambda z, b, m: ((z + b).relu() * m) * (1 / 0.9))
+
+    def run(fused):
+        z = torch_rs.tensor(zv, device="cuda").with_requires_grad(True)
+        b = torch_rs.tensor(bv, device="cuda")
+        w = torch_rs.tensor(rng_w, device="cuda")
+        d = act(z, b, mask) if fused else F.dropout((z + b).relu(), 0.1, training=True, mask=mask)
+        (d * w).sum().backward()
+        return d, z
+
+    rng_w = np.random.default_rng(32).standard_normal((R, C)).astype(np.float32)
+    de, ze = run(False)
+    df, zf = run(True)
+    assert df._grad_fn_name == "FusedBackward0"
+    assert_bitwise_equal(df.numpy().ravel(), de.numpy().ravel())
+    assert_bitwise_equal(zf.grad.numpy().ravel(), ze.grad.numpy().ravel())
+    # the mask stays a byte buffer: a second backward through the node raises
+    with pytest.raises(RuntimeError, match="backward through the graph a second time"):
+        df.sum().backward()
