@@ -274,10 +274,14 @@ PYBIND11_MODULE(_trs_native, m) {
         .def("clone", &Tensor::clone)
         .def("select", &Tensor::select)
         .def("__getitem__", [](const Tensor &t, int64_t i) { return t.select(i); })
-        .def("add", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Add, false); })
-        .def("sub", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Sub, false); })
-        .def("mul", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Mul, false); })
-        .def("div", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Div, false); })
+        .def("add", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Add, false); },
+             py::arg("other"))
+        .def("sub", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Sub, false); },
+             py::arg("other"))
+        .def("mul", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Mul, false); },
+             py::arg("other"))
+        .def("div", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Div, false); },
+             py::arg("other"))
         .def("__add__", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Add, false); })
         .def("__radd__", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Add, true); })
         .def("__sub__", [](const Tensor &t, const py::object &o) { return binary_operation(t, o, BinOp::Sub, false); })

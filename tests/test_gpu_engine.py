@@ -490,3 +490,59 @@ def test_scalar_operands_convert_to_f32_as_the_reference_does():
     assert (x - np.bool_(True)).numpy().tolist() == [0.0, -4.0]
     assert (np.float32(2) / x).numpy().tolist() == (np.float32(2) / np.float32([1.0, -3.0])).tolist()
     assert (x + np.int64(-7)).numpy().tolist() == [-6.0, -10.0]
+
+
+def test_mul_method_spellings_match_the_operator():
+    """tests/test_mul.py's cases on device tensors: Tensor.mul(other) and
+    mul(other=) equal `*` in values, strides and offset, for tensors and
+    every scalar kind, strided empties and special bit patterns; autograd
+    through the method equals the operator's."""
+    def same(a, b):
+        assert a.shape == b.shape and a.stride() == b.stride() and a.storage_offset() == b.storage_offset()
+        assert a.requires_grad == b.requires_grad
+        assert_bitwise_equal(vals(a), vals(b))
+
+    left = cuda(np.array([[[1.0, 4.0], [2.0, 5.0], [3.0, 6.0]]], np.float32)).transpose(0, 2)
+    right = cuda(np.array([[2.0], [3.0], [4.0]], np.float32))
+    same(left.mul(right), left * right)
+    same(left.mul(other=right), left * right)
+    view = left[1]
+    for s in (True, -2, 2.5, np.bool_(False), np.int64(3), np.float32(-0.0)):
+        same(view.mul(s), view * s)
+        same(view.mul(other=s), view * s)
+    empty = torch_rs.zeros((2, 0, 3), device="cuda").transpose(0, 2)
+    ones = torch_rs.ones((1, 1, 2), device="cuda")
+    same(empty.mul(other=ones), empty * ones)
+    special = cuda(np.array([0x00000000, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC12345], np.uint32).view(np.float32))
+    got, want = special.mul(-0.0), special * -0.0
+    assert got.shape == want.shape
+    assert_bitwise_equal(vals(got), vals(want))
+
+    ml = cuda(np.array([[2.0, 3.0]], np.float32), True)
+    mr = cuda(np.array([[5.0], [7.0], [11.0]], np.float32), True)
+    ol = cuda(np.array([[2.0, 3.0]], np.float32), True)
+    orr = cuda(np.array([[5.0], [7.0], [11.0]], np.float32), True)
+    mo = ml.transpose(0, 1).mul(other=mr.transpose(0, 1))
+    oo = ol.transpose(0, 1) * orr.transpose(0, 1)
+    same(mo, oo)
+    mo.sum().backward()
+    oo.sum().backward()
+    same(ml.grad, ol.grad)
+    same(mr.grad, orr.grad)
+    shared_m = cuda(np.array([2.0, -3.0], np.float32), True)
+    shared_o = cuda(np.array([2.0, -3.0], np.float32), True)
+    shared_m.mul(shared_m).sum().backward()
+    (shared_o * shared_o).sum().backward()
+    same(shared_m.grad, shared_o.grad)
+    assert vals(shared_m.grad).tolist() == [4.0, -6.0]
+    em = torch_rs.zeros((2, 0, 3), device="cuda", requires_grad=True)
+    eo = torch_rs.zeros((2, 0, 3), device="cuda", requires_grad=True)
+    em.mul(other=torch_rs.ones((1, 1, 3), device="cuda")).sum().backward()
+    (eo * torch_rs.ones((1, 1, 3), device="cuda")).sum().backward()
+    same(em.grad, eo.grad)
+    a = cuda(np.array([[1.0, 2.0]], np.float32), True)
+    b = cuda(np.array([[3.0], [4.0]], np.float32), True)
+    with torch_rs.no_grad():
+        assert not a.transpose(0, 1).mul(b.transpose(0, 1)).requires_grad
+        assert not a.mul(other=2.0).requires_grad
+    assert a.mul(b.transpose(0, 1)).requires_grad
