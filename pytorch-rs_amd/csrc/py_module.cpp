@@ -238,6 +238,8 @@ PYBIND11_MODULE(_trs_native, m) {
             return py::str(n);
         })
         .def("_storage_id", [](const Tensor &t) { return (uintptr_t)t.storage.get(); })
+        // Address of the first element (storage base + offset), as Tensor.data_ptr.
+        .def("data_ptr", [](const Tensor &t) { return (uintptr_t)(t.storage->data() + t.offset); })
         .def("with_requires_grad", &Tensor::with_requires_grad)
         // In place, as Tensor.requires_grad_ is: the same Python object, now a leaf.
         .def(

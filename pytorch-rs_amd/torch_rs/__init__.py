@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import builtins as _builtins
 import contextlib
+import operator as _operator
 
 import numpy as _np
 
@@ -178,7 +179,7 @@ def sum(input: Tensor) -> Tensor:  # noqa: A001
 
 
 def permute(input: Tensor, dims) -> Tensor:
-    return input.permute(tuple(dims))
+    return input.permute(dims)
 
 
 def transpose(input: Tensor, dim0: int, dim1: int) -> Tensor:
@@ -359,6 +360,103 @@ def _cuda(self, device=None):
     return _native_to(self, _device_str(d, "cuda"))
 
 
+_native_permute = Tensor.permute
+
+
+def _py_type_name(x) -> str:
+    if isinstance(x, Tensor):
+        return "Tensor"
+    t = type(x)
+    return t.__name__ if t.__module__ == "builtins" else f"{t.__module__}.{t.__qualname__}"
+
+
+def _is_dim(x) -> bool:
+    if isinstance(x, bool):
+        return False
+    try:
+        _operator.index(x)
+        return True
+    except TypeError:
+        return False
+
+
+def _permute_dims(args, kwargs) -> list:
+    """bind_permute_dimensions / parse_permute_dimensions (src/python.rs:9321-9510):
+    permute(*dims), permute(dims) with a tuple or list, or permute(dims=...)."""
+    keyword, error = None, None
+    for key, value in kwargs.items():
+        if key == "dims" and not args and keyword is None:
+            keyword = value
+        elif key == "dims":
+            error = error or TypeError("permute() got multiple values for argument 'dims'")
+        else:
+            error = error or TypeError(f"permute() got an unexpected keyword argument '{key}'")
+
+    def sequence(value, position):
+        where = f" (position {position})" if position is not None else ""
+        if not isinstance(value, (tuple, list)):
+            raise TypeError(f"permute(): argument 'dims'{where} must be tuple of ints, not {_py_type_name(value)}")
+        if value and not _is_dim(value[0]):
+            if position is None:
+                raise TypeError(f"permute(): argument 'dims' must be tuple of ints, not {_py_type_name(value)}")
+            raise TypeError(f"permute(): argument 'dims'{where} must be tuple of ints, but found element of type "
+                            f"{_py_type_name(value[0])} at pos 0")
+        return list(value)
+
+    if not args:
+        if keyword is None:
+            raise TypeError('permute() missing 1 required positional arguments: "dims"')
+        dims = sequence(keyword, None)
+    elif len(args) == 1:
+        if isinstance(args[0], (tuple, list)):
+            dims = sequence(args[0], 1)
+        elif _is_dim(args[0]):
+            dims = list(args)
+        else:
+            raise TypeError(f"permute(): argument 'dims' (position 1) must be tuple of ints, not "
+                            f"{_py_type_name(args[0])}")
+    else:
+        if not _is_dim(args[0]):
+            raise TypeError(f"permute() takes 1 positional argument but {len(args)} were given")
+        dims = list(args)
+    if error is not None:
+        raise error
+    out = []
+    for pos, d in enumerate(dims, 1):
+        try:
+            v = _operator.index(d)
+        except TypeError:
+            raise TypeError(f"permute(): argument 'dims' failed to unpack the object at pos {pos} with error "
+                            f"\"type must be tuple of ints,but got {_py_type_name(d)}\"") from None
+        if not -(2**63) <= v < 2**63:
+            raise TypeError(f"permute(): argument 'dims' failed to unpack the object at pos {pos} with error "
+                            "\"Overflow when unpacking long long\"")
+        out.append(v)
+    return out
+
+
+def _permute(self, *args, **kwargs):
+    """Tensor.permute (src/python.rs:823-831, 9512-9553): negative dims are
+    normalised here; the view itself is the engine's permute_axes."""
+    dims = _permute_dims(args, kwargs)
+    rank = len(self.shape)
+    if len(dims) != rank:
+        raise RuntimeError("permute(sparse_coo): number of dimensions in the tensor input does not match the length "
+                           f"of the desired ordering of dimensions i.e. input.dim() = {rank} is not equal to "
+                           f"len(dims) = {len(dims)}")
+    seen, normalized = set(), []
+    for d in dims:
+        if d < -rank or d >= rank:
+            raise IndexError(f"Dimension out of range (expected to be in range of [{-rank}, {rank - 1}], but got {d})")
+        d = d + rank if d < 0 else d
+        if d in seen:
+            raise RuntimeError("permute(): duplicate dims are not allowed.")
+        seen.add(d)
+        normalized.append(d)
+    return _native_permute(self, *normalized)
+
+
+Tensor.permute = _permute
 Tensor.device = property(_tensor_device)
 Tensor.is_cpu = property(lambda self: not self.is_cuda)
 Tensor.get_device = lambda self: -1 if not self.is_cuda else int(self._device_str.split(":")[1])

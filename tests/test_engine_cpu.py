@@ -604,3 +604,46 @@ def test_fusion_tracer_drops_dead_code_and_unused_inputs():
     g = torch_rs.fuse(lambda x, y: ((x + 1.0) * 3.0, y - x)[1])
     ir, _, _, used = g.trace(torch_rs.zeros(4), torch_rs.zeros(4))
     assert used == [0, 1] and "add" not in ir
+
+
+def test_permute_spellings_negative_dims_and_errors():
+    """tests/test_permute.py's forms (variadic, tuple, list, dims=; negative
+    dims normalised) and the binding's errors (src/python.rs:9321-9553)."""
+    base = torch_rs.zeros(2, 3, 4)
+    source = base.transpose(0, 2)[1]  # shape (3, 2), offset view
+    for view in (source.permute(-1, -2), source.permute((-1, -2)), source.permute([-1, -2]),
+                 source.permute(dims=(-1, -2)), source.permute(dims=[-1, -2])):
+        assert view.shape == (2, 3) and view.stride() == (source.stride()[1], source.stride()[0])
+        assert view.storage_offset() == source.storage_offset() and view.data_ptr() == source.data_ptr()
+    scalar = torch_rs.tensor([2.5, 3.5])[1]
+    for view in (scalar.permute(()), scalar.permute([]), scalar.permute(dims=()), scalar.permute(dims=[])):
+        assert view.shape == () and view.stride() == () and view.storage_offset() == 1
+    empty = torch_rs.zeros(4, 2, 0, 3).transpose(0, 3)[2]
+    view = empty.permute(-1, -3, -2)
+    assert view.shape == (4, 2, 0) and view.stride() == (empty.stride()[2], empty.stride()[0], empty.stride()[1])
+    assert torch_rs.permute(base, dims=(2, 0, 1)).shape == (4, 2, 3)
+    leaf = torch_rs.zeros(2, 3, 4).with_requires_grad(True)
+    assert leaf.permute(-1, 0, 1)._grad_fn_name == "PermuteBackward0"
+    cases = [
+        (lambda: base.permute(0, 1), RuntimeError,
+         "permute(sparse_coo): number of dimensions in the tensor input does not match the length of the desired "
+         "ordering of dimensions i.e. input.dim() = 3 is not equal to len(dims) = 2"),
+        (lambda: base.permute(0, 0, 1), RuntimeError, "permute(): duplicate dims are not allowed."),
+        (lambda: base.permute(0, -4, 1), IndexError,
+         "Dimension out of range (expected to be in range of [-3, 2], but got -4)"),
+        (lambda: base.permute(), TypeError, 'permute() missing 1 required positional arguments: "dims"'),
+        (lambda: base.permute((0, 1, 2), dims=(0, 1, 2)), TypeError,
+         "permute() got multiple values for argument 'dims'"),
+        (lambda: base.permute(dims=(0, 1, 2), axes=1), TypeError, "permute() got an unexpected keyword argument 'axes'"),
+        (lambda: base.permute("a"), TypeError, "permute(): argument 'dims' (position 1) must be tuple of ints, not str"),
+        (lambda: base.permute(("a", 1, 2)), TypeError,
+         "permute(): argument 'dims' (position 1) must be tuple of ints, but found element of type str at pos 0"),
+        (lambda: base.permute((0, "a", 2)), TypeError,
+         "permute(): argument 'dims' failed to unpack the object at pos 2 with error \"type must be tuple of ints,"
+         "but got str\""),
+        (lambda: base.permute(1.5, 0), TypeError, "permute() takes 1 positional argument but 2 were given"),
+    ]
+    for call, exc, msg in cases:
+        with pytest.raises(exc) as info:
+            call()
+        assert str(info.value) == msg
