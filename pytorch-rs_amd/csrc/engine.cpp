@@ -1559,6 +1559,17 @@ Tensor Tensor::grad() const {
     return out;
 }
 
+// Tensor::live_grad (src/tensor.rs:835-861): the leaf's gradient storage
+// itself, contiguous, with no graph history.  Later backward passes
+// accumulate into that storage in place, so the alias sees them.
+Tensor Tensor::live_grad() const {
+    if (!autograd || !autograd->leaf) throw TensorError("tensor has no gradient");
+    std::lock_guard<std::mutex> gl(autograd->grad_mu);
+    if (!autograd->grad) throw TensorError("tensor has no gradient");
+    const Dims &shp = autograd->leaf_shape;
+    return make_tensor(autograd->grad, shp, layout::contiguous_strides(shp), 0);
+}
+
 // ---- byte buffers (dropout masks) ----------------------------------------------------
 
 ByteBuffer::~ByteBuffer() {

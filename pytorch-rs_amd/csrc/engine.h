@@ -211,7 +211,8 @@ public:
     // autograd
     void backward() const;
     bool has_grad() const;
-    Tensor grad() const;
+    Tensor grad() const;       // a detached contiguous copy (Tensor::grad)
+    Tensor live_grad() const;  // an alias of the accumulated storage (Tensor::live_grad)
 
 private:
     Tensor binary_op(int op, const Tensor &o) const;

@@ -218,7 +218,7 @@ PYBIND11_MODULE(_trs_native, m) {
               return ByteBuffer::from_host(arr.data(), shape, Device::parse(device));
           });
 
-    py::class_<Tensor>(m, "Tensor")
+    py::class_<Tensor>(m, "Tensor", py::dynamic_attr())
         .def_property_readonly("shape", [](const Tensor &t) { return to_tuple(t.shape); })
         .def("_strides", [](const Tensor &t) { return to_tuple(t.strides); })
         .def("storage_offset", [](const Tensor &t) { return t.offset; })
@@ -238,6 +238,8 @@ PYBIND11_MODULE(_trs_native, m) {
             return py::str(n);
         })
         .def("_storage_id", [](const Tensor &t) { return (uintptr_t)t.storage.get(); })
+        .def("_autograd_id", [](const Tensor &t) { return (uintptr_t)t.autograd.get(); })
+        .def("_live_grad", &Tensor::live_grad)
         // Address of the first element (storage base + offset), as Tensor.data_ptr.
         .def("data_ptr", [](const Tensor &t) { return (uintptr_t)(t.storage->data() + t.offset); })
         .def("with_requires_grad", &Tensor::with_requires_grad)

@@ -269,7 +269,18 @@ def _grad_fn(self):
 
 
 def _grad(self):
-    return self._grad() if self._has_grad() else None
+    """Tensor.grad (src/python_tensor_leaf_grad.rs:50-66): None until a backward
+    reaches this leaf, then one cached tensor aliasing the accumulated
+    gradient, so a retained `.grad` sees later accumulation in place."""
+    key = self._autograd_id()
+    cached = self.__dict__.get("_grad_cache")
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    if not self._has_grad():
+        return None
+    g = self._live_grad()
+    self.__dict__["_grad_cache"] = (key, g)
+    return g
 
 
 _EXP_LOW, _EXP_HIGH = _np.float32(1e-4), _np.float32(1e16)

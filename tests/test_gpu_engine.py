@@ -546,3 +546,30 @@ def test_mul_method_spellings_match_the_operator():
         assert not a.transpose(0, 1).mul(b.transpose(0, 1)).requires_grad
         assert not a.mul(other=2.0).requires_grad
     assert a.mul(b.transpose(0, 1)).requires_grad
+
+
+def test_leaf_grad_is_one_live_object_that_sees_accumulation():
+    """tests/test_autograd.py's leaf contract: `.grad` is None before backward,
+    then the same object on every read, and a retained `.grad` shows the
+    next backward's accumulation (in place in the leaf's storage)."""
+    x = cuda(np.array([-2.0, 0.5, 3.0], np.float32), True)
+    assert x.grad is None
+    (x * x).sum().backward()
+    g = x.grad
+    assert g is x.grad and not g.requires_grad and g.is_leaf
+    assert vals(g).tolist() == [-4.0, 1.0, 6.0]
+    (x * x).sum().backward()
+    assert g is x.grad
+    assert vals(g).tolist() == [-8.0, 2.0, 12.0]
+    # a non-leaf has no .grad; a fresh leaf of the same values starts empty
+    y = x * 2.0
+    assert y.grad is None
+    z = x.detach().with_requires_grad(True)
+    assert z.grad is None
+    # repeated backward through a graph with no saved values accumulates
+    w = cuda(np.array([2.0, 3.0], np.float32), True)
+    loss = (w + 1.0).sum()
+    loss.backward()
+    kept = w.grad
+    loss.backward()
+    assert kept is w.grad and vals(kept).tolist() == [2.0, 2.0]
