@@ -624,9 +624,26 @@ Tensor Tensor::to(Device dev) const {
 
 // ---- graph recording ----------------------------------------------------------
 
+// SavedTensor::try_from_tensor (src/tensor.rs:2809-2825): storages are
+// immutable once written and are shared, except a leaf's accumulated
+// gradient, which later backward passes change in place: its values are
+// snapshotted (Storage::try_clone_for_saved), in stream order.
+static StoragePtr saved_values(const StoragePtr &st) {
+    if (!st->shared_gradient) return st;
+    StoragePtr copy = Storage::allocate(st->device, st->numel);
+    if (st->numel == 0) return copy;
+    if (st->device.is_cuda()) {
+        select_device(st->device);
+        check(trs_memcpy_d2d(copy->dptr, st->dptr, (size_t)st->numel * sizeof(float)));
+    } else {
+        copy->host = st->host;
+    }
+    return copy;
+}
+
 static SavedTensor save(const Tensor &t, bool values) {
     SavedTensor s;
-    if (values) s.values = t.storage;  // storages are immutable once written
+    if (values) s.values = saved_values(t.storage);
     s.values_required = values;
     s.shape = t.shape;
     s.strides = t.strides;
@@ -1534,6 +1551,7 @@ void Tensor::backward() const {
             if (n) check(trs_accumulate_f32(m.grad->dptr, lg.second.st->dptr, (size_t)n));
         } else {
             m.grad = lg.second.st;
+            m.grad->shared_gradient = true;
         }
     }
 }

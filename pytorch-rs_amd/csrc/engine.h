@@ -50,6 +50,9 @@ struct Storage {
     int64_t numel = 0;
     std::vector<float> host;
     float *dptr = nullptr;
+    // A leaf's accumulated gradient (StorageData::SharedGradient,
+    // src/storage.rs:7-18): later backward passes add into it in place.
+    bool shared_gradient = false;
     ~Storage();
     float *data() { return device.is_cuda() ? dptr : host.data(); }
     static std::shared_ptr<Storage> allocate(Device device, int64_t numel);

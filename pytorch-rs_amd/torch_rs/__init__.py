@@ -61,9 +61,20 @@ def _flatten(data):
     return flat, (len(seq),) + shape0
 
 
+def _requires_grad_arg(function: str, value, allow_none: bool) -> bool:
+    """parse_requires_grad / parse_factory_requires_grad (src/python.rs:4189-4215):
+    an exact builtin bool (or None where the factory allows it)."""
+    if value is None and allow_none:
+        return False
+    if type(value) is bool:
+        return value
+    raise TypeError(f"{function}(): argument 'requires_grad' must be bool, not {_py_type_name(value)}")
+
+
 def tensor(data, *, dtype=None, device=None, requires_grad=False) -> Tensor:
     """torch_rs.tensor (src/python.rs:4139-4170): float32 values from a
     number, a nested sequence, or any buffer/array (copied, row-major)."""
+    requires_grad = _requires_grad_arg("tensor", requires_grad, False)
     if dtype not in (None, float32):
         raise TypeError("torch_rs supports only float32 tensors")
     if isinstance(data, Tensor):
@@ -89,10 +100,15 @@ def ones(*shape, device=None, requires_grad=False) -> Tensor:
 
 
 def full(shape, fill_value, *, device=None, requires_grad=False) -> Tensor:
-    return _full("full", shape, fill_value, device, requires_grad)
+    return _full("full", (shape,), fill_value, device, requires_grad)
 
 
 def _full(function, shape, fill_value, device, requires_grad) -> Tensor:
+    """The size is one sequence or int (bind_creation_arguments,
+    src/python.rs:4527-4560), or, as in PyTorch, several ints."""
+    requires_grad = _requires_grad_arg(function, requires_grad, True)
+    if shape and not isinstance(shape[0], int) and len(shape) > 1:
+        raise TypeError(f"{function}() takes 1 positional argument but {len(shape)} were given")
     if len(shape) == 1 and not isinstance(shape[0], int):
         shape = tuple(shape[0])
     return _C.full([int(d) for d in shape], _np.float32(fill_value),
@@ -375,10 +391,18 @@ _native_permute = Tensor.permute
 
 
 def _py_type_name(x) -> str:
-    if isinstance(x, Tensor):
-        return "Tensor"
+    """python_type_name (src/python.rs:9635-9701): "Tensor" / "torch.device"
+    for the package's own types, else CPython's tp_name: the bare name for
+    classes defined in Python, "module.name" for extension types
+    (numpy.bool, numpy.float64)."""
     t = type(x)
-    return t.__name__ if t.__module__ == "builtins" else f"{t.__module__}.{t.__qualname__}"
+    if t is Tensor:
+        return "Tensor"
+    if t is device:
+        return "torch.device"
+    if t.__flags__ & (1 << 9) or t.__module__ == "builtins":  # Py_TPFLAGS_HEAPTYPE
+        return t.__name__
+    return f"{t.__module__}.{t.__name__}"
 
 
 def _is_dim(x) -> bool:

@@ -647,3 +647,33 @@ def test_permute_spellings_negative_dims_and_errors():
         with pytest.raises(exc) as info:
             call()
         assert str(info.value) == msg
+
+
+def test_requires_grad_arguments_are_builtin_bools():
+    """tests/test_autograd.py: tensor() takes an exact bool; zeros/ones/full
+    take an exact bool or None, keyword-only (src/python.rs:4189-4215)."""
+    class Truthy:
+        def __bool__(self):
+            return True
+
+    for bad, name in ((np.bool_(True), "numpy.bool"), (1, "int"), (0, "int"), (None, "NoneType"),
+                      ("true", "str"), (Truthy(), "Truthy")):
+        with pytest.raises(TypeError) as info:
+            torch_rs.tensor([1.0], requires_grad=bad)
+        assert str(info.value) == f"tensor(): argument 'requires_grad' must be bool, not {name}"
+    for fname in ("zeros", "ones"):
+        factory = getattr(torch_rs, fname)
+        assert not factory((), requires_grad=None).requires_grad
+        assert factory((2, 2), requires_grad=True).requires_grad
+        for bad, name in ((np.bool_(False), "numpy.bool"), (1, "int"), (1.0, "float"), (object(), "object"),
+                          (Truthy(), "Truthy")):
+            with pytest.raises(TypeError) as info:
+                factory((1,), requires_grad=bad)
+            assert str(info.value) == f"{fname}(): argument 'requires_grad' must be bool, not {name}"
+        with pytest.raises(TypeError) as info:
+            factory((1,), True)
+        assert str(info.value) == f"{fname}() takes 1 positional argument but 2 were given"
+        assert factory(2, 3).shape == (2, 3) and factory([2, 3]).shape == (2, 3)
+    assert torch_rs.full((2,), 1.5, requires_grad=None).shape == (2,)
+    with pytest.raises(TypeError, match=r"^full\(\): argument 'requires_grad' must be bool, not int$"):
+        torch_rs.full((2,), 1.5, requires_grad=1)

@@ -573,3 +573,19 @@ def test_leaf_grad_is_one_live_object_that_sees_accumulation():
     kept = w.grad
     loss.backward()
     assert kept is w.grad and vals(kept).tolist() == [2.0, 2.0]
+
+
+def test_saved_values_of_a_live_gradient_are_frozen_at_forward():
+    """tests/test_autograd.py: a product saved with a live `.grad` operand
+    keeps the values of forward time although the gradient accumulates in
+    place afterwards (SavedTensor::try_from_tensor snapshots shared-gradient
+    storage, src/tensor.rs:2809-2825)."""
+    source = cuda([4.0, 5.0], True)
+    source.sum().backward()
+    live = source.grad
+    weights = cuda([2.0, 3.0], True)
+    saved_loss = (weights * live).sum()
+    source.sum().backward()
+    assert vals(live).tolist() == [2.0, 2.0]
+    saved_loss.backward()
+    assert vals(weights.grad).tolist() == [1.0, 1.0]
