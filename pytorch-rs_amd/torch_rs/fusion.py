@@ -23,9 +23,9 @@ for relu, sign flips for neg and reflected sub; division records nothing, as
 in the reference).  Broadcast inputs are then reduced in the reference's
 order.  That reproduces eager autograd bit for bit when every value the
 gradient reaches has the output's shape, no such value feeds more than two
-gradient-carrying uses (two contributions add commutatively) and each input
-feeds exactly one; other programs run ``fn`` eagerly so autograd records op
-by op.
+gradient-carrying uses (two contributions add commutatively) and each
+broadcast input feeds at most one; other programs run ``fn`` eagerly so
+autograd records op by op.
 """
 from __future__ import annotations
 
@@ -230,10 +230,14 @@ def _gradient_program(tr, out, requires, out_shape):
                 reach.add(a)
                 uses[a] = uses.get(a, 0) + 1
     for v in reach:
+        full = tr.shapes.get(v) == tuple(out_shape)
         if ins[v][0] == "in":
-            if uses.get(v, 0) > 1:
+            # A broadcast input reduces each contribution on its own in eager
+            # autograd, so it may have only one; a full-shape input may have
+            # two, which add commutatively as the engine accumulates them.
+            if uses.get(v, 0) > (2 if full else 1):
                 return None
-        elif tr.shapes.get(v) != tuple(out_shape) or uses.get(v, 0) > 2:
+        elif not full or uses.get(v, 0) > 2:
             return None
 
     n_in = len(requires)  # the upstream gradient's argument slot

@@ -571,8 +571,16 @@ def test_fusion_backward_program_is_the_reverse_mode_of_the_ir():
     # x reaches the output only through a division: no gradient for x
     assert plan(lambda x, y, z, t: (x * y) / z + t, (True, False, False, True)) == ("in f32\nout %0\n", [-1], [3])
     assert plan(lambda x, y, z, t: (x * y) / z + t, (True, False, False, False)) == F._NO_GRAD
-    # an input with two gradient-carrying uses: eager
-    assert plan(lambda x, y: (x * y).exp() - x.relu(), (True, True)) is None
+    # a full-shape input with two gradient-carrying uses: its two
+    # contributions are summed in the program (x*x: up*x + up*x)
+    ir, args, targets = plan(lambda x, y: (x * y).exp() - x.relu(), (True, True))
+    assert targets == [0, 1]
+    assert plan(lambda x, y: x * x, (True, False)) == ("in f32\nin f32\nmul %1 %0\nmul %1 %0\nadd %2 %3\nout %4\n",
+                                                     [0, -1], [0])
+    # three uses, or two uses of a broadcast input: eager
+    assert plan(lambda x, y: x * x * x, (True, False)) is None
+    tr_b, out_b = torch_rs.fuse(lambda x, b: x * b + b)._trace((torch_rs.zeros(4, 3), torch_rs.zeros(3)))
+    assert F._gradient_program(tr_b, out_b.vid, (False, True), out_b.shape) is None
 
     def two_uses(x, y):
         s = x * y

@@ -458,3 +458,32 @@ def test_fused_dropout_activation_with_byte_mask_equals_eager_under_autograd():
     # the mask stays a byte buffer: a second backward through the node raises
     with pytest.raises(RuntimeError, match="backward through the graph a second time"):
         df.sum().backward()
+
+
+def test_fused_backward_input_with_two_uses_equals_eager():
+    """x feeds two gradient-carrying uses (x*y and the relu): the fused node
+    sums the two contributions at full shape, as eager accumulation does."""
+    import torch_rs
+    rng = np.random.default_rng(17)
+    shape = (33, 65)
+    xv, yv = (rng.standard_normal(shape).astype(np.float32) for _ in range(2))
+    fn = lambda x, y: (x * y).exp() - x.relu() + x * x
+
+    def run(f):
+        x = torch_rs.tensor(xv, device="cuda").with_requires_grad(True)
+        y = torch_rs.tensor(yv, device="cuda").with_requires_grad(True)
+        out = f(x, y)
+        out.sum().backward()
+        return out, x, y
+
+    oe, xe, ye = run(fn)
+    of, xf, yf = run(torch_rs.fuse(lambda x, y: (x * y).exp() - x.relu()))
+    assert of._grad_fn_name == "FusedBackward0"
+    oe2, xe2, ye2 = run(lambda x, y: (x * y).exp() - x.relu())
+    assert_bitwise_equal(of.numpy().ravel(), oe2.numpy().ravel())
+    assert_bitwise_equal(xf.grad.numpy().ravel(), xe2.grad.numpy().ravel())
+    assert_bitwise_equal(yf.grad.numpy().ravel(), ye2.grad.numpy().ravel())
+    sq_e = run(lambda x, y: x * x)
+    sq_f = run(torch_rs.fuse(lambda x, y: x * x))
+    assert sq_f[0]._grad_fn_name == "FusedBackward0" and sq_f[2].grad is None
+    assert_bitwise_equal(sq_f[1].grad.numpy().ravel(), sq_e[1].grad.numpy().ravel())
