@@ -1,8 +1,10 @@
-"""torch_rs.nn.functional -- relu and dropout (python/torch_rs/nn/functional.py:108-143,
-src/python_nn_functional.rs:117-200)."""
-from __future__ import annotations
+"""Functional interface."""
+# torch_rs.nn.functional: relu and the dropout family, as the reference's
+# python/torch_rs/nn/functional.py:1-265 and src/python_nn_functional.rs:13-200.
+# The module docstring, relu's docstring and signature are the reference's.
 
 import math
+import sys as _sys
 import warnings
 
 import numpy as _np
@@ -10,10 +12,20 @@ import numpy as _np
 from .._native import native as _C
 
 
-def relu(input, inplace: bool = False):
+def relu(input: _C.Tensor, inplace: bool = False) -> _C.Tensor:
     if inplace:
         raise NotImplementedError("torch_rs.nn.functional.relu does not support inplace=True")
     return input.relu()
+
+
+relu.__doc__ = ("relu(input, inplace=False) -> Tensor\n\n"
+                "Applies the rectified linear unit function element-wise. See\n"
+                ":class:`~torch.nn.ReLU` for more details.\n") if _sys.version_info >= (3, 13) else (
+    """relu(input, inplace=False) -> Tensor
+
+    Applies the rectified linear unit function element-wise. See
+    :class:`~torch.nn.ReLU` for more details.
+    """)
 
 
 def _autograd_suffix(t) -> str:
