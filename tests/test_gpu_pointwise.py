@@ -212,3 +212,62 @@ def test_shape_mismatch_is_an_error_not_a_launch():
                                 ctypes.byref(abi.layout_of((4,))), out.ptr, ctypes.byref(abi.layout_of((2, 2))))
     assert rc == -4
     assert "must match the size of tensor" in abi.lib.trs_last_error().decode()
+
+
+def _random_layout_view(rng, shape):
+    """A view of `shape` with a random physical dim order, inner stride 1 or
+    2, random gaps between dims and a random offset."""
+    r = len(shape)
+    perm = rng.permutation(r)
+    strides = [0] * r
+    step = int(rng.integers(1, 3))
+    for d in reversed(perm):
+        strides[d] = step
+        step *= max(shape[d], 1) + int(rng.integers(0, 2))
+    return _view(rng, shape, strides, int(rng.integers(0, 3)))
+
+
+def _random_broadcast_shape(rng, oshape):
+    """A right-aligned operand shape that broadcasts to oshape."""
+    rank = int(rng.integers(0, len(oshape) + 1))
+    return tuple(1 if rng.random() < 0.3 else d for d in oshape[len(oshape) - rank:])
+
+
+@pytest.mark.parametrize("op", [O.ADD, O.SUB, O.MUL, O.DIV])
+def test_random_layouts_binary_bit_exact(op):
+    """150 random layouts per op (rank 1-5, size-1 and broadcast dims,
+    permuted strides with gaps, offsets): the host planner's dim dropping,
+    ordering and merging plus every kernel variant agree with the oracle bit
+    for bit."""
+    rng = np.random.default_rng(4242 + op)
+    for case in range(150):
+        rank = int(rng.integers(1, 6))
+        oshape = tuple(int(rng.choice([1, 2, 3, 5, 8, 17])) for _ in range(rank))
+        ash, bsh = _random_broadcast_shape(rng, oshape), _random_broadcast_shape(rng, oshape)
+        if rng.random() < 0.5:
+            ash = oshape
+        a, ash, ast, aoff = _random_layout_view(rng, ash)
+        b, bsh, bst, boff = _random_layout_view(rng, bsh)
+        osh, ostr = O.binary_output_layout(ash, ast, bsh, bst)
+        want = O.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ostr)
+        got = U.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ostr)
+        try:
+            assert_bitwise_equal(got, want)
+        except AssertionError as e:
+            raise AssertionError(f"case {case}: a {ash} {ast} +{aoff}, b {bsh} {bst} +{boff}: {e}") from None
+
+
+@pytest.mark.parametrize("op", [O.RELU, O.NEG])
+def test_random_layouts_unary_bit_exact(op):
+    rng = np.random.default_rng(777 + op)
+    for case in range(150):
+        rank = int(rng.integers(0, 6))
+        shape = tuple(int(rng.choice([1, 2, 3, 5, 8, 17])) for _ in range(rank))
+        a, sh, st, off = _random_layout_view(rng, shape) if rank else _view(rng, ())
+        ostr = O.unary_output_strides(sh, st)
+        want = O.unary(op, a, sh, st, off, ostr)
+        got = U.unary(op, a, sh, st, off, ostr)
+        try:
+            assert_bitwise_equal(got, want, nan_equal=False)  # relu and neg are exact on NaNs too
+        except AssertionError as e:
+            raise AssertionError(f"case {case}: {sh} {st} +{off}: {e}") from None
