@@ -166,3 +166,46 @@ def test_accumulate_and_fill():
     src = U.dev(np.array([2.5], np.float32))
     check(abi.lib.trs_fill_from_device_f32(da.ptr, 77, src.ptr))
     assert (da.to_numpy(count=77) == 2.5).all()
+
+
+def _rand_bshape(rng, oshape):
+    rank = int(rng.integers(0, len(oshape) + 1))
+    return tuple(1 if rng.random() < 0.35 else d for d in oshape[len(oshape) - rank:])
+
+
+def _rand_strides(rng, shape):
+    r = len(shape)
+    perm = rng.permutation(r)
+    strides = [0] * r
+    step = 1
+    for d in reversed(perm):
+        strides[d] = step
+        step *= max(shape[d], 1) + int(rng.integers(0, 2))
+    return tuple(strides)
+
+
+def test_random_broadcast_mul_vjp_and_reduce_bit_exact():
+    """150 random (output, other, self) broadcast shapes of rank 0-5 with the
+    other operand in random layouts: the mul VJP and the add VJP's
+    reduce_to_shape accumulate in the reference's order (from +0.0 over the
+    reduced dims in output row-major order, or as-is with no broadcast) bit
+    for bit."""
+    rng = np.random.default_rng(515)
+    for case in range(150):
+        rank = int(rng.integers(0, 6))
+        oshape = tuple(int(rng.choice([1, 2, 3, 4, 7, 9])) for _ in range(rank))
+        self_shape = _rand_bshape(rng, oshape)
+        oth_shape = _rand_bshape(rng, oshape) if rng.random() < 0.6 else oshape
+        oth_strides = _rand_strides(rng, oth_shape)
+        oth_off = int(rng.integers(0, 3))
+        n = int(np.prod(oshape)) if oshape else 1
+        up = U.special_mix(rng, max(n, 1))[:n]
+        other = U.special_mix(rng, max(O.storage_size(oth_shape, oth_strides, oth_off), 1))
+        try:
+            want = O.mul_backward(up, oshape, other, oth_shape, oth_strides, oth_off, self_shape)
+            got = gpu_mul_backward(up, oshape, other, oth_shape, oth_strides, oth_off, self_shape)
+            assert_bitwise_equal(got, want)
+            assert_bitwise_equal(gpu_reduce(up, oshape, self_shape), O.reduce_to_shape(up, oshape, self_shape))
+        except AssertionError as e:
+            raise AssertionError(f"case {case}: out {oshape}, other {oth_shape} {oth_strides} +{oth_off}, "
+                                 f"self {self_shape}: {e}") from None
