@@ -151,3 +151,31 @@ def test_large_tile_all_layouts_exact_on_small_integers(ta, tb):
     bst, boff = (np.ascontiguousarray(b.T), (1, k)) if tb else (b, (n, 1))
     got = U.matmul(ast.ravel(), (m, k), aoff, 0, bst.ravel(), (k, n), boff, 0)
     assert np.array_equal(got, want)
+
+
+def test_random_shapes_layouts_and_offsets_exact_on_small_integers():
+    """40 random products: M, N, K in 1-300 (ragged edge tiles), each operand
+    plain or transposed (.mT) and at a random storage offset, rank 2 or a
+    batch of 1-3.  Small-integer entries make every partial sum exact, so the
+    GPU result equals the integer product bit for bit."""
+    rng = np.random.default_rng(808)
+    for case in range(40):
+        m, k, n = (int(rng.integers(1, 301)) for _ in range(3))
+        batch = int(rng.integers(1, 4)) if rng.random() < 0.4 else 0
+        ta, tb = bool(rng.random() < 0.5), bool(rng.random() < 0.5)
+        oa, ob = int(rng.integers(0, 5)), int(rng.integers(0, 5))
+        nb = max(batch, 1)
+        a = rng.integers(-3, 4, size=(nb, m, k)).astype(np.float32)
+        b = rng.integers(-3, 4, size=(nb, k, n)).astype(np.float32)
+        sa = np.concatenate([np.zeros(oa, np.float32), (np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a).ravel()])
+        sb = np.concatenate([np.zeros(ob, np.float32), (np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b).ravel()])
+        ast = (1, m) if ta else (k, 1)
+        bst = (1, k) if tb else (n, 1)
+        if batch:
+            la = ((batch, m, k), (m * k,) + ast, oa)
+            lb = ((batch, k, n), (k * n,) + bst, ob)
+        else:
+            la, lb = ((m, k), ast, oa), ((k, n), bst, ob)
+        got = U.matmul(sa, *la, sb, *lb).reshape(-1)
+        want = np.matmul(a.astype(np.int64), b.astype(np.int64)).astype(np.float32).reshape(-1)
+        assert np.array_equal(got, want), (case, m, k, n, batch, ta, tb, oa, ob)
