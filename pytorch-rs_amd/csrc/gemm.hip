@@ -9,8 +9,9 @@
 //
 // Tiling: a block of WGM x WGN waves owns a BM x BN tile of C; each wave owns
 // (BM/WGM) x (BN/WGN) as a grid of 16x16 MFMA tiles held in accumulators.
-// Three shapes are used: 256x256x16 with 16 waves (one block per CU, 4 waves
-// per SIMD) when the output has at least one such tile per CU; else
+// Three shapes are used: 256x256x32 with 16 waves (one block per CU, 4 waves
+// per SIMD, 140 KB of LDS) when the output has at least one such tile per CU
+// and K is a multiple of 32; else
 // 128x128x32 with 4 waves (two blocks per CU), or 64x128x32 when 128x128
 // would give fewer than two blocks per CU.  Measured on the MI355X at 4096^3:
 // 84-88% of the FP32 MFMA peak for the large shape in every operand layout,
@@ -184,7 +185,10 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
         const bool more = s + 1 < kslices;
         if (more) load_slice((s + 1) * BK);
         if constexpr (VK) {
-#pragma unroll
+            // Kept rolled: unrolled, the groups' fragment reads are all
+            // hoisted and BK=32 spills at 16 waves; rolled, one barrier per
+            // 32 k measured ~1% faster than BK=16 at 4096^3.
+#pragma unroll 1
             for (int kg = 0; kg < BK; kg += 16) {
                 const int k4 = kg + 4 * fk;  // first of this lane's 4 k in the group
                 vf4 a4[TM], b4[TN];
@@ -287,7 +291,10 @@ struct Tiles {
 // The large and medium tiles run only on shapes they divide.  Float4
 // fragment reads measured +0.9% (NT) to -0.1% on the large tile and -2 to -3%
 // on the 4-wave tiles, so only the large tile uses them.
-using LargeTiles = Tiles<256, 256, 16, 4, 4, 1, true, false>;
+using LargeTiles = Tiles<256, 256, 32, 4, 4, 1, true, false>;
+// The NT layout (B transposed) holds more fragment registers and spills at
+// BK=32 with 16 waves; it keeps BK=16.
+using LargeTilesNT = Tiles<256, 256, 16, 4, 4, 1, true, false>;
 using SmallTiles = Tiles<128, 128, 32, 2, 2, 2, false, true>;
 using MediumTiles = Tiles<64, 128, 32, 2, 2, 2, false, false>;  // halves M per block when 128x128 leaves CUs idle
 
@@ -320,6 +327,14 @@ int launch_layout(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipS
     if (a_plain) return launch_tiled<T, false, true>(g, full, s);
     if (b_plain) return launch_tiled<T, true, false>(g, full, s);
     return launch_tiled<T, true, true>(g, full, s);
+}
+
+// The large tile in each layout (full tiles only).
+int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
+    if (a_plain && b_plain) return launch_tiled<LargeTiles, false, false>(g, true, s);
+    if (a_plain) return launch_tiled<LargeTilesNT, false, true>(g, true, s);
+    if (b_plain) return launch_tiled<LargeTiles, true, false>(g, true, s);
+    return launch_tiled<LargeTiles, true, true>(g, true, s);
 }
 
 }  // namespace
@@ -400,9 +415,10 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
     // The large tile only when it divides the problem and still gives every
     // CU a block; otherwise the small tile (full or edge-guarded).
     const int64_t large_tiles = (M / LargeTiles::BM) * (N / LargeTiles::BN) * batch;
-    if (aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0 && K % LargeTiles::BK == 0 &&
+    const int64_t large_bk = (a_plain && !b_plain) ? LargeTilesNT::BK : LargeTiles::BK;
+    if (aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0 && K % large_bk == 0 &&
         large_tiles >= dev->cu_count)
-        return launch_layout<LargeTiles>(g, a_plain, b_plain, true, dev->stream);
+        return launch_large(g, a_plain, b_plain, dev->stream);
     const bool full = aligned && M % SmallTiles::BM == 0 && N % SmallTiles::BN == 0 && K % SmallTiles::BK == 0;
     // Fewer than two 128x128 blocks per CU (e.g. a 4096x1024 weight gradient
     // with K = 8192): 64x128 blocks double the count (76% against 69% of peak
