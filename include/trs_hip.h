@@ -202,7 +202,8 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
  * Operands may be transposed views (unit stride in either matrix dim,
  * e.g. `.mT`); other strides are packed first.  `lc` must be contiguous.
  * Tolerance versus the reference's sequential order: |dC| <= 1e-5*sqrt(K) *
- * (|A||B|) elementwise. */
+ * (|A||B|) elementwise.  Empty outputs launch nothing; K = 0 writes +0.0 and
+ * then the operands may be null (src/tensor.rs:4817-4839). */
 int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
                    float *c, const trs_layout *lc);
 

@@ -368,7 +368,8 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
         return set_error(TRS_E_SHAPE_MISMATCH, "matmul output layout has the wrong shape");
     if (!layout_is_contiguous(lc)) return set_error(TRS_E_INVALID_ARGUMENT, "matmul output must be contiguous");
     if (M == 0 || N == 0 || batch == 0) return TRS_OK;
-    if (!a || !b || !c) return set_error(TRS_E_INVALID_ARGUMENT, "null matmul operand");
+    // With K = 0 the operands are empty (no storage is needed) and C is +0.0.
+    if (!c || (K > 0 && (!a || !b))) return set_error(TRS_E_INVALID_ARGUMENT, "null matmul operand");
     {
         // C is written while A and B are still being read: no shared memory.
         const ByteRange out_bytes = byte_range(c, lc, 4);

@@ -179,3 +179,46 @@ def test_random_shapes_layouts_and_offsets_exact_on_small_integers():
         got = U.matmul(sa, *la, sb, *lb).reshape(-1)
         want = np.matmul(a.astype(np.int64), b.astype(np.int64)).astype(np.float32).reshape(-1)
         assert np.array_equal(got, want), (case, m, k, n, batch, ta, tb, oa, ob)
+
+
+def test_special_values_propagate_as_the_reference():
+    """src/tensor.rs:4711-4815 vectors on the GPU: NaN and signed-infinity
+    positions equal the oracle's exactly; finite elements are within the
+    matmul tolerance.  Element 0 of the first product (1e20 - 1e20 + 1) may
+    legitimately differ from the sequential 1.0, by cancellation in MFMA
+    order, within the bound 1e-5*sqrt(K)*(|A||B|)."""
+    from helpers import f32_from_bits
+    g = G["matmul_contiguous_specials"]
+    cases = [(f32_from_bits(g["left_bits"]).reshape(2, 3), f32_from_bits(g["right_bits"]).reshape(3, 3))]
+    g = G["matmul_blocked_pattern"]
+    rows, inner, cols, fb = g["rows"], g["inner"], g["columns"], g["finite_bits"]
+    left = f32_from_bits([fb[(i * 5 + i // inner) % 8] for i in range(rows * inner)]).reshape(rows, inner)
+    special = {(3, 7): 0x7F800000, (4, 11): 0xFF800000, (5, 13): 0x7FC12345}
+    right = f32_from_bits([special.get((c % 8, d), fb[(d * 3 + c) % 8]) for d in range(inner) for c in range(cols)])
+    cases.append((left, right.reshape(inner, cols)))
+    for a, b in cases:
+        m, k = a.shape
+        n = b.shape[1]
+        got = U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+        want = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(np.isposinf(got), np.isposinf(want))
+        assert np.array_equal(np.isneginf(got), np.isneginf(want))
+        fin = np.isfinite(want)
+        with np.errstate(invalid="ignore", over="ignore"):
+            bound = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+        tol = 1e-5 * np.sqrt(k) * bound
+        assert (np.abs(got[fin].astype(np.float64) - want[fin].astype(np.float64)) <= tol[fin]).all()
+
+
+def test_empty_dimensions_on_the_device():
+    """src/tensor.rs:4817-4839 through torch_rs on the GPU: empty outputs
+    keep their shapes; K = 0 gives +0.0 everywhere (no launch reads A or B)."""
+    import torch_rs
+    no_rows = torch_rs.zeros((0, 3), device="cuda") @ torch_rs.ones((3, 4), device="cuda")
+    assert no_rows.shape == (0, 4) and no_rows.numel() == 0
+    no_cols = torch_rs.ones((2, 3), device="cuda") @ torch_rs.zeros((3, 0), device="cuda")
+    assert no_cols.shape == (2, 0) and no_cols.numel() == 0
+    no_inner = torch_rs.ones((2, 0), device="cuda") @ torch_rs.zeros((0, 4), device="cuda")
+    assert no_inner.shape == (2, 4)
+    assert (no_inner.numpy().view(np.uint32) == 0).all()

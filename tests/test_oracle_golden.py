@@ -243,3 +243,61 @@ def test_permute_vjp_transform():
     # reshape-copy of the transposed [3,2] view: gradient (= weights) maps back through permute [1,0].
     grad = O.permute_backward(w, (3, 2), (1, 0), (2, 3))
     assert grad.tolist() == g["leaf_grad"]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).ravel()
+
+
+def test_matmul_paths_agree_on_special_values():
+    """src/tensor.rs:4711-4886: every matmul path gives the same bits (NaN
+    payloads included) on inf/NaN/huge-cancellation inputs, with the pinned
+    elements: the oracle's general strided loop and the reference's 4-row
+    blocked loop agree, and element 0 is 1e20 + (-1e20) + 1 = 1.0."""
+    g = G["matmul_contiguous_specials"]
+    a = f32_from_bits(g["left_bits"]).reshape(g["left_shape"])
+    b = f32_from_bits(g["right_bits"]).reshape(g["right_shape"])
+    plain = O.matmul(a.ravel(), (2, 3), (3, 1), 0, b.ravel(), (3, 3), (3, 1), 0)
+    assert int(_bits(plain)[0]) == g["expected_first_bits"]
+    assert np.array_equal(_bits(plain), _bits(O.matmul_row_blocked(a, b)))
+
+    g = G["matmul_blocked_pattern"]
+    rows, inner, cols, fb = g["rows"], g["inner"], g["columns"], g["finite_bits"]
+    left = f32_from_bits([fb[(i * 5 + i // inner) % 8] for i in range(rows * inner)]).reshape(rows, inner)
+
+    def rbits(d, c):
+        if c % 8 == 3 and d == 7:
+            return 0x7F800000
+        if c % 8 == 4 and d == 11:
+            return 0xFF800000
+        if c % 8 == 5 and d == 13:
+            return 0x7FC12345
+        return fb[(d * 3 + c) % 8]
+
+    right = f32_from_bits([rbits(d, c) for d in range(inner) for c in range(cols)]).reshape(inner, cols)
+    plain = O.matmul(left.ravel(), (rows, inner), (inner, 1), 0, right.ravel(), (inner, cols), (cols, 1), 0)
+    blocked = O.matmul_row_blocked(left, right)
+    assert np.array_equal(_bits(plain), _bits(blocked))
+    assert np.isnan(blocked[:, 5]).all() and np.isnan(blocked).sum() >= rows
+
+    g = G["matmul_strided_specials"]
+    lay = g["layout"]
+    ls = np.concatenate([np.zeros(9, np.float32), f32_from_bits(g["left_bits"])])
+    rs = np.concatenate([np.zeros(9, np.float32), f32_from_bits(g["right_bits"])])
+    strided = O.matmul(ls, tuple(lay["shape"]), tuple(lay["strides"]), lay["offset"],
+                       rs, tuple(lay["shape"]), tuple(lay["strides"]), lay["offset"])
+    assert int(_bits(strided)[3]) == g["expected_index3_bits"]
+    lc = f32_from_bits(g["left_bits"]).reshape(3, 3).T
+    rc = f32_from_bits(g["right_bits"]).reshape(3, 3).T
+    assert np.array_equal(_bits(strided), _bits(O.matmul_row_blocked(lc, rc)))
+
+
+def test_matmul_empty_dimensions():
+    """src/tensor.rs:4817-4839: empty outputs stay empty; K = 0 gives +0.0."""
+    for case in G["matmul_empty_dims"]["cases"]:
+        (m, k), (_, n) = case["left"], case["right"]
+        out = O.matmul(np.zeros(max(m * k, 1), np.float32), (m, k), (max(k, 1), 1), 0,
+                       np.zeros(max(k * n, 1), np.float32), (k, n), (max(n, 1), 1), 0)
+        assert out.size == m * n
+        if "all_bits" in case:
+            assert (_bits(out) == case["all_bits"]).all()
