@@ -271,3 +271,29 @@ def test_random_layouts_unary_bit_exact(op):
             assert_bitwise_equal(got, want, nan_equal=False)  # relu and neg are exact on NaNs too
         except AssertionError as e:
             raise AssertionError(f"case {case}: {sh} {st} +{off}: {e}") from None
+
+
+def test_reference_fast_path_vectors_on_gpu():
+    """The operands of src/tensor.rs:4887-5024 (signalling NaNs, infinities,
+    signed zeros and denormals; an offset transposed view, a rank-mixing
+    broadcast, a row view and an offset rank-0 NaN) through every binary op:
+    the planner's output strides, including [1, 3] for strided + row
+    (src/tensor.rs:5015), and values bit-exact against the oracle (any NaN
+    equals any NaN, as the payload is the ISA's)."""
+    def strided(bits):  # offset_strided_matrix (src/tensor.rs:4700-4709)
+        return (np.concatenate([np.zeros(9, np.float32), f32_from_bits(bits)]), (3, 3), (1, 3), 9)
+
+    left = strided([0x7F812345, 0xFFC54321, 0x7F800000, 0xFF800000, 0x0, 0x80000000, 0x1, 0x80000001, 0x3F800000])
+    right = strided([0xFF854321, 0x7FC12345, 0xFF800000, 0x7F800000, 0x80000000, 0x0, 0x80000001, 0x1, 0xBF800000])
+    bcast_l = (f32_from_bits([0x7F812345, 0xFFC54321, 0x7F800000, 0xFF800000, 0x0, 0x80000000]), (2, 1, 3), (3, 3, 1), 0)
+    bcast_r = (f32_from_bits([0xFF854321, 0x80000001]), (1, 2, 1), (2, 1, 1), 0)
+    row = (f32_from_bits([0, 0, 0, 0xFF854321, 0x80000001, 0xBF800000]), (3,), (1,), 3)
+    nan_scalar = (f32_from_bits([0, 0xFF812345]), (), (), 1)
+    pairs = [(left, right), (bcast_l, bcast_r), (left, row), (nan_scalar, left), (left, nan_scalar)]
+    assert O.binary_output_layout(left[1], left[2], row[1], row[2])[1] == (1, 3)
+    for (a, ash, ast, aoff), (b, bsh, bst, boff) in pairs:
+        osh, ostr = O.binary_output_layout(ash, ast, bsh, bst)
+        for op in (O.ADD, O.SUB, O.MUL, O.DIV):
+            want = O.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ostr)
+            got = U.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ostr)
+            assert_bitwise_equal(got, want)
