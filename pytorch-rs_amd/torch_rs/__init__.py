@@ -521,5 +521,5 @@ Tensor.__array_priority__ = 1000.0  # numpy operands defer to the tensor's refle
 Tensor.__bool__ = _bool
 Tensor.multiply = Tensor.mul
 
-from . import accelerator, autograd, cuda, nn  # noqa: E402,F401
+from . import accelerator, autograd, compiler, cuda, nn  # noqa: E402,F401
 from .fusion import fuse  # noqa: E402,F401

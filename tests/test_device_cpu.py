@@ -163,3 +163,31 @@ def test_accelerator_discovery_goes_through_one_probe(monkeypatch):
     assert acc.current_accelerator() == torch.device("cuda")
     assert acc.current_accelerator(check_available=True) is None
     assert acc.__all__ == ["current_accelerator", "device_count", "is_available"]
+
+
+def test_compiler_namespace_is_the_reference_eager_surface():
+    """python/torch_rs/compiler/__init__.py and README.md:178: eager queries
+    return the False singleton; the default backend is stored as given (None
+    restores "inductor") and survives a reload; assume_constant_result marks
+    and returns the same function."""
+    import importlib
+    c = torch.compiler
+    assert c.is_compiling() is False and c.is_dynamo_compiling() is False and c.is_exporting() is False
+    assert c.get_default_backend() == "inductor"
+    backend = lambda *a: None  # noqa: E731
+    assert c.set_default_backend(backend) is None and c.get_default_backend() is backend
+    importlib.reload(c)
+    assert torch.compiler.get_default_backend() is backend
+    with pytest.raises(TypeError, match="backend must be a string or callable"):
+        c.set_default_backend(3)
+    c.set_default_backend("eager")
+    assert c.get_default_backend() == "eager" and c.reset() is None
+    c.set_default_backend(None)
+    assert c.get_default_backend() == "inductor"
+
+    def f():
+        return 1
+
+    assert c.assume_constant_result(f) is f and f._dynamo_marked_constant is True
+    assert c.__all__ == ["assume_constant_result", "reset", "set_default_backend", "get_default_backend",
+                         "is_compiling", "is_dynamo_compiling", "is_exporting"]
