@@ -4,7 +4,7 @@ from __future__ import annotations
 
 import operator as _operator
 
-from ._native import native as _C
+from .._native import native as _C
 
 
 def _require_default(name, value, *, allow_none):
@@ -38,12 +38,7 @@ def backward(tensors, grad_tensors=None, retain_graph=None, create_graph=False, 
     root.backward()
 
 
-def __getattr__(name):
-    # no_grad lives in the package root; re-exported here as the reference does.
-    if name == "no_grad":
-        from . import no_grad
-        return no_grad
-    raise AttributeError(name)
+from . import grad_mode  # noqa: E402
+from .grad_mode import no_grad  # noqa: E402
 
-
-__all__ = ["backward", "no_grad"]
+__all__ = ["backward", "grad_mode", "no_grad"]

@@ -685,3 +685,13 @@ def test_requires_grad_arguments_are_builtin_bools():
     assert torch_rs.full((2,), 1.5, requires_grad=None).shape == (2,)
     with pytest.raises(TypeError, match=r"^full\(\): argument 'requires_grad' must be bool, not int$"):
         torch_rs.full((2,), 1.5, requires_grad=1)
+
+
+def test_autograd_package_exports_grad_mode():
+    """python/torch_rs/autograd/__init__.py:133 and grad_mode.py:81: the
+    autograd package exports backward, grad_mode and no_grad, and no_grad is
+    one object under every spelling."""
+    import importlib
+    gm = importlib.import_module("torch_rs.autograd.grad_mode")
+    assert torch_rs.autograd.__all__ == ["backward", "grad_mode", "no_grad"]
+    assert gm.__all__ == ["no_grad"] and gm.no_grad is torch_rs.no_grad is torch_rs.autograd.no_grad
