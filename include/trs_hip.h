@@ -14,7 +14,9 @@
  *   - Every function returns int: 0 on success, a negative TRS_E_* code on
  *     failure; trs_last_error() then holds a thread-local message.  The codes
  *     mirror TensorError (src/tensor_error.rs:7-108).  No C++ exception
- *     crosses this boundary.
+ *     crosses this boundary: a failed host allocation inside the library
+ *     returns TRS_E_ALLOCATION_FAILED, and the message buffer itself is a
+ *     fixed thread-local array.
  *   - Tensor operands are (base pointer, trs_layout): `base` is element 0 of
  *     the storage and layout.offset the element offset of the view, as in the
  *     reference Tensor struct (src/tensor.rs:212-221).  Strides are in

@@ -358,32 +358,34 @@ using namespace trs;
 extern "C" {
 
 int trs_fusion_compile(const char *ir, size_t ir_len, uint64_t *kernel_id) {
-    if (!ir || !kernel_id) return set_error(TRS_E_INVALID_ARGUMENT, "null IR or kernel id pointer");
-    const std::string text(ir, ir_len);
-    {
+    return abi_guard([&]() -> int {
+        if (!ir || !kernel_id) return set_error(TRS_E_INVALID_ARGUMENT, "null IR or kernel id pointer");
+        const std::string text(ir, ir_len);
+        {
+            std::lock_guard<std::mutex> lock(g_mu);
+            auto it = g_by_ir.find(text);
+            if (it != g_by_ir.end()) {
+                *kernel_id = it->second;
+                return TRS_OK;
+            }
+        }
+        auto prog = std::make_unique<Program>();
+        prog->ir = text;
+        int rc = generate(text, prog.get());
+        if (rc) return rc;
+        rc = compile(prog.get());
+        if (rc) return rc;
         std::lock_guard<std::mutex> lock(g_mu);
-        auto it = g_by_ir.find(text);
+        auto it = g_by_ir.find(text);  // another thread may have won the race
         if (it != g_by_ir.end()) {
             *kernel_id = it->second;
             return TRS_OK;
         }
-    }
-    auto prog = std::make_unique<Program>();
-    prog->ir = text;
-    int rc = generate(text, prog.get());
-    if (rc) return rc;
-    rc = compile(prog.get());
-    if (rc) return rc;
-    std::lock_guard<std::mutex> lock(g_mu);
-    auto it = g_by_ir.find(text);  // another thread may have won the race
-    if (it != g_by_ir.end()) {
-        *kernel_id = it->second;
+        g_programs.push_back(std::move(prog));
+        *kernel_id = g_programs.size();
+        g_by_ir[text] = *kernel_id;
         return TRS_OK;
-    }
-    g_programs.push_back(std::move(prog));
-    *kernel_id = g_programs.size();
-    g_by_ir[text] = *kernel_id;
-    return TRS_OK;
+    });
 }
 
 int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *inputs, const trs_layout *in_layouts,
@@ -394,44 +396,46 @@ int trs_fusion_launch(uint64_t kernel_id, int n_inputs, const void *const *input
 int trs_fusion_launch_multi(uint64_t kernel_id, int n_inputs, const void *const *inputs,
                             const trs_layout *in_layouts, int n_outputs, float *const *outputs,
                             const trs_layout *lo) {
-    Program *prog = lookup(kernel_id);
-    if (!prog) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id %llu", (unsigned long long)kernel_id);
-    if (n_inputs != prog->nin)
-        return set_error(TRS_E_INVALID_ARGUMENT, "program takes %d inputs, got %d", prog->nin, n_inputs);
-    if (n_outputs != prog->nout)
-        return set_error(TRS_E_INVALID_ARGUMENT, "program has %d outputs, got %d", prog->nout, n_outputs);
-    if (!inputs || !in_layouts || !outputs) return set_error(TRS_E_INVALID_ARGUMENT, "null inputs or outputs");
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    const trs_layout *ls[kMaxIn];
-    int eb[kMaxIn];
-    for (int i = 0; i < n_inputs; i++) {
-        ls[i] = &in_layouts[i];
-        eb[i] = ((prog->u8mask >> i) & 1u) ? 1 : 4;
-    }
-    PwPlan pl;
-    int rc = plan_pointwise(lo, outputs[0], n_inputs, inputs, ls, eb, dev->cu_count, &pl, n_outputs, outputs + 1);
-    if (rc) return rc;
-    std::string name;
-    switch (pl.variant) {
-    case PwVariant::Empty: return TRS_OK;
-    case PwVariant::Flat:
-        name = pl.contig ? "trs_fused_flat_c" : pl.vec ? "trs_fused_flat_v" : "trs_fused_flat_s";
-        break;
-    case PwVariant::Rows: name = pl.vec ? "trs_fused_rows_v" : "trs_fused_rows_s"; break;
-    case PwVariant::Tiled:
-        name = std::string(pl.vec ? "trs_fused_tiled_v" : "trs_fused_tiled_s") + std::to_string(pl.ntransposed);
-        break;
-    case PwVariant::Generic: name = "trs_fused_generic"; break;
-    }
-    hipFunction_t fn;
-    rc = get_function(prog, dev, name, &fn);
-    if (rc) return rc;
-    void *args[] = {(void *)&pl.g, (void *)&pl.p};
-    TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, (unsigned)pl.block, 1, 1, 0, dev->stream, args,
-                                        nullptr),
-                  "hipModuleLaunchKernel");
-    return TRS_OK;
+    return abi_guard([&]() -> int {
+        Program *prog = lookup(kernel_id);
+        if (!prog) return set_error(TRS_E_INVALID_ARGUMENT, "unknown fusion kernel id %llu", (unsigned long long)kernel_id);
+        if (n_inputs != prog->nin)
+            return set_error(TRS_E_INVALID_ARGUMENT, "program takes %d inputs, got %d", prog->nin, n_inputs);
+        if (n_outputs != prog->nout)
+            return set_error(TRS_E_INVALID_ARGUMENT, "program has %d outputs, got %d", prog->nout, n_outputs);
+        if (!inputs || !in_layouts || !outputs) return set_error(TRS_E_INVALID_ARGUMENT, "null inputs or outputs");
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        const trs_layout *ls[kMaxIn];
+        int eb[kMaxIn];
+        for (int i = 0; i < n_inputs; i++) {
+            ls[i] = &in_layouts[i];
+            eb[i] = ((prog->u8mask >> i) & 1u) ? 1 : 4;
+        }
+        PwPlan pl;
+        int rc = plan_pointwise(lo, outputs[0], n_inputs, inputs, ls, eb, dev->cu_count, &pl, n_outputs, outputs + 1);
+        if (rc) return rc;
+        std::string name;
+        switch (pl.variant) {
+        case PwVariant::Empty: return TRS_OK;
+        case PwVariant::Flat:
+            name = pl.contig ? "trs_fused_flat_c" : pl.vec ? "trs_fused_flat_v" : "trs_fused_flat_s";
+            break;
+        case PwVariant::Rows: name = pl.vec ? "trs_fused_rows_v" : "trs_fused_rows_s"; break;
+        case PwVariant::Tiled:
+            name = std::string(pl.vec ? "trs_fused_tiled_v" : "trs_fused_tiled_s") + std::to_string(pl.ntransposed);
+            break;
+        case PwVariant::Generic: name = "trs_fused_generic"; break;
+        }
+        hipFunction_t fn;
+        rc = get_function(prog, dev, name, &fn);
+        if (rc) return rc;
+        void *args[] = {(void *)&pl.g, (void *)&pl.p};
+        TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, (unsigned)pl.block, 1, 1, 0, dev->stream, args,
+                                            nullptr),
+                      "hipModuleLaunchKernel");
+        return TRS_OK;
+    });
 }
 
 int trs_fusion_outputs(uint64_t kernel_id, int *n_outputs) {

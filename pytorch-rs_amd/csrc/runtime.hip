@@ -16,7 +16,7 @@ namespace trs {
 
 namespace {
 
-thread_local std::string g_last_error;
+thread_local char g_last_error[1024];
 thread_local int g_device = 0;
 
 constexpr int kMaxDevices = 16;
@@ -78,7 +78,7 @@ int set_error(int code, const char *fmt, ...) {
     va_start(ap, fmt);
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
-    g_last_error = buf;
+    std::memcpy(g_last_error, buf, sizeof buf);
     return code;
 }
 
@@ -183,11 +183,13 @@ using namespace trs;
 
 extern "C" {
 
-const char *trs_last_error(void) { return g_last_error.c_str(); }
+const char *trs_last_error(void) { return g_last_error; }
 
 int trs_init(void) {
-    DeviceState *dev = device_state();
-    return dev ? TRS_OK : TRS_E_NO_DEVICE;
+    return abi_guard([&]() -> int {
+        DeviceState *dev = device_state();
+        return dev ? TRS_OK : TRS_E_NO_DEVICE;
+    });
 }
 
 int trs_device_count(int *count) {
@@ -198,12 +200,14 @@ int trs_device_count(int *count) {
 }
 
 int trs_set_device(int device) {
-    int rc = count_devices();
-    if (rc) return rc;
-    if (device < 0 || device >= g_device_count)
-        return set_error(TRS_E_INVALID_ARGUMENT, "device %d out of range [0, %d)", device, g_device_count);
-    g_device = device;
-    return device_state() ? TRS_OK : TRS_E_HIP;
+    return abi_guard([&]() -> int {
+        int rc = count_devices();
+        if (rc) return rc;
+        if (device < 0 || device >= g_device_count)
+            return set_error(TRS_E_INVALID_ARGUMENT, "device %d out of range [0, %d)", device, g_device_count);
+        g_device = device;
+        return device_state() ? TRS_OK : TRS_E_HIP;
+    });
 }
 
 int trs_get_device(int *device) {
@@ -213,89 +217,99 @@ int trs_get_device(int *device) {
 }
 
 int trs_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    if (name && name_len) std::snprintf(name, name_len, "%s", dev->name);
-    if (cu_count) *cu_count = dev->cu_count;
-    if (clock_khz) *clock_khz = dev->clock_khz;
-    return TRS_OK;
+    return abi_guard([&]() -> int {
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        if (name && name_len) std::snprintf(name, name_len, "%s", dev->name);
+        if (cu_count) *cu_count = dev->cu_count;
+        if (clock_khz) *clock_khz = dev->clock_khz;
+        return TRS_OK;
+    });
 }
 
 int trs_alloc(size_t bytes, void **ptr) {
-    if (!ptr) return set_error(TRS_E_INVALID_ARGUMENT, "null out pointer");
-    *ptr = nullptr;
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    if (bytes == 0) return TRS_OK;
-    const size_t rounded = round_block(bytes);
-    {
-        std::lock_guard<std::mutex> lock(dev->cache_mu);
-        auto it = dev->free_blocks.find(rounded);
-        if (it != dev->free_blocks.end()) {
-            *ptr = it->second;
-            dev->free_blocks.erase(it);
-            dev->cached_bytes -= rounded;
-            dev->live_blocks[*ptr] = rounded;
-            return TRS_OK;
-        }
-    }
-    hipError_t e = hipMalloc(ptr, rounded);
-    if (e != hipSuccess) {
-        // Out of memory with blocks parked in the cache: release them and retry once.
-        (void)hipGetLastError();
-        int rc = release_cache(dev);
-        if (rc) return rc;
-        e = hipMalloc(ptr, rounded);
-    }
-    if (e != hipSuccess) {
+    return abi_guard([&]() -> int {
+        if (!ptr) return set_error(TRS_E_INVALID_ARGUMENT, "null out pointer");
         *ptr = nullptr;
-        (void)hipGetLastError();
-        return set_error(TRS_E_ALLOCATION_FAILED, "hipMalloc of %zu bytes failed: %s", bytes,
-                         hipGetErrorString(e));
-    }
-    std::lock_guard<std::mutex> lock(dev->cache_mu);
-    dev->live_blocks[*ptr] = rounded;
-    return TRS_OK;
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        if (bytes == 0) return TRS_OK;
+        const size_t rounded = round_block(bytes);
+        {
+            std::lock_guard<std::mutex> lock(dev->cache_mu);
+            auto it = dev->free_blocks.find(rounded);
+            if (it != dev->free_blocks.end()) {
+                *ptr = it->second;
+                dev->free_blocks.erase(it);
+                dev->cached_bytes -= rounded;
+                dev->live_blocks[*ptr] = rounded;
+                return TRS_OK;
+            }
+        }
+        hipError_t e = hipMalloc(ptr, rounded);
+        if (e != hipSuccess) {
+            // Out of memory with blocks parked in the cache: release them and retry once.
+            (void)hipGetLastError();
+            int rc = release_cache(dev);
+            if (rc) return rc;
+            e = hipMalloc(ptr, rounded);
+        }
+        if (e != hipSuccess) {
+            *ptr = nullptr;
+            (void)hipGetLastError();
+            return set_error(TRS_E_ALLOCATION_FAILED, "hipMalloc of %zu bytes failed: %s", bytes,
+                             hipGetErrorString(e));
+        }
+        std::lock_guard<std::mutex> lock(dev->cache_mu);
+        dev->live_blocks[*ptr] = rounded;
+        return TRS_OK;
+    });
 }
 
 int trs_free(void *ptr) {
-    if (!ptr) return TRS_OK;
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    {
-        std::lock_guard<std::mutex> lock(dev->cache_mu);
-        auto it = dev->live_blocks.find(ptr);
-        if (it != dev->live_blocks.end()) {
-            // Stream-ordered release: work already queued on the device
-            // stream may still read the block; anything that reuses it is
-            // queued behind that work.
-            dev->free_blocks.emplace(it->second, ptr);
-            dev->cached_bytes += it->second;
-            dev->live_blocks.erase(it);
-            return TRS_OK;
+    return abi_guard([&]() -> int {
+        if (!ptr) return TRS_OK;
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        {
+            std::lock_guard<std::mutex> lock(dev->cache_mu);
+            auto it = dev->live_blocks.find(ptr);
+            if (it != dev->live_blocks.end()) {
+                // Stream-ordered release: work already queued on the device
+                // stream may still read the block; anything that reuses it is
+                // queued behind that work.
+                dev->free_blocks.emplace(it->second, ptr);
+                dev->cached_bytes += it->second;
+                dev->live_blocks.erase(it);
+                return TRS_OK;
+            }
         }
-    }
-    // Not a block of this cache: drain queued readers, then hand it back.
-    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "free sync");
-    TRS_HIP_CHECK(hipFree(ptr), "hipFree");
-    return TRS_OK;
+        // Not a block of this cache: drain queued readers, then hand it back.
+        TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "free sync");
+        TRS_HIP_CHECK(hipFree(ptr), "hipFree");
+        return TRS_OK;
+    });
 }
 
 int trs_empty_cache(void) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    return release_cache(dev);
+    return abi_guard([&]() -> int {
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        return release_cache(dev);
+    });
 }
 
 int trs_memory_stats(size_t *live_bytes, size_t *cached_bytes) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    std::lock_guard<std::mutex> lock(dev->cache_mu);
-    size_t live = 0;
-    for (auto &kv : dev->live_blocks) live += kv.second;
-    if (live_bytes) *live_bytes = live;
-    if (cached_bytes) *cached_bytes = dev->cached_bytes;
-    return TRS_OK;
+    return abi_guard([&]() -> int {
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        std::lock_guard<std::mutex> lock(dev->cache_mu);
+        size_t live = 0;
+        for (auto &kv : dev->live_blocks) live += kv.second;
+        if (live_bytes) *live_bytes = live;
+        if (cached_bytes) *cached_bytes = dev->cached_bytes;
+        return TRS_OK;
+    });
 }
 
 int trs_memcpy_d2d(void *dst, const void *src, size_t bytes) {

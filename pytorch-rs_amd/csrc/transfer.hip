@@ -184,52 +184,60 @@ using namespace trs;
 extern "C" {
 
 int trs_host_alloc(size_t bytes, void **ptr) {
-    if (!ptr) return set_error(TRS_E_INVALID_ARGUMENT, "null out pointer");
-    *ptr = nullptr;
-    if (bytes == 0) return TRS_OK;
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    hipError_t e = hipHostMalloc(ptr, bytes, hipHostMallocDefault);
-    if (e != hipSuccess) {
+    return abi_guard([&]() -> int {
+        if (!ptr) return set_error(TRS_E_INVALID_ARGUMENT, "null out pointer");
         *ptr = nullptr;
-        (void)hipGetLastError();
-        return set_error(TRS_E_ALLOCATION_FAILED, "hipHostMalloc of %zu bytes failed: %s", bytes, hipGetErrorString(e));
-    }
-    return TRS_OK;
+        if (bytes == 0) return TRS_OK;
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        hipError_t e = hipHostMalloc(ptr, bytes, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            *ptr = nullptr;
+            (void)hipGetLastError();
+            return set_error(TRS_E_ALLOCATION_FAILED, "hipHostMalloc of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+        }
+        return TRS_OK;
+    });
 }
 
 int trs_host_free(void *ptr) {
-    if (!ptr) return TRS_OK;
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    // Copies queued from or to this buffer must finish before it is released.
-    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "host free sync");
-    TRS_HIP_CHECK(hipHostFree(ptr), "hipHostFree");
-    return TRS_OK;
+    return abi_guard([&]() -> int {
+        if (!ptr) return TRS_OK;
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        // Copies queued from or to this buffer must finish before it is released.
+        TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "host free sync");
+        TRS_HIP_CHECK(hipHostFree(ptr), "hipHostFree");
+        return TRS_OK;
+    });
 }
 
 int trs_memcpy_h2d(void *dst, const void *src, size_t bytes) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    if (bytes == 0) return TRS_OK;
-    if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in h2d copy");
-    if (bytes >= kStageMinH2D && !is_page_locked(src)) return staged_h2d(dev, (char *)dst, (const char *)src, bytes);
-    // Small or page-locked: one DMA.  Returning after the sync means `src`
-    // has been consumed and may be reused by the caller.
-    TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream), "h2d copy");
-    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "h2d sync");
-    return TRS_OK;
+    return abi_guard([&]() -> int {
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        if (bytes == 0) return TRS_OK;
+        if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in h2d copy");
+        if (bytes >= kStageMinH2D && !is_page_locked(src)) return staged_h2d(dev, (char *)dst, (const char *)src, bytes);
+        // Small or page-locked: one DMA.  Returning after the sync means `src`
+        // has been consumed and may be reused by the caller.
+        TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream), "h2d copy");
+        TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "h2d sync");
+        return TRS_OK;
+    });
 }
 
 int trs_memcpy_d2h(void *dst, const void *src, size_t bytes) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    if (bytes == 0) return TRS_OK;
-    if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in d2h copy");
-    if (bytes >= kStageMinD2H && !is_page_locked(dst)) return staged_d2h(dev, (char *)dst, (const char *)src, bytes);
-    TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream), "d2h copy");
-    TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "d2h sync");
-    return TRS_OK;
+    return abi_guard([&]() -> int {
+        DeviceState *dev = device_state();
+        if (!dev) return TRS_E_NO_DEVICE;
+        if (bytes == 0) return TRS_OK;
+        if (!dst || !src) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer in d2h copy");
+        if (bytes >= kStageMinD2H && !is_page_locked(dst)) return staged_d2h(dev, (char *)dst, (const char *)src, bytes);
+        TRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream), "d2h copy");
+        TRS_HIP_CHECK(hipStreamSynchronize(dev->stream), "d2h sync");
+        return TRS_OK;
+    });
 }
 
 }  // extern "C"

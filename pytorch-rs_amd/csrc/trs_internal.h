@@ -1,6 +1,9 @@
 // trs_internal.h -- host-side internals shared by the libtrs_hip.so sources.
 #pragma once
 
+#include <exception>
+#include <new>
+
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -45,6 +48,22 @@ DeviceState *device_state();
 
 // Records a thread-local error message and returns `code`.
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Runs an entry point's body and turns any C++ exception (a failed host
+// allocation in a container, a thread that cannot start) into an error code,
+// so that none crosses the C ABI.
+template <class Fn>
+int abi_guard(Fn &&fn) noexcept {
+    try {
+        return fn();
+    } catch (const std::bad_alloc &) {
+        return set_error(TRS_E_ALLOCATION_FAILED, "host memory allocation failed");
+    } catch (const std::exception &e) {
+        return set_error(TRS_E_INVALID_ARGUMENT, "internal error: %s", e.what());
+    } catch (...) {
+        return set_error(TRS_E_INVALID_ARGUMENT, "internal error");
+    }
+}
 // Maps a HIP failure to TRS_E_HIP with the runtime's message.
 int hip_fail(hipError_t e, const char *what);
 
