@@ -174,3 +174,44 @@ def test_fusion_disk_cache_persists_across_processes_and_rejects_bad_files(tmp_p
     before = sorted(p.name for p in tmp_path.rglob("*"))
     assert _compile_in_child(ir, "")[0] == 0
     assert sorted(p.name for p in tmp_path.rglob("*")) == before
+
+
+_C_HOST = r"""
+#include <stdio.h>
+#include "trs_hip.h"
+
+int main(void) {
+    int n = -1;
+    int rc = trs_device_count(&n);
+    /* No GPU in this container: a status code and a message, never a crash. */
+    printf("%d %d %s\n", rc, n, rc ? trs_last_error() : "ok");
+    trs_layout l = {.rank = 1, .shape = {4}, .stride = {1}, .offset = 0};
+    rc = trs_binary_f32(99, NULL, &l, NULL, &l, NULL, &l);
+    printf("%d\n", rc);
+    return 0;
+}
+"""
+
+
+def test_header_compiles_as_c_and_a_c_host_links_the_library(tmp_path):
+    """include/trs_hip.h is plain C (C11): a C program compiles against it,
+    links libtrs_hip.so and calls entry points; without a GPU they return
+    status codes."""
+    import subprocess
+    from pathlib import Path
+    repo = Path(__file__).resolve().parent.parent
+    lib_dir = abi.LIB_DIR
+    src = tmp_path / "host.c"
+    src.write_text(_C_HOST)
+    exe = tmp_path / "host"
+    cc = subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{repo / 'include'}", str(src), "-o", str(exe),
+                         f"-L{lib_dir}", "-ltrs_hip", f"-Wl,-rpath,{lib_dir}"], capture_output=True, text=True)
+    assert cc.returncode == 0, cc.stderr
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    first, second = out.stdout.splitlines()[:2]
+    rc, n = (int(v) for v in first.split()[:2])
+    # Either a device count, or (no GPU) a negative status with a message.
+    assert (rc == 0 and n >= 0) or (rc < 0 and first.split(maxsplit=2)[2] != "ok")
+    # An unknown op code is rejected before any device work.
+    assert int(second) == abi.TRS_E_INVALID_ARGUMENT
