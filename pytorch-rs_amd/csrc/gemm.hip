@@ -291,10 +291,13 @@ struct Tiles {
 // The large and medium tiles run only on shapes they divide.  Float4
 // fragment reads measured +0.9% (NT) to -0.1% on the large tile and -2 to -3%
 // on the 4-wave tiles, so only the large tile uses them.
+// BK=32 pays only in the plain layout: 138.8 against 137.3 TFLOP/s at
+// 8192x4096x4096, while a transposed A runs 1.6-1.9% slower at BK=32 than at
+// BK=16 (134.6 against 137.2 TFLOP/s at 4096x4096x8192) and a transposed B
+// holds more fragment registers and spills at BK=32 with 16 waves.  The k
+// order, and so every result bit, is the same at both depths.
 using LargeTiles = Tiles<256, 256, 32, 4, 4, 1, true, false>;
-// The NT layout (B transposed) holds more fragment registers and spills at
-// BK=32 with 16 waves; it keeps BK=16.
-using LargeTilesNT = Tiles<256, 256, 16, 4, 4, 1, true, false>;
+using LargeTilesK16 = Tiles<256, 256, 16, 4, 4, 1, true, false>;
 using SmallTiles = Tiles<128, 128, 32, 2, 2, 2, false, true>;
 using MediumTiles = Tiles<64, 128, 32, 2, 2, 2, false, false>;  // halves M per block when 128x128 leaves CUs idle
 
@@ -332,9 +335,9 @@ int launch_layout(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipS
 // The large tile in each layout (full tiles only).
 int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
     if (a_plain && b_plain) return launch_tiled<LargeTiles, false, false>(g, true, s);
-    if (a_plain) return launch_tiled<LargeTilesNT, false, true>(g, true, s);
-    if (b_plain) return launch_tiled<LargeTiles, true, false>(g, true, s);
-    return launch_tiled<LargeTiles, true, true>(g, true, s);
+    if (a_plain) return launch_tiled<LargeTilesK16, false, true>(g, true, s);
+    if (b_plain) return launch_tiled<LargeTilesK16, true, false>(g, true, s);
+    return launch_tiled<LargeTilesK16, true, true>(g, true, s);
 }
 
 }  // namespace
@@ -416,7 +419,7 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
     // The large tile only when it divides the problem and still gives every
     // CU a block; otherwise the small tile (full or edge-guarded).
     const int64_t large_tiles = (M / LargeTiles::BM) * (N / LargeTiles::BN) * batch;
-    const int64_t large_bk = (a_plain && !b_plain) ? LargeTilesNT::BK : LargeTiles::BK;
+    const int64_t large_bk = (a_plain && b_plain) ? LargeTiles::BK : LargeTilesK16::BK;
     if (aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0 && K % large_bk == 0 &&
         large_tiles >= dev->cu_count)
         return launch_large(g, a_plain, b_plain, dev->stream);
