@@ -202,10 +202,16 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
 /* C = A @ B in fp32 on CDNA4 FP32 MFMA.  Rank 2 ([M,K] @ [K,N]) or rank 3
  * ([b,M,K] @ [b,K,N], the batch the reference spells as rank-2 calls).
  * Operands may be transposed views (unit stride in either matrix dim,
- * e.g. `.mT`); other strides are packed first.  `lc` must be contiguous.
+ * e.g. `.mT`); other strides run a one-thread-per-output kernel in the
+ * reference's own k order.  `lc` must be contiguous.
  * Tolerance versus the reference's sequential order: |dC| <= 1e-5*sqrt(K) *
- * (|A||B|) elementwise.  Empty outputs launch nothing; K = 0 writes +0.0 and
- * then the operands may be null (src/tensor.rs:4817-4839). */
+ * (|A||B|) elementwise.  An output with fewer 256x256 tiles than the device
+ * has CUs and a long K splits K into slices summed in slice order; the
+ * partial products then take S*M*N floats of device memory from the
+ * library's block cache for the duration of the call (S <= 8).  Results are
+ * deterministic for a given shape and layout.  Empty outputs launch nothing;
+ * K = 0 writes +0.0 and then the operands may be null
+ * (src/tensor.rs:4817-4839). */
 int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
                    float *c, const trs_layout *lc);
 

@@ -258,6 +258,23 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
     }
 }
 
+// Split-K epilogue: c = ((p0 + p1) + p2) + ... over the S partial products,
+// in slice order, four floats per lane.
+__global__ void __launch_bounds__(256) splitk_sum(const float4 *__restrict__ parts, float4 *__restrict__ c,
+                                                  int64_t n4, int S) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    float4 acc = parts[i];
+    for (int s = 1; s < S; s++) {
+        const float4 v = parts[(int64_t)s * n4 + i];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    c[i] = acc;
+}
+
 // Simple fallback for operands with no unit stride: one thread per output,
 // sequential k (the reference's own order).
 __global__ void __launch_bounds__(256) gemm_f32_strided(const float *a, const float *b, float *c, int64_t M,
@@ -340,6 +357,38 @@ int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
     return launch_tiled<LargeTilesK16, true, true>(g, true, s);
 }
 
+// Split K: an output with fewer 256x256 tiles than CUs (the MLP's 8192x1024
+// and 4096x1024 GEMMs) runs its K in S slices as S batches of the large tile,
+// into a workspace of S partial products that one more pass sums in slice
+// order.  The workspace comes from the block cache and returns to it in
+// stream order.  `sak`/`sbk` are the operands' k strides.
+constexpr int64_t kMaxSplitK = 8;
+constexpr int64_t kMinSplitDepth = 1024;
+
+int launch_split_k(GemmArgs g, bool a_plain, bool b_plain, int64_t sak, int64_t sbk, int64_t S, hipStream_t s) {
+    float *const C = g.c;
+    const int64_t mn = g.M * g.N, Ks = g.K / S;
+    void *ws = nullptr;
+    int rc = trs_alloc((size_t)(S * mn) * sizeof(float), &ws);
+    if (rc) return rc;
+    g.c = (float *)ws;
+    g.K = Ks;
+    g.bsa = Ks * sak;
+    g.bsb = Ks * sbk;
+    g.bsc = mn;
+    g.batch = S;
+    rc = launch_large(g, a_plain, b_plain, s);
+    if (rc == TRS_OK) {
+        const int64_t n4 = mn / 4;
+        hipLaunchKernelGGL(splitk_sum, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, (const float4 *)ws,
+                           (float4 *)C, n4, (int)S);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) rc = hip_fail(e, "split-k sum launch");
+    }
+    const int frc = trs_free(ws);
+    return rc ? rc : frc;
+}
+
 }  // namespace
 
 }  // namespace trs
@@ -417,9 +466,17 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
     const bool aligned = al16(A) && al16(B) && al16(C) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                          (batch == 1 || (bsa % 4 == 0 && bsb % 4 == 0));
     // The large tile only when it divides the problem and still gives every
-    // CU a block; otherwise the small tile (full or edge-guarded).
+    // CU a block, or when splitting a long K gives every CU one; otherwise
+    // the small tile (full or edge-guarded).
     const int64_t large_tiles = (M / LargeTiles::BM) * (N / LargeTiles::BN) * batch;
     const int64_t large_bk = (a_plain && b_plain) ? LargeTiles::BK : LargeTilesK16::BK;
+    if (batch == 1 && aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0 && large_tiles < dev->cu_count) {
+        int64_t S = 1;
+        while (S < kMaxSplitK && large_tiles * S * 2 <= dev->cu_count && K % (S * 2 * large_bk) == 0 &&
+               K / (S * 2) >= kMinSplitDepth)
+            S *= 2;
+        if (S > 1) return launch_split_k(g, a_plain, b_plain, sak, sbk, S, dev->stream);
+    }
     if (aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0 && K % large_bk == 0 &&
         large_tiles >= dev->cu_count)
         return launch_large(g, a_plain, b_plain, dev->stream);

@@ -153,6 +153,66 @@ def test_large_tile_all_layouts_exact_on_small_integers(ta, tb):
     assert np.array_equal(got, want)
 
 
+def _layouts(a, b, ta, tb):
+    (m, k), n = a.shape, b.shape[1]
+    ast, astr = (np.ascontiguousarray(a.T), (1, m)) if ta else (a, (k, 1))
+    bst, bstr = (np.ascontiguousarray(b.T), (1, k)) if tb else (b, (n, 1))
+    return ast.ravel(), ((m, k), astr, 0), bst.ravel(), ((k, n), bstr, 0)
+
+
+# On a 256-CU device these outputs hold fewer 256x256 tiles than CUs and K is
+# long, so K is split into S slices (8, 4, 4 and 2 here) summed in slice order.
+SPLIT_K = [(256, 8192, 256), (512, 4096, 1024), (4096, 8192, 1024), (8192, 4096, 1024)]
+
+
+@pytest.mark.parametrize("m,k,n", SPLIT_K)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_split_k_all_layouts_exact_on_small_integers(m, k, n, ta, tb):
+    """Every partial and total sum of small integers is exact, so the split
+    result equals the float64 product exactly."""
+    if m * n > 512 * 1024 and (ta, tb) not in ((False, False), (True, False)):
+        pytest.skip("the MLP's two split shapes run in the layouts the MLP uses (NN forward, TN weight gradient)")
+    rng = np.random.default_rng(m + k + n + 2 * ta + tb)
+    a = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    b = rng.integers(-3, 4, (k, n)).astype(np.float32)
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    sa, la, sb, lb = _layouts(a, b, ta, tb)
+    assert np.array_equal(U.matmul(sa, *la, sb, *lb), want)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_split_k_normal_inputs_within_tolerance(ta, tb):
+    m, k, n = 256, 4096, 256
+    rng = np.random.default_rng(77 + 2 * ta + tb)
+    a = (rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
+    b = (rng.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
+    sa, la, sb, lb = _layouts(a, b, ta, tb)
+    got = U.matmul(sa, *la, sb, *lb)
+    want = O.matmul(sa, *la, sb, *lb).reshape(m, n)
+    _check_tol(got, want, _abs_bound(a, b), k)
+
+
+def test_split_k_special_values_across_slices():
+    """Infinities and a NaN in different k slices: NaN and signed-infinity
+    positions equal the oracle's sequential sum; the rest within tolerance."""
+    m, k, n = 256, 4096, 256
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    a[5, 100], a[5, 3000], a[7, 2000], a[9, 1100] = np.inf, -np.inf, np.nan, np.inf
+    b[1500, 9] = -np.inf
+    got = U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0)
+    want = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+    for pred in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(pred(got), pred(want))
+    assert np.isnan(want[5]).any() and np.isnan(want[7]).all() and np.isinf(want[:, 9]).sum() > 200
+    fin = np.isfinite(want)
+    with np.errstate(invalid="ignore", over="ignore"):
+        bound = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    err = np.abs(got[fin].astype(np.float64) - want[fin].astype(np.float64))
+    assert (err <= 1e-5 * np.sqrt(k) * bound[fin]).all()
+
+
 def test_random_shapes_layouts_and_offsets_exact_on_small_integers():
     """40 random products: M, N, K in 1-300 (ragged edge tiles), each operand
     plain or transposed (.mT) and at a random storage offset, rank 2 or a
