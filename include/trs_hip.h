@@ -208,7 +208,8 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
  * (|A||B|) elementwise.  An output with fewer 256x256 tiles than the device
  * has CUs and a long K splits K into slices summed in slice order; the
  * partial products then take S*M*N floats of device memory from the
- * library's block cache for the duration of the call (S <= 8).  Results are
+ * library's block cache for the duration of the call (S <= 8, and S*M*N is
+ * at most 65,536 floats per CU: 64 MiB on a 256-CU device).  Results are
  * deterministic for a given shape and layout.  Empty outputs launch nothing;
  * K = 0 writes +0.0 and then the operands may be null
  * (src/tensor.rs:4817-4839). */
