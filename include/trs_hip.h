@@ -163,7 +163,11 @@ int trs_mask_apply_f32(const float *h, const trs_layout *lh, const uint8_t *mask
 /* *out (one device float) = sum of x.  Replaces Tensor::sum
  * (src/tensor.rs:2413-2431); a fixed-order two-level tree rather than the
  * reference's sequential fold, so it matches within the float summation
- * bound, not bit for bit. */
+ * bound, not bit for bit: |sum - exact| <= (d u / (1 - d u)) * sum|x| with
+ * u = 2^-24 and d = ceil(n/256) + 8 up to 32,768 elements, else
+ * ceil(ceil(n/1024)/256) + 20.  Every partial sum starts from -0.0, as
+ * Rust's f32 Sum does, so an all-(-0.0) input gives -0.0; an empty one gives
+ * -0.0 too. */
 int trs_sum_f32(const float *x, const trs_layout *lx, float *out);
 /* out[0..n) = *value (a device float): the Sum VJP fill (src/tensor.rs:3008-3013). */
 int trs_fill_from_device_f32(float *out, size_t n, const float *value);
@@ -205,16 +209,31 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
  * e.g. `.mT`); other strides run a one-thread-per-output kernel in the
  * reference's own k order.  `lc` must be contiguous.
  * Tolerance versus the reference's sequential order: |dC| <= 1e-5*sqrt(K) *
- * (|A||B|) elementwise.  An output with fewer 256x256 tiles than the device
- * has CUs and a long K splits K into slices summed in slice order; the
- * partial products then take S*M*N floats of device memory from the
- * library's block cache for the duration of the call (S <= 8, and S*M*N is
- * at most 65,536 floats per CU: 64 MiB on a 256-CU device).  Results are
- * deterministic for a given shape and layout.  Empty outputs launch nothing;
- * K = 0 writes +0.0 and then the operands may be null
- * (src/tensor.rs:4817-4839). */
+ * (|A||B|) elementwise.  A single 16-byte-aligned matrix whose M and N are
+ * multiples of 256, with fewer 256x256 tiles than the device has CUs and a
+ * long K, may split K into S slices summed in slice order (when S slices
+ * fill at least half the CUs, or give at least as many blocks as the
+ * unsplit tile); the partial products then take S*M*N floats of device
+ * memory from the library's block cache for the duration of the call
+ * (S <= 8, and S*M*N is at most 65,536 floats per CU: 64 MiB on a 256-CU
+ * device).  If that memory cannot be allocated the call runs the unsplit
+ * tile instead.  The order of summation, and so the low bits of a result,
+ * depends on the shape, the layout, the device's CU count and the operands'
+ * 16-byte alignment; for fixed values of these the result is deterministic.
+ * Empty outputs launch nothing; K = 0 writes +0.0 and then the operands may
+ * be null (src/tensor.rs:4817-4839). */
 int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
                    float *c, const trs_layout *lc);
+/* Diagnostic (no counterpart in the reference): the kernel trs_matmul_f32
+ * would run for these operands on the current device, without launching or
+ * allocating.  Pointers are used only for their alignment and may be null.
+ * *tile_m x *tile_n x *tile_k is one block's C tile and k depth (all 0 for
+ * the one-thread-per-output strided kernel, or when nothing is launched),
+ * *splits the number of K slices (1 = unsplit), *blocks the blocks of the
+ * main launch.  Any out pointer may be null. */
+int trs_matmul_plan_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
+                        const float *c, const trs_layout *lc, int *tile_m, int *tile_n, int *tile_k,
+                        int64_t *splits, int64_t *blocks);
 
 /* ---- pointwise fusion compiler (new; no counterpart in the reference) */
 

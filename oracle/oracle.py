@@ -80,6 +80,8 @@ def lib() -> ctypes.CDLL:
             "orc_sum_abs_f64": ([c_void_p, c_uint64], c_double),
             "orc_matmul_f32": ([c_void_p, _LP, c_void_p, _LP, c_void_p, c_int64, c_int64, c_int64], c_int),
             "orc_matmul_row_blocked_f32": ([c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_uint64], None),
+            "orc_matmul_row_blocked_threads_f32": ([c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_uint64,
+                                                    c_int], None),
             "orc_matmul_rows_f32": ([c_void_p, _LP, c_void_p, _LP, c_void_p, c_int64, c_void_p], c_int),
             "orc_matmul_abs_rows_f64": ([c_void_p, _LP, c_void_p, _LP, c_void_p, c_int64, c_void_p], c_int),
             "orc_relu_backward_f32": ([c_void_p, _LP, c_void_p, c_void_p], None),
@@ -292,6 +294,20 @@ def exp_max_ulp(got: np.ndarray, first_bits: int, threads: int = 8):
     idx = c_uint64()
     worst = lib().orc_exp_max_ulp(_p(got), first_bits, got.size, threads, ctypes.byref(idx))
     return int(worst), int(idx.value)
+
+
+def matmul_threads(a: np.ndarray, b: np.ndarray, threads: int = 16) -> np.ndarray:
+    """Contiguous [M,K] @ [K,N] in the reference's order (k ascending from
+    +0.0 per element), the row-blocked loop split over threads by output rows;
+    bit-identical to matmul_row_blocked."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    out = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_row_blocked_threads_f32(_p(a), _p(b), _p(out), m, k, n, threads)
+    return out
 
 
 def matmul_row_blocked(a: np.ndarray, b: np.ndarray) -> np.ndarray:

@@ -664,6 +664,50 @@ void orc_matmul_row_blocked_f32(const float *left, const float *right, float *ou
     }
 }
 
+/* The row-blocked loop above split over `threads` POSIX threads by ranges of
+ * output rows (multiples of 4, so every thread's rows are blocked exactly as
+ * the single-threaded loop blocks them).  Each output element still starts at
+ * +0.0 and adds left[i,k]*right[k,j] for k ascending, so the result is
+ * bit-identical to orc_matmul_row_blocked_f32 and orc_matmul_f32 (pinned by
+ * tests/test_oracle_properties.py).  Checker only: it lets the full-size
+ * parity tests compare every element of a large product. */
+typedef struct {
+    const float *left, *right;
+    float *out;
+    uint64_t rows, inner, cols;
+} mm_chunk;
+
+static void *mm_chunk_worker(void *arg) {
+    mm_chunk *c = (mm_chunk *)arg;
+    orc_matmul_row_blocked_f32(c->left, c->right, c->out, c->rows, c->inner, c->cols);
+    return NULL;
+}
+
+void orc_matmul_row_blocked_threads_f32(const float *left, const float *right, float *out, uint64_t rows,
+                                        uint64_t inner, uint64_t cols, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    uint64_t per = (rows + (uint64_t)threads - 1) / (uint64_t)threads;
+    per = (per + 3) / 4 * 4;
+    pthread_t tid[64];
+    mm_chunk ch[64];
+    int started[64] = {0};
+    int nt = 0;
+    for (uint64_t r0 = 0; r0 < rows && nt < 64; r0 += per, nt++) {
+        const uint64_t n = r0 + per < rows ? per : rows - r0;
+        ch[nt].left = left + r0 * inner;
+        ch[nt].right = right;
+        ch[nt].out = out + r0 * cols;
+        ch[nt].rows = n;
+        ch[nt].inner = inner;
+        ch[nt].cols = cols;
+        started[nt] = pthread_create(&tid[nt], NULL, mm_chunk_worker, &ch[nt]) == 0;
+        if (!started[nt]) mm_chunk_worker(&ch[nt]);
+    }
+    for (int t = 0; t < nt; t++)
+        if (started[t]) pthread_join(tid[t], NULL);
+}
+
 int orc_matmul_rows_f32(const float *a, const orc_layout *la, const float *b, const orc_layout *lb,
                         const int64_t *rows, int64_t nrows, float *out_rows) {
     uint64_t K = la->shape[1], N = lb->shape[1];
@@ -846,8 +890,8 @@ uint64_t orc_exp_max_ulp(const float *got, uint32_t first_bits, uint64_t n, int 
     if (threads > 64) threads = 64;
     pthread_t tid[64];
     exp_chunk ch[64];
+    int started[64] = {0};
     const uint64_t per = (n + (uint64_t)threads - 1) / (uint64_t)threads;
-    int started = 0;
     for (int t = 0; t < threads; t++) {
         ch[t].got = got;
         ch[t].first = first_bits;
@@ -855,14 +899,12 @@ uint64_t orc_exp_max_ulp(const float *got, uint32_t first_bits, uint64_t n, int 
         ch[t].end = ch[t].begin + per < n ? ch[t].begin + per : n;
         ch[t].worst = 0;
         ch[t].worst_index = 0;
-        if (pthread_create(&tid[t], NULL, exp_check_worker, &ch[t]) == 0) started = t + 1;
-        else {
-            exp_check_worker(&ch[t]);
-        }
+        started[t] = pthread_create(&tid[t], NULL, exp_check_worker, &ch[t]) == 0;
+        if (!started[t]) exp_check_worker(&ch[t]);
     }
     uint64_t worst = 0, wi = 0;
     for (int t = 0; t < threads; t++) {
-        if (t < started) pthread_join(tid[t], NULL);
+        if (started[t]) pthread_join(tid[t], NULL);
         if (ch[t].worst > worst) {
             worst = ch[t].worst;
             wi = ch[t].worst_index;

@@ -365,6 +365,8 @@ int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
 constexpr int64_t kMaxSplitK = 8;
 constexpr int64_t kMinSplitDepth = 1024;
 
+// Runs the split; returns TRS_E_ALLOCATION_FAILED without launching anything
+// when the workspace cannot be had (the caller then runs the unsplit tile).
 int launch_split_k(GemmArgs g, bool a_plain, bool b_plain, int64_t sak, int64_t sbk, int64_t S, hipStream_t s) {
     float *const C = g.c;
     const int64_t mn = g.M * g.N, Ks = g.K / S;
@@ -389,16 +391,87 @@ int launch_split_k(GemmArgs g, bool a_plain, bool b_plain, int64_t sak, int64_t 
     return rc ? rc : frc;
 }
 
-}  // namespace
+// Which kernel a product runs.  Tile choice:
+//   - the 256x256 tile when it divides M, N and K and gives every CU a block;
+//   - else, for an aligned single matrix with M, N multiples of 256 and a long
+//     K, the 256x256 tile over S K-slices, when S*tiles reaches half the CUs
+//     or at least the block count of the tile it replaces;
+//   - else 64x128 when 128x128 would give fewer than two blocks per CU (76%
+//     against 69% of peak measured at 4096x1024x8192), else 128x128 (full or
+//     edge-guarded).
+enum class GemmKind { Strided, Large, SplitK, Medium, Small };
+struct GemmPlan {
+    GemmKind kind = GemmKind::Strided;
+    int bm = 0, bn = 0, bk = 0;
+    int64_t splits = 1;
+    int64_t blocks = 0;
+    bool full = false;
+    // SplitK only: the unsplit tile, run when no workspace can be allocated.
+    GemmKind fallback = GemmKind::Small;
+    bool fallback_full = false;
+};
 
-}  // namespace trs
+GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, bool b_trans, bool aligned,
+                   int cu_count) {
+    GemmPlan p;
+    const int64_t M = g.M, N = g.N, K = g.K, batch = g.batch;
+    if (!(a_plain || a_trans) || !(b_plain || b_trans)) {
+        p.kind = GemmKind::Strided;
+        p.blocks = std::min<int64_t>((M * N * batch + 255) / 256, (int64_t)cu_count * 16);
+        return p;
+    }
+    const int64_t large_tiles = (M / LargeTiles::BM) * (N / LargeTiles::BN) * batch;
+    const int64_t large_bk = (a_plain && b_plain) ? LargeTiles::BK : LargeTilesK16::BK;
+    const bool large_fits = aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0;
+    if (large_fits && K % large_bk == 0 && large_tiles >= cu_count) {
+        p.kind = GemmKind::Large;
+        p.bm = LargeTiles::BM, p.bn = LargeTiles::BN, p.bk = (int)large_bk;
+        p.blocks = large_tiles;
+        p.full = true;
+        return p;
+    }
+    const bool full = aligned && M % SmallTiles::BM == 0 && N % SmallTiles::BN == 0 && K % SmallTiles::BK == 0;
+    const int64_t small_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+    if (full && small_tiles < 2 * (int64_t)cu_count) {
+        p.kind = GemmKind::Medium;
+        p.bm = MediumTiles::BM, p.bn = MediumTiles::BN, p.bk = MediumTiles::BK;
+        p.blocks = ((M + 63) / 64) * ((N + 127) / 128) * batch;
+    } else {
+        p.kind = GemmKind::Small;
+        p.bm = SmallTiles::BM, p.bn = SmallTiles::BN, p.bk = SmallTiles::BK;
+        p.blocks = small_tiles;
+    }
+    p.full = full;
+    if (batch == 1 && large_fits && large_tiles > 0 && large_tiles < cu_count) {
+        int64_t S = 1;
+        while (S < kMaxSplitK && large_tiles * S * 2 <= cu_count && K % (S * 2 * large_bk) == 0 &&
+               K / (S * 2) >= kMinSplitDepth)
+            S *= 2;
+        if (S > 1 && (2 * large_tiles * S >= cu_count || large_tiles * S >= p.blocks)) {
+            p.fallback = p.kind;
+            p.fallback_full = p.full;
+            p.kind = GemmKind::SplitK;
+            p.bm = LargeTiles::BM, p.bn = LargeTiles::BN, p.bk = (int)large_bk;
+            p.splits = S;
+            p.blocks = large_tiles * S;
+            p.full = true;
+        }
+    }
+    return p;
+}
 
-using namespace trs;
+// Operand analysis shared by trs_matmul_f32 and trs_matmul_plan_f32: checks
+// the layouts and fills the GEMM arguments.  *empty is set when nothing is
+// to be computed (an empty output, or K = 0).
+struct GemmSetup {
+    GemmArgs g{};
+    bool a_plain = false, a_trans = false, b_plain = false, b_trans = false, aligned = false;
+    int64_t sam = 0, sak = 0, sbk = 0, sbn = 0;
+    bool empty_output = false, zero_k = false;
+};
 
-extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
-                              float *c, const trs_layout *lc) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
+int setup_gemm(const float *a, const trs_layout *la, const float *b, const trs_layout *lb, float *c,
+               const trs_layout *lc, bool check_pointers, GemmSetup *st) {
     int rc = check_layout(la, "left");
     if (!rc) rc = check_layout(lb, "right");
     if (!rc) rc = check_layout(lc, "output");
@@ -419,73 +492,104 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
     if (lc->rank != r || lc->shape[r - 2] != M || lc->shape[r - 1] != N || (r == 3 && lc->shape[0] != batch))
         return set_error(TRS_E_SHAPE_MISMATCH, "matmul output layout has the wrong shape");
     if (!layout_is_contiguous(lc)) return set_error(TRS_E_INVALID_ARGUMENT, "matmul output must be contiguous");
-    if (M == 0 || N == 0 || batch == 0) return TRS_OK;
-    // With K = 0 the operands are empty (no storage is needed) and C is +0.0.
-    if (!c || (K > 0 && (!a || !b))) return set_error(TRS_E_INVALID_ARGUMENT, "null matmul operand");
-    {
+    st->empty_output = M == 0 || N == 0 || batch == 0;
+    st->zero_k = K == 0;
+    if (st->empty_output) return TRS_OK;
+    if (check_pointers) {
+        // With K = 0 the operands are empty (no storage is needed) and C is +0.0.
+        if (!c || (K > 0 && (!a || !b))) return set_error(TRS_E_INVALID_ARGUMENT, "null matmul operand");
         // C is written while A and B are still being read: no shared memory.
         const ByteRange out_bytes = byte_range(c, lc, 4);
         if (K > 0 && (ranges_overlap(out_bytes, byte_range(a, la, 4)) || ranges_overlap(out_bytes, byte_range(b, lb, 4))))
             return set_error(TRS_E_INVALID_ARGUMENT, "matmul output overlaps an operand");
     }
-    float *C = c + lc->offset;
-    if (K == 0) return trs_memset_zero(C, (size_t)(M * N * batch) * sizeof(float));
-
-    const int64_t sam = la->stride[r - 2], sak = la->stride[r - 1];
-    const int64_t sbk = lb->stride[r - 2], sbn = lb->stride[r - 1];
+    st->sam = la->stride[r - 2], st->sak = la->stride[r - 1];
+    st->sbk = lb->stride[r - 2], st->sbn = lb->stride[r - 1];
     const int64_t bsa = r == 3 ? la->stride[0] : 0, bsb = r == 3 ? lb->stride[0] : 0;
     // A unit-stride along k (plain) or along m (transposed view); same for B.
-    const bool a_plain = sak == 1 || K == 1, a_trans = !a_plain && (sam == 1 || M == 1);
-    const bool b_plain = sbn == 1 || N == 1, b_trans = !b_plain && (sbk == 1 || K == 1);
-    const float *A = a + la->offset, *B = b + lb->offset;
-
-    if (!(a_plain || a_trans) || !(b_plain || b_trans)) {
-        const int64_t total = M * N * batch;
-        const int64_t grid = std::min<int64_t>((total + 255) / 256, (int64_t)dev->cu_count * 16);
-        hipLaunchKernelGGL(gemm_f32_strided, dim3((unsigned)grid), dim3(256), 0, dev->stream, A, B, C, M, N, K,
-                           sam, sak, sbk, sbn, bsa, bsb, batch);
-        TRS_LAUNCH_CHECK("strided gemm launch");
-        return TRS_OK;
-    }
-
-    GemmArgs g{};
-    g.a = A;
-    g.b = B;
-    g.c = C;
+    st->a_plain = st->sak == 1 || K == 1;
+    st->a_trans = !st->a_plain && (st->sam == 1 || M == 1);
+    st->b_plain = st->sbn == 1 || N == 1;
+    st->b_trans = !st->b_plain && (st->sbk == 1 || K == 1);
+    GemmArgs &g = st->g;
+    g.a = a ? a + la->offset : nullptr;
+    g.b = b ? b + lb->offset : nullptr;
+    g.c = c ? c + lc->offset : nullptr;
     g.M = M;
     g.N = N;
     g.K = K;
-    g.lda = a_plain ? sam : sak;
-    g.ldb = b_plain ? sbk : sbn;
+    g.lda = st->a_plain ? st->sam : st->sak;
+    g.ldb = st->b_plain ? st->sbk : st->sbn;
     g.ldc = N;
     g.bsa = bsa;
     g.bsb = bsb;
     g.bsc = M * N;
     g.batch = batch;
     auto al16 = [](const float *p) { return ((uintptr_t)p % 16) == 0; };
-    const bool aligned = al16(A) && al16(B) && al16(C) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
-                         (batch == 1 || (bsa % 4 == 0 && bsb % 4 == 0));
-    // The large tile only when it divides the problem and still gives every
-    // CU a block, or when splitting a long K gives every CU one; otherwise
-    // the small tile (full or edge-guarded).
-    const int64_t large_tiles = (M / LargeTiles::BM) * (N / LargeTiles::BN) * batch;
-    const int64_t large_bk = (a_plain && b_plain) ? LargeTiles::BK : LargeTilesK16::BK;
-    if (batch == 1 && aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0 && large_tiles < dev->cu_count) {
-        int64_t S = 1;
-        while (S < kMaxSplitK && large_tiles * S * 2 <= dev->cu_count && K % (S * 2 * large_bk) == 0 &&
-               K / (S * 2) >= kMinSplitDepth)
-            S *= 2;
-        if (S > 1) return launch_split_k(g, a_plain, b_plain, sak, sbk, S, dev->stream);
+    st->aligned = al16(g.a) && al16(g.b) && al16(g.c) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                  (batch == 1 || (bsa % 4 == 0 && bsb % 4 == 0));
+    return TRS_OK;
+}
+
+int run_unsplit(const GemmPlan &p, const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
+    switch (p.kind) {
+    case GemmKind::Large:
+    case GemmKind::SplitK: return launch_large(g, a_plain, b_plain, s);
+    case GemmKind::Medium: return launch_layout<MediumTiles>(g, a_plain, b_plain, true, s);
+    default: return launch_layout<SmallTiles>(g, a_plain, b_plain, p.full, s);
     }
-    if (aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0 && K % large_bk == 0 &&
-        large_tiles >= dev->cu_count)
-        return launch_large(g, a_plain, b_plain, dev->stream);
-    const bool full = aligned && M % SmallTiles::BM == 0 && N % SmallTiles::BN == 0 && K % SmallTiles::BK == 0;
-    // Fewer than two 128x128 blocks per CU (e.g. a 4096x1024 weight gradient
-    // with K = 8192): 64x128 blocks double the count (76% against 69% of peak
-    // measured for that shape).
-    const int64_t small_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batch;
-    if (full && small_tiles < 2 * (int64_t)dev->cu_count)
-        return launch_layout<MediumTiles>(g, a_plain, b_plain, true, dev->stream);
-    return launch_layout<SmallTiles>(g, a_plain, b_plain, full, dev->stream);
+}
+
+}  // namespace
+
+}  // namespace trs
+
+using namespace trs;
+
+extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
+                              float *c, const trs_layout *lc) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    GemmSetup st;
+    int rc = setup_gemm(a, la, b, lb, c, lc, true, &st);
+    if (rc || st.empty_output) return rc;
+    const GemmArgs &g = st.g;
+    if (st.zero_k) return trs_memset_zero(g.c, (size_t)(g.M * g.N * g.batch) * sizeof(float));
+    const GemmPlan p = plan_gemm(g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, st.aligned, dev->cu_count);
+    if (p.kind == GemmKind::Strided) {
+        hipLaunchKernelGGL(gemm_f32_strided, dim3((unsigned)p.blocks), dim3(256), 0, dev->stream, g.a, g.b, g.c, g.M,
+                           g.N, g.K, st.sam, st.sak, st.sbk, st.sbn, g.bsa, g.bsb, g.batch);
+        TRS_LAUNCH_CHECK("strided gemm launch");
+        return TRS_OK;
+    }
+    if (p.kind == GemmKind::SplitK) {
+        rc = launch_split_k(g, st.a_plain, st.b_plain, st.sak, st.sbk, p.splits, dev->stream);
+        if (rc != TRS_E_ALLOCATION_FAILED) return rc;
+        // No workspace: the split is only an optimisation, so run the tile the
+        // plan would otherwise have chosen (nothing was launched).
+        GemmPlan fb;
+        fb.kind = p.fallback;
+        fb.full = p.fallback_full;
+        return run_unsplit(fb, g, st.a_plain, st.b_plain, dev->stream);
+    }
+    return run_unsplit(p, g, st.a_plain, st.b_plain, dev->stream);
+}
+
+extern "C" int trs_matmul_plan_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
+                                   const float *c, const trs_layout *lc, int *tile_m, int *tile_n, int *tile_k,
+                                   int64_t *splits, int64_t *blocks) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    GemmSetup st;
+    int rc = setup_gemm(a, la, b, lb, const_cast<float *>(c), lc, false, &st);
+    if (rc) return rc;
+    GemmPlan p;
+    if (!st.empty_output && !st.zero_k)
+        p = plan_gemm(st.g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, st.aligned, dev->cu_count);
+    if (tile_m) *tile_m = p.bm;
+    if (tile_n) *tile_n = p.bn;
+    if (tile_k) *tile_k = p.bk;
+    if (splits) *splits = p.splits;
+    if (blocks) *blocks = p.blocks;
+    return TRS_OK;
 }

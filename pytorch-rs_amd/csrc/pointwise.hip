@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdio>
 
 #include "pw_core.h"
 #include "pw_host.h"
@@ -148,15 +149,22 @@ constexpr int64_t kSumOneBlock = 32768;  // at most 128 elements per lane in one
 
 // Fixed-order two-level sum.  Pass 1: block b sums the contiguous element
 // range [b*chunk, (b+1)*chunk) -- lane l adds elements l, l+256, ... in order,
-// then a fixed shuffle/LDS tree over the 256 lanes.  Pass 2 sums the block
-// partials in the same way.  Up to kSumOneBlock elements, pass 1 runs as one
-// block over the whole range.  The order depends only on the element count.
+// then a fixed LDS tree over the 256 lanes.  Pass 2 sums the block partials
+// in the same way.  Up to kSumOneBlock elements, pass 1 runs as one block
+// over the whole range.  The order depends only on the element count.
+// Every lane starts from -0.0, the additive identity (x + -0.0 == x for every
+// x, +0.0 included), as Rust's f32 Sum does: an all-(-0.0) input sums to
+// -0.0 and every other result is unchanged by the start value.
+// Error bound: an element passes through at most ceil(chunk/256) in-lane
+// additions, 8 tree levels, 4 in-lane additions of pass 2 and 8 more tree
+// levels, so |sum - exact| <= (ceil(chunk/256) + 20) * 2^-24 * sum|x|
+// (one block: ceil(n/256) + 8).
 template <bool CONTIG>
 __global__ void __launch_bounds__(256) sum_pass1(const float *x, PwGeom g, int64_t chunk, float *partial) {
     __shared__ float red[256];
     const int64_t begin = (int64_t)blockIdx.x * chunk;
     const int64_t end = begin + chunk < g.numel ? begin + chunk : g.numel;
-    float acc = 0.0f;
+    float acc = -0.0f;
     for (int64_t e = begin + threadIdx.x; e < end; e += 256) {
         int64_t off;
         if constexpr (CONTIG) {
@@ -179,7 +187,7 @@ __global__ void __launch_bounds__(256) sum_pass1(const float *x, PwGeom g, int64
 
 __global__ void __launch_bounds__(256) sum_pass2(const float *partial, int n, float *out) {
     __shared__ float red[256];
-    float acc = 0.0f;
+    float acc = -0.0f;
     for (int e = threadIdx.x; e < n; e += 256) acc += partial[e];
     red[threadIdx.x] = acc;
     __syncthreads();
@@ -315,6 +323,69 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
                            (const float *)nullptr, rg, grad);
     TRS_LAUNCH_CHECK("broadcast reduction kernel");
     return TRS_OK;
+}
+
+// Sum of x into out[0]; pass 1's partials go to `partial` (kSumBlocks floats)
+// or, when it is null, to a buffer from the block cache.
+int sum_launch(DeviceState *dev, const float *x, const trs_layout *lx, float *out, float *partial) {
+    int rc = check_layout(lx, "input");
+    if (rc) return rc;
+    if (!out) return set_error(TRS_E_INVALID_ARGUMENT, "null output");
+    const int64_t n = layout_numel(lx);
+    if (n == 0) return trs_fill_f32(out, 1, -0.0f);
+    if (!x) return set_error(TRS_E_INVALID_ARGUMENT, "null input");
+    // Geometry for logical-order decode of a strided input.
+    PwGeom g;
+    std::memset(&g, 0, sizeof g);
+    g.numel = n;
+    g.rank = lx->rank;
+    g.ioff[0] = lx->offset;
+    for (int d = 0; d < lx->rank; d++) {
+        g.size[d] = lx->shape[d];
+        g.istride[0][d] = lx->stride[d];
+        if (lx->shape[d] > (int64_t)UINT32_MAX) g.wide = 1;
+        g.fd[d] = make_fast_div(lx->shape[d] > (int64_t)UINT32_MAX ? 1u : (uint32_t)lx->shape[d]);
+    }
+    const bool contig = layout_is_contiguous(lx);
+    // Up to kSumOneBlock elements: pass 1 alone, one block writing the result
+    // (one launch and no partials; the order is still fixed by n).
+    if (n <= kSumOneBlock) {
+        if (contig)
+            hipLaunchKernelGGL(sum_pass1<true>, dim3(1), dim3(256), 0, dev->stream, x, g, n, out);
+        else
+            hipLaunchKernelGGL(sum_pass1<false>, dim3(1), dim3(256), 0, dev->stream, x, g, n, out);
+        TRS_LAUNCH_CHECK("sum one pass");
+        return TRS_OK;
+    }
+    const int64_t chunk = (n + kSumBlocks - 1) / kSumBlocks;
+    const int blocks = (int)((n + chunk - 1) / chunk);  // <= kSumBlocks partials for every n
+    if (blocks > kSumBlocks)  // cannot happen; the scratch holds kSumBlocks partials
+        return set_error(TRS_E_INVALID_ARGUMENT, "sum of %lld elements needs %d partials, above the %d the scratch holds",
+                         (long long)n, blocks, kSumBlocks);
+    // Without a caller buffer, the partials take a buffer of this call's own:
+    // the block cache returns it in stream order, so concurrent callers on
+    // one device never share it.
+    void *owned = nullptr;
+    if (!partial) {
+        rc = trs_alloc(kSumBlocks * sizeof(float), &owned);
+        if (rc) return rc;
+        partial = (float *)owned;
+    }
+    if (contig)
+        hipLaunchKernelGGL(sum_pass1<true>, dim3(blocks), dim3(256), 0, dev->stream, x, g, chunk, partial);
+    else
+        hipLaunchKernelGGL(sum_pass1<false>, dim3(blocks), dim3(256), 0, dev->stream, x, g, chunk, partial);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(sum_pass2, dim3(1), dim3(256), 0, dev->stream, partial, blocks, out);
+        e = hipGetLastError();
+    }
+    rc = e == hipSuccess ? TRS_OK : hip_fail(e, "sum launch");
+    if (owned) {
+        const int frc = trs_free(owned);
+        if (!rc) rc = frc;
+    }
+    return rc;
 }
 
 // Contiguous layout of `shape` (for gradients, which are logical-order).
@@ -476,50 +547,7 @@ int trs_reduce_to_shape_f32(const float *up, const trs_layout *lout, const trs_l
 int trs_sum_f32(const float *x, const trs_layout *lx, float *out) {
     DeviceState *dev = device_state();
     if (!dev) return TRS_E_NO_DEVICE;
-    int rc = check_layout(lx, "input");
-    if (rc) return rc;
-    if (!out) return set_error(TRS_E_INVALID_ARGUMENT, "null output");
-    const int64_t n = layout_numel(lx);
-    if (n == 0) return trs_fill_f32(out, 1, -0.0f);
-    if (!x) return set_error(TRS_E_INVALID_ARGUMENT, "null input");
-    // Geometry for logical-order decode of a strided input.
-    PwGeom g;
-    std::memset(&g, 0, sizeof g);
-    g.numel = n;
-    g.rank = lx->rank;
-    g.ioff[0] = lx->offset;
-    for (int d = 0; d < lx->rank; d++) {
-        g.size[d] = lx->shape[d];
-        g.istride[0][d] = lx->stride[d];
-        if (lx->shape[d] > (int64_t)UINT32_MAX) g.wide = 1;
-        g.fd[d] = make_fast_div(lx->shape[d] > (int64_t)UINT32_MAX ? 1u : (uint32_t)lx->shape[d]);
-    }
-    // Up to kSumOneBlock elements: pass 1 alone, one block writing the result
-    // (one launch and no partials buffer; the order is still fixed by n).
-    if (n <= kSumOneBlock) {
-        if (layout_is_contiguous(lx))
-            hipLaunchKernelGGL(sum_pass1<true>, dim3(1), dim3(256), 0, dev->stream, x, g, n, out);
-        else
-            hipLaunchKernelGGL(sum_pass1<false>, dim3(1), dim3(256), 0, dev->stream, x, g, n, out);
-        TRS_LAUNCH_CHECK("sum one pass");
-        return TRS_OK;
-    }
-    // Block partials in a buffer of this call's own: the block cache returns
-    // it in stream order, so concurrent callers on one device never share it.
-    void *partial_buf = nullptr;
-    rc = trs_alloc(kSumBlocks * sizeof(float), &partial_buf);
-    if (rc) return rc;
-    const int64_t chunk = (n + kSumBlocks - 1) / kSumBlocks;
-    const int blocks = (int)((n + chunk - 1) / chunk);
-    float *partial = (float *)partial_buf;
-    if (layout_is_contiguous(lx))
-        hipLaunchKernelGGL(sum_pass1<true>, dim3(blocks), dim3(256), 0, dev->stream, x, g, chunk, partial);
-    else
-        hipLaunchKernelGGL(sum_pass1<false>, dim3(blocks), dim3(256), 0, dev->stream, x, g, chunk, partial);
-    TRS_LAUNCH_CHECK("sum pass 1");
-    hipLaunchKernelGGL(sum_pass2, dim3(1), dim3(256), 0, dev->stream, partial, blocks, out);
-    TRS_LAUNCH_CHECK("sum pass 2");
-    return trs_free(partial_buf);
+    return sum_launch(dev, x, lx, out, nullptr);
 }
 
 }  // extern "C"

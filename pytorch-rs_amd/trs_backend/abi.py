@@ -109,6 +109,8 @@ _SIGNATURES = {
     "trs_reduce_to_shape_f32": ([c_void_p, _LP, _LP, c_void_p], c_int),
     "trs_accumulate_f32": ([c_void_p, c_void_p, c_size_t], c_int),
     "trs_matmul_f32": ([c_void_p, _LP, c_void_p, _LP, c_void_p, _LP], c_int),
+    "trs_matmul_plan_f32": ([c_void_p, _LP, c_void_p, _LP, c_void_p, _LP, POINTER(c_int), POINTER(c_int),
+                             POINTER(c_int), POINTER(ctypes.c_int64), POINTER(ctypes.c_int64)], c_int),
     "trs_fusion_compile": ([c_char_p, c_size_t, POINTER(c_uint64)], c_int),
     "trs_fusion_launch": ([c_uint64, c_int, POINTER(c_void_p), _LP, c_void_p, _LP], c_int),
     "trs_fusion_launch_multi": ([c_uint64, c_int, POINTER(c_void_p), _LP, c_int, POINTER(c_void_p), _LP], c_int),

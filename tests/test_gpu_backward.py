@@ -3,8 +3,9 @@
 relu VJP, Multiply VJP (with and without broadcast), the add VJP
 (reduce-to-shape), accumulation and fills are bit-exact: the device kernels
 keep the reference's per-element expressions and its output-major
-accumulation order.  sum uses a fixed-order tree, checked within the float
-summation bound against the reference's sequential fold.
+accumulation order.  sum uses a fixed-order tree, checked within the tree's
+own depth bound against the exact sum, exact on small integers, and with the
+reference's -0.0 start value.
 """
 import ctypes
 
@@ -123,15 +124,55 @@ def test_add_vjp_reduce_to_shape_bit_exact(oshape, self_shape):
     assert_bitwise_equal(gpu_reduce(up, oshape, self_shape), O.reduce_to_shape(up, oshape, self_shape))
 
 
+def sum_tree_depth(n: int) -> int:
+    """Most roundings any element passes through in trs_sum_f32's fixed tree:
+    one block (n <= 32768) adds ceil(n/256) terms per lane, then 8 tree
+    levels; above that each of at most 1024 blocks adds ceil(chunk/256) per
+    lane and 8 levels, and pass 2 adds 4 partials per lane and 8 levels."""
+    if n <= 32768:
+        return -(-n // 256) + 8
+    chunk = -(-n // 1024)
+    return -(-chunk // 256) + 8 + 4 + 8
+
+
 @pytest.mark.parametrize("n", [1, 3, 1000, 32768, 32769, 1 << 20, (1 << 23) + 5])
-def test_sum_within_summation_bound(n):
+@pytest.mark.parametrize("dist", ["normal", "positive"])
+def test_sum_within_its_tree_bound(n, dist):
+    """|device - exact| <= d * 2^-24 * sum|x| with d the tree's depth (52 at
+    the MLP loss's 2^23 elements, against 2^24 for a sequential fold), the
+    exact sum taken with math.fsum over the float64 values.  Positive data
+    (no cancellation) makes a dropped or doubled block show as a gross error.
+    The sequential oracle fold is compared within the sum of both bounds."""
+    import math
     rng = np.random.default_rng(n)
-    x = rng.standard_normal(n).astype(np.float32)
-    got = gpu_sum(x, (n,))
+    x = rng.standard_normal(n) if dist == "normal" else rng.uniform(0.5, 1.5, n)
+    x = x.astype(np.float32)
+    got = float(gpu_sum(x, (n,)))
+    exact = math.fsum(x.astype(np.float64))
+    abs_sum = O.sum_abs(x)
+    d = sum_tree_depth(n)
+
+    def gamma(k):  # Higham's gamma_k = k u / (1 - k u), u = 2^-24
+        return k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
+
+    assert abs(got - exact) <= gamma(d) * abs_sum, (got, exact, d)
+    want = float(O.sum_f32(x, (n,)))
+    assert abs(want - exact) <= gamma(n - 1) * abs_sum
+    assert abs(got - want) <= (gamma(d) + gamma(n - 1)) * abs_sum
+
+
+@pytest.mark.parametrize("n", [1, 2, 257, 32768, 40000, 1 << 20])
+def test_sum_of_negative_zeros_is_negative_zero(n):
+    """Rust's f32 Sum starts from -0.0 (the oracle's fold does too): an
+    all-(-0.0) input sums to -0.0 on the one-block and two-pass paths, while
+    one +0.0 among them gives +0.0."""
+    x = np.full(n, -0.0, np.float32)
+    got = np.float32(gpu_sum(x, (n,)))
     want = O.sum_f32(x, (n,))
-    # Any two float orderings of an n-term sum differ by at most 2 * (n-1) * u * sum|x|.
-    bound = 2 * (n - 1) * 2.0 ** -24 * O.sum_abs(x)
-    assert abs(float(got) - float(want)) <= bound
+    assert got.view(np.uint32) == want.view(np.uint32) == 0x80000000
+    x[n // 2] = 0.0
+    got = np.float32(gpu_sum(x, (n,)))
+    assert got.view(np.uint32) == O.sum_f32(x, (n,)).view(np.uint32) == 0
 
 
 @pytest.mark.parametrize("n", [257, 32768, 32769, 100003])

@@ -160,18 +160,49 @@ def _layouts(a, b, ta, tb):
     return ast.ravel(), ((m, k), astr, 0), bst.ravel(), ((k, n), bstr, 0)
 
 
-# On a 256-CU device these outputs hold fewer 256x256 tiles than CUs and K is
-# long, so K is split into S slices (8, 4, 4 and 2 here) summed in slice order.
-SPLIT_K = [(256, 8192, 256), (512, 4096, 1024), (4096, 8192, 1024), (8192, 4096, 1024)]
+def _cu_count() -> int:
+    import ctypes
+    from trs_backend import abi
+    name, cus, clk = ctypes.create_string_buffer(256), ctypes.c_int(), ctypes.c_int()
+    abi.check(abi.lib.trs_device_info(name, 256, ctypes.byref(cus), ctypes.byref(clk)))
+    return cus.value
 
 
-@pytest.mark.parametrize("m,k,n", SPLIT_K)
+def _plan(m, k, n, ta=False, tb=False):
+    """(tile_m, tile_n, tile_k, splits, blocks) trs_matmul_f32 chooses for a
+    16-byte-aligned product in the given layout on this device."""
+    import ctypes
+    from trs_backend import abi
+    la = abi.layout_of((m, k), (1, m) if ta else (k, 1))
+    lb = abi.layout_of((k, n), (1, k) if tb else (n, 1))
+    lc = abi.layout_of((m, n))
+    tm, tn, tk = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    sp, bl = ctypes.c_int64(), ctypes.c_int64()
+    abi.check(abi.lib.trs_matmul_plan_f32(None, ctypes.byref(la), None, ctypes.byref(lb), None, ctypes.byref(lc),
+                                          ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk), ctypes.byref(sp),
+                                          ctypes.byref(bl)))
+    return tm.value, tn.value, tk.value, sp.value, bl.value
+
+
+# Outputs with fewer 256x256 tiles than CUs and a long K.  On a 256-CU device
+# K is split into S slices (the value given here) summed in slice order: S
+# slices fill half the CUs, or give as many blocks as the unsplit tile.
+SPLIT_K = [(256, 8192, 256, 8), (1024, 8192, 1024, 8), (4096, 8192, 1024, 4), (8192, 4096, 1024, 2)]
+
+
+def _expect_split(m, k, n, s, ta, tb):
+    if _cu_count() != 256:
+        pytest.skip(f"the split counts listed are those of a 256-CU device (this one has {_cu_count()})")
+    plan = _plan(m, k, n, ta, tb)
+    assert plan[:2] == (256, 256) and plan[3] == s, plan
+
+
+@pytest.mark.parametrize("m,k,n,s", SPLIT_K)
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
-def test_split_k_all_layouts_exact_on_small_integers(m, k, n, ta, tb):
-    """Every partial and total sum of small integers is exact, so the split
-    result equals the float64 product exactly."""
-    if m * n > 512 * 1024 and (ta, tb) not in ((False, False), (True, False)):
-        pytest.skip("the MLP's two split shapes run in the layouts the MLP uses (NN forward, TN weight gradient)")
+def test_split_k_all_layouts_exact_on_small_integers(m, k, n, s, ta, tb):
+    """The plan splits K as listed, and every partial and total sum of small
+    integers is exact, so the split result equals the float64 product."""
+    _expect_split(m, k, n, s, ta, tb)
     rng = np.random.default_rng(m + k + n + 2 * ta + tb)
     a = rng.integers(-3, 4, (m, k)).astype(np.float32)
     b = rng.integers(-3, 4, (k, n)).astype(np.float32)
@@ -180,9 +211,25 @@ def test_split_k_all_layouts_exact_on_small_integers(m, k, n, ta, tb):
     assert np.array_equal(U.matmul(sa, *la, sb, *lb), want)
 
 
+@pytest.mark.parametrize("m,k,n", [(256, 2048, 256), (1024, 4096, 1024), (512, 4096, 1024)])
+def test_split_k_not_taken_where_it_gives_fewer_blocks(m, k, n):
+    """Splitting these into 256x256 slices would give fewer blocks than the
+    64x128 tile (and fill less than half the CUs), so they run unsplit on it;
+    the products are exact on small integers."""
+    if _cu_count() != 256:
+        pytest.skip("plan expectations are those of a 256-CU device")
+    assert _plan(m, k, n)[:4] == (64, 128, 32, 1)
+    rng = np.random.default_rng(m + n)
+    a = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    b = rng.integers(-3, 4, (k, n)).astype(np.float32)
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0), want)
+
+
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
 def test_split_k_normal_inputs_within_tolerance(ta, tb):
-    m, k, n = 256, 4096, 256
+    m, k, n = 256, 8192, 256
+    _expect_split(m, k, n, 8, ta, tb)
     rng = np.random.default_rng(77 + 2 * ta + tb)
     a = (rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
     b = (rng.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
@@ -195,12 +242,13 @@ def test_split_k_normal_inputs_within_tolerance(ta, tb):
 def test_split_k_special_values_across_slices():
     """Infinities and a NaN in different k slices: NaN and signed-infinity
     positions equal the oracle's sequential sum; the rest within tolerance."""
-    m, k, n = 256, 4096, 256
+    m, k, n = 256, 8192, 256
+    _expect_split(m, k, n, 8, False, False)
     rng = np.random.default_rng(5)
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((k, n)).astype(np.float32)
-    a[5, 100], a[5, 3000], a[7, 2000], a[9, 1100] = np.inf, -np.inf, np.nan, np.inf
-    b[1500, 9] = -np.inf
+    a[5, 100], a[5, 6000], a[7, 4000], a[9, 2100] = np.inf, -np.inf, np.nan, np.inf
+    b[3500, 9] = -np.inf
     got = U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0)
     want = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
     for pred in (np.isnan, np.isposinf, np.isneginf):

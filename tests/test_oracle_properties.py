@@ -208,3 +208,65 @@ def test_row_blocked_matmul_is_bit_identical_to_the_plain_loop(m, k, n):
     plain = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
     blocked = O.matmul_row_blocked(a, b)
     assert_bitwise_equal(blocked, plain)
+
+
+@pytest.mark.parametrize("m,k,n,threads", [(1, 3, 5, 4), (6, 17, 9, 3), (37, 64, 70, 8), (130, 41, 33, 64)])
+def test_threaded_matmul_is_bit_identical_to_the_plain_loop(m, k, n, threads):
+    """Splitting the row-blocked loop over threads by output rows keeps every
+    element's k-ascending order, so the result equals the plain loop bit for
+    bit, also with more threads than rows and rows not a multiple of 4."""
+    rng = _rng(60 + m)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    plain = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+    assert_bitwise_equal(O.matmul_threads(a, b, threads=threads), plain)
+
+
+def _exact_exp(first_bits, n):
+    x = np.arange(first_bits, first_bits + n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    return O.unary_contig(O.EXP, x)
+
+
+def test_exp_checker_reports_planted_ulp_errors():
+    """orc_exp_max_ulp must report the largest planted distance and where it
+    is: exact glibc values give 0; values moved by known counts of
+    representable floats (across thread boundaries) give those counts."""
+    first = 0x3F000000  # 0.5 upward: finite, normal results
+    n = 100_003
+    exact = _exact_exp(first, n)
+    assert O.exp_max_ulp(exact, first, threads=7) == (0, 0)
+    for idx, steps in ((5, 1), (n // 2, 3), (n - 1, 2), (14_286, -4)):
+        got = exact.copy()
+        got.view(np.int32)[idx] += steps  # positive finite values: bits are monotone
+        assert O.exp_max_ulp(got, first, threads=7) == (abs(steps), idx)
+    got = exact.copy()
+    got.view(np.int32)[10] += 2
+    got.view(np.int32)[70_000] -= 5
+    assert O.exp_max_ulp(got, first, threads=7) == (5, 70_000)
+
+
+def test_exp_checker_nan_handling_and_signed_results():
+    """A NaN where glibc gives a number (or the reverse) is the largest
+    distance; NaN where glibc gives NaN is 0.  Distances across zero count
+    the representable floats between (here at the underflow edge)."""
+    first = 0x7F800000 - 8  # the last finite floats, +inf, then NaN patterns
+    n = 16
+    exact = _exact_exp(first, n)
+    assert np.isnan(exact[-1]) and np.isinf(exact[7])
+    assert O.exp_max_ulp(exact, first, threads=2)[0] == 0
+    got = exact.copy()
+    got[3] = np.nan
+    assert O.exp_max_ulp(got, first, threads=2) == (2 ** 64 - 1, 3)
+    got = exact.copy()
+    got[-1] = np.float32(1.0)
+    assert O.exp_max_ulp(got, first, threads=2) == (2 ** 64 - 1, n - 1)
+    # exp of large negative inputs is +0.0; -0.0 counts as the same value and
+    # the smallest subnormal as one float away
+    first = int(np.float32(-120.0).view(np.uint32))
+    exact = _exact_exp(first, 4)
+    assert (exact == 0).all()
+    got = exact.copy()
+    got[1] = -0.0
+    assert O.exp_max_ulp(got, first) == (0, 0)
+    got[2] = np.float32(1e-45)
+    assert O.exp_max_ulp(got, first) == (1, 2)
