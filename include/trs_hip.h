@@ -169,6 +169,18 @@ int trs_mask_apply_f32(const float *h, const trs_layout *lh, const uint8_t *mask
  * Rust's f32 Sum does, so an all-(-0.0) input gives -0.0; an empty one gives
  * -0.0 too. */
 int trs_sum_f32(const float *x, const trs_layout *lx, float *out);
+/* trs_sum_f32 that allocates nothing: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same kernels and
+ * the same result bits as trs_sum_f32.  Above 32,768 elements the block
+ * partials (at most 1,024 floats for any input size, so no size is refused)
+ * go to a static 4 KiB device array that each GPU holds until the process
+ * ends, shared by every call on that GPU: the calls are ordered on the
+ * device's library stream, and calls that ran on different streams of one
+ * GPU at once would race on it.  Nothing needs clearing between calls (pass
+ * 1 writes every partial pass 2 reads).  Its device address is looked up
+ * once per device when the library sets the device up (trs_init). */
+int trs_sum_f32_noalloc(const float *x, const trs_layout *lx, float *out);
 /* out[0..n) = *value (a device float): the Sum VJP fill (src/tensor.rs:3008-3013). */
 int trs_fill_from_device_f32(float *out, size_t n, const float *value);
 /* out[0..n) = value. */

@@ -198,6 +198,12 @@ __global__ void __launch_bounds__(256) sum_pass2(const float *partial, int n, fl
     if (threadIdx.x == 0) out[0] = red[0];
 }
 
+// Scratch of trs_sum_f32_noalloc: pass 1's block partials, kSumBlocks floats
+// (4 KiB) in a file-scope device array that each GPU holds until the process
+// ends.  In host code `scratch` names a host-side stand-in, not device
+// memory: kernels receive only the address setup_sum_scratch looks up.
+static __device__ __align__(256) float scratch[kSumBlocks];
+
 __global__ void __launch_bounds__(256) fill_kernel(float *out, size_t n, float value, const float *src) {
     const float v = src ? src[0] : value;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -323,6 +329,20 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
                            (const float *)nullptr, rg, grad);
     TRS_LAUNCH_CHECK("broadcast reduction kernel");
     return TRS_OK;
+}
+
+// Called by device_state() at a device's set-up, with that device current.
+void setup_sum_scratch(DeviceState *dev) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        dev->sum_scratch = nullptr;
+        std::snprintf(dev->sum_scratch_error, sizeof dev->sum_scratch_error, "hipGetSymbolAddress(scratch): %s (%d)",
+                      hipGetErrorString(e), (int)e);
+        return;
+    }
+    dev->sum_scratch = (float *)p;
 }
 
 // Sum of x into out[0]; pass 1's partials go to `partial` (kSumBlocks floats)
@@ -548,6 +568,15 @@ int trs_sum_f32(const float *x, const trs_layout *lx, float *out) {
     DeviceState *dev = device_state();
     if (!dev) return TRS_E_NO_DEVICE;
     return sum_launch(dev, x, lx, out, nullptr);
+}
+
+int trs_sum_f32_noalloc(const float *x, const trs_layout *lx, float *out) {
+    DeviceState *dev = device_state();
+    if (!dev) return TRS_E_NO_DEVICE;
+    if (!dev->sum_scratch)
+        return set_error(TRS_E_HIP, "the no-allocation sum's scratch is unavailable on device %d: %s", dev->index,
+                         dev->sum_scratch_error);
+    return sum_launch(dev, x, lx, out, dev->sum_scratch);
 }
 
 }  // extern "C"

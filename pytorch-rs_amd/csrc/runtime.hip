@@ -173,6 +173,7 @@ DeviceState *device_state() {
     dev->cu_count = prop.multiProcessorCount;
     dev->clock_khz = prop.clockRate;
     std::snprintf(dev->name, sizeof dev->name, "%s (%s)", prop.name[0] ? prop.name : "AMD GPU", prop.gcnArchName);
+    setup_sum_scratch(dev);
     dev->ready = true;
     return dev;
 }

@@ -39,7 +39,16 @@ struct DeviceState {
     std::mutex stage_mu;
     void *stage[2] = {nullptr, nullptr};
     hipEvent_t stage_done[2] = {nullptr, nullptr};
+    // Device address of this device's copy of the sum's static scratch array
+    // (pointwise.hip), looked up once at set-up; null if the lookup failed,
+    // with the failure's message kept for trs_sum_f32_noalloc to report.
+    float *sum_scratch = nullptr;
+    char sum_scratch_error[160] = {0};
 };
+
+// Looks up the device address of the static sum scratch array for `dev`
+// (the device must be current); called once per device at set-up.
+void setup_sum_scratch(DeviceState *dev);
 
 // Returns the current device's state, initialising it on first use.
 // On failure returns nullptr with the error recorded.

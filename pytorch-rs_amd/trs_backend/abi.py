@@ -101,6 +101,7 @@ _SIGNATURES = {
     "trs_unary_f32": ([c_int, c_void_p, _LP, c_void_p, _LP], c_int),
     "trs_mask_apply_f32": ([c_void_p, _LP, c_void_p, _LP, c_float, c_void_p, _LP], c_int),
     "trs_sum_f32": ([c_void_p, _LP, c_void_p], c_int),
+    "trs_sum_f32_noalloc": ([c_void_p, _LP, c_void_p], c_int),
     "trs_fill_from_device_f32": ([c_void_p, c_size_t, c_void_p], c_int),
     "trs_fill_f32": ([c_void_p, c_size_t, c_float], c_int),
     "trs_mask_backward_f32": ([c_void_p, _LP, c_void_p, _LP, c_float, c_void_p, _LP], c_int),
