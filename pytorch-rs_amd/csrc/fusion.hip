@@ -40,17 +40,27 @@ const char kPwCoreSource[] =
 #include "pw_core_src.inc"
     ;
 
+// A code object and its per-device modules and functions.
+struct CodeObject {
+    std::vector<char> code;
+    hipModule_t module[16] = {};
+    std::map<std::string, hipFunction_t> functions[16];
+};
+
 struct Program {
     std::string ir;
-    std::string source;
+    std::string functor;  // the TrsFused struct
+    std::string source;   // functor + the standard kernel wrappers
     int nin = 0;
     int nout = 1;
     unsigned u8mask = 0;
     double compile_ms = 0.0;
     bool from_disk = false;
-    std::vector<char> code;
-    hipModule_t module[16] = {};
-    std::map<std::string, hipFunction_t> functions[16];
+    CodeObject base;
+    // pw_xpose kernels specialised on operand roles, built on first launch
+    // of each role signature (kernel name -> code object).
+    std::mutex spec_mu;
+    std::map<std::string, std::unique_ptr<CodeObject>> specs;
 };
 
 std::mutex g_mu;
@@ -176,23 +186,20 @@ int generate(const std::string &ir, Program *prog) {
         for (int o = 0; o < nout; o++) s << "    r[" << o << "] = v" << results[o] << ";\n";
     }
     s << "  }\n};\n";
+    prog->functor = s.str();
     const std::string mask = std::to_string(u8mask) + "u";
     auto wrap = [&](const char *name, const std::string &body, const char *lanes = "256") {
         s << "extern \"C\" __global__ void __launch_bounds__(" << lanes << ") " << name
           << "(trs::PwGeom g, trs::PwPtrs p) { " << body << "(TrsFused{}, g, p); }\n";
     };
+    // Compiled with the program: the variants that need no launch-time
+    // specialisation.  Vector flat/rows kernels (specialised on the inputs
+    // read once) and pw_xpose kernels (also on operand roles) are compiled on
+    // their first launch: get_spec_function.
     wrap("trs_fused_flat_c", "trs::pw_flat_contig_body<TrsFused, " + mask + ">", "trs::kFlatBlock");
-    wrap("trs_fused_flat_v", "trs::pw_flat_body<TrsFused, " + mask + ", true>", "trs::kFlatBlock");
     wrap("trs_fused_flat_s", "trs::pw_flat_body<TrsFused, " + mask + ", false>", "trs::kFlatBlock");
-    wrap("trs_fused_rows_v", "trs::pw_rows_body<TrsFused, " + mask + ", true>");
     wrap("trs_fused_rows_s", "trs::pw_rows_body<TrsFused, " + mask + ", false>");
     wrap("trs_fused_generic", "trs::pw_generic_body<TrsFused, " + mask + ">");
-    for (int nt = 1; nt <= nin && nt <= 4; nt++) {
-        const std::string v = "trs_fused_tiled_v" + std::to_string(nt);
-        const std::string sc = "trs_fused_tiled_s" + std::to_string(nt);
-        wrap(v.c_str(), "trs::pw_tiled_body<TrsFused, " + mask + ", true, " + std::to_string(nt) + ">");
-        wrap(sc.c_str(), "trs::pw_tiled_body<TrsFused, " + mask + ", false, " + std::to_string(nt) + ">");
-    }
     prog->nin = nin;
     prog->nout = nout;
     prog->u8mask = u8mask;
@@ -293,17 +300,19 @@ void cache_store(const std::string &dir, const std::string &path, const std::str
     if (std::rename(tmp.c_str(), path.c_str()) != 0) std::remove(tmp.c_str());
 }
 
-int compile(Program *prog) {
-    std::string full = std::string(kPwCoreSource) + "\n" + prog->source;
+// Compiles pw_core.h + `tail` into `co->code` (or loads it from the disk
+// cache); `ms` receives the time taken and `from_disk` whether it was a hit.
+int compile_source(const std::string &tail, CodeObject *co, double *ms, bool *from_disk) {
+    std::string full = std::string(kPwCoreSource) + "\n" + tail;
     const auto t0 = std::chrono::steady_clock::now();
     const std::string dir = cache_dir();
     std::string key, path;
     if (!dir.empty()) {
         key = cache_key(full);
         path = cache_path(dir, key);
-        if (cache_load(path, key, &prog->code)) {
-            prog->from_disk = true;
-            prog->compile_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        if (cache_load(path, key, &co->code)) {
+            if (from_disk) *from_disk = true;
+            if (ms) *ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
             return TRS_OK;
         }
     }
@@ -311,7 +320,7 @@ int compile(Program *prog) {
     hiprtcResult r = hiprtcCreateProgram(&rp, full.c_str(), "trs_fused.hip", 0, nullptr, nullptr);
     if (r != HIPRTC_SUCCESS) return set_error(TRS_E_FUSION, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
     r = hiprtcCompileProgram(rp, (int)(sizeof kRtcOpts / sizeof kRtcOpts[0]), kRtcOpts);
-    prog->compile_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    if (ms) *ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     if (r != HIPRTC_SUCCESS) {
         size_t n = 0;
         hiprtcGetProgramLogSize(rp, &n);
@@ -322,12 +331,15 @@ int compile(Program *prog) {
     }
     size_t n = 0;
     hiprtcGetCodeSize(rp, &n);
-    prog->code.resize(n);
-    hiprtcGetCode(rp, prog->code.data());
+    co->code.resize(n);
+    hiprtcGetCode(rp, co->code.data());
     hiprtcDestroyProgram(&rp);
-    if (!dir.empty()) cache_store(dir, path, key, prog->code);
+    if (from_disk) *from_disk = false;
+    if (!dir.empty()) cache_store(dir, path, key, co->code);
     return TRS_OK;
 }
+
+int compile(Program *prog) { return compile_source(prog->source, &prog->base, &prog->compile_ms, &prog->from_disk); }
 
 Program *lookup(uint64_t id) {
     std::lock_guard<std::mutex> lock(g_mu);
@@ -335,18 +347,75 @@ Program *lookup(uint64_t id) {
     return g_programs[id - 1].get();
 }
 
-int get_function(Program *prog, DeviceState *dev, const std::string &name, hipFunction_t *fn) {
+int get_function(CodeObject *co, DeviceState *dev, const std::string &name, hipFunction_t *fn) {
     std::lock_guard<std::mutex> lock(g_mu);
     const int d = dev->index;
-    if (!prog->module[d]) TRS_HIP_CHECK(hipModuleLoadData(&prog->module[d], prog->code.data()), "hipModuleLoadData");
-    auto it = prog->functions[d].find(name);
-    if (it != prog->functions[d].end()) {
+    if (!co->module[d]) TRS_HIP_CHECK(hipModuleLoadData(&co->module[d], co->code.data()), "hipModuleLoadData");
+    auto it = co->functions[d].find(name);
+    if (it != co->functions[d].end()) {
         *fn = it->second;
         return TRS_OK;
     }
-    TRS_HIP_CHECK(hipModuleGetFunction(fn, prog->module[d], name.c_str()), "hipModuleGetFunction");
-    prog->functions[d][name] = *fn;
+    TRS_HIP_CHECK(hipModuleGetFunction(fn, co->module[d], name.c_str()), "hipModuleGetFunction");
+    co->functions[d][name] = *fn;
     return TRS_OK;
+}
+
+// A kernel specialised for a launch (streamed-input mask, pw_xpose operand
+// roles), compiled on the first launch that needs it and kept, like the
+// program, in the process and in the disk cache.  `name` identifies the
+// specialisation; `body` is the kernel body call.
+int get_spec_function(Program *prog, DeviceState *dev, const std::string &name, const std::string &body,
+                      int lanes, hipFunction_t *fn) {
+    CodeObject *co = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(prog->spec_mu);
+        auto it = prog->specs.find(name);
+        if (it == prog->specs.end()) {
+            std::ostringstream w;
+            w << prog->functor << "extern \"C\" __global__ void __launch_bounds__(" << lanes << ") " << name
+              << "(trs::PwGeom g, trs::PwPtrs p) { " << body << "(TrsFused{}, g, p); }\n";
+            auto spec = std::make_unique<CodeObject>();
+            const int rc = compile_source(w.str(), spec.get(), nullptr, nullptr);
+            if (rc) return rc;
+            it = prog->specs.emplace(name, std::move(spec)).first;
+        }
+        co = it->second.get();
+    }
+    return get_function(co, dev, name, fn);
+}
+
+int get_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunction_t *fn) {
+    const unsigned strm = pl.g.streamed & ((1u << prog->nin) - 1u);
+    const std::string mask = std::to_string(prog->u8mask) + "u";
+    char name[128];
+    switch (pl.variant) {
+    case PwVariant::Flat:
+        if (pl.contig) return get_function(&prog->base, dev, "trs_fused_flat_c", fn);
+        if (!pl.vec) return get_function(&prog->base, dev, "trs_fused_flat_s", fn);
+        std::snprintf(name, sizeof name, "trs_fused_flat_v_%u", strm);
+        return get_spec_function(prog, dev, name,
+                                 "trs::pw_flat_body<TrsFused, " + mask + ", true, " + std::to_string(strm) + "u>",
+                                 kFlatBlock, fn);
+    case PwVariant::Rows:
+        if (!pl.vec) return get_function(&prog->base, dev, "trs_fused_rows_s", fn);
+        std::snprintf(name, sizeof name, "trs_fused_rows_v_%u", strm);
+        return get_spec_function(prog, dev, name,
+                                 "trs::pw_rows_body<TrsFused, " + mask + ", true, " + std::to_string(strm) + "u>", 256,
+                                 fn);
+    case PwVariant::Xpose: {
+        std::snprintf(name, sizeof name, "trs_fused_xpose_%c_%u_%u_%u_%u_%d_%u", pl.vec ? 'v' : 's', pl.trans, pl.held,
+                      pl.once, pl.xbc, pl.walk, strm);
+        std::ostringstream b;
+        b << "trs::pw_xpose_body<TrsFused, " << mask << ", " << (pl.vec ? "true" : "false") << ", " << kXposeWT << ", "
+          << kXposeWX << ", " << pl.trans << "u, " << pl.held << "u, " << pl.once << "u, " << pl.walk << ", "
+          << (pl.vec ? strm : 0u) << "u, " << pl.xbc << "u>";
+        return get_spec_function(prog, dev, name, b.str(), 64 * kXposeWT * kXposeWX, fn);
+    }
+    case PwVariant::Generic: return get_function(&prog->base, dev, "trs_fused_generic", fn);
+    case PwVariant::Empty: break;
+    }
+    return set_error(TRS_E_INVALID_ARGUMENT, "no kernel for an empty launch");
 }
 
 }  // namespace
@@ -413,22 +482,12 @@ int trs_fusion_launch_multi(uint64_t kernel_id, int n_inputs, const void *const 
             eb[i] = ((prog->u8mask >> i) & 1u) ? 1 : 4;
         }
         PwPlan pl;
-        int rc = plan_pointwise(lo, outputs[0], n_inputs, inputs, ls, eb, dev->cu_count, &pl, n_outputs, outputs + 1);
+        int rc = plan_pointwise(lo, outputs[0], n_inputs, inputs, ls, eb, dev->cu_count, &pl, n_outputs, outputs + 1,
+                                /*roles=*/true);
         if (rc) return rc;
-        std::string name;
-        switch (pl.variant) {
-        case PwVariant::Empty: return TRS_OK;
-        case PwVariant::Flat:
-            name = pl.contig ? "trs_fused_flat_c" : pl.vec ? "trs_fused_flat_v" : "trs_fused_flat_s";
-            break;
-        case PwVariant::Rows: name = pl.vec ? "trs_fused_rows_v" : "trs_fused_rows_s"; break;
-        case PwVariant::Tiled:
-            name = std::string(pl.vec ? "trs_fused_tiled_v" : "trs_fused_tiled_s") + std::to_string(pl.ntransposed);
-            break;
-        case PwVariant::Generic: name = "trs_fused_generic"; break;
-        }
+        if (pl.variant == PwVariant::Empty) return TRS_OK;
         hipFunction_t fn;
-        rc = get_function(prog, dev, name, &fn);
+        rc = get_plan_function(prog, dev, pl, &fn);
         if (rc) return rc;
         void *args[] = {(void *)&pl.g, (void *)&pl.p};
         TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, (unsigned)pl.block, 1, 1, 0, dev->stream, args,

@@ -83,45 +83,71 @@ struct ReluBackwardF {
 };
 
 // ---- AOT wrappers -----------------------------------------------------------
+// S: inputs read once (loaded non-temporally), a compile-time mask.
 
-template <class F, unsigned M, bool V>
-__global__ void __launch_bounds__(kFlatBlock) k_flat(F f, PwGeom g, PwPtrs p) { pw_flat_body<F, M, V>(f, g, p); }
+template <class F, unsigned M, bool V, unsigned S>
+__global__ void __launch_bounds__(kFlatBlock) k_flat(F f, PwGeom g, PwPtrs p) { pw_flat_body<F, M, V, S>(f, g, p); }
 template <class F, unsigned M>
 __global__ void __launch_bounds__(kFlatBlock) k_flat_contig(F f, PwGeom g, PwPtrs p) {
     pw_flat_contig_body<F, M>(f, g, p);
 }
-template <class F, unsigned M, bool V>
-__global__ void __launch_bounds__(256) k_rows(F f, PwGeom g, PwPtrs p) { pw_rows_body<F, M, V>(f, g, p); }
-template <class F, unsigned M, bool V, int NT>
-__global__ void __launch_bounds__(256) k_tiled(F f, PwGeom g, PwPtrs p) { pw_tiled_body<F, M, V, NT>(f, g, p); }
+template <class F, unsigned M, bool V, unsigned S>
+__global__ void __launch_bounds__(256) k_rows(F f, PwGeom g, PwPtrs p) { pw_rows_body<F, M, V, S>(f, g, p); }
+template <class F, unsigned M, bool V, unsigned TR, unsigned S>
+__global__ void __launch_bounds__(64 * kXposeWT * kXposeWX) k_xpose(F f, PwGeom g, PwPtrs p) {
+    pw_xpose_body<F, M, V, kXposeWT, kXposeWX, TR, 0u, 0u, 1, S>(f, g, p);
+}
 template <class F, unsigned M>
 __global__ void __launch_bounds__(256) k_generic(F f, PwGeom g, PwPtrs p) { pw_generic_body<F, M>(f, g, p); }
 
+// Calls fn.template operator()<K>() with K the compile-time value of the
+// run-time mask `m` over NIN bits (NIN is 1 or 2 here).
+template <int NIN, class Fn>
+void with_mask(unsigned m, Fn &&fn) {
+    static_assert(NIN >= 1 && NIN <= 2, "AOT functors take one or two inputs");
+    if constexpr (NIN == 1) {
+        if (m & 1u) fn.template operator()<1u>();
+        else fn.template operator()<0u>();
+    } else {
+        switch (m & 3u) {
+        case 0u: fn.template operator()<0u>(); break;
+        case 1u: fn.template operator()<1u>(); break;
+        case 2u: fn.template operator()<2u>(); break;
+        default: fn.template operator()<3u>(); break;
+        }
+    }
+}
+
 template <class F, unsigned M>
 int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
+    constexpr int NIN = F::NIN;
     const dim3 grid((unsigned)pl.grid), block((unsigned)pl.block);
+    const unsigned sm = pl.g.streamed & ((1u << NIN) - 1u);
     switch (pl.variant) {
     case PwVariant::Empty:
         return TRS_OK;
     case PwVariant::Flat:
         if (pl.contig) hipLaunchKernelGGL((k_flat_contig<F, M>), grid, block, 0, s, f, pl.g, pl.p);
-        else if (pl.vec) hipLaunchKernelGGL((k_flat<F, M, true>), grid, block, 0, s, f, pl.g, pl.p);
-        else hipLaunchKernelGGL((k_flat<F, M, false>), grid, block, 0, s, f, pl.g, pl.p);
+        else if (pl.vec)
+            with_mask<NIN>(sm, [&]<unsigned S>() { hipLaunchKernelGGL((k_flat<F, M, true, S>), grid, block, 0, s, f, pl.g, pl.p); });
+        else hipLaunchKernelGGL((k_flat<F, M, false, 0u>), grid, block, 0, s, f, pl.g, pl.p);
         break;
     case PwVariant::Rows:
-        if (pl.vec) hipLaunchKernelGGL((k_rows<F, M, true>), grid, block, 0, s, f, pl.g, pl.p);
-        else hipLaunchKernelGGL((k_rows<F, M, false>), grid, block, 0, s, f, pl.g, pl.p);
+        if (pl.vec)
+            with_mask<NIN>(sm, [&]<unsigned S>() { hipLaunchKernelGGL((k_rows<F, M, true, S>), grid, block, 0, s, f, pl.g, pl.p); });
+        else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, f, pl.g, pl.p);
         break;
-    case PwVariant::Tiled:
-        if constexpr (F::NIN >= 2) {
-            if (pl.ntransposed == 2) {
-                if (pl.vec) hipLaunchKernelGGL((k_tiled<F, M, true, 2>), grid, block, 0, s, f, pl.g, pl.p);
-                else hipLaunchKernelGGL((k_tiled<F, M, false, 2>), grid, block, 0, s, f, pl.g, pl.p);
-                break;
+    case PwVariant::Xpose:
+        // One outer tuple per block (no roles): every transposed-operand mask.
+        with_mask<NIN>(pl.trans, [&]<unsigned TR>() {
+            if constexpr (TR != 0u) {
+                if (pl.vec)
+                    with_mask<NIN>(sm, [&]<unsigned S>() {
+                        hipLaunchKernelGGL((k_xpose<F, M, true, TR, S>), grid, block, 0, s, f, pl.g, pl.p);
+                    });
+                else hipLaunchKernelGGL((k_xpose<F, M, false, TR, 0u>), grid, block, 0, s, f, pl.g, pl.p);
             }
-        }
-        if (pl.vec) hipLaunchKernelGGL((k_tiled<F, M, true, 1>), grid, block, 0, s, f, pl.g, pl.p);
-        else hipLaunchKernelGGL((k_tiled<F, M, false, 1>), grid, block, 0, s, f, pl.g, pl.p);
+        });
         break;
     case PwVariant::Generic:
         hipLaunchKernelGGL((k_generic<F, M>), grid, block, 0, s, f, pl.g, pl.p);

@@ -15,9 +15,11 @@
 //               one (outer row, 1024-column chunk) tile per block;
 //               the outer-row decode is wave-uniform (scalar registers), the
 //               lanes stream 16-byte vectors along the row.
-//   pw_tiled -- an operand is unit-stride along another dim (a transposed or
-//               permuted view such as c.mT): 64x64 tiles staged through LDS
-//               so both its reads and the output writes are coalesced.
+//   pw_xpose -- an operand is unit-stride along another dim (a transposed or
+//               permuted view such as c.mT): each lane transposes a 4x4
+//               block in registers, so reads and writes are both 16-byte
+//               vectors; blocks walk the remaining dims, keeping operands
+//               that do not move along them in registers.
 //   pw_generic -- any strides: per-element decode with magic-number division.
 //
 // Every op is written so that hipcc and hipRTC (both run with
@@ -43,7 +45,6 @@ constexpr int kMaxRank = 8;
 constexpr int kMaxIn = 8;
 constexpr int kMaxOut = 8;  // outputs of one program (all share one layout)
 constexpr int kRowChunk = 1024;  // columns per pw_rows tile (256 lanes x 4)
-constexpr int kTile = 64;        // pw_tiled tile edge
 // Largest grid a launch uses (256-lane blocks).  Launches are one-shot --
 // one tile per block -- up to this many blocks; beyond it the bodies loop.
 constexpr int64_t kMaxGrid = 1 << 20;
@@ -69,7 +70,7 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &d) {
 
 struct PwGeom {
     int32_t rank;   // >= 1 after normalisation
-    int32_t tdim;   // pw_tiled: dim along which transposed operands are unit-stride
+    int32_t tdim;   // pw_xpose: dim along which transposed operands are unit-stride
     int32_t wide;   // a dim exceeds 32 bits: always decode with 64-bit division
     int32_t pad0;
     int64_t numel;
@@ -79,11 +80,12 @@ struct PwGeom {
     int64_t istride[kMaxIn][kMaxRank];
     int64_t ooff;
     int64_t ioff[kMaxIn];
-    uint32_t transposed;  // pw_tiled: bit i set when input i goes through LDS
+    uint32_t transposed;  // pw_xpose: bit i set when input i is unit-stride along tdim
     uint32_t streamed;    // bit i set when input i is read once (no broadcast dim)
-    int64_t rows;         // pw_rows / pw_tiled: number of outer index tuples
-    int64_t chunks;       // pw_rows: column chunks per row; pw_tiled: tiles per outer tuple
-    int64_t ttiles;       // pw_tiled: tiles along tdim
+    int64_t rows;         // pw_rows / pw_xpose: number of outer index tuples
+    int64_t chunks;       // pw_rows: column chunks per row; pw_xpose: tiles per outer tuple
+    int64_t ttiles;       // pw_xpose: tiles along tdim
+    int64_t groups;       // pw_xpose: block groups G; a block walks outer tuples c, c+G, c+2G, ...
 };
 
 typedef float vf4 __attribute__((ext_vector_type(4)));
@@ -109,22 +111,29 @@ __device__ __forceinline__ float ld1(const PwPtrs &p, int64_t off) {
 }
 
 // Four consecutive elements (unit stride) or one broadcast element (stride 0).
-// Operands read exactly once use non-temporal loads; re-read (broadcast)
-// operands keep normal caching.
-template <unsigned U8MASK, int I>
-__device__ __forceinline__ void ld4(const PwPtrs &p, int64_t off, bool unit, float *v,
-                                    bool stream = false) {
+// STREAM: the operand is read once, so it is loaded non-temporally; re-read
+// (broadcast) operands keep normal caching.  The choice is a template
+// parameter because a function holding both kinds of load to one address is
+// optimised, before it is inlined, into a single plain load: a run-time flag
+// would silently lose the non-temporal hint.
+template <unsigned U8MASK, int I, bool STREAM = false>
+__device__ __forceinline__ void ld4(const PwPtrs &p, int64_t off, bool unit, float *v) {
     if (!unit) {
         float s = ld1<U8MASK, I>(p, off);
         v[0] = s; v[1] = s; v[2] = s; v[3] = s;
         return;
     }
     if constexpr (((U8MASK >> I) & 1u) != 0u) {
-        vu8x4 q = *(const vu8x4 *)(((const uint8_t *)p.in[I]) + off);
+        const vu8x4 *src = (const vu8x4 *)(((const uint8_t *)p.in[I]) + off);
+        vu8x4 q;
+        if constexpr (STREAM) q = __builtin_nontemporal_load(src);
+        else q = *src;
         v[0] = (float)q.x; v[1] = (float)q.y; v[2] = (float)q.z; v[3] = (float)q.w;
     } else {
         const vf4 *src = (const vf4 *)(((const float *)p.in[I]) + off);
-        vf4 q = stream ? __builtin_nontemporal_load(src) : *src;
+        vf4 q;
+        if constexpr (STREAM) q = __builtin_nontemporal_load(src);
+        else q = *src;
         v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
     }
 }
@@ -236,8 +245,9 @@ __device__ __forceinline__ void decode_outer(const PwGeom &g, int ndims, int64_t
 // rank 1; ostride 1; istride in {0, 1}.  VEC requires numel % 4 == 0 is NOT
 // assumed: the vector body covers floor(numel/4) groups and a scalar tail the
 // rest.  VEC is chosen by the host only when every unit-stride operand and
-// the output are 16-byte aligned (4-byte for u8).
-template <class F, unsigned U8MASK, bool VEC>
+// the output are 16-byte aligned (4-byte for u8).  STRM: bit i set when input
+// i is read once (g.streamed), loaded non-temporally.
+template <class F, unsigned U8MASK, bool VEC, unsigned STRM = 0u>
 __device__ __forceinline__ void pw_flat_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
     constexpr int NOUT = nout_of<F>();
@@ -258,7 +268,7 @@ __device__ __forceinline__ void pw_flat_body(const F &f, const PwGeom &g, const 
             const int64_t e = gi << 2;
             float v[NIN > 0 ? NIN : 1][4];
             static_for<NIN>([&]<int I>() {
-                ld4<U8MASK, I>(p, g.ioff[I] + (unit[I] ? e : 0), unit[I], v[I], (g.streamed >> I) & 1u);
+                ld4<U8MASK, I, ((STRM >> I) & 1u) != 0u>(p, g.ioff[I] + (unit[I] ? e : 0), unit[I], v[I]);
             });
             float r[NOUT][4];
             eval4(f, v, r);
@@ -320,7 +330,8 @@ __device__ __forceinline__ void pw_flat_contig_body(const F &f, const PwGeom &g,
 // Innermost dim (size[rank-1] columns) has ostride 1 and istride in {0, 1}.
 // g.rows = product of the outer dims, g.chunks = ceil(cols / kRowChunk).
 // VEC: cols % 4 == 0 and every unit-stride row start 16-byte aligned.
-template <class F, unsigned U8MASK, bool VEC>
+// STRM: as for pw_flat.
+template <class F, unsigned U8MASK, bool VEC, unsigned STRM = 0u>
 __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
     constexpr int NOUT = nout_of<F>();
@@ -341,7 +352,7 @@ __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const 
             if (c < cols) {
                 float v[NIN > 0 ? NIN : 1][4];
                 static_for<NIN>([&]<int I>() {
-                    ld4<U8MASK, I>(p, io[I] + (unit[I] ? c : 0), unit[I], v[I], (g.streamed >> I) & 1u);
+                    ld4<U8MASK, I, ((STRM >> I) & 1u) != 0u>(p, io[I] + (unit[I] ? c : 0), unit[I], v[I]);
                 });
                 float r[NOUT][4];
                 eval4(f, v, r);
@@ -364,117 +375,210 @@ __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const 
     }
 }
 
-// ---- pw_tiled -------------------------------------------------------------
-// Output unit-stride along the innermost dim `x` (size[rank-1]); operands in
-// g.transposed are unit-stride along dim `t` = g.tdim (< rank-1) instead and
-// are staged through a 64x65 LDS tile per operand (padding keeps both the
-// column writes and the row reads free of bank conflicts).  Other operands
-// have stride 0 or 1 along x.  Block = 256 lanes; one 64(t) x 64(x) tile per
-// block iteration.  g.rows = product of the remaining dims, g.ttiles = tiles
-// along t, g.chunks = ttiles * tiles along x.
-template <class F, unsigned U8MASK, bool VEC, int NT>
-__device__ __forceinline__ void pw_tiled_body(const F &f, const PwGeom &g, const PwPtrs &p) {
+// ---- pw_xpose -------------------------------------------------------------
+// Output unit-stride along x = dim rank-1; operands in TRANS are unit-stride
+// along t = g.tdim, every other operand has stride 0 or 1 along x (the
+// planner's Xpose layouts).  A lane owns a 4(t) x 4(x) block: it reads a
+// TRANS operand as four 16-byte vectors along t (one per x) and any other
+// operand, and writes the output, as four vectors along x (one per t), so the
+// transpose happens in registers with no LDS and no barrier.  A wave is 8 x 8
+// lanes covering 32 t x 32 x, so each of its vector accesses is 8 runs of
+// 128 B; a block of WT x WX waves covers a (32 WT) x (32 WX) tile.  Measured
+// on (a + b) * c.mT over [64, 512, 1024], the 128 x 64 tile's transpose alone
+// runs at the speed of the same access pattern without any data exchange.
+// The other dims ("outer" tuples, g.rows of them) are walked: block
+// (c, tile) takes the NW tuples c, c + G, ..., c + (NW-1) G with
+// G = g.groups = g.rows / NW, so
+//   HELD operands (stride 0 over every outer dim) are loaded once per block,
+//   ONCE operands (stride 0 along t) once per outer tuple,
+// and each tuple's loads are issued before the previous tuple's stores.
+// NW = 1 walks nothing (one tuple per block).  g.ttiles = t tiles,
+// g.chunks = t tiles * x tiles.
+template <unsigned M, int I>
+constexpr int mask_rank() {  // set bits of M below bit I
+    return __builtin_popcount(M & ((1u << I) - 1u));
+}
+
+// XBC (inputs with stride 0 along x) equal to kRuntimeMask is read from the
+// geometry at run time; otherwise it is fixed at compile time.
+constexpr unsigned kRuntimeMask = 0xffffffffu;
+
+template <class F, unsigned U8MASK, bool VEC, int WT, int WX, unsigned TRANS, unsigned HELD, unsigned ONCE, int NW,
+          unsigned STRM, unsigned XBC = kRuntimeMask>
+__device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
+    constexpr int NIN1 = NIN > 0 ? NIN : 1;
     constexpr int NOUT = nout_of<F>();
-    __shared__ float lds[NT > 0 ? NT : 1][kTile][kTile + 1];
-    const int xd = g.rank - 1;
-    const int td = g.tdim;
+    constexpr int NH = __builtin_popcount(HELD);
+    constexpr int BT = 32 * WT, BX = 32 * WX;
+    const int xd = g.rank - 1, td = g.tdim;
     const int64_t xs = g.size[xd], ts = g.size[td];
-    const int64_t ntiles = g.rows * g.chunks;
-    const int lane = threadIdx.x;
-    // Map transposed input index -> LDS slot.
-    int slot[NIN > 0 ? NIN : 1];
-    {
-        int s = 0;
-        for (int i = 0; i < NIN; i++) slot[i] = ((g.transposed >> i) & 1u) ? s++ : -1;
-    }
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t outer = tile / g.chunks;
-        const int64_t rest = tile - outer * g.chunks;
-        const int64_t tt = rest % g.ttiles;
-        const int64_t xt = rest / g.ttiles;
-        // Decode the outer tuple over all dims except t and x (wave-uniform).
-        int64_t oo = g.ooff, io[NIN > 0 ? NIN : 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t ntiles = g.groups * g.chunks;
+    // Operand I moves along x with unit stride (else stride 0): compile-time
+    // unless XBC is kRuntimeMask.  STRM: inputs read once (non-temporal).
+    auto unit_x = [&]<int I>() -> bool {
+        if constexpr (XBC == kRuntimeMask) return g.istride[I][xd] != 0;
+        else return ((XBC >> I) & 1u) == 0u;
+    };
+    // Offsets of outer tuple `o`: a wave-uniform decode over the dims other
+    // than t and x (32-bit magic-number division when o fits).
+    auto decode = [&](int64_t o, int64_t &oo, int64_t *io) {
+        oo = g.ooff;
         for (int i = 0; i < NIN; i++) io[i] = g.ioff[i];
-        {
-            int64_t rem = outer;
+        if (!g.wide && o < 0x100000000LL) {
+            uint32_t rem = (uint32_t)o;
             for (int d = xd - 1; d >= 0; d--) {
                 if (d == td) continue;
-                const int64_t c = rem % g.size[d];
-                rem /= g.size[d];
+                const uint32_t q = fast_div(rem, g.fd[d]);
+                const int64_t c = (int64_t)(rem - q * g.fd[d].div);
+                rem = q;
+                oo += c * g.ostride[d];
+                for (int i = 0; i < NIN; i++) io[i] += c * g.istride[i][d];
+            }
+        } else {
+            for (int d = xd - 1; d >= 0; d--) {
+                if (d == td) continue;
+                const int64_t q = o / g.size[d];
+                const int64_t c = o - q * g.size[d];
+                o = q;
                 oo += c * g.ostride[d];
                 for (int i = 0; i < NIN; i++) io[i] += c * g.istride[i][d];
             }
         }
-        const int64_t t0 = tt * kTile, x0 = xt * kTile;
-        // Stage transposed operands: lane reads 4 consecutive t at one x.
-        if constexpr (NT > 0) {
-            const int a = lane & 15;  // t group
-            const int b0 = lane >> 4; // x row (0..15), +16j
+    };
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t c = tile / g.chunks;
+        const int64_t rest = tile - c * g.chunks;
+        const int64_t t0 = (rest % g.ttiles) * BT, x0 = (rest / g.ttiles) * BX;
+        const int64_t t = t0 + (wave % WT) * 32 + 4 * (lane & 7);
+        const int64_t x = x0 + (wave / WT) * 32 + 4 * (lane >> 3);
+        // Per-operand lane offset within an outer tuple and the step between
+        // its four vectors: along x for TRANS operands (each vector runs along
+        // t), along t for the others (each vector runs along x).
+        int64_t loff[NIN1], lstep[NIN1];
+        static_for<NIN>([&]<int I>() {
+            if constexpr ((TRANS >> I) & 1u) {
+                loff[I] = x * g.istride[I][xd] + t;
+                lstep[I] = g.istride[I][xd];
+            } else {
+                loff[I] = t * g.istride[I][td] + (unit_x.template operator()<I>() ? x : 0);
+                lstep[I] = g.istride[I][td];
+            }
+        });
+        const int64_t ooff_lane = t * g.ostride[td] + x;
+        // The block runs its whole tile with 16-byte vectors when the tile
+        // is interior and the operands aligned (a wave-uniform test), else
+        // every access is scalar and bounds-checked.
+        auto run = [&]<bool FAST, bool ONE_OUTER>() {
+            // Operand I's four vectors (raw[j][e]: vector j, element e) at
+            // tuple base b.  Element (t+k, x+i) is raw[i][k] for TRANS
+            // operands and raw[k][i] for the others.
+            auto load_block = [&]<int I>(int64_t b, float (&raw)[4][4], int nvec) {
+                const int64_t base = b + loff[I];
+                constexpr bool tr = ((TRANS >> I) & 1u) != 0;
+                const bool unit = tr || unit_x.template operator()<I>();
+                if constexpr (FAST) {
+                    constexpr bool stream = ((HELD >> I) & 1u) == 0u && ((STRM >> I) & 1u) != 0u;
+                    for (int j = 0; j < nvec; j++) ld4<U8MASK, I, stream>(p, base + j * lstep[I], unit, raw[j]);
+                } else {
+                    for (int j = 0; j < nvec; j++)
+                        for (int e = 0; e < 4; e++) {
+                            const bool in = tr ? (t + e < ts && x + j < xs) : (t + j < ts && x + e < xs);
+                            raw[j][e] = in ? ld1<U8MASK, I>(p, base + j * lstep[I] + (unit ? e : 0)) : 0.0f;
+                        }
+                }
+            };
+            float held[NH > 0 ? NH : 1][4][4];
             static_for<NIN>([&]<int I>() {
-                if (slot[I] >= 0) {
-                    for (int j = 0; j < 4; j++) {
-                        const int xb = b0 + 16 * j;
-                        const int64_t x = x0 + xb;
-                        const int64_t t = t0 + 4 * a;
-                        const int64_t base = io[I] + x * g.istride[I][xd] + t;
-                        if (VEC && x < xs && t + 3 < ts) {
-                            float v[4];
-                            ld4<U8MASK, I>(p, base, true, v, (g.streamed >> I) & 1u);
-                            for (int k = 0; k < 4; k++) lds[slot[I]][4 * a + k][xb] = v[k];
-                        } else {
-                            for (int k = 0; k < 4; k++) {
-                                lds[slot[I]][4 * a + k][xb] =
-                                    (x < xs && t + k < ts) ? ld1<U8MASK, I>(p, base + k) : 0.0f;
+                if constexpr ((HELD >> I) & 1u) load_block.template operator()<I>(g.ioff[I], held[mask_rank<HELD, I>()], 4);
+            });
+            // One outer tuple's loads (all operands but HELD) into `dst`.
+            auto loads = [&](const int64_t *io, float (&dst)[NIN1][4][4]) {
+                static_for<NIN>([&]<int I>() {
+                    if constexpr (!((HELD >> I) & 1u))
+                        load_block.template operator()<I>(io[I], dst[I], ((ONCE >> I) & 1u) ? 1 : 4);
+                });
+            };
+            // Compute and store one outer tuple from its loaded values.
+            auto compute = [&](const float (&v)[NIN1][4][4], int64_t oo) {
+                const int64_t ob0 = oo + ooff_lane;
+                for (int k = 0; k < 4; k++) {
+                    float a[NIN1][4];
+                    static_for<NIN>([&]<int I>() {
+                        for (int i = 0; i < 4; i++) {
+                            if constexpr ((HELD >> I) & 1u) {
+                                constexpr int h = mask_rank<HELD, I>();
+                                a[I][i] = ((TRANS >> I) & 1u) ? held[h][i][k] : held[h][k][i];
+                            } else if constexpr ((ONCE >> I) & 1u) {
+                                a[I][i] = v[I][0][i];
+                            } else if constexpr ((TRANS >> I) & 1u) {
+                                a[I][i] = v[I][i][k];
+                            } else {
+                                a[I][i] = v[I][k][i];
+                            }
+                        }
+                    });
+                    float r[NOUT][4];
+                    eval4(f, a, r);
+                    const int64_t ob = ob0 + k * g.ostride[td];
+                    if constexpr (FAST) {
+                        store4(p, ob, r);
+                    } else if (t + k < ts) {
+                        for (int i = 0; i < 4; i++) {
+                            if (x + i < xs) {
+                                float ov[NOUT];
+                                for (int q = 0; q < NOUT; q++) ov[q] = r[q][i];
+                                store1<NOUT>(p, ob + i, ov);
                             }
                         }
                     }
                 }
-            });
-            __syncthreads();
-        }
-        // Compute: lane handles 4 consecutive x at t rows (lane>>4) + 16j.
-        {
-            const int c = lane & 15;
-            const int r0 = lane >> 4;
-            for (int j = 0; j < 4; j++) {
-                const int tb = r0 + 16 * j;
-                const int64_t t = t0 + tb;
-                const int64_t x = x0 + 4 * c;
-                if (t >= ts) continue;
-                const int64_t ob = oo + t * g.ostride[td] + x;
-                float v[NIN > 0 ? NIN : 1][4];
-                const bool full = VEC && x + 3 < xs;
-                static_for<NIN>([&]<int I>() {
-                    if (slot[I] >= 0) {
-                        for (int k = 0; k < 4; k++) v[I][k] = lds[slot[I]][tb][4 * c + k];
-                    } else {
-                        const bool unit = g.istride[I][xd] != 0;
-                        const int64_t base = io[I] + t * g.istride[I][td] + (unit ? x : 0);
-                        if (full) {
-                            ld4<U8MASK, I>(p, base, unit, v[I], (g.streamed >> I) & 1u);
-                        } else {
-                            for (int k = 0; k < 4; k++)
-                                v[I][k] = (x + k < xs) ? ld1<U8MASK, I>(p, base + (unit ? k : 0)) : 0.0f;
-                        }
-                    }
-                });
-                float r[NOUT][4];
-                eval4(f, v, r);
-                if (full) {
-                    store4(p, ob, r);
-                } else {
-                    for (int k = 0; k < 4; k++) {
-                        if (x + k < xs) {
-                            float o[NOUT];
-                            for (int q = 0; q < NOUT; q++) o[q] = r[q][k];
-                            store1<NOUT>(p, ob + k, o);
-                        }
-                    }
-                }
+            };
+            // Tuple offsets: with one outer dim (rank 3) tuple o + groups is
+            // tuple o advanced by constant per-operand steps; otherwise each
+            // tuple is decoded.
+            int64_t dstep[NIN1], ostep = 0;
+            if constexpr (ONE_OUTER) {
+                const int wd = (td == 0) ? 1 : 0;
+                for (int i = 0; i < NIN; i++) dstep[i] = g.groups * g.istride[i][wd];
+                ostep = g.groups * g.ostride[wd];
             }
+            int64_t io[NIN1], oo = 0;
+            // Exactly NW tuples per block (the host sets g.rows = g.groups *
+            // NW).  The walk is unrolled at compile time: tuple s+1's loads
+            // are issued before tuple s computes and stores, with no branch
+            // between them, so each compute waits only for its own loads.
+            float nv[NIN1][4][4];
+            decode(c, oo, io);
+            loads(io, nv);
+#pragma unroll
+            for (int s = 0; s < NW; s++) {
+                float v[NIN1][4][4];
+                for (int i = 0; i < NIN; i++)
+                    for (int j = 0; j < 4; j++)
+                        for (int e = 0; e < 4; e++) v[i][j][e] = nv[i][j][e];
+                const int64_t ocur = oo;
+                if (s + 1 < NW) {
+                    if constexpr (ONE_OUTER) {
+                        oo += ostep;
+                        for (int i = 0; i < NIN; i++) io[i] += dstep[i];
+                    } else {
+                        decode(c + (int64_t)(s + 1) * g.groups, oo, io);
+                    }
+                    loads(io, nv);
+                }
+                compute(v, ocur);
+            }
+        };
+        const bool fast = VEC && t0 + BT <= ts && x0 + BX <= xs;
+        if (g.rank == 3) {
+            if (fast) run.template operator()<true, true>();
+            else run.template operator()<false, true>();
+        } else {
+            if (fast) run.template operator()<true, false>();
+            else run.template operator()<false, false>();
         }
-        if constexpr (NT > 0) __syncthreads();
     }
 }
 

@@ -7,7 +7,7 @@
 //   2. drop size-1 dims, order dims by decreasing output stride so the kernel
 //      walks the output in physical order, and merge adjacent dims that are
 //      contiguous for every operand;
-//   3. choose flat / rows / tiled / generic and whether 16-byte vector
+//   3. choose flat / rows / xpose / generic and whether 16-byte vector
 //      accesses are legal (alignment of every unit-stride operand).
 #pragma once
 
@@ -19,13 +19,27 @@
 
 namespace trs {
 
-enum class PwVariant { Empty, Flat, Rows, Tiled, Generic };
+enum class PwVariant { Empty, Flat, Rows, Xpose, Generic };
+
+// pw_xpose tile: 4 x 2 waves = 128 (t) x 64 (x).  On (a + b) * c.mT over
+// [64, 512, 1024] this shape's access pattern measured fastest of 64-256 x
+// 32-256 (its reads of c are 512 B runs); walking 8 outer tuples per block
+// with the invariant operand held in registers measured faster than one
+// tuple per block, which reloads it from L2 for every tuple.
+constexpr int kXposeWT = 4, kXposeWX = 2;
+constexpr int kXposeBT = 32 * kXposeWT, kXposeBX = 32 * kXposeWX;
+constexpr int kXposeWalk = 8;  // largest walk: 8, 4 or 2 tuples, dividing the tuple count
 
 struct PwPlan {
     PwVariant variant = PwVariant::Empty;
     bool vec = false;
     bool contig = false;  // Flat + vec with every input unit-stride and read once
     int ntransposed = 0;
+    // Xpose: operand role masks (transposed, held over the outer tuples,
+    // loaded once per tuple, stride 0 along x) and the tuples each block
+    // walks (g.rows = g.groups * walk).
+    uint32_t trans = 0, held = 0, once = 0, xbc = 0;
+    int walk = 1;
     int nin = 0;
     int block = 256;  // lanes per block (kFlatBlock for the flat variants)
     int64_t grid = 0;
@@ -47,10 +61,12 @@ inline FastDiv make_fast_div(uint32_t d) {
 
 // `elem_bytes[i]` is 4 for f32 inputs and 1 for u8 inputs.  A program with
 // several outputs passes outputs 1.. in `more` (nout - 1 of them); they share
-// the output layout `lo`.
+// the output layout `lo`.  `roles`: the launcher can run pw_xpose specialised
+// on held / once-per-tuple operands (the fusion compiler); otherwise an
+// Xpose plan takes one outer tuple per block and no roles.
 inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void *const *bases,
                           const trs_layout *const *lins, const int *elem_bytes, int cu_count,
-                          PwPlan *plan, int nout = 1, float *const *more = nullptr) {
+                          PwPlan *plan, int nout = 1, float *const *more = nullptr, bool roles = false) {
     int rc = check_layout(lo, "output");
     if (rc) return rc;
     if (nin > kMaxIn) return set_error(TRS_E_INVALID_ARGUMENT, "too many pointwise inputs (%d)", nin);
@@ -249,9 +265,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             tmask |= 1u << i;
         }
         int nt = __builtin_popcount(tmask);
-        if (ok && tdim >= 0 && nt <= 4) {
-            plan->variant = PwVariant::Tiled;
-            plan->ntransposed = nt;
+        if (ok && tdim >= 0) {
             g.tdim = tdim;
             g.transposed = tmask;
             bool vec = outputs_aligned();
@@ -263,11 +277,37 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
                 }
             }
             plan->vec = vec;
-            g.ttiles = (size[tdim] + kTile - 1) / kTile;
-            const int64_t xtiles = (size[inner] + kTile - 1) / kTile;
-            g.chunks = g.ttiles * xtiles;
+            plan->ntransposed = nt;
             g.rows = numel / (size[tdim] * size[inner]);
-            plan->grid = std::min<int64_t>(g.rows * g.chunks, want);
+            plan->variant = PwVariant::Xpose;
+            plan->trans = tmask;
+            plan->block = 64 * kXposeWT * kXposeWX;
+            if (roles) {
+                for (int i = 0; i < nin; i++) {
+                    if ((tmask >> i) & 1u) continue;
+                    if (is[i][inner] == 0) plan->xbc |= 1u << i;
+                    bool outer_zero = true;
+                    for (int d = 0; d < inner; d++)
+                        if (d != tdim && is[i][d] != 0) outer_zero = false;
+                    if (outer_zero) plan->held |= 1u << i;
+                    else if (is[i][tdim] == 0) plan->once |= 1u << i;
+                }
+            }
+            // When an operand is held, each block walks the largest of 8, 4
+            // or 2 tuples that divides the tuple count (the held operand is
+            // then loaded once for all of them); else one tuple per block.
+            plan->walk = 1;
+            if (plan->held)
+                for (int w = kXposeWalk; w >= 2; w /= 2)
+                    if (g.rows % w == 0) {
+                        plan->walk = w;
+                        break;
+                    }
+            g.groups = g.rows / plan->walk;
+            g.ttiles = (size[tdim] + kXposeBT - 1) / kXposeBT;
+            const int64_t xtiles = (size[inner] + kXposeBX - 1) / kXposeBX;
+            g.chunks = g.ttiles * xtiles;
+            plan->grid = std::min<int64_t>(g.groups * g.chunks, want);
             return TRS_OK;
         }
     }

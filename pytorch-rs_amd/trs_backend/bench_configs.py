@@ -3,9 +3,13 @@
 Each returns device-time figures measured with HIP events on the library
 stream: the average over a region of back-to-back launches (the rate used
 for GB/s and TFLOPS) and the median, min and max of single launches (the
-dispersion).  Working sets that fit the 256 MB Infinity Cache are rotated
-over several buffer sets so the GB/s figures reflect HBM.  Every output is
-read back and summed in float64 as a checksum of the materialised result.
+dispersion).  Inputs of a size the 256 MB Infinity Cache could hold are
+rotated over enough buffer sets that the streamed inputs alone total at
+least 512 MiB, so the GB/s figures reflect HBM: outputs written with
+non-temporal stores do not displace cached inputs, and with three 64 MiB
+sets a plain copy measured 0.98 of the HBM peak out of that cache.  Launch
+arguments are built once per set.  Every output is read back and summed in
+float64 as a checksum of the materialised result.
 """
 from __future__ import annotations
 
@@ -39,14 +43,20 @@ def _fusion(ir: str) -> int:
     return kid.value
 
 
-def _fuse_launch(kid, devs, lays, out, lo):
-    n = len(devs)
-    ptrs = (ctypes.c_void_p * n)(*[d.addr for d in devs])
-    la = (abi.Layout * n)(*lays)
-    check(abi.lib.trs_fusion_launch(kid, n, ptrs, la, out.ptr, ctypes.byref(lo)))
+class _FusedCall:
+    """A fused launch with its ctypes arguments built once."""
+
+    def __init__(self, kid, devs, lays, out, lo):
+        n = len(devs)
+        self.args = (kid, n, (ctypes.c_void_p * n)(*[d.addr for d in devs]), (abi.Layout * n)(*lays), out.ptr,
+                     ctypes.byref(lo))
+        self.keep = (devs, lays, out, lo)
+
+    def __call__(self):
+        check(abi.lib.trs_fusion_launch(*self.args))
 
 
-def relu_bias(log, reps: int = 20, sets: int = 3) -> dict:
+def relu_bias(log, reps: int = 20, sets: int = 8) -> dict:
     """Config 0: relu(x + b), x [4096,4096], b [4096] row-broadcast, seed 0."""
     R = C = 4096
     x = generate("relu_bias", "x")
@@ -70,11 +80,12 @@ def relu_bias(log, reps: int = 20, sets: int = 3) -> dict:
     # broadcast row b is declared first (loaded before the streamed x), and
     # the add still computes x + b.
     kid = _fusion("in f32\nin f32\nadd %1 %0\nrelu %2\nout %3\n")
+    calls = [_FusedCall(kid, [db, xs[k]], [lb, lx], outs[k], lx) for k in range(sets)]
 
     def fused():
         k = i[0] % sets
         i[0] += 1
-        _fuse_launch(kid, [db, xs[k]], [lb, lx], outs[k], lx)
+        calls[k]()
 
     e = time_region(eager, reps)
     f = time_region(fused, reps)
@@ -86,7 +97,7 @@ def relu_bias(log, reps: int = 20, sets: int = 3) -> dict:
                           "output_checksum": _checksum(outs[(i[0] - 1) % sets], R * C)}}
 
 
-def broadcast_strided(log, reps: int = 20, sets: int = 2) -> dict:
+def broadcast_strided(log, reps: int = 20, sets: int = 4) -> dict:
     """Config 2: (a + b) * c.mT, a [64,1,1024], b [1,512,1024], c [64,1024,512]."""
     B, M, N = 64, 512, 1024
     a = generate("broadcast_strided", "a")
@@ -111,11 +122,12 @@ def broadcast_strided(log, reps: int = 20, sets: int = 2) -> dict:
                                      ctypes.byref(lo)))
 
     kid = _fusion("in f32\nin f32\nin f32\nadd %0 %1\nmul %3 %2\nout %4\n")
+    calls = [_FusedCall(kid, [da, db, dcs[k]], [la, lb, lc], outs[k], lo) for k in range(sets)]
 
     def fused():
         k = i[0] % sets
         i[0] += 1
-        _fuse_launch(kid, [da, db, dcs[k]], [la, lb, lc], outs[k], lo)
+        calls[k]()
 
     e = time_region(eager, reps)
     f = time_region(fused, reps)

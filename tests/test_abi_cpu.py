@@ -81,7 +81,7 @@ def test_fusion_compiler_generates_and_compiles_on_the_host():
     src = buf.value.decode()
     assert "v3 = v0 * v1" in src and "v4 = v3 + v2" in src
     assert "trs::exp_value(v4)" in src and "__uint_as_float(0x3f800000u)" in src
-    assert "trs_fused_flat_v" in src and "trs_fused_tiled_v1" in src
+    assert "trs_fused_flat_c" in src and "trs_fused_rows_s" in src and "trs_fused_generic" in src
     ms = ctypes.c_double()
     abi.check(abi.lib.trs_fusion_compile_ms(kid, ctypes.byref(ms)))
     assert ms.value > 0
