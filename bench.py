@@ -167,6 +167,21 @@ def main() -> int:
 
         uev = time_launches(unfused_step, reps=5, warmup=1)
         u_ms = statistics.median(uev)
+        # Ceilings of the same launch shape: x*y + z (the same bytes, no exp)
+        # and a plain 1 GiB copy (half the bytes), both flat one-shot kernels.
+        kid_fma = ctypes.c_uint64()
+        fma_ir = "in f32\nin f32\nin f32\nmul %0 %1\nadd %3 %2\nout %4\n"
+        check(abi.lib.trs_fusion_compile(fma_ir.encode(), len(fma_ir), ctypes.byref(kid_fma)))
+        from trs_backend.timing import time_region
+        fma_ms = time_region(lambda: check(abi.lib.trs_fusion_launch(kid_fma, 3, ptrs, lays, dout.ptr, ctypes.byref(lay))),
+                             reps=args.steps, warmup=2)
+        copy_ms = time_region(lambda: check(abi.lib.trs_unary_f32(3, dx.ptr, ctypes.byref(lay), dout.ptr, ctypes.byref(lay))),
+                              reps=args.steps, warmup=2)
+        extra["fused_chain"]["same_bytes_no_exp_us"] = fma_ms * 1e3
+        extra["fused_chain"]["same_bytes_no_exp_frac_hbm"] = bytes_per_step / (fma_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+        extra["fused_chain"]["copy_1GiB_us"] = copy_ms * 1e3
+        extra["fused_chain"]["copy_1GiB_frac_hbm"] = 8 * n / (copy_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+        log(f"same-shape ceilings: x*y+z {fma_ms * 1e3:.1f} us, 1 GiB copy {copy_ms * 1e3:.1f} us")
         extra["fused_chain"]["unfused_eager_ms"] = u_ms
         extra["fused_chain"]["unfused_GBps_algorithmic"] = bytes_per_step / (u_ms * 1e-3) / 1e9
         extra["fused_chain"]["unfused_GBps_moved"] = 48 * n / (u_ms * 1e-3) / 1e9
@@ -200,7 +215,10 @@ def main() -> int:
         "config": {"workload": "fused_chain: relu(exp(x*y + z) - 1.0), x,y,z contiguous f32 [2^28], one fused kernel",
                    "elements": n, "bytes_per_step": bytes_per_step, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic()},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "traffic_source": "profiles/fused_chain_traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of "
+                                       "this kernel, scaled by the same counters on a plain copy (not measured in "
+                                       "this run)"},
         "cpu_baseline": cpu,
         "extra": extra,
     }
@@ -297,12 +315,7 @@ def cpu_configs() -> int:
     res["mlp"] = {"seconds": t * (8192 // bs) + t_tr, "sample": f"batch {bs} of 8192, x{8192 // bs}, "
                   f"plus the W1^T/W2^T .contiguous() once ({t_tr:.2f} s)"}
     log(f"cpu mlp step: {res['mlp']['seconds']:.1f} s (scaled)")
-    cpu = ""
-    try:
-        cpu = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
-    except Exception:
-        pass
-    print(json.dumps({"cpu_configs": res, "threads": 1, "host_cpu": cpu, "host_cores": host_cores(),
+    print(json.dumps({"cpu_configs": res, "threads": 1, "host_cpu": host_cpu_model(), "host_cores": host_cores(),
                       "libc": O.libc_version()}), flush=True)
     return 0
 
@@ -426,8 +439,18 @@ def read_traffic():
         return None
 
 
+def host_cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except Exception:
+        return ""
+
+
 def cpu_baseline(x, y, z, n, log):
-    """The reference's CPU path (oracle restatement, one thread) on a bounded sample."""
+    """The reference's CPU path (oracle restatement, one thread) on a bounded
+    sample, with this process pinned to one core for the duration (restored
+    afterwards; no re-launch)."""
     try:
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as O
@@ -436,23 +459,31 @@ def cpu_baseline(x, y, z, n, log):
         return None
     sample = 1 << 25
     xs, ys, zs = x[:sample], y[:sample], z[:sample]
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        t = O.binary_contig(O.MUL, xs, ys)
-        t = O.binary_contig(O.ADD, t, zs)
-        t = O.unary_contig(O.EXP, t)
-        t = O.scalar_contig(O.S_SUB, t, 1.0)
-        t = O.unary_contig(O.RELU, t)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 200:
-            break
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[0]
+    os.sched_setaffinity(0, {core})
+    try:
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            t = O.binary_contig(O.MUL, xs, ys)
+            t = O.binary_contig(O.ADD, t, zs)
+            t = O.unary_contig(O.EXP, t)
+            t = O.scalar_contig(O.S_SUB, t, 1.0)
+            t = O.unary_contig(O.RELU, t)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > 10.0 or reps >= 200:
+                break
+    finally:
+        os.sched_setaffinity(0, set(allowed))
     gbs = 16 * sample * reps / el / 1e9
-    log(f"cpu baseline: {gbs:.2f} GB/s over {reps} x 2^25 elements in {el:.1f}s")
+    log(f"cpu baseline: {gbs:.2f} GB/s over {reps} x 2^25 elements in {el:.1f}s on core {core}")
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "host_cpu": host_cpu_model(), "host_cores": len(allowed), "pinned_core": core,
             "sample": f"first 2^25 of the 2^28 elements, reference 5-pass chain (mul, add, exp, sub_scalar, relu), "
-                      f"{reps} rep(s), {el:.1f}s, oracle built -O3 -march=x86-64 -ffp-contract=off"}
+                      f"{reps} rep(s), {el:.1f}s, one thread pinned to core {core} of the {len(allowed)} this "
+                      f"process may use, oracle built -O3 -march=x86-64 -ffp-contract=off"}
 
 
 if __name__ == "__main__":

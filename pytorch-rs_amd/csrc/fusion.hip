@@ -22,6 +22,7 @@
 #include <fstream>
 #include <map>
 #include <thread>
+#include <unordered_map>
 #include <memory>
 #include <mutex>
 #include <sstream>
@@ -61,6 +62,9 @@ struct Program {
     // of each role signature (kernel name -> code object).
     std::mutex spec_mu;
     std::map<std::string, std::unique_ptr<CodeObject>> specs;
+    // Launch-plan signature -> function, per device: a repeated launch looks
+    // its kernel up here without building names or sources.
+    std::unordered_map<uint64_t, hipFunction_t> by_plan[16];
 };
 
 std::mutex g_mu;
@@ -385,7 +389,7 @@ int get_spec_function(Program *prog, DeviceState *dev, const std::string &name, 
     return get_function(co, dev, name, fn);
 }
 
-int get_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunction_t *fn) {
+int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunction_t *fn) {
     const unsigned strm = pl.g.streamed & ((1u << prog->nin) - 1u);
     const std::string mask = std::to_string(prog->u8mask) + "u";
     char name[128];
@@ -416,6 +420,28 @@ int get_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunc
     case PwVariant::Empty: break;
     }
     return set_error(TRS_E_INVALID_ARGUMENT, "no kernel for an empty launch");
+}
+
+// The kernel of a launch plan: looked up by the plan's signature (variant,
+// vector access, role masks, walk, streamed inputs), resolved on a miss.
+int get_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunction_t *fn) {
+    const uint64_t strm = pl.g.streamed & ((1u << prog->nin) - 1u);
+    const uint64_t key = (uint64_t)pl.variant | (uint64_t)pl.vec << 3 | (uint64_t)pl.contig << 4 |
+                         (uint64_t)pl.walk << 5 | strm << 9 | (uint64_t)pl.trans << 17 | (uint64_t)pl.held << 25 |
+                         (uint64_t)pl.once << 33 | (uint64_t)pl.xbc << 41;
+    {
+        std::lock_guard<std::mutex> lock(prog->spec_mu);
+        auto it = prog->by_plan[dev->index].find(key);
+        if (it != prog->by_plan[dev->index].end()) {
+            *fn = it->second;
+            return TRS_OK;
+        }
+    }
+    const int rc = resolve_plan_function(prog, dev, pl, fn);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(prog->spec_mu);
+    prog->by_plan[dev->index][key] = *fn;
+    return TRS_OK;
 }
 
 }  // namespace

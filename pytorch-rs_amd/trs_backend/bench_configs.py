@@ -56,7 +56,13 @@ class _FusedCall:
         check(abi.lib.trs_fusion_launch(*self.args))
 
 
-def relu_bias(log, reps: int = 20, sets: int = 8) -> dict:
+# Back-to-back launches per timed region for the short pointwise kernels: the
+# region opens with one host launch latency before the queue fills, so it is
+# sized to span milliseconds and that latency adds well under 1% per launch.
+SHORT_KERNEL_REPS = 200
+
+
+def relu_bias(log, reps: int = SHORT_KERNEL_REPS, sets: int = 8) -> dict:
     """Config 0: relu(x + b), x [4096,4096], b [4096] row-broadcast, seed 0."""
     R = C = 4096
     x = generate("relu_bias", "x")
@@ -87,17 +93,30 @@ def relu_bias(log, reps: int = 20, sets: int = 8) -> dict:
         i[0] += 1
         calls[k]()
 
+    # The ceiling of this launch shape: a plain copy of x (the product's COPY
+    # op, one float4 per lane, 16,384 blocks -- the rows kernel's grid) over
+    # the same buffer sets.
+    ln = layout_of((R * C,))
+
+    def copy():
+        k = i[0] % sets
+        i[0] += 1
+        check(abi.lib.trs_unary_f32(3, xs[k].ptr, ctypes.byref(ln), tmp[k].ptr, ctypes.byref(ln)))
+
     e = time_region(eager, reps)
     f = time_region(fused, reps)
-    spread = _spread(time_launches(fused, reps))
-    log(f"relu_bias: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us")
+    cp = time_region(copy, reps)
+    spread = _spread(time_launches(fused, 20))
+    log(f"relu_bias: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us, same-shape copy {cp * 1e3:.1f} us")
     return {"relu_bias": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
                           "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
                           "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS, "fused_spread": spread,
+                          "copy_same_shape_us": cp * 1e3, "copy_same_shape_frac_hbm": 2 * R * C * 4 / (cp * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                          "fused_time_over_copy": f / cp, "buffer_sets": sets,
                           "output_checksum": _checksum(outs[(i[0] - 1) % sets], R * C)}}
 
 
-def broadcast_strided(log, reps: int = 20, sets: int = 4) -> dict:
+def broadcast_strided(log, reps: int = SHORT_KERNEL_REPS, sets: int = 4) -> dict:
     """Config 2: (a + b) * c.mT, a [64,1,1024], b [1,512,1024], c [64,1024,512]."""
     B, M, N = 64, 512, 1024
     a = generate("broadcast_strided", "a")
@@ -129,14 +148,24 @@ def broadcast_strided(log, reps: int = 20, sets: int = 4) -> dict:
         i[0] += 1
         calls[k]()
 
+    # c.mT copied to a contiguous tensor: the transposing kernel with no
+    # broadcast operands, the access pattern's own cost.
+    def transpose_copy():
+        k = i[0] % sets
+        i[0] += 1
+        check(abi.lib.trs_unary_f32(3, dcs[k].ptr, ctypes.byref(lc), tmps[k].ptr, ctypes.byref(lo)))
+
     e = time_region(eager, reps)
     f = time_region(fused, reps)
-    spread = _spread(time_launches(fused, reps))
-    log(f"broadcast_strided: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us")
+    tc = time_region(transpose_copy, reps)
+    spread = _spread(time_launches(fused, 20))
+    log(f"broadcast_strided: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us, c.mT copy {tc * 1e3:.1f} us")
     return {"broadcast_strided": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
                                   "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
                                   "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS, "fused_spread": spread,
-                                  "output_checksum": _checksum(outs[(i[0] - 1) % sets], B * M * N)}}
+                                  "transpose_copy_us": tc * 1e3,
+                                  "transpose_copy_frac_hbm": 2 * B * M * N * 4 / (tc * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                  "buffer_sets": sets, "output_checksum": _checksum(outs[(i[0] - 1) % sets], B * M * N)}}
 
 
 # MFMA-bound kernels reach steady clocks only after ~25 ms of sustained
