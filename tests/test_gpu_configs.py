@@ -5,8 +5,11 @@ oracle restatement runs the reference's loops in a few seconds at these
 sizes.  The MLP (config 4) runs through torch_rs autograd at full size.
 Its gradients are first checked bit for bit against the same step composed
 explicitly from device ops.  That composition is then checked stage by stage
-against the oracle: elementwise stages over every element, GEMM stages on
-sampled rows within 1e-5*sqrt(K)*(|A||B|).  exp is checked exhaustively,
+against the oracle over every element: elementwise stages bit for bit, GEMM
+stages within 1e-5*sqrt(K)*(|A||B|) against the reference-order product
+(the oracle's row-blocked loop split over threads), and the loss within the
+summation bounds.  The timed MLP step (fused activation, split-K GEMMs) is
+checked bit for bit against the eager step.  exp is checked exhaustively,
 over all 2^32 inputs, against glibc.
 """
 import numpy as np
@@ -86,17 +89,23 @@ def test_exp_exhaustive_over_all_bit_patterns():
     assert worst <= 2
 
 
-def _mm_rows(a, b, rows):
-    """Oracle rows (reference order) and |A||B| bound rows for C = a @ b."""
-    m, k = a.shape
-    _, n = b.shape
-    return O.matmul_rows(np.ascontiguousarray(a).ravel(), (m, k), (k, 1), np.ascontiguousarray(b).ravel(),
-                         (k, n), (n, 1), rows)
+def _threads():
+    import os
+    return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
-def _within(got_rows, want_rows, bound_rows, k):
-    err = np.abs(got_rows.astype(np.float64) - want_rows)
-    return np.all(err <= 1e-5 * np.sqrt(k) * bound_rows + 1e-30), err.max()
+def _check_gemm(name, got, a, b):
+    """Every element of got = a @ b against the reference-order oracle,
+    within 1e-5*sqrt(K)*(|a||b|) (the bound in float64)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    k = a.shape[1]
+    want = O.matmul_threads(a, b, threads=_threads())
+    bound = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    lim = 1e-5 * np.sqrt(k) * bound
+    ok = err <= lim
+    assert ok.all(), (name, int((~ok).sum()), float(err.max()))
 
 
 def _relu_backward_on_device(z1, up):
@@ -119,7 +128,8 @@ def test_config4_mlp_full_size_autograd_and_stagewise_parity():
     b1, b2 = torch_rs.zeros(4096, device="cuda"), torch_rs.zeros(1024, device="cuda")
     mdev = F.keep_mask(mask)
     out = F.dropout((X @ W1 + b1).relu(), 0.1, mask=mdev) @ W2 + b2
-    out.sum().backward()
+    loss = out.sum()
+    loss.backward()
     gW1, gW2, gX = W1.grad.numpy(), W2.grad.numpy(), X.grad.numpy()
 
     # 1. the same step composed explicitly from device ops, outside autograd
@@ -142,30 +152,54 @@ def test_config4_mlp_full_size_autograd_and_stagewise_parity():
     assert_bitwise_equal(dw1.numpy().ravel(), gW1.ravel())
     assert_bitwise_equal(dx.numpy().ravel(), gX.ravel())
 
-    # 2. each stage of the composition against the oracle
-    rows = np.array([0, 1, 777, 4095, 4096, 8191])
-    cols = np.array([0, 5, 2047, 4095])
+    # 2. each stage of the composition against the oracle, every element
     z1h, hh, dhh, ddh, dh_h, dz1h = (t.numpy() for t in (z1, h, d, dd, dh, dz1))
-    want, bound = _mm_rows(x, w1, rows)
-    ok, e = _within(z1h[rows], want, bound, 4096)  # + b1 (zeros) is exact
-    assert ok, ("Z1", e)
+    oh = o.numpy()
+    _check_gemm("Z1", z1h, x, w1)  # + b1 (zeros) is exact
     assert_bitwise_equal(hh.ravel(), O.unary_contig(O.RELU, z1h.ravel()))
     assert_bitwise_equal(dhh.ravel(), O.mask_apply(hh.ravel(), mask.ravel(), scale))
-    want, bound = _mm_rows(dhh, w2, rows)
-    ok, e = _within(o.numpy()[rows], want, bound, 4096)
-    assert ok, ("out", e)
-    want, bound = _mm_rows(np.ones((8192, 1024), np.float32), np.ascontiguousarray(w2.T), rows)
-    ok, e = _within(ddh[rows], want, bound, 1024)
-    assert ok, ("dD", e)
+    _check_gemm("out", oh, dhh, w2)
+    ones = np.ones((8192, 1024), np.float32)
+    _check_gemm("dD", ddh, ones, w2.T)
     assert_bitwise_equal(dh_h.ravel(), O.mask_apply(O.scalar_contig(O.S_MUL, ddh.ravel(), scale), mask.ravel(),
                                                      np.float32(1.0)))
     assert_bitwise_equal(dz1h.ravel(), O.relu_backward(z1h.ravel(), (8192, 4096), (4096, 1), 0, dh_h.ravel()))
-    want, bound = _mm_rows(np.ascontiguousarray(x.T), dz1h, cols)  # rows of dW1 = X^T dZ1
-    ok, e = _within(gW1[cols], want, bound, 8192)
-    assert ok, ("dW1", e)
-    want, bound = _mm_rows(dz1h, np.ascontiguousarray(w1.T), rows)
-    ok, e = _within(gX[rows], want, bound, 4096)
-    assert ok, ("dX", e)
-    want, bound = _mm_rows(np.ascontiguousarray(dhh.T), np.ones((8192, 1024), np.float32), cols)
-    ok, e = _within(gW2[cols], want, bound, 8192)
-    assert ok, ("dW2", e)
+    _check_gemm("dW1", gW1, x.T, dz1h)
+    _check_gemm("dX", gX, dz1h, w1.T)
+    _check_gemm("dW2", gW2, dhh.T, ones)
+
+    # 3. the loss (a sum over the 2^23 outputs) against the reference's
+    # sequential fold and the exact sum: the device tree's own bound
+    # gamma_d * sum|out| with d = ceil(8192/256) + 20 = 52, the fold's
+    # gamma_(n-1) * sum|out|, and their sum between the two.
+    import math
+    n = oh.size
+    loss_dev = float(np.float32(loss.item()))
+    fold = float(O.sum_f32(oh.ravel(), (n,)))
+    exact = math.fsum(oh.ravel().astype(np.float64))
+    abs_sum = O.sum_abs(oh.ravel())
+
+    def gamma(k):
+        return k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
+
+    assert abs(loss_dev - exact) <= gamma(52) * abs_sum, (loss_dev, exact)
+    assert abs(fold - exact) <= gamma(n - 1) * abs_sum
+    assert abs(loss_dev - fold) <= (gamma(52) + gamma(n - 1)) * abs_sum
+
+
+def test_config4_timed_mlp_step_equals_eager_bitwise():
+    """The step bench.py times (mlp_bench.build(): bias add, relu and
+    dropout-apply fused into one autograd node, split-K GEMMs) against the
+    eager step at full size: loss and the three gradients bit for bit."""
+    from trs_backend import mlp_bench
+    fused = mlp_bench.build(fused=True)
+    eager = mlp_bench.build(fused=False)
+    lf, xf, w1f, w2f = fused()
+    le, xe, w1e, w2e = eager()
+    assert_bitwise_equal(lf.numpy().ravel(), le.numpy().ravel())
+    for a, b in ((xf, xe), (w1f, w1e), (w2f, w2e)):
+        assert_bitwise_equal(a.grad.numpy().ravel(), b.grad.numpy().ravel())
+    # a second fused step (cached blocks and kernels) repeats the first exactly
+    lf2, xf2, w1f2, w2f2 = fused()
+    assert_bitwise_equal(lf2.numpy().ravel(), lf.numpy().ravel())
+    assert_bitwise_equal(w1f2.grad.numpy().ravel(), w1f.grad.numpy().ravel())
