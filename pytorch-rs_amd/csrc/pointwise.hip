@@ -254,6 +254,12 @@ struct ReduceGeom {
     int64_t other_off;
 };
 
+// One lane per operand element j: its reduced dims walked with an odometer,
+// kUnroll loads issued ahead of their ordered adds (the adds are the
+// reference's sequence; only the loads run ahead).  Used for short chains
+// and for layouts whose reduced or kept dims do not merge.
+constexpr int kRedUnroll = 8;
+
 template <bool HAS_OTHER>
 __global__ void __launch_bounds__(256) reduce_bcast_kernel(const float *up, const float *other, ReduceGeom rg,
                                                            float *grad) {
@@ -270,24 +276,314 @@ __global__ void __launch_bounds__(256) reduce_bcast_kernel(const float *up, cons
         int64_t cnt[kMaxRank];
         for (int d = 0; d < rg.nred; d++) cnt[d] = 0;
         int64_t uo = ub, oo = ob;
-        for (int64_t r = 0; r < rg.nred_total; r++) {
-            float c = up[uo];
-            if constexpr (HAS_OTHER) c = c * other[oo];
-            acc += c;
-            // odometer over reduced dims, innermost last
-            for (int d = rg.nred - 1; d >= 0; d--) {
-                if (++cnt[d] < rg.red_size[d]) {
-                    uo += rg.red_up[d];
-                    oo += rg.red_other[d];
-                    break;
+        for (int64_t r0 = 0; r0 < rg.nred_total; r0 += kRedUnroll) {
+            float c[kRedUnroll];
+#pragma unroll
+            for (int i = 0; i < kRedUnroll; i++) {
+                if (r0 + i < rg.nred_total) {
+                    c[i] = up[uo];
+                    if constexpr (HAS_OTHER) c[i] = c[i] * other[oo];
+                    // odometer over reduced dims, innermost last
+                    for (int d = rg.nred - 1; d >= 0; d--) {
+                        if (++cnt[d] < rg.red_size[d]) {
+                            uo += rg.red_up[d];
+                            oo += rg.red_other[d];
+                            break;
+                        }
+                        cnt[d] = 0;
+                        uo -= rg.red_up[d] * (rg.red_size[d] - 1);
+                        oo -= rg.red_other[d] * (rg.red_size[d] - 1);
+                    }
                 }
-                cnt[d] = 0;
-                uo -= rg.red_up[d] * (rg.red_size[d] - 1);
-                oo -= rg.red_other[d] * (rg.red_size[d] - 1);
             }
+#pragma unroll
+            for (int i = 0; i < kRedUnroll; i++)
+                if (r0 + i < rg.nred_total) acc += c[i];
         }
         grad[j] = acc;
     }
+}
+
+// Staged broadcast reduction for `up` viewed as [KO, R, KI]: the reduced dims
+// merged into R rows, the operand's kept dims into KO outer and KI inner, KI
+// unit-stride in up.  grad[ko, ki] = sum over r in order of up[ko, r, ki]
+// (times other[ko, r, ki]) from +0.0.  Each of the KO*KI sums is a chain of R
+// dependent adds that the reference's order forbids splitting, so the chains
+// are few and long (a bias gradient over [8192, 4096] has 4096 chains of
+// 8192): one lane per chain could keep far too few loads in flight, and a
+// chain costs R dependent adds whatever the layout (about 6 cycles each for a
+// wave fed from LDS).
+//
+// A block owns 32 chains.  Eight producer waves load stages of SR rows of
+// those 32 columns AHEAD stages in advance into registers: each lane SR/256
+// blocks of 4x4 (4 rows of 4 chains), multiplied by `other` (one rounding, as
+// the reference's up * other), transposed in registers and stored
+// chain-major into a double-buffered LDS stage.  A ninth wave adds: lane c
+// reads chain c's rows 4 at a time (ds_read_b128) and adds them in row order,
+// one stage behind the producers, so its adds overlap the next stage's loads
+// and stores.  The producer and adder roles are wave-uniform and each runs
+// the same number of barriers.  The launcher uses SR = 256 (66.5 KB of LDS,
+// two blocks per CU); 512-row stages measured no faster.
+constexpr int kStRows = 256;
+constexpr int kStChains = 32;                    // chains per block (adder lanes 0..31)
+constexpr int kStProducers = 8;                  // producer waves; wave 8 adds
+constexpr int kStLanes = (kStProducers + 1) * 64;
+constexpr int kStQuads = kStProducers * 8;       // row quads per producer pass (256 rows)
+
+struct RedColsGeom {
+    int64_t KO, R, KI;
+    int64_t up_ko, up_r;          // up strides (the ki stride is 1)
+    int64_t ot_ko, ot_r, ot_ki;   // other strides
+    int64_t other_off;
+};
+
+// How the producers read `other`: not at all, as 16-byte vectors along ki
+// (4 chains of a row), as vectors along r (4 rows of a chain, a transposed
+// view such as c.mT), or one float at a time.
+enum RedOther { kOtNone = 0, kOtVecKi = 1, kOtVecR = 2, kOtScalar = 3 };
+
+// Raw buffer descriptor word 3 (32-bit data format: untyped loads, no
+// swizzle).
+constexpr int kRawBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t stage_rsrc(const float *base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, bytes, kRawBufferWord3);
+}
+
+// Bytes a stage's descriptor covers: from the stage's first row through
+// `tail` floats past the start of the last of `rem` remaining rows (rows
+// `row_stride` floats apart); none when no rows remain.
+__device__ __forceinline__ int stage_span(int64_t rem, int64_t row_stride, int64_t tail) {
+    if (rem <= 0) return 0;
+    const int64_t b = ((rem - 1) * row_stride + tail) * 4;
+    return (int)(uint32_t)(b < 0xFFFFFFFFll ? b : 0xFFFFFFFFll);
+}
+
+__device__ __forceinline__ vf4 buffer_vf4(__amdgpu_buffer_rsrc_t rs, int off) {
+    return __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+}
+
+// A register copy the compiler cannot move or merge: without a product the
+// transpose is plain copies, which the register allocator would otherwise
+// gather at the loop's back edge, where they wait for every load in flight.
+__device__ __forceinline__ float stage_copy(float x) {
+    float y;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
+    return y;
+}
+
+template <int OT, int AHEAD, int SR>
+__global__ void __launch_bounds__(kStLanes) reduce_stage_kernel(const float *up, const float *other, RedColsGeom g,
+                                                                 float *grad) {
+    constexpr int NQ = SR / (4 * kStQuads);  // 4x4 blocks per producer lane per stage
+    // Floats per chain in a stage: (SR + 4) / 4 is 1 mod 16, so the b128
+    // accesses of 8 consecutive lanes (chain-strided for the adder,
+    // row-strided for the producers) fall on distinct 4-bank groups.
+    constexpr int PITCH = SR + 4;
+    static_assert(NQ >= 1 && NQ * 4 * kStQuads == SR && (PITCH / 4) % 16 == 1, "stage shape");
+    __shared__ __attribute__((aligned(16))) float stage[2][kStChains][PITCH];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t groups = g.KI / kStChains;
+    const int64_t ko = blockIdx.x / groups;
+    const int64_t ki0 = (blockIdx.x % groups) * kStChains;
+    const int64_t nst = (g.R + SR - 1) / SR;
+    const int64_t nit = (nst + AHEAD - 1) / AHEAD * AHEAD;  // stages run, padded to whole rings
+    if (wave < kStProducers) {
+        const int cq = lane >> 3;  // chains cq*4 .. cq*4+3
+        // row quads j*64 + wave*8 + (lane&7) of a stage, j < NQ
+        const int quad0 = wave * 8 + (lane & 7);
+        // Loads go through a buffer descriptor per stage, built in scalar
+        // registers from the block's base and the stage index: a lane's byte
+        // offsets within a stage never change, and the descriptor's extent
+        // ends after the last row below R, so the hardware returns 0 for the
+        // rows past R (never added) without any per-row address arithmetic.
+        const float *ub = up + ko * g.up_ko + ki0;
+        const float *ob = OT != kOtNone ? other + g.other_off + ko * g.ot_ko + ki0 * g.ot_ki : nullptr;
+        int vu[NQ][4], vo[NQ][4];
+#pragma unroll
+        for (int j = 0; j < NQ; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int64_t row = (j * kStQuads + quad0) * 4 + i;
+                vu[j][i] = (int)((row * g.up_r + cq * 4) * 4);
+                if constexpr (OT == kOtVecKi) vo[j][i] = (int)((row * g.ot_r + cq * 4) * 4);
+                else if constexpr (OT == kOtVecR)
+                    vo[j][i] = (int)(((int64_t)(cq * 4 + i) * g.ot_ki + (j * kStQuads + quad0) * 4) * 4);
+                else vo[j][i] = 0;
+            }
+        // ru[s][j][i]: row i's 4 chains; ro[s][j][i]: the same for kOtVecKi
+        // and kOtScalar, chain i's 4 rows for kOtVecR.
+        vf4 ru[AHEAD][NQ][4], ro[AHEAD][NQ][4];
+        auto issue = [&](int slot, int64_t st) {
+            const int64_t sc = st < nst ? st : nst - 1;  // past the end: no rows, base kept in range
+            const int64_t rem = g.R - st * SR;            // rows from this stage's first on
+            const auto rs = stage_rsrc(ub + sc * SR * g.up_r, stage_span(rem, g.up_r, kStChains));
+#pragma unroll
+            for (int j = 0; j < NQ; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) ru[slot][j][i] = buffer_vf4(rs, vu[j][i]);
+            if constexpr (OT == kOtVecKi) {
+                const auto os = stage_rsrc(ob + sc * SR * g.ot_r, stage_span(rem, g.ot_r, kStChains));
+#pragma unroll
+                for (int j = 0; j < NQ; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) ro[slot][j][i] = buffer_vf4(os, vo[j][i]);
+            } else if constexpr (OT == kOtVecR) {
+                // chain 31's remaining rows end the extent
+                const auto os = stage_rsrc(ob + sc * SR, stage_span(rem, 1, (kStChains - 1) * g.ot_ki + 1));
+#pragma unroll
+                for (int j = 0; j < NQ; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) ro[slot][j][i] = buffer_vf4(os, vo[j][i]);
+            } else if constexpr (OT == kOtScalar) {
+                const float *oc = ob + cq * 4 * g.ot_ki;
+#pragma unroll
+                for (int j = 0; j < NQ; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int64_t r = st * SR + (j * kStQuads + quad0) * 4 + i;
+                        const float *op = oc + (r < g.R ? r : g.R - 1) * g.ot_r;
+                        ro[slot][j][i] = vf4{op[0], op[g.ot_ki], op[2 * g.ot_ki], op[3 * g.ot_ki]};
+                    }
+            }
+        };
+        // The ring starts at zero and the loop starts AHEAD stages early (the
+        // stores of stages below 0 are never read): the first loads are then
+        // issued by the loop's own code, into the registers every later load
+        // of their slot uses, and the wait before each stage's transpose
+        // covers that stage's loads only.
+#pragma unroll
+        for (int k = 0; k < AHEAD; k++)
+#pragma unroll
+            for (int j = 0; j < NQ; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) ru[k][j][i] = ro[k][j][i] = vf4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int64_t s0 = -AHEAD; s0 < nit; s0 += AHEAD) {
+#pragma unroll
+            for (int k = 0; k < AHEAD; k++) {
+                const int64_t st = s0 + k;
+                // keeps this stage's register transpose (which waits for this
+                // stage's loads only) from being hoisted with the others
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < NQ; j++) {
+                    vf4 w[4];  // w[c]: chain c's 4 rows
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            float v;
+                            if constexpr (OT == kOtVecR) v = ru[k][j][i][c] * ro[k][j][c][i];
+                            else if constexpr (OT != kOtNone) v = ru[k][j][i][c] * ro[k][j][i][c];
+                            else v = stage_copy(ru[k][j][i][c]);
+                            w[c][i] = v;
+                        }
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        *(vf4 *)&stage[st & 1][cq * 4 + c][(j * kStQuads + quad0) * 4] = w[c];
+                }
+                issue(k, st + AHEAD);
+                __syncthreads();
+            }
+        }
+    } else {
+        float acc = 0.0f;
+        const bool active = lane < kStChains;
+        auto add_stage = [&](int64_t st) {
+            const float *row = &stage[st & 1][lane & (kStChains - 1)][0];
+            const int64_t left = g.R - st * SR;
+            if (left >= SR) {
+                // SR/4 quads in groups of 8, the next group read before the
+                // current one is added
+                vf4 a[8], b[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) a[q] = *(const vf4 *)&row[q * 4];
+#pragma unroll
+                for (int grp = 0; grp < SR / 32; grp++) {
+                    if (grp + 1 < SR / 32) {
+#pragma unroll
+                        for (int q = 0; q < 8; q++) b[q] = *(const vf4 *)&row[(grp + 1) * 32 + q * 4];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of these adds
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        acc += a[q][0];
+                        acc += a[q][1];
+                        acc += a[q][2];
+                        acc += a[q][3];
+                    }
+#pragma unroll
+                    for (int q = 0; q < 8; q++) a[q] = b[q];
+                }
+            } else {
+                for (int64_t r = 0; r < left; r++) acc += row[r];
+            }
+        };
+        for (int64_t it = -AHEAD; it < nit; it++) {
+            if (it >= 1 && it - 1 < nst && active) add_stage(it - 1);
+            __syncthreads();
+        }
+        if (nit == nst && active) add_stage(nst - 1);  // written before the last barrier
+        if (active) grad[ko * g.KI + ki0 + lane] = acc;
+    }
+}
+
+// Merges a reduction's dims into [KO, R, KI] for the staged kernel: the
+// reduced dims (in order) into one of R rows, the trailing kept dims into KI
+// (unit stride in up), the other kept dims into KO.  Adjacent dims merge when
+// the outer one's stride is the inner one's stride times its size, for up and
+// (when present) for other.  False when the layout does not reduce to that.
+bool reduce_cols_plan(const ReduceGeom &rg, bool has_other, RedColsGeom *cg) {
+    auto merge = [&](int n, const int64_t *size, const int64_t *su, const int64_t *so, int first, int last,
+                     int64_t *msize, int64_t *mu, int64_t *mo) -> bool {
+        // dims [first, last] merge into one (row-major)
+        int64_t sz = 1, u = 0, o = 0;
+        for (int d = last; d >= first; d--) {
+            if (d == last) {
+                sz = size[d];
+                u = su[d];
+                o = so[d];
+                continue;
+            }
+            if (su[d] != su[d + 1] * size[d + 1]) return false;
+            if (has_other && so[d] != so[d + 1] * size[d + 1]) return false;
+            sz *= size[d];
+        }
+        (void)n;
+        *msize = sz;
+        *mu = u;
+        *mo = o;
+        return true;
+    };
+    if (rg.nred < 1 || rg.nkept < 1) return false;
+    int64_t R, ur, orr;
+    if (!merge(rg.nred, rg.red_size, rg.red_up, rg.red_other, 0, rg.nred - 1, &R, &ur, &orr)) return false;
+    // KI: the longest run of trailing kept dims that merges and ends with up
+    // stride 1; KO: the rest (one merged dim, or none).
+    if (rg.kept_up[rg.nkept - 1] != 1) return false;
+    int first = rg.nkept - 1;
+    while (first > 0) {
+        const int d = first - 1;
+        if (rg.kept_up[d] != rg.kept_up[d + 1] * rg.kept_size[d + 1]) break;
+        if (has_other && rg.kept_other[d] != rg.kept_other[d + 1] * rg.kept_size[d + 1]) break;
+        first = d;
+    }
+    int64_t KI, uki, oki;
+    if (!merge(rg.nkept, rg.kept_size, rg.kept_up, rg.kept_other, first, rg.nkept - 1, &KI, &uki, &oki)) return false;
+    int64_t KO = 1, uko = 0, oko = 0;
+    if (first > 0 && !merge(rg.nkept, rg.kept_size, rg.kept_up, rg.kept_other, 0, first - 1, &KO, &uko, &oko))
+        return false;
+    cg->KO = KO;
+    cg->R = R;
+    cg->KI = KI;
+    cg->up_ko = uko;
+    cg->up_r = ur;
+    cg->ot_ko = oko;
+    cg->ot_r = orr;
+    cg->ot_ki = oki;
+    cg->other_off = rg.other_off;
+    return true;
 }
 
 int reduce_to_operand(const float *up, const trs_layout *lout, const float *other,
@@ -344,6 +640,34 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
         hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream, grad,
                            (size_t)rg.nself, 0.0f, (const float *)nullptr);
         TRS_LAUNCH_CHECK("fill kernel");
+        return TRS_OK;
+    }
+    // The staged kernel: reduced dims merging into at least one full stage
+    // of rows, kept dims merging into an outer and an inner part whose up
+    // stride is 1 and whose size is a multiple of 32, 16-byte aligned.
+    // Byte offsets within a stage are 32-bit: (256 * stride + 32) * 4 must
+    // stay below 2^31 for each operand read through a descriptor.
+    auto fits = [](int64_t extent) { return extent >= 0 && extent * 4 < (int64_t)INT32_MAX; };
+    RedColsGeom cg{};
+    if (reduce_cols_plan(rg, other != nullptr, &cg) && cg.R >= kStRows && cg.KI % kStChains == 0 &&
+        cg.KO * (cg.KI / kStChains) <= INT32_MAX && (uintptr_t)up % 16 == 0 && cg.up_ko % 4 == 0 &&
+        cg.up_r % 4 == 0 && fits(kStRows * cg.up_r + kStChains) &&
+        (!other || (cg.ot_ko >= 0 && cg.ot_r >= 0 && cg.ot_ki >= 0))) {
+        const int64_t grid = cg.KO * (cg.KI / kStChains);
+        const dim3 gd((unsigned)grid), bd(kStLanes);
+        constexpr int SR = kStRows;
+        if (!other) {
+            hipLaunchKernelGGL((reduce_stage_kernel<kOtNone, 2, SR>), gd, bd, 0, dev->stream, up, other, cg, grad);
+        } else {
+            const bool base16 = (uintptr_t)(other + cg.other_off) % 16 == 0 && cg.ot_ko % 4 == 0;
+            if (base16 && cg.ot_ki == 1 && cg.ot_r % 4 == 0 && fits(SR * cg.ot_r + kStChains))
+                hipLaunchKernelGGL((reduce_stage_kernel<kOtVecKi, 2, SR>), gd, bd, 0, dev->stream, up, other, cg, grad);
+            else if (base16 && cg.ot_r == 1 && cg.ot_ki % 4 == 0 && cg.R % 4 == 0 && fits(kStChains * cg.ot_ki + SR))
+                hipLaunchKernelGGL((reduce_stage_kernel<kOtVecR, 2, SR>), gd, bd, 0, dev->stream, up, other, cg, grad);
+            else
+                hipLaunchKernelGGL((reduce_stage_kernel<kOtScalar, 2, SR>), gd, bd, 0, dev->stream, up, other, cg, grad);
+        }
+        TRS_LAUNCH_CHECK("staged broadcast reduction kernel");
         return TRS_OK;
     }
     const int64_t grid = std::min<int64_t>((rg.nself + 255) / 256, (int64_t)dev->cu_count * 8);

@@ -216,9 +216,56 @@ def mlp(log, reps: int = 20) -> dict:
     return {"mlp": mlp_bench.run(log, reps)}
 
 
+def reduce_vjp(log, reps: int = 50) -> dict:
+    """Broadcast-reduction VJPs, each a set of ordered chains of adds:
+    the bias gradient [8192,4096] -> [4096] (trs_reduce_to_shape_f32, 4096
+    chains of 8192) and config 2's operand a [64,1,1024] through the mul VJP
+    against c.mT (trs_mul_backward_f32: up * other added along the 512 rows,
+    65,536 chains).  GB/s counts the bytes read (up, and other) and written."""
+    rng = np.random.default_rng(12)
+    out = {}
+    R, C = 8192, 4096
+    # 4 inputs: 512 MiB rotated, twice the 256 MB MALL
+    ups = [DeviceArray.from_numpy(rng.standard_normal(R * C).astype(np.float32)) for _ in range(4)]
+    g = DeviceArray(C * 4)
+    lo, ls = layout_of((R, C)), layout_of((C,))
+    i = [0]
+
+    def bias():
+        k = i[0] % len(ups)
+        i[0] += 1
+        check(abi.lib.trs_reduce_to_shape_f32(ups[k].ptr, ctypes.byref(lo), ctypes.byref(ls), g.ptr))
+
+    t = time_region(bias, reps)
+    byts = R * C * 4 + C * 4
+    out["bias_grad_8192x4096"] = {"us": t * 1e3, "bytes": byts, "GBps": byts / (t * 1e-3) / 1e9,
+                                  "frac_hbm": byts / (t * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    log(f"reduce bias grad [8192,4096]->[4096]: {t * 1e3:.1f} us, {byts / (t * 1e-3) / 1e9:.0f} GB/s")
+    del ups
+    B, M, N = 64, 512, 1024
+    # 3 (up, c) pairs: 768 MiB rotated, three times the 256 MB MALL
+    ups = [DeviceArray.from_numpy(rng.standard_normal(B * M * N).astype(np.float32)) for _ in range(3)]
+    cs = [DeviceArray.from_numpy(rng.standard_normal(B * M * N).astype(np.float32)) for _ in range(3)]
+    ga = DeviceArray(B * N * 4)
+    lout, lc, la = layout_of((B, M, N)), layout_of((B, M, N), (N * M, 1, M)), layout_of((B, 1, N))
+
+    def mul_a():
+        k = i[0] % len(cs)
+        i[0] += 1
+        check(abi.lib.trs_mul_backward_f32(ups[k].ptr, ctypes.byref(lout), cs[k].ptr, ctypes.byref(lc),
+                                           ctypes.byref(la), ga.ptr))
+
+    t = time_region(mul_a, reps)
+    byts = 2 * B * M * N * 4 + B * N * 4
+    out["mul_vjp_a_64x512x1024"] = {"us": t * 1e3, "bytes": byts, "GBps": byts / (t * 1e-3) / 1e9,
+                                    "frac_hbm": byts / (t * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    log(f"mul VJP a [64,512,1024] x c.mT -> [64,1,1024]: {t * 1e3:.1f} us, {byts / (t * 1e-3) / 1e9:.0f} GB/s")
+    return {"reduce_vjp": out}
+
+
 def run_all(log) -> dict:
     res = {}
-    for fn in (relu_bias, broadcast_strided, matmul, mlp):
+    for fn in (relu_bias, broadcast_strided, reduce_vjp, matmul, mlp):
         try:
             res.update(fn(log))
         except Exception as exc:

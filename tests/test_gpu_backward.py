@@ -124,6 +124,77 @@ def test_add_vjp_reduce_to_shape_bit_exact(oshape, self_shape):
     assert_bitwise_equal(gpu_reduce(up, oshape, self_shape), O.reduce_to_shape(up, oshape, self_shape))
 
 
+# Shapes that take the staged reduction (the reduced dims merge into at least
+# one 256-row stage, the kept inner part is a multiple of 32 chains): the bias
+# gradient of the MLP, config 2's `a` operand, a partial last stage, a single
+# stage, outer kept dims, a reduced dim between kept ones, 32 chains only, and
+# a row count that is not a multiple of 4.
+STAGED = [((8192, 4096), (4096,)), ((8192, 1024), (1024,)), ((64, 512, 1024), (64, 1, 1024)),
+          ((300, 128), (128,)), ((256, 64), (64,)), ((3, 1000, 192), (3, 1, 192)), ((2, 258, 96), (2, 1, 96)),
+          ((2, 700, 5, 128), (2, 1, 5, 128)), ((1030, 2, 64), (2, 64)), ((4099, 32), (32,))]
+
+
+@pytest.mark.parametrize("oshape,self_shape", STAGED)
+def test_staged_reduce_to_shape_bit_exact(oshape, self_shape):
+    """The add VJP through the staged kernel: every chain added in the
+    reference's row-major order from +0.0, bit for bit."""
+    rng = np.random.default_rng(sum(oshape))
+    up = rng.standard_normal(int(np.prod(oshape))).astype(np.float32)
+    up[::977] = -0.0
+    assert_bitwise_equal(gpu_reduce(up, oshape, self_shape), O.reduce_to_shape(up, oshape, self_shape))
+
+
+@pytest.mark.parametrize("oshape,self_shape", STAGED[:7])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_staged_mul_vjp_bit_exact(oshape, self_shape, transposed):
+    """The Multiply VJP of a broadcast operand through the staged kernel:
+    contributions up*other (one rounding) added in order; `other` contiguous
+    (vectors of 4 chains) or a transposed view of its last two dims, as c.mT
+    in config 2 (vectors of 4 rows; one float at a time when the row count
+    or the chain stride is not a multiple of 4)."""
+    rng = np.random.default_rng(7 * sum(oshape) + transposed)
+    n = int(np.prod(oshape))
+    up = rng.standard_normal(n).astype(np.float32)
+    other = rng.standard_normal(n).astype(np.float32)
+    if transposed and len(oshape) >= 2:
+        *lead, m, k = oshape
+        base = O.contiguous_strides(tuple(lead) + (k, m))
+        ostr = tuple(base[:-2]) + (base[-1], base[-2])
+    else:
+        ostr = O.contiguous_strides(oshape)
+    got = gpu_mul_backward(up, oshape, other, oshape, ostr, 0, self_shape)
+    want = O.mul_backward(up, oshape, other, oshape, ostr, 0, self_shape)
+    assert_bitwise_equal(got, want)
+
+
+@pytest.mark.parametrize("oshape,other_shape", [((1024, 4096), (4096,)), ((2, 300, 64), (2, 1, 64))])
+def test_staged_mul_vjp_other_broadcast_along_rows(oshape, other_shape):
+    """other constant along the reduced rows (stride 0 there): the 4-chain
+    vectors re-read one row of other for every row of up."""
+    rng = np.random.default_rng(len(oshape))
+    n = int(np.prod(oshape))
+    up = rng.standard_normal(n).astype(np.float32)
+    other = rng.standard_normal(int(np.prod(other_shape))).astype(np.float32)
+    ostr = O.contiguous_strides(other_shape)
+    self_shape = other_shape
+    got = gpu_mul_backward(up, oshape, other, other_shape, ostr, 0, self_shape)
+    assert_bitwise_equal(got, O.mul_backward(up, oshape, other, other_shape, ostr, 0, self_shape))
+
+
+def test_staged_reduction_unaligned_input_takes_the_unrolled_kernel():
+    """up at an odd float offset cannot be read as 16-byte vectors: the
+    unrolled one-lane-per-chain kernel runs instead, with the same bits."""
+    rng = np.random.default_rng(99)
+    oshape, self_shape = (1024, 256), (256,)
+    up = rng.standard_normal(1024 * 256 + 1).astype(np.float32)
+    du = U.dev(up)
+    do = U.out_buffer(256)
+    # up starts one float into the buffer (4-byte, not 16-byte, aligned)
+    check(abi.lib.trs_reduce_to_shape_f32(ctypes.c_void_p(du.addr + 4), ctypes.byref(layout_of(oshape)),
+                                          ctypes.byref(layout_of(self_shape)), do.ptr))
+    assert_bitwise_equal(do.to_numpy(count=256), O.reduce_to_shape(up[1:], oshape, self_shape))
+
+
 def sum_tree_depth(n: int) -> int:
     """Most roundings any element passes through in trs_sum_f32's fixed tree:
     one block (n <= 32768) adds ceil(n/256) terms per lane, then 8 tree
