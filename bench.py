@@ -62,10 +62,14 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-configs", action="store_true",
                     help="time the reference's CPU path (oracle, one thread) on every BASELINE config and exit")
-    ap.add_argument("--workload", choices=("fused_chain", "copy", "transfer", "matmul"), default="fused_chain",
+    ap.add_argument("--workload", choices=("fused_chain", "copy", "transfer", "matmul", "config"),
+                    default="fused_chain",
                     help="copy: a plain 2^28-float copy kernel, the calibration run for rocprofv3 byte counters; "
                          "transfer: host<->device copy rates (pageable and page-locked host memory); "
-                         "matmul: the 4096^3 fp32 GEMM alone, for rocprofv3 MFMA counters")
+                         "matmul: the 4096^3 fp32 GEMM alone, for rocprofv3 MFMA counters; "
+                         "config: one of the extra configs alone (--config), for per-kernel profiles")
+    ap.add_argument("--config", choices=("relu_bias", "broadcast_strided", "reduce_vjp", "matmul", "mlp"),
+                    default="broadcast_strided", help="the extra config --workload config runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -97,6 +101,10 @@ def main() -> int:
         return transfer_rates()
     if args.workload == "matmul":
         return matmul_only(args)
+    if args.workload == "config":
+        from trs_backend import bench_configs
+        print(json.dumps(getattr(bench_configs, args.config)(log)), flush=True)
+        return 0
     t0 = time.time()
     x, y, z = (generate("fused_chain", k, threads=min(16, host_cores())) for k in ("x", "y", "z"))
     log(f"generated 3 x 2^28 inputs in {time.time() - t0:.1f}s")
