@@ -344,9 +344,9 @@ def _multi_cases():
             rng.standard_normal(R * C).astype(np.float32)]
     yield "rows", rows, [layout_of((R, C)), layout_of((C,)), layout_of((R, C))], (R, C), None
     B, M, N = 3, 70, 130
-    tiled = [rng.standard_normal(B * N).astype(np.float32), rng.standard_normal(M * N).astype(np.float32),
+    xpose = [rng.standard_normal(B * N).astype(np.float32), rng.standard_normal(M * N).astype(np.float32),
              rng.standard_normal(B * N * M).astype(np.float32)]
-    yield ("tiled", tiled, [layout_of((B, 1, N)), layout_of((1, M, N)), layout_of((B, M, N), (N * M, 1, M))],
+    yield ("xpose", xpose, [layout_of((B, 1, N)), layout_of((1, M, N)), layout_of((B, M, N), (N * M, 1, M))],
            (B, M, N), None)
     A, D = 9, 11
     gen = [rng.standard_normal(A * D * 3).astype(np.float32) for _ in range(3)]
@@ -358,7 +358,7 @@ def _multi_cases():
 def test_multi_output_program_equals_single_output_programs(case):
     """A four-output program writes, in one launch, exactly what the four
     one-output programs over the same instructions write, on every kernel
-    variant (flat, unaligned flat, row broadcast, LDS-tiled transpose,
+    variant (flat, unaligned flat, row broadcast, in-register transpose,
     generic strides)."""
     _, arrays, lays, oshape, ostr = case
     n = int(np.prod(oshape))
