@@ -91,8 +91,8 @@ template <class F, unsigned M>
 __global__ void __launch_bounds__(kFlatBlock) k_flat_contig(F f, PwGeom g, PwPtrs p) {
     pw_flat_contig_body<F, M>(f, g, p);
 }
-template <class F, unsigned M, bool V, unsigned S>
-__global__ void __launch_bounds__(256) k_rows(F f, PwGeom g, PwPtrs p) { pw_rows_body<F, M, V, S>(f, g, p); }
+template <class F, unsigned M, bool V, unsigned S, int RK = 0>
+__global__ void __launch_bounds__(256) k_rows(F f, PwGeom g, PwPtrs p) { pw_rows_body<F, M, V, S, RK>(f, g, p); }
 template <class F, unsigned M, bool V, unsigned TR, unsigned S>
 __global__ void __launch_bounds__(64 * kXposeWT * kXposeWX) k_xpose(F f, PwGeom g, PwPtrs p) {
     pw_xpose_body<F, M, V, kXposeWT, kXposeWX, TR, 0u, 0u, 1, S>(f, g, p);
@@ -134,7 +134,10 @@ int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
         break;
     case PwVariant::Rows:
         if (pl.vec)
-            with_mask<NIN>(sm, [&]<unsigned S>() { hipLaunchKernelGGL((k_rows<F, M, true, S>), grid, block, 0, s, f, pl.g, pl.p); });
+            with_mask<NIN>(sm, [&]<unsigned S>() {
+                if (pl.r2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, f, pl.g, pl.p);
+                else hipLaunchKernelGGL((k_rows<F, M, true, S, 0>), grid, block, 0, s, f, pl.g, pl.p);
+            });
         else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, f, pl.g, pl.p);
         break;
     case PwVariant::Xpose:

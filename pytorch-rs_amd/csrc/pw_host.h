@@ -40,6 +40,7 @@ struct PwPlan {
     // walks (g.rows = g.groups * walk).
     uint32_t trans = 0, held = 0, once = 0, xbc = 0;
     int walk = 1;
+    bool r2 = false;  // Rows: rank 2 and fewer than 2^32 tiles (the compile-time fast case)
     int nin = 0;
     int block = 256;  // lanes per block (kFlatBlock for the flat variants)
     int64_t grid = 0;
@@ -244,7 +245,10 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             plan->variant = PwVariant::Rows;
             plan->vec = vec && size[inner] % 4 == 0;
             g.rows = numel / size[inner];
-            g.chunks = (size[inner] + kRowChunk - 1) / kRowChunk;
+            const int64_t chunk = plan->vec ? kRowChunkVec : kRowChunk;
+            g.chunks = (size[inner] + chunk - 1) / chunk;
+            g.fdchunks = make_fast_div(g.chunks > (int64_t)UINT32_MAX ? 1u : (uint32_t)g.chunks);
+            plan->r2 = rank == 2 && g.rows * g.chunks <= (int64_t)UINT32_MAX;
             plan->grid = std::min<int64_t>(g.rows * g.chunks, want);
         }
         return TRS_OK;
