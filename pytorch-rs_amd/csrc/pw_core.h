@@ -85,7 +85,8 @@ struct PwGeom {
     uint32_t streamed;    // bit i set when input i is read once (no broadcast dim)
     int64_t rows;         // pw_rows / pw_xpose: number of outer index tuples
     int64_t chunks;       // pw_rows: column chunks per row; pw_xpose: tiles per outer tuple
-    FastDiv fdchunks;     // pw_rows: divides a tile index below 2^32 by chunks
+    FastDiv fdchunks;     // pw_rows / pw_xpose: divides a tile index below 2^32 by chunks
+    FastDiv fdttiles;     // pw_xpose: divides by ttiles
     int64_t ttiles;       // pw_xpose: tiles along tdim
     int64_t groups;       // pw_xpose: block groups G; a block walks outer tuples c, c+G, c+2G, ...
 };
@@ -458,15 +459,19 @@ constexpr int mask_rank() {  // set bits of M below bit I
 // geometry at run time; otherwise it is fixed at compile time.
 constexpr unsigned kRuntimeMask = 0xffffffffu;
 
+// RK = 3: the host planned a rank-3 launch of fewer than 2^32 tiles, compiled
+// with no run-time geometry branches and a direct offset for the one outer
+// dim; RK = 0: any launch, dispatched at run time.  Tile indices below 2^32
+// split into (tuple, t tile, x tile) by multiply-shift either way.
 template <class F, unsigned U8MASK, bool VEC, int WT, int WX, unsigned TRANS, unsigned HELD, unsigned ONCE, int NW,
-          unsigned STRM, unsigned XBC = kRuntimeMask>
+          unsigned STRM, unsigned XBC = kRuntimeMask, int RK = 0>
 __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
     constexpr int NIN1 = NIN > 0 ? NIN : 1;
     constexpr int NOUT = nout_of<F>();
     constexpr int NH = __builtin_popcount(HELD);
     constexpr int BT = 32 * WT, BX = 32 * WX;
-    const int xd = g.rank - 1, td = g.tdim;
+    const int xd = RK == 3 ? 2 : g.rank - 1, td = g.tdim;
     const int64_t xs = g.size[xd], ts = g.size[td];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t ntiles = g.groups * g.chunks;
@@ -481,7 +486,12 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
     auto decode = [&](int64_t o, int64_t &oo, int64_t *io) {
         oo = g.ooff;
         for (int i = 0; i < NIN; i++) io[i] = g.ioff[i];
-        if (!g.wide && o < 0x100000000LL) {
+        if constexpr (RK == 3) {
+            // the one outer dim is the dim of 0 and 1 that is not t
+            const int wd = td == 0 ? 1 : 0;
+            oo += o * g.ostride[wd];
+            for (int i = 0; i < NIN; i++) io[i] += o * g.istride[i][wd];
+        } else if (!g.wide && o < 0x100000000LL) {
             uint32_t rem = (uint32_t)o;
             for (int d = xd - 1; d >= 0; d--) {
                 if (d == td) continue;
@@ -502,10 +512,23 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
             }
         }
     };
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t c = tile / g.chunks;
-        const int64_t rest = tile - c * g.chunks;
-        const int64_t t0 = (rest % g.ttiles) * BT, x0 = (rest / g.ttiles) * BX;
+    const bool small = RK == 3 || ntiles <= 0xFFFFFFFFll;
+    auto do_tile = [&](int64_t tile) {
+        int64_t c, tt, xt;
+        if (small) {
+            const uint32_t q = fast_div((uint32_t)tile, g.fdchunks);
+            const uint32_t rest = (uint32_t)tile - q * g.fdchunks.div;
+            const uint32_t q2 = fast_div(rest, g.fdttiles);
+            c = q;
+            xt = q2;
+            tt = rest - q2 * g.fdttiles.div;
+        } else {
+            c = tile / g.chunks;
+            const int64_t rest = tile - c * g.chunks;
+            tt = rest % g.ttiles;
+            xt = rest / g.ttiles;
+        }
+        const int64_t t0 = tt * BT, x0 = xt * BX;
         const int64_t t = t0 + (wave % WT) * 32 + 4 * (lane & 7);
         const int64_t x = x0 + (wave / WT) * 32 + 4 * (lane >> 3);
         // Per-operand lane offset within an outer tuple and the step between
@@ -627,14 +650,21 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
             }
         };
         const bool fast = VEC && t0 + BT <= ts && x0 + BX <= xs;
-        if (g.rank == 3) {
+        if (RK == 3 || g.rank == 3) {
             if (fast) run.template operator()<true, true>();
             else run.template operator()<false, true>();
         } else {
-            if (fast) run.template operator()<true, false>();
-            else run.template operator()<false, false>();
+            if constexpr (RK != 3) {
+                if (fast) run.template operator()<true, false>();
+                else run.template operator()<false, false>();
+            }
         }
-    }
+    };
+    // The first tile runs outside the loop: a block with one tile ends
+    // without waiting at the loop's back edge for its own stores.
+    if ((int64_t)blockIdx.x >= ntiles) return;
+    do_tile(blockIdx.x);
+    for (int64_t tile = (int64_t)blockIdx.x + gridDim.x; tile < ntiles; tile += gridDim.x) do_tile(tile);
 }
 
 // ---- pw_generic -----------------------------------------------------------

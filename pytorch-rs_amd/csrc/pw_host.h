@@ -41,6 +41,7 @@ struct PwPlan {
     uint32_t trans = 0, held = 0, once = 0, xbc = 0;
     int walk = 1;
     bool r2 = false;  // Rows: rank 2 and fewer than 2^32 tiles (the compile-time fast case)
+    bool r3 = false;  // Xpose: rank 3 and fewer than 2^32 tiles (likewise)
     int nin = 0;
     int block = 256;  // lanes per block (kFlatBlock for the flat variants)
     int64_t grid = 0;
@@ -311,6 +312,10 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             g.ttiles = (size[tdim] + kXposeBT - 1) / kXposeBT;
             const int64_t xtiles = (size[inner] + kXposeBX - 1) / kXposeBX;
             g.chunks = g.ttiles * xtiles;
+            const bool small = g.groups * g.chunks <= (int64_t)UINT32_MAX;
+            g.fdchunks = make_fast_div(small ? (uint32_t)g.chunks : 1u);
+            g.fdttiles = make_fast_div(small ? (uint32_t)g.ttiles : 1u);
+            plan->r3 = rank == 3 && small;
             plan->grid = std::min<int64_t>(g.groups * g.chunks, want);
             return TRS_OK;
         }
