@@ -403,11 +403,14 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
                                  kFlatBlock, fn);
     case PwVariant::Rows:
         if (!pl.vec) return get_function(&prog->base, dev, "trs_fused_rows_s", fn);
-        std::snprintf(name, sizeof name, "trs_fused_rows_v%d_%u", pl.r2 ? 2 : 0, strm);
+    {
+        const int rk = pl.r2 ? 2 : pl.r3 ? 3 : 0;
+        std::snprintf(name, sizeof name, "trs_fused_rows_v%d_%u", rk, strm);
         return get_spec_function(prog, dev, name,
                                  "trs::pw_rows_body<TrsFused, " + mask + ", true, " + std::to_string(strm) + "u, " +
-                                     (pl.r2 ? "2" : "0") + ">",
+                                     std::to_string(rk) + ">",
                                  256, fn);
+    }
     case PwVariant::Xpose: {
         std::snprintf(name, sizeof name, "trs_fused_xpose_%c%d_%u_%u_%u_%u_%d_%u", pl.vec ? 'v' : 's', pl.r3 ? 3 : 0,
                       pl.trans, pl.held, pl.once, pl.xbc, pl.walk, strm);

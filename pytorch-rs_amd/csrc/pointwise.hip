@@ -136,6 +136,7 @@ int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
         if (pl.vec)
             with_mask<NIN>(sm, [&]<unsigned S>() {
                 if (pl.r2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, f, pl.g, pl.p);
+                else if (pl.r3) hipLaunchKernelGGL((k_rows<F, M, true, S, 3>), grid, block, 0, s, f, pl.g, pl.p);
                 else hipLaunchKernelGGL((k_rows<F, M, true, S, 0>), grid, block, 0, s, f, pl.g, pl.p);
             });
         else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, f, pl.g, pl.p);

@@ -69,6 +69,12 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &d) {
     return (uint32_t)(((uint64_t)t + n) >> d.shift);
 }
 
+// Element offsets: 32-bit where the host planned every offset of a launch
+// below 2^32 (strides are non-negative, so no partial sum of an in-range
+// offset wraps), else 64-bit.
+template <bool O32> struct OffsetT { using type = int64_t; };
+template <> struct OffsetT<true> { using type = uint32_t; };
+
 struct PwGeom {
     int32_t rank;   // >= 1 after normalisation
     int32_t tdim;   // pw_xpose: dim along which transposed operands are unit-stride
@@ -221,8 +227,13 @@ __device__ __forceinline__ void decode_outer(const PwGeom &g, int ndims, int64_t
     oo = g.ooff;
     for (int i = 0; i < NIN; i++) io[i] = g.ioff[i];
     if (!g.wide && outer < 0x100000000LL) {
+        // Unrolled over every possible dim so each geometry field has a
+        // constant index (loads the compiler can issue up front); dims at or
+        // above ndims are skipped by a uniform branch.
         uint32_t rem = (uint32_t)outer;
-        for (int d = ndims - 1; d >= 0; d--) {
+#pragma unroll
+        for (int d = kMaxRank - 2; d >= 0; d--) {
+            if (d >= ndims) continue;
             uint32_t q = fast_div(rem, g.fd[d]);
             uint32_t c = rem - q * g.fd[d].div;
             rem = q;
@@ -339,17 +350,23 @@ __device__ __forceinline__ void pw_flat_contig_body(const F &f, const PwGeom &g,
 // [4096, 4096] measured 5% slower than a plain copy of the same shape, with
 // two it is within 1%.
 // STRM: as for pw_flat.
-// R2: rank 2, so the row is the one outer dim and every geometry field the
-// tile needs has a constant index (no decode loop).  SMALL: fewer than 2^32
-// tiles, so a tile index splits into (row, chunk) by multiply-shift instead
-// of a 64-bit division.  Both ran before the first load of every block, as
-// chains of dependent scalar loads and branches, and together cost about 5%
-// of a [4096, 4096] launch.
-template <class F, unsigned U8MASK, bool VEC, unsigned STRM, bool R2, bool SMALL>
+// RANK = 2 or 3: the rank is fixed, so every geometry field the tile needs
+// has a constant index (no decode loop): the row is the one outer dim (rank
+// 2), or splits into its two outer indices by one multiply-shift (rank 3).
+// RANK = 0: any rank, through decode_outer.  O32 (RANK 2 or 3): every element
+// offset of the launch is below 2^32, so the row's offsets are 32-bit
+// products.  SMALL: fewer than 2^32 tiles, so a tile index splits into (row,
+// chunk) by multiply-shift instead of a 64-bit division.  All of this runs
+// before the first load of every block: the decode loop's dependent scalar
+// loads cost about 5% of a [4096, 4096] launch, and on a [64, 512, 1024] one
+// whose blocks each write one 4 KiB row, the decode loop took half the time
+// and 64-bit stride products a further sixth.
+template <class F, unsigned U8MASK, bool VEC, unsigned STRM, int RANK, bool O32, bool SMALL>
 __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const PwPtrs &p) {
+    static_assert(!O32 || RANK == 2 || RANK == 3, "32-bit offsets need a fixed rank");
     constexpr int NIN = F::NIN;
     constexpr int NOUT = nout_of<F>();
-    const int inner = R2 ? 1 : g.rank - 1;
+    const int inner = RANK == 2 ? 1 : RANK == 3 ? 2 : g.rank - 1;
     const int64_t cols = g.size[inner];
     const int64_t ntiles = g.rows * g.chunks;
     bool unit[NIN > 0 ? NIN : 1];
@@ -360,14 +377,38 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
     // next tile's loads reuse the registers the stores read).
     auto do_tile = [&](int64_t tile) {
         // Wave-uniform decode of the outer tuple (held in scalar registers).
-        int64_t row;
-        if constexpr (SMALL) row = fast_div((uint32_t)tile, g.fdchunks);
-        else row = tile / g.chunks;
-        const int64_t chunk = tile - row * g.chunks;
+        int64_t row, chunk;
+        if constexpr (SMALL) {
+            const uint32_t r = fast_div((uint32_t)tile, g.fdchunks);
+            row = r;
+            chunk = (uint32_t)tile - r * g.fdchunks.div;
+        } else {
+            row = tile / g.chunks;
+            chunk = tile - row * g.chunks;
+        }
         int64_t oo, io[NIN > 0 ? NIN : 1];
-        if constexpr (R2) {
+        if constexpr (RANK == 2 && O32) {
+            // every offset < 2^32 and every term non-negative: no partial
+            // sum wraps in 32 bits
+            const uint32_t r = (uint32_t)row;
+            oo = (uint32_t)g.ooff + r * (uint32_t)g.ostride[0];
+            for (int i = 0; i < NIN; i++) io[i] = (uint32_t)g.ioff[i] + r * (uint32_t)g.istride[i][0];
+        } else if constexpr (RANK == 2) {
             oo = g.ooff + row * g.ostride[0];
             for (int i = 0; i < NIN; i++) io[i] = g.ioff[i] + row * g.istride[i][0];
+        } else if constexpr (RANK == 3) {
+            // row < 2^32 (SMALL): row = w * size[1] + t
+            const uint32_t w = fast_div((uint32_t)row, g.fd[1]);
+            const uint32_t t = (uint32_t)row - w * g.fd[1].div;
+            if constexpr (O32) {
+                oo = (uint32_t)g.ooff + w * (uint32_t)g.ostride[0] + t * (uint32_t)g.ostride[1];
+                for (int i = 0; i < NIN; i++)
+                    io[i] = (uint32_t)g.ioff[i] + w * (uint32_t)g.istride[i][0] + t * (uint32_t)g.istride[i][1];
+            } else {
+                oo = g.ooff + (int64_t)w * g.ostride[0] + (int64_t)t * g.ostride[1];
+                for (int i = 0; i < NIN; i++)
+                    io[i] = g.ioff[i] + (int64_t)w * g.istride[i][0] + (int64_t)t * g.istride[i][1];
+            }
         } else {
             decode_outer<NIN>(g, inner, row, oo, io);
         }
@@ -417,17 +458,19 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
     for (int64_t tile = (int64_t)blockIdx.x + gridDim.x; tile < ntiles; tile += gridDim.x) do_tile(tile);
 }
 
-// RK = 2: the host planned a rank-2 launch of fewer than 2^32 tiles (the
-// common case, compiled with no run-time geometry branches); RK = 0: any
-// rows launch, dispatched at run time.
+// RK = 2 or 3: the host planned a launch of that rank, fewer than 2^32 tiles
+// and every element offset below 2^32 (the common cases, compiled with no
+// run-time geometry branches and 32-bit offsets); RK = 0: any rows launch,
+// dispatched at run time with 64-bit offsets.
 template <class F, unsigned U8MASK, bool VEC, unsigned STRM = 0u, int RK = 0>
 __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const PwPtrs &p) {
-    if constexpr (RK == 2) {
-        pw_rows_loop<F, U8MASK, VEC, STRM, true, true>(f, g, p);
+    if constexpr (RK == 2 || RK == 3) {
+        pw_rows_loop<F, U8MASK, VEC, STRM, RK, true, true>(f, g, p);
     } else {
-        if (g.rows * g.chunks > 0xFFFFFFFFll) pw_rows_loop<F, U8MASK, VEC, STRM, false, false>(f, g, p);
-        else if (g.rank == 2) pw_rows_loop<F, U8MASK, VEC, STRM, true, true>(f, g, p);
-        else pw_rows_loop<F, U8MASK, VEC, STRM, false, true>(f, g, p);
+        if (g.rows * g.chunks > 0xFFFFFFFFll) pw_rows_loop<F, U8MASK, VEC, STRM, 0, false, false>(f, g, p);
+        else if (g.rank == 2) pw_rows_loop<F, U8MASK, VEC, STRM, 2, false, true>(f, g, p);
+        else if (g.rank == 3) pw_rows_loop<F, U8MASK, VEC, STRM, 3, false, true>(f, g, p);
+        else pw_rows_loop<F, U8MASK, VEC, STRM, 0, false, true>(f, g, p);
     }
 }
 
@@ -459,10 +502,11 @@ constexpr int mask_rank() {  // set bits of M below bit I
 // geometry at run time; otherwise it is fixed at compile time.
 constexpr unsigned kRuntimeMask = 0xffffffffu;
 
-// RK = 3: the host planned a rank-3 launch of fewer than 2^32 tiles, compiled
-// with no run-time geometry branches and a direct offset for the one outer
-// dim; RK = 0: any launch, dispatched at run time.  Tile indices below 2^32
-// split into (tuple, t tile, x tile) by multiply-shift either way.
+// RK = 3: the host planned a rank-3 launch of fewer than 2^32 tiles and every
+// element offset below 2^32, compiled with no run-time geometry branches, a
+// direct offset for the one outer dim and 32-bit offsets; RK = 0: any launch,
+// dispatched at run time with 64-bit offsets.  Tile indices below 2^32 split
+// into (tuple, t tile, x tile) by multiply-shift either way.
 template <class F, unsigned U8MASK, bool VEC, int WT, int WX, unsigned TRANS, unsigned HELD, unsigned ONCE, int NW,
           unsigned STRM, unsigned XBC = kRuntimeMask, int RK = 0>
 __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const PwPtrs &p) {
@@ -471,6 +515,7 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
     constexpr int NOUT = nout_of<F>();
     constexpr int NH = __builtin_popcount(HELD);
     constexpr int BT = 32 * WT, BX = 32 * WX;
+    using Off = typename OffsetT<RK == 3>::type;
     const int xd = RK == 3 ? 2 : g.rank - 1, td = g.tdim;
     const int64_t xs = g.size[xd], ts = g.size[td];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -483,14 +528,14 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
     };
     // Offsets of outer tuple `o`: a wave-uniform decode over the dims other
     // than t and x (32-bit magic-number division when o fits).
-    auto decode = [&](int64_t o, int64_t &oo, int64_t *io) {
-        oo = g.ooff;
-        for (int i = 0; i < NIN; i++) io[i] = g.ioff[i];
+    auto decode = [&](int64_t o, Off &oo, Off *io) {
+        oo = (Off)g.ooff;
+        for (int i = 0; i < NIN; i++) io[i] = (Off)g.ioff[i];
         if constexpr (RK == 3) {
             // the one outer dim is the dim of 0 and 1 that is not t
             const int wd = td == 0 ? 1 : 0;
-            oo += o * g.ostride[wd];
-            for (int i = 0; i < NIN; i++) io[i] += o * g.istride[i][wd];
+            oo += (Off)o * (Off)g.ostride[wd];
+            for (int i = 0; i < NIN; i++) io[i] += (Off)o * (Off)g.istride[i][wd];
         } else if (!g.wide && o < 0x100000000LL) {
             uint32_t rem = (uint32_t)o;
             for (int d = xd - 1; d >= 0; d--) {
@@ -534,17 +579,19 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
         // Per-operand lane offset within an outer tuple and the step between
         // its four vectors: along x for TRANS operands (each vector runs along
         // t), along t for the others (each vector runs along x).
-        int64_t loff[NIN1], lstep[NIN1];
+        // (A lane past the tensor's edge forms offsets past its end, which
+        // may wrap in 32 bits; the edge path never loads or stores them.)
+        Off loff[NIN1], lstep[NIN1];
         static_for<NIN>([&]<int I>() {
             if constexpr ((TRANS >> I) & 1u) {
-                loff[I] = x * g.istride[I][xd] + t;
-                lstep[I] = g.istride[I][xd];
+                loff[I] = (Off)x * (Off)g.istride[I][xd] + (Off)t;
+                lstep[I] = (Off)g.istride[I][xd];
             } else {
-                loff[I] = t * g.istride[I][td] + (unit_x.template operator()<I>() ? x : 0);
-                lstep[I] = g.istride[I][td];
+                loff[I] = (Off)t * (Off)g.istride[I][td] + (unit_x.template operator()<I>() ? (Off)x : (Off)0);
+                lstep[I] = (Off)g.istride[I][td];
             }
         });
-        const int64_t ooff_lane = t * g.ostride[td] + x;
+        const Off ooff_lane = (Off)t * (Off)g.ostride[td] + (Off)x;
         // The block runs its whole tile with 16-byte vectors when the tile
         // is interior and the operands aligned (a wave-uniform test), else
         // every access is scalar and bounds-checked.
@@ -556,38 +603,38 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
             // a register array indexed at run time is moved to LDS or
             // scratch by the compiler (this cost a fifth of the transposed
             // copy's time).
-            auto load_block = [&]<int I, int NV>(int64_t b, float (&raw)[4][4]) {
-                const int64_t base = b + loff[I];
+            auto load_block = [&]<int I, int NV>(Off b, float (&raw)[4][4]) {
+                const Off base = b + loff[I];
                 constexpr bool tr = ((TRANS >> I) & 1u) != 0;
                 const bool unit = tr || unit_x.template operator()<I>();
                 if constexpr (FAST) {
                     constexpr bool stream = ((HELD >> I) & 1u) == 0u && ((STRM >> I) & 1u) != 0u;
 #pragma unroll
-                    for (int j = 0; j < NV; j++) ld4<U8MASK, I, stream>(p, base + j * lstep[I], unit, raw[j]);
+                    for (int j = 0; j < NV; j++) ld4<U8MASK, I, stream>(p, base + (Off)j * lstep[I], unit, raw[j]);
                 } else {
 #pragma unroll
                     for (int j = 0; j < NV; j++)
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
                             const bool in = tr ? (t + e < ts && x + j < xs) : (t + j < ts && x + e < xs);
-                            raw[j][e] = in ? ld1<U8MASK, I>(p, base + j * lstep[I] + (unit ? e : 0)) : 0.0f;
+                            raw[j][e] = in ? ld1<U8MASK, I>(p, base + (Off)j * lstep[I] + (unit ? (Off)e : (Off)0)) : 0.0f;
                         }
                 }
             };
             float held[NH > 0 ? NH : 1][4][4];
             static_for<NIN>([&]<int I>() {
-                if constexpr ((HELD >> I) & 1u) load_block.template operator()<I, 4>(g.ioff[I], held[mask_rank<HELD, I>()]);
+                if constexpr ((HELD >> I) & 1u) load_block.template operator()<I, 4>((Off)g.ioff[I], held[mask_rank<HELD, I>()]);
             });
             // One outer tuple's loads (all operands but HELD) into `dst`.
-            auto loads = [&](const int64_t *io, float (&dst)[NIN1][4][4]) {
+            auto loads = [&](const Off *io, float (&dst)[NIN1][4][4]) {
                 static_for<NIN>([&]<int I>() {
                     if constexpr (!((HELD >> I) & 1u))
                         load_block.template operator()<I, ((ONCE >> I) & 1u) ? 1 : 4>(io[I], dst[I]);
                 });
             };
             // Compute and store one outer tuple from its loaded values.
-            auto compute = [&](const float (&v)[NIN1][4][4], int64_t oo) {
-                const int64_t ob0 = oo + ooff_lane;
+            auto compute = [&](const float (&v)[NIN1][4][4], Off oo) {
+                const Off ob0 = oo + ooff_lane;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     // Element (t+k, x+i), one functor call per element with
@@ -617,7 +664,7 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
 #pragma unroll
                         for (int q = 0; q < NOUT; q++) r[q][i] = o[q];
                     }
-                    const int64_t ob = ob0 + k * g.ostride[td];
+                    const Off ob = ob0 + (Off)k * (Off)g.ostride[td];
                     if constexpr (FAST) {
                         store4(p, ob, r);
                     } else if (t + k < ts) {
@@ -626,7 +673,7 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
                             if (x + i < xs) {
                                 float ov[NOUT];
                                 for (int q = 0; q < NOUT; q++) ov[q] = r[q][i];
-                                store1<NOUT>(p, ob + i, ov);
+                                store1<NOUT>(p, ob + (Off)i, ov);
                             }
                         }
                     }
@@ -635,13 +682,13 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
             // Tuple offsets: with one outer dim (rank 3) tuple o + groups is
             // tuple o advanced by constant per-operand steps; otherwise each
             // tuple is decoded.
-            int64_t dstep[NIN1], ostep = 0;
+            Off dstep[NIN1], ostep = 0;
             if constexpr (ONE_OUTER) {
                 const int wd = (td == 0) ? 1 : 0;
-                for (int i = 0; i < NIN; i++) dstep[i] = g.groups * g.istride[i][wd];
-                ostep = g.groups * g.ostride[wd];
+                for (int i = 0; i < NIN; i++) dstep[i] = (Off)g.groups * (Off)g.istride[i][wd];
+                ostep = (Off)g.groups * (Off)g.ostride[wd];
             }
-            int64_t io[NIN1], oo = 0;
+            Off io[NIN1], oo = 0;
             // Exactly NW tuples per block (the host sets g.rows = g.groups *
             // NW).  The walk is unrolled at compile time: tuple s+1's loads
             // are issued before tuple s computes and stores, with no branch
@@ -658,7 +705,7 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
                     for (int j = 0; j < 4; j++)
 #pragma unroll
                         for (int e = 0; e < 4; e++) v[i][j][e] = nv[i][j][e];
-                const int64_t ocur = oo;
+                const Off ocur = oo;
                 if (s + 1 < NW) {
                     if constexpr (ONE_OUTER) {
                         oo += ostep;

@@ -40,8 +40,10 @@ struct PwPlan {
     // walks (g.rows = g.groups * walk).
     uint32_t trans = 0, held = 0, once = 0, xbc = 0;
     int walk = 1;
-    bool r2 = false;  // Rows: rank 2 and fewer than 2^32 tiles (the compile-time fast case)
-    bool r3 = false;  // Xpose: rank 3 and fewer than 2^32 tiles (likewise)
+    // Rank 2 (r2, Rows only) or 3 (r3, Rows or Xpose), fewer than 2^32 tiles
+    // and every element offset below 2^32: the compile-time fast cases.
+    bool r2 = false;
+    bool r3 = false;
     int nin = 0;
     int block = 256;  // lanes per block (kFlatBlock for the flat variants)
     int64_t grid = 0;
@@ -224,6 +226,18 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         for (int o = 1; o < nout; o++) ok = ok && aligned(more[o - 1], lo->offset, os, inner, 4);
         return ok;
     };
+    // Every element offset the launch forms is below 2^32: strides are
+    // non-negative, so the largest is offset + sum (size - 1) * stride.
+    auto offsets_fit32 = [&]() {
+        auto last = [&](int64_t off, const int64_t *st) {
+            for (int d = 0; d < rank; d++) off += (size[d] - 1) * st[d];
+            return off;
+        };
+        if (last(g.ooff, os) > (int64_t)UINT32_MAX) return false;
+        for (int i = 0; i < nin; i++)
+            if (last(g.ioff[i], is[i]) > (int64_t)UINT32_MAX) return false;
+        return true;
+    };
     bool unit_or_bcast = os[inner] == 1;
     for (int i = 0; i < nin; i++) unit_or_bcast &= is[i][inner] == 0 || is[i][inner] == 1;
     (void)cu_count;
@@ -249,7 +263,9 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             const int64_t chunk = plan->vec ? kRowChunkVec : kRowChunk;
             g.chunks = (size[inner] + chunk - 1) / chunk;
             g.fdchunks = make_fast_div(g.chunks > (int64_t)UINT32_MAX ? 1u : (uint32_t)g.chunks);
-            plan->r2 = rank == 2 && g.rows * g.chunks <= (int64_t)UINT32_MAX;
+            const bool fast = g.rows * g.chunks <= (int64_t)UINT32_MAX && offsets_fit32();
+            plan->r2 = rank == 2 && fast;
+            plan->r3 = rank == 3 && fast;
             plan->grid = std::min<int64_t>(g.rows * g.chunks, want);
         }
         return TRS_OK;
@@ -315,7 +331,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             const bool small = g.groups * g.chunks <= (int64_t)UINT32_MAX;
             g.fdchunks = make_fast_div(small ? (uint32_t)g.chunks : 1u);
             g.fdttiles = make_fast_div(small ? (uint32_t)g.ttiles : 1u);
-            plan->r3 = rank == 3 && small;
+            plan->r3 = rank == 3 && small && offsets_fit32();
             plan->grid = std::min<int64_t>(g.groups * g.chunks, want);
             return TRS_OK;
         }

@@ -84,6 +84,59 @@ def test_flat_kernels_beyond_two_to_the_32_elements():
     check(abi.lib.trs_empty_cache())  # hand the 32 GiB back to HIP for the tests that follow
 
 
+def _put(big, off, arr):
+    """Copy `arr` into the allocation `big` at element offset `off`."""
+    arr = np.ascontiguousarray(arr, dtype=np.float32)
+    check(abi.lib.trs_memcpy_h2d(ctypes.c_void_p(big.addr + off * 4), arr.ctypes.data, arr.nbytes))
+
+
+def _get(big, off, n):
+    out = np.empty(n, dtype=np.float32)
+    check(abi.lib.trs_memcpy_d2h(out.ctypes.data, ctypes.c_void_p(big.addr + off * 4), n * 4))
+    return out
+
+
+def test_row_and_transposing_layouts_on_both_sides_of_two_to_the_32_element_offsets():
+    """Rank-2 and rank-3 row launches and the rank-3 transposing one are
+    compiled with 32-bit offsets when every element offset of the launch is
+    below 2^32, else they take the run-time path with 64-bit offsets.  Each
+    layout runs with its views ending exactly at element 2^32 - 1 of one
+    allocation (32-bit) and again past 2^32 (64-bit), bit-exact against the
+    oracle on the same values."""
+    two32 = 1 << 32
+    big = DeviceArray((two32 + (1 << 22)) * 4)
+    rng = np.random.default_rng(77)
+    # (name, op, left (shape, strides), right (shape, strides), output shape):
+    # the left operand and the output live in `big`, the right one apart.
+    cases = [
+        ("rows rank 2", O.ADD, ((300, 2112), None), ((2112,), None), (300, 2112)),
+        ("rows rank 3", O.MUL, ((8, 1, 1024), None), ((96, 1024), None), (8, 96, 1024)),
+        ("transposed rank 3", O.SUB, ((8, 192, 320), (320 * 192, 1, 192)), ((8, 192, 320), None), (8, 192, 320)),
+    ]
+    for name, op, (lsh, lst), (rsh, rst), osh in cases:
+        lst = lst or O.contiguous_strides(lsh)
+        rst = rst or O.contiguous_strides(rsh)
+        ln = O.storage_size(lsh, lst)
+        on = int(np.prod(osh))
+        l = rng.standard_normal(ln).astype(np.float32)
+        r = rng.standard_normal(O.storage_size(rsh, rst)).astype(np.float32)
+        ostr = O.contiguous_strides(osh)
+        want = O.binary(op, l, lsh, lst, 0, r, rsh, rst, 0, osh, ostr)
+        dr = DeviceArray.from_numpy(r)
+        # output ending at element 2^32 - 1, left operand just below it; then
+        # both past 2^32
+        for loff, ooff in [(two32 - on - ln - 64, two32 - on), (two32 + 64, two32 + ln + 128)]:
+            _put(big, loff, l)
+            check(abi.lib.trs_binary_f32(op, big.ptr, ctypes.byref(layout_of(lsh, lst, loff)), dr.ptr,
+                                         ctypes.byref(layout_of(rsh, rst)), big.ptr,
+                                         ctypes.byref(layout_of(osh, ostr, ooff))))
+            got = _get(big, ooff, on)
+            assert np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32)), (name, ooff)
+        del dr
+    del big
+    check(abi.lib.trs_empty_cache())
+
+
 def test_outputs_may_alias_inputs_only_as_the_same_view():
     """In place is allowed element for element; any other overlap with an
     input (shifted, transposed, broadcast) or with a matmul operand is
