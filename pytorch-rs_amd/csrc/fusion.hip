@@ -194,7 +194,7 @@ int generate(const std::string &ir, Program *prog) {
     const std::string mask = std::to_string(u8mask) + "u";
     auto wrap = [&](const char *name, const std::string &body, const char *lanes = "256") {
         s << "extern \"C\" __global__ void __launch_bounds__(" << lanes << ") " << name
-          << "(trs::PwGeom g, trs::PwPtrs p) { " << body << "(TrsFused{}, g, p); }\n";
+          << "(trs::PwGeom, trs::PwPtrs p) { " << body << "(TrsFused{}, trs::kernarg_geom(), p); }\n";
     };
     // Compiled with the program: the variants that need no launch-time
     // specialisation.  Vector flat/rows kernels (specialised on the inputs
@@ -378,7 +378,7 @@ int get_spec_function(Program *prog, DeviceState *dev, const std::string &name, 
         if (it == prog->specs.end()) {
             std::ostringstream w;
             w << prog->functor << "extern \"C\" __global__ void __launch_bounds__(" << lanes << ") " << name
-              << "(trs::PwGeom g, trs::PwPtrs p) { " << body << "(TrsFused{}, g, p); }\n";
+              << "(trs::PwGeom, trs::PwPtrs p) { " << body << "(TrsFused{}, trs::kernarg_geom(), p); }\n";
             auto spec = std::make_unique<CodeObject>();
             const int rc = compile_source(w.str(), spec.get(), nullptr, nullptr);
             if (rc) return rc;

@@ -85,20 +85,26 @@ struct ReluBackwardF {
 // ---- AOT wrappers -----------------------------------------------------------
 // S: inputs read once (loaded non-temporally), a compile-time mask.
 
+// The geometry is every wrapper's first argument: the bodies read it in place
+// (kernarg_geom); the functor, which may carry a scalar, comes last.
 template <class F, unsigned M, bool V, unsigned S>
-__global__ void __launch_bounds__(kFlatBlock) k_flat(F f, PwGeom g, PwPtrs p) { pw_flat_body<F, M, V, S>(f, g, p); }
+__global__ void __launch_bounds__(kFlatBlock) k_flat(PwGeom, PwPtrs p, F f) {
+    pw_flat_body<F, M, V, S>(f, kernarg_geom(), p);
+}
 template <class F, unsigned M>
-__global__ void __launch_bounds__(kFlatBlock) k_flat_contig(F f, PwGeom g, PwPtrs p) {
-    pw_flat_contig_body<F, M>(f, g, p);
+__global__ void __launch_bounds__(kFlatBlock) k_flat_contig(PwGeom, PwPtrs p, F f) {
+    pw_flat_contig_body<F, M>(f, kernarg_geom(), p);
 }
 template <class F, unsigned M, bool V, unsigned S, int RK = 0>
-__global__ void __launch_bounds__(256) k_rows(F f, PwGeom g, PwPtrs p) { pw_rows_body<F, M, V, S, RK>(f, g, p); }
+__global__ void __launch_bounds__(256) k_rows(PwGeom, PwPtrs p, F f) {
+    pw_rows_body<F, M, V, S, RK>(f, kernarg_geom(), p);
+}
 template <class F, unsigned M, bool V, unsigned TR, unsigned S>
-__global__ void __launch_bounds__(64 * kXposeWT * kXposeWX) k_xpose(F f, PwGeom g, PwPtrs p) {
-    pw_xpose_body<F, M, V, kXposeWT, kXposeWX, TR, 0u, 0u, 1, S>(f, g, p);
+__global__ void __launch_bounds__(64 * kXposeWT * kXposeWX) k_xpose(PwGeom, PwPtrs p, F f) {
+    pw_xpose_body<F, M, V, kXposeWT, kXposeWX, TR, 0u, 0u, 1, S>(f, kernarg_geom(), p);
 }
 template <class F, unsigned M>
-__global__ void __launch_bounds__(256) k_generic(F f, PwGeom g, PwPtrs p) { pw_generic_body<F, M>(f, g, p); }
+__global__ void __launch_bounds__(256) k_generic(PwGeom, PwPtrs p, F f) { pw_generic_body<F, M>(f, kernarg_geom(), p); }
 
 // Calls fn.template operator()<K>() with K the compile-time value of the
 // run-time mask `m` over NIN bits (NIN is 1 or 2 here).
@@ -127,19 +133,19 @@ int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
     case PwVariant::Empty:
         return TRS_OK;
     case PwVariant::Flat:
-        if (pl.contig) hipLaunchKernelGGL((k_flat_contig<F, M>), grid, block, 0, s, f, pl.g, pl.p);
+        if (pl.contig) hipLaunchKernelGGL((k_flat_contig<F, M>), grid, block, 0, s, pl.g, pl.p, f);
         else if (pl.vec)
-            with_mask<NIN>(sm, [&]<unsigned S>() { hipLaunchKernelGGL((k_flat<F, M, true, S>), grid, block, 0, s, f, pl.g, pl.p); });
-        else hipLaunchKernelGGL((k_flat<F, M, false, 0u>), grid, block, 0, s, f, pl.g, pl.p);
+            with_mask<NIN>(sm, [&]<unsigned S>() { hipLaunchKernelGGL((k_flat<F, M, true, S>), grid, block, 0, s, pl.g, pl.p, f); });
+        else hipLaunchKernelGGL((k_flat<F, M, false, 0u>), grid, block, 0, s, pl.g, pl.p, f);
         break;
     case PwVariant::Rows:
         if (pl.vec)
             with_mask<NIN>(sm, [&]<unsigned S>() {
-                if (pl.r2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, f, pl.g, pl.p);
-                else if (pl.r3) hipLaunchKernelGGL((k_rows<F, M, true, S, 3>), grid, block, 0, s, f, pl.g, pl.p);
-                else hipLaunchKernelGGL((k_rows<F, M, true, S, 0>), grid, block, 0, s, f, pl.g, pl.p);
+                if (pl.r2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, pl.g, pl.p, f);
+                else if (pl.r3) hipLaunchKernelGGL((k_rows<F, M, true, S, 3>), grid, block, 0, s, pl.g, pl.p, f);
+                else hipLaunchKernelGGL((k_rows<F, M, true, S, 0>), grid, block, 0, s, pl.g, pl.p, f);
             });
-        else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, f, pl.g, pl.p);
+        else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, pl.g, pl.p, f);
         break;
     case PwVariant::Xpose:
         // One outer tuple per block (no roles): every transposed-operand mask.
@@ -147,14 +153,14 @@ int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
             if constexpr (TR != 0u) {
                 if (pl.vec)
                     with_mask<NIN>(sm, [&]<unsigned S>() {
-                        hipLaunchKernelGGL((k_xpose<F, M, true, TR, S>), grid, block, 0, s, f, pl.g, pl.p);
+                        hipLaunchKernelGGL((k_xpose<F, M, true, TR, S>), grid, block, 0, s, pl.g, pl.p, f);
                     });
-                else hipLaunchKernelGGL((k_xpose<F, M, false, TR, 0u>), grid, block, 0, s, f, pl.g, pl.p);
+                else hipLaunchKernelGGL((k_xpose<F, M, false, TR, 0u>), grid, block, 0, s, pl.g, pl.p, f);
             }
         });
         break;
     case PwVariant::Generic:
-        hipLaunchKernelGGL((k_generic<F, M>), grid, block, 0, s, f, pl.g, pl.p);
+        hipLaunchKernelGGL((k_generic<F, M>), grid, block, 0, s, pl.g, pl.p, f);
         break;
     }
     TRS_LAUNCH_CHECK("pointwise kernel launch");

@@ -79,7 +79,7 @@ struct PwGeom {
     int32_t rank;   // >= 1 after normalisation
     int32_t tdim;   // pw_xpose: dim along which transposed operands are unit-stride
     int32_t wide;   // a dim exceeds 32 bits: always decode with 64-bit division
-    int32_t pad0;
+    int32_t skew;   // pw_xpose: a tuple's tiles are taken in diagonal order (x tile += t tile)
     int64_t numel;
     int64_t size[kMaxRank];
     FastDiv fd[kMaxRank];
@@ -93,9 +93,21 @@ struct PwGeom {
     int64_t chunks;       // pw_rows: column chunks per row; pw_xpose: tiles per outer tuple
     FastDiv fdchunks;     // pw_rows / pw_xpose: divides a tile index below 2^32 by chunks
     FastDiv fdttiles;     // pw_xpose: divides by ttiles
+    FastDiv fdxtiles;     // pw_xpose: divides by the x tiles of a tuple (skewed order)
     int64_t ttiles;       // pw_xpose: tiles along tdim
     int64_t groups;       // pw_xpose: block groups G; a block walks outer tuples c, c+G, c+2G, ...
 };
+
+// The launch geometry, read in place in the kernel-argument segment: every
+// kernel of this engine takes its PwGeom as the first argument, at offset 0
+// of the segment.  Bound to the by-value parameter instead, the body's
+// reference made the compiler copy the parameter, and wherever the body
+// indexes the geometry at run time (dims chosen at run time) the copy stayed:
+// 936 bytes per lane written to scratch memory and read back, in the
+// transposing kernel's run-time-rank path, and SGPR spills elsewhere.
+__device__ __forceinline__ const PwGeom &kernarg_geom() {
+    return *(const PwGeom *)__builtin_amdgcn_kernarg_segment_ptr();
+}
 
 typedef float vf4 __attribute__((ext_vector_type(4)));
 typedef uint8_t vu8x4 __attribute__((ext_vector_type(4)));
@@ -492,7 +504,14 @@ __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const 
 //   ONCE operands (stride 0 along t) once per outer tuple,
 // and each tuple's loads are issued before the previous tuple's stores.
 // NW = 1 walks nothing (one tuple per block).  g.ttiles = t tiles,
-// g.chunks = t tiles * x tiles.
+// g.chunks = t tiles * x tiles.  Consecutive blocks take consecutive t tiles
+// of one x tile.  When a tuple has more tiles than the GPU holds at once
+// (g.skew), block (tt, xt) takes x tile (xt + tt) mod x tiles instead: in the
+// plain order the resident blocks then share a few x tiles, so their output
+// rows are written at the same few offsets within each row, which with a
+// large power-of-two row stride fall on the same memory channels.  x + y.mT
+// over [8192, 8192] measured 205 us plain and 141 us skewed (0.49 -> 0.71 of
+// HBM); a tuple of config 2's [64, 512, 1024] (4 x 16 tiles) gains nothing.
 template <unsigned M, int I>
 constexpr int mask_rank() {  // set bits of M below bit I
     return __builtin_popcount(M & ((1u << I) - 1u));
@@ -567,11 +586,16 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
             c = q;
             xt = q2;
             tt = rest - q2 * g.fdttiles.div;
+            if (g.skew) {  // xt + tt < xtiles * ttiles < 2^32
+                const uint32_t sk = q2 + (uint32_t)tt;
+                xt = sk - fast_div(sk, g.fdxtiles) * g.fdxtiles.div;
+            }
         } else {
             c = tile / g.chunks;
             const int64_t rest = tile - c * g.chunks;
             tt = rest % g.ttiles;
             xt = rest / g.ttiles;
+            if (g.skew) xt = (xt + tt) % (g.chunks / g.ttiles);
         }
         const int64_t t0 = tt * BT, x0 = xt * BX;
         const int64_t t = t0 + (wave % WT) * 32 + 4 * (lane & 7);

@@ -29,6 +29,7 @@ enum class PwVariant { Empty, Flat, Rows, Xpose, Generic };
 constexpr int kXposeWT = 4, kXposeWX = 2;
 constexpr int kXposeBT = 32 * kXposeWT, kXposeBX = 32 * kXposeWX;
 constexpr int kXposeWalk = 8;  // largest walk: 8, 4 or 2 tuples, dividing the tuple count
+constexpr int kXposeResident = 4;  // about the pw_xpose blocks (512 lanes) resident per CU
 
 struct PwPlan {
     PwVariant variant = PwVariant::Empty;
@@ -240,7 +241,6 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
     };
     bool unit_or_bcast = os[inner] == 1;
     for (int i = 0; i < nin; i++) unit_or_bcast &= is[i][inner] == 0 || is[i][inner] == 1;
-    (void)cu_count;
     const int64_t want = kMaxGrid;
 
     if (unit_or_bcast) {
@@ -331,6 +331,10 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             const bool small = g.groups * g.chunks <= (int64_t)UINT32_MAX;
             g.fdchunks = make_fast_div(small ? (uint32_t)g.chunks : 1u);
             g.fdttiles = make_fast_div(small ? (uint32_t)g.ttiles : 1u);
+            // Diagonal tile order when one tuple has more tiles than the GPU
+            // holds at once (about kXposeResident blocks per CU).
+            g.skew = xtiles > 1 && g.chunks > (int64_t)kXposeResident * cu_count;
+            g.fdxtiles = make_fast_div(small ? (uint32_t)xtiles : 1u);
             plan->r3 = rank == 3 && small && offsets_fit32();
             plan->grid = std::min<int64_t>(g.groups * g.chunks, want);
             return TRS_OK;

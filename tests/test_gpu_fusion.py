@@ -57,10 +57,12 @@ def test_fused_chain_matches_eager_bitwise_and_oracle_within_exp_bound(n):
     assert (err <= 2 * ulp_of(np.exp(t.astype(np.float64)).astype(np.float32))).all()
 
 
-def test_fused_broadcast_transposed_chain_bit_exact():
-    """(a + b) * c.mT on a mini config-3 shape: a [B,1,N], b [1,M,N], c [B,N,M]."""
-    rng = np.random.default_rng(2)
-    B, M, N = 4, 96, 160
+@pytest.mark.parametrize("B,M,N", [(4, 96, 160), (2, 4096, 4096), (2, 4100, 4099)])
+def test_fused_broadcast_transposed_chain_bit_exact(B, M, N):
+    """(a + b) * c.mT on a config-3-like shape: a [B,1,N], b [1,M,N], c [B,N,M].
+    The larger shapes have more tiles per batch than the GPU holds at once
+    (diagonal tile order), aligned and ragged."""
+    rng = np.random.default_rng(2 + M)
     a = rng.standard_normal(B * N).astype(np.float32)
     b = rng.standard_normal(M * N).astype(np.float32)
     c = rng.standard_normal(B * N * M).astype(np.float32)

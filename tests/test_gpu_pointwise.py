@@ -58,6 +58,9 @@ BINARY_CASES = {
     "permuted_3d": lambda rng: (_view(rng, (16, 32, 8), (1, 128, 16)), _view(rng, (16, 32, 8))),
     "empty": lambda rng: (_view(rng, (0, 5)), _view(rng, (5,))),
     "large_transposed_ragged": lambda rng: (_transposed(rng, (1000, 999)), _view(rng, (999, 1000))),
+    # more tiles in one tuple than the GPU holds at once: diagonal tile order
+    "skewed_transposed": lambda rng: (_view(rng, (4096, 4096)), _transposed(rng, (4096, 4096))),
+    "skewed_transposed_ragged": lambda rng: (_transposed(rng, (4099, 4100)), _view(rng, (4100, 4099))),
 }
 
 
