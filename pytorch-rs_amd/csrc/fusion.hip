@@ -404,7 +404,7 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
     case PwVariant::Rows:
         if (!pl.vec) return get_function(&prog->base, dev, "trs_fused_rows_s", fn);
     {
-        const int rk = pl.r2 ? 2 : pl.r3 ? 3 : 0;
+        const int rk = pl.rk;
         std::snprintf(name, sizeof name, "trs_fused_rows_v%d_%u", rk, strm);
         return get_spec_function(prog, dev, name,
                                  "trs::pw_rows_body<TrsFused, " + mask + ", true, " + std::to_string(strm) + "u, " +
@@ -412,12 +412,12 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
                                  256, fn);
     }
     case PwVariant::Xpose: {
-        std::snprintf(name, sizeof name, "trs_fused_xpose_%c%d_%u_%u_%u_%u_%d_%u", pl.vec ? 'v' : 's', pl.r3 ? 3 : 0,
+        std::snprintf(name, sizeof name, "trs_fused_xpose_%c%d_%u_%u_%u_%u_%d_%u", pl.vec ? 'v' : 's', pl.rk,
                       pl.trans, pl.held, pl.once, pl.xbc, pl.walk, strm);
         std::ostringstream b;
         b << "trs::pw_xpose_body<TrsFused, " << mask << ", " << (pl.vec ? "true" : "false") << ", " << kXposeWT << ", "
           << kXposeWX << ", " << pl.trans << "u, " << pl.held << "u, " << pl.once << "u, " << pl.walk << ", "
-          << (pl.vec ? strm : 0u) << "u, " << pl.xbc << "u, " << (pl.r3 ? 3 : 0) << ">";
+          << (pl.vec ? strm : 0u) << "u, " << pl.xbc << "u, " << pl.rk << ">";
         return get_spec_function(prog, dev, name, b.str(), 64 * kXposeWT * kXposeWX, fn);
     }
     case PwVariant::Generic: return get_function(&prog->base, dev, "trs_fused_generic", fn);
@@ -427,14 +427,13 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
 }
 
 // The kernel of a launch plan: looked up by the plan's signature (variant,
-// vector access, role masks, walk, streamed inputs, rank-2 rows, rank-3
-// transposes), resolved on a miss.
+// vector access, role masks, walk, streamed inputs, fixed rank), resolved on
+// a miss.
 int get_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunction_t *fn) {
     const uint64_t strm = pl.g.streamed & ((1u << prog->nin) - 1u);
     const uint64_t key = (uint64_t)pl.variant | (uint64_t)pl.vec << 3 | (uint64_t)pl.contig << 4 |
                          (uint64_t)pl.walk << 5 | strm << 9 | (uint64_t)pl.trans << 17 | (uint64_t)pl.held << 25 |
-                         (uint64_t)pl.once << 33 | (uint64_t)pl.xbc << 41 | (uint64_t)pl.r2 << 49 |
-                         (uint64_t)pl.r3 << 50;
+                         (uint64_t)pl.once << 33 | (uint64_t)pl.xbc << 41 | (uint64_t)pl.rk << 49;
     {
         std::lock_guard<std::mutex> lock(prog->spec_mu);
         auto it = prog->by_plan[dev->index].find(key);

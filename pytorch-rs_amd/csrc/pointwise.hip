@@ -141,8 +141,9 @@ int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
     case PwVariant::Rows:
         if (pl.vec)
             with_mask<NIN>(sm, [&]<unsigned S>() {
-                if (pl.r2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, pl.g, pl.p, f);
-                else if (pl.r3) hipLaunchKernelGGL((k_rows<F, M, true, S, 3>), grid, block, 0, s, pl.g, pl.p, f);
+                if (pl.rk == 2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, pl.g, pl.p, f);
+                else if (pl.rk == 3) hipLaunchKernelGGL((k_rows<F, M, true, S, 3>), grid, block, 0, s, pl.g, pl.p, f);
+                else if (pl.rk == 4) hipLaunchKernelGGL((k_rows<F, M, true, S, 4>), grid, block, 0, s, pl.g, pl.p, f);
                 else hipLaunchKernelGGL((k_rows<F, M, true, S, 0>), grid, block, 0, s, pl.g, pl.p, f);
             });
         else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, pl.g, pl.p, f);

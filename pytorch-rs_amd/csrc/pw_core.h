@@ -362,23 +362,27 @@ __device__ __forceinline__ void pw_flat_contig_body(const F &f, const PwGeom &g,
 // [4096, 4096] measured 5% slower than a plain copy of the same shape, with
 // two it is within 1%.
 // STRM: as for pw_flat.
-// RANK = 2 or 3: the rank is fixed, so every geometry field the tile needs
-// has a constant index (no decode loop): the row is the one outer dim (rank
-// 2), or splits into its two outer indices by one multiply-shift (rank 3).
-// RANK = 0: any rank, through decode_outer.  O32 (RANK 2 or 3): every element
-// offset of the launch is below 2^32, so the row's offsets are 32-bit
-// products.  SMALL: fewer than 2^32 tiles, so a tile index splits into (row,
-// chunk) by multiply-shift instead of a 64-bit division.  All of this runs
-// before the first load of every block: the decode loop's dependent scalar
-// loads cost about 5% of a [4096, 4096] launch, and on a [64, 512, 1024] one
-// whose blocks each write one 4 KiB row, the decode loop took half the time
-// and 64-bit stride products a further sixth.
+// RANK = 2, 3 or 4: the rank is fixed, so the row splits into its outer
+// indices by RANK - 2 multiply-shifts with every geometry field at a constant
+// index (no decode loop, no run-time branch).  RANK = 0: any rank, through
+// decode_outer.  O32 (a fixed RANK): every element offset of the launch is
+// below 2^32, so the row's offsets are 32-bit products.  SMALL: fewer than
+// 2^32 tiles, so a tile index splits into (row, chunk) by multiply-shift
+// instead of a 64-bit division.  All of this runs before the first load of
+// every block: the decode loop's dependent scalar loads cost about 5% of a
+// [4096, 4096] launch, and on a [64, 512, 1024] one whose blocks each write
+// one 4 KiB row, the decode loop took half the time and 64-bit stride
+// products a further sixth.  A loop unrolled over all 8 possible dims (rank
+// 4 to 8 in one variant) held too many fields for the scalar registers and
+// reloaded them dim by dim: 32 us where the fixed rank 4 takes 24.5 (rank
+// 3: 22; the 64-bit run-time path: 41.5).
 template <class F, unsigned U8MASK, bool VEC, unsigned STRM, int RANK, bool O32, bool SMALL>
 __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const PwPtrs &p) {
-    static_assert(!O32 || RANK == 2 || RANK == 3, "32-bit offsets need a fixed rank");
+    static_assert(RANK == 0 || (RANK >= 2 && RANK <= 4 && SMALL), "a fixed rank is 2, 3 or 4, below 2^32 tiles");
+    static_assert(!O32 || RANK != 0, "32-bit offsets need a fixed rank");
     constexpr int NIN = F::NIN;
     constexpr int NOUT = nout_of<F>();
-    const int inner = RANK == 2 ? 1 : RANK == 3 ? 2 : g.rank - 1;
+    const int inner = RANK != 0 ? RANK - 1 : g.rank - 1;
     const int64_t cols = g.size[inner];
     const int64_t ntiles = g.rows * g.chunks;
     bool unit[NIN > 0 ? NIN : 1];
@@ -399,28 +403,24 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
             chunk = tile - row * g.chunks;
         }
         int64_t oo, io[NIN > 0 ? NIN : 1];
-        if constexpr (RANK == 2 && O32) {
-            // every offset < 2^32 and every term non-negative: no partial
-            // sum wraps in 32 bits
-            const uint32_t r = (uint32_t)row;
-            oo = (uint32_t)g.ooff + r * (uint32_t)g.ostride[0];
-            for (int i = 0; i < NIN; i++) io[i] = (uint32_t)g.ioff[i] + r * (uint32_t)g.istride[i][0];
-        } else if constexpr (RANK == 2) {
-            oo = g.ooff + row * g.ostride[0];
-            for (int i = 0; i < NIN; i++) io[i] = g.ioff[i] + row * g.istride[i][0];
-        } else if constexpr (RANK == 3) {
-            // row < 2^32 (SMALL): row = w * size[1] + t
-            const uint32_t w = fast_div((uint32_t)row, g.fd[1]);
-            const uint32_t t = (uint32_t)row - w * g.fd[1].div;
-            if constexpr (O32) {
-                oo = (uint32_t)g.ooff + w * (uint32_t)g.ostride[0] + t * (uint32_t)g.ostride[1];
-                for (int i = 0; i < NIN; i++)
-                    io[i] = (uint32_t)g.ioff[i] + w * (uint32_t)g.istride[i][0] + t * (uint32_t)g.istride[i][1];
-            } else {
-                oo = g.ooff + (int64_t)w * g.ostride[0] + (int64_t)t * g.ostride[1];
-                for (int i = 0; i < NIN; i++)
-                    io[i] = g.ioff[i] + (int64_t)w * g.istride[i][0] + (int64_t)t * g.istride[i][1];
+        if constexpr (RANK != 0) {
+            // outer dims RANK-2 .. 0, innermost first; row < 2^32 (SMALL).
+            // With O32 every offset is below 2^32 and every term
+            // non-negative, so no partial sum wraps in 32 bits.
+            using Off = typename OffsetT<O32>::type;
+            uint32_t rem = (uint32_t)row;
+            Off o = (Off)g.ooff, ii[NIN > 0 ? NIN : 1];
+            for (int i = 0; i < NIN; i++) ii[i] = (Off)g.ioff[i];
+#pragma unroll
+            for (int d = RANK - 2; d >= 0; d--) {
+                const uint32_t q = d == 0 ? 0u : fast_div(rem, g.fd[d]);
+                const Off c = (Off)(rem - q * g.fd[d].div);
+                rem = q;
+                o += c * (Off)g.ostride[d];
+                for (int i = 0; i < NIN; i++) ii[i] += c * (Off)g.istride[i][d];
             }
+            oo = (int64_t)o;
+            for (int i = 0; i < NIN; i++) io[i] = (int64_t)ii[i];
         } else {
             decode_outer<NIN>(g, inner, row, oo, io);
         }
@@ -470,13 +470,13 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
     for (int64_t tile = (int64_t)blockIdx.x + gridDim.x; tile < ntiles; tile += gridDim.x) do_tile(tile);
 }
 
-// RK = 2 or 3: the host planned a launch of that rank, fewer than 2^32 tiles
-// and every element offset below 2^32 (the common cases, compiled with no
-// run-time geometry branches and 32-bit offsets); RK = 0: any rows launch,
+// RK = 2, 3 or 4: the host planned a launch of that rank, fewer than 2^32
+// tiles and every element offset below 2^32 (the common cases, compiled with
+// no run-time geometry branches and 32-bit offsets); RK = 0: any rows launch,
 // dispatched at run time with 64-bit offsets.
 template <class F, unsigned U8MASK, bool VEC, unsigned STRM = 0u, int RK = 0>
 __device__ __forceinline__ void pw_rows_body(const F &f, const PwGeom &g, const PwPtrs &p) {
-    if constexpr (RK == 2 || RK == 3) {
+    if constexpr (RK != 0) {
         pw_rows_loop<F, U8MASK, VEC, STRM, RK, true, true>(f, g, p);
     } else {
         if (g.rows * g.chunks > 0xFFFFFFFFll) pw_rows_loop<F, U8MASK, VEC, STRM, 0, false, false>(f, g, p);

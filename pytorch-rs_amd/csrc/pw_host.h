@@ -41,10 +41,10 @@ struct PwPlan {
     // walks (g.rows = g.groups * walk).
     uint32_t trans = 0, held = 0, once = 0, xbc = 0;
     int walk = 1;
-    // Rank 2 (r2, Rows only) or 3 (r3, Rows or Xpose), fewer than 2^32 tiles
-    // and every element offset below 2^32: the compile-time fast cases.
-    bool r2 = false;
-    bool r3 = false;
+    // The compile-time fast case, 0 if none: the rank (Rows: 2, 3 or 4;
+    // Xpose: 3) of a launch with fewer than 2^32 tiles and every element
+    // offset below 2^32.
+    int rk = 0;
     int nin = 0;
     int block = 256;  // lanes per block (kFlatBlock for the flat variants)
     int64_t grid = 0;
@@ -264,8 +264,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             g.chunks = (size[inner] + chunk - 1) / chunk;
             g.fdchunks = make_fast_div(g.chunks > (int64_t)UINT32_MAX ? 1u : (uint32_t)g.chunks);
             const bool fast = g.rows * g.chunks <= (int64_t)UINT32_MAX && offsets_fit32();
-            plan->r2 = rank == 2 && fast;
-            plan->r3 = rank == 3 && fast;
+            plan->rk = fast && rank <= 4 ? rank : 0;
             plan->grid = std::min<int64_t>(g.rows * g.chunks, want);
         }
         return TRS_OK;
@@ -335,7 +334,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             // holds at once (about kXposeResident blocks per CU).
             g.skew = xtiles > 1 && g.chunks > (int64_t)kXposeResident * cu_count;
             g.fdxtiles = make_fast_div(small ? (uint32_t)xtiles : 1u);
-            plan->r3 = rank == 3 && small && offsets_fit32();
+            plan->rk = rank == 3 && small && offsets_fit32() ? 3 : 0;
             plan->grid = std::min<int64_t>(g.groups * g.chunks, want);
             return TRS_OK;
         }

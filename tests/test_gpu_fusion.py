@@ -79,6 +79,26 @@ def test_fused_broadcast_transposed_chain_bit_exact(B, M, N):
     assert_bitwise_equal(fused, want)
 
 
+@pytest.mark.parametrize("ash,bsh,osh", [
+    ((2, 1, 4, 256), (1, 3, 1, 256), (2, 3, 4, 256)),          # rank 4, fixed-rank rows kernel
+    ((4, 1, 6, 2052), (1, 5, 1, 2052), (4, 5, 6, 2052)),       # rank 4, ragged last chunk
+    ((2, 1, 3, 1, 128), (1, 2, 1, 4, 128), (2, 2, 3, 4, 128)),  # rank 5, run-time decode
+])
+def test_fused_rows_of_rank_four_and_five_bit_exact(ash, bsh, osh):
+    """(a + b) * c with a and b broadcast so that no dims merge: rows
+    launches of rank 4 and 5."""
+    rng = np.random.default_rng(sum(osh))
+    a = rng.standard_normal(int(np.prod(ash))).astype(np.float32)
+    b = rng.standard_normal(int(np.prod(bsh))).astype(np.float32)
+    c = rng.standard_normal(int(np.prod(osh))).astype(np.float32)
+    ast, bst, ost = O.contiguous_strides(ash), O.contiguous_strides(bsh), O.contiguous_strides(osh)
+    fused = gpu_fused(BCAST_IR, [a, b, c], [layout_of(ash), layout_of(bsh), layout_of(osh)], osh)
+    sh1, st1 = O.binary_output_layout(ash, ast, bsh, bst)
+    s = O.binary(O.ADD, a, ash, ast, 0, b, bsh, bst, 0, sh1, st1)
+    want = O.binary(O.MUL, s, sh1, st1, 0, c, osh, ost, 0, osh, ost)
+    assert_bitwise_equal(fused, want)
+
+
 def test_fused_mask_apply_with_u8_input():
     rng = np.random.default_rng(9)
     n = 10_000

@@ -58,6 +58,12 @@ BINARY_CASES = {
     "permuted_3d": lambda rng: (_view(rng, (16, 32, 8), (1, 128, 16)), _view(rng, (16, 32, 8))),
     "empty": lambda rng: (_view(rng, (0, 5)), _view(rng, (5,))),
     "large_transposed_ragged": lambda rng: (_transposed(rng, (1000, 999)), _view(rng, (999, 1000))),
+    # broadcasts that merge to no lower rank: the fixed rank-4 rows kernel, and
+    # rank 5 through the run-time decode
+    "rank4_broadcast": lambda rng: (_view(rng, (3, 1, 5, 64)), _view(rng, (1, 4, 1, 64))),
+    "rank4_broadcast_wide": lambda rng: (_view(rng, (8, 1, 16, 1024)), _view(rng, (1, 8, 1, 1024))),
+    "rank4_broadcast_ragged": lambda rng: (_view(rng, (5, 1, 7, 2051)), _view(rng, (1, 3, 1, 2051))),
+    "rank5_broadcast": lambda rng: (_view(rng, (2, 1, 3, 1, 64)), _view(rng, (1, 3, 1, 4, 64))),
     # more tiles in one tuple than the GPU holds at once: diagonal tile order
     "skewed_transposed": lambda rng: (_view(rng, (4096, 4096)), _transposed(rng, (4096, 4096))),
     "skewed_transposed_ragged": lambda rng: (_transposed(rng, (4099, 4100)), _view(rng, (4100, 4099))),

@@ -97,8 +97,8 @@ def _get(big, off, n):
 
 
 def test_row_and_transposing_layouts_on_both_sides_of_two_to_the_32_element_offsets():
-    """Rank-2 and rank-3 row launches and the rank-3 transposing one are
-    compiled with 32-bit offsets when every element offset of the launch is
+    """Rank-2, rank-3 and rank-4 row launches and the rank-3 transposing one
+    are compiled with 32-bit offsets when every element offset of the launch is
     below 2^32, else they take the run-time path with 64-bit offsets.  Each
     layout runs with its views ending exactly at element 2^32 - 1 of one
     allocation (32-bit) and again past 2^32 (64-bit), bit-exact against the
@@ -111,6 +111,7 @@ def test_row_and_transposing_layouts_on_both_sides_of_two_to_the_32_element_offs
     cases = [
         ("rows rank 2", O.ADD, ((300, 2112), None), ((2112,), None), (300, 2112)),
         ("rows rank 3", O.MUL, ((8, 1, 1024), None), ((96, 1024), None), (8, 96, 1024)),
+        ("rows rank 4", O.ADD, ((4, 1, 8, 1024), None), ((6, 1, 1024), None), (4, 6, 8, 1024)),
         ("transposed rank 3", O.SUB, ((8, 192, 320), (320 * 192, 1, 192)), ((8, 192, 320), None), (8, 192, 320)),
     ]
     for name, op, (lsh, lst), (rsh, rst), osh in cases:
