@@ -1,9 +1,9 @@
-// pointwise.hip -- ahead-of-time pointwise, reduction and backward kernels.
-//
-// Each entry point replaces the per-element loop of one reference function
-// (cited at the entry point) and runs it through the shared engine in
-// pw_core.h.  Ops are functors with the reference's scalar semantics; the
-// file is compiled with -ffp-contract=off so `a * b + c` is never fused.
+// pointwise.hip -- reductions and the backward helpers built on them: the
+// device sum, the ordered broadcast-reduction VJPs (add and mul unbroadcast),
+// fills and in-place accumulation.  The pointwise op families live in
+// pw_binary.hip, pw_scalar.hip, pw_unary.hip and pw_mask.hip over pw_ops.h.
+// Each entry point replaces the loop of one reference function, cited at the
+// entry point.  Compiled with -ffp-contract=off.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -14,170 +14,6 @@
 #include "trs_internal.h"
 
 namespace trs {
-
-// ---- op functors ----------------------------------------------------------
-
-template <int OP>
-struct BinaryF {
-    static constexpr int NIN = 2;
-    __device__ __forceinline__ float operator()(const float *a) const {
-        if constexpr (OP == TRS_ADD) return a[0] + a[1];
-        else if constexpr (OP == TRS_SUB) return a[0] - a[1];
-        else if constexpr (OP == TRS_MUL) return a[0] * a[1];
-        else return a[0] / a[1];
-    }
-};
-
-template <int OP>
-struct ScalarF {
-    static constexpr int NIN = 1;
-    float s;
-    __device__ __forceinline__ float operator()(const float *a) const {
-        if constexpr (OP == TRS_S_ADD) return a[0] + s;
-        else if constexpr (OP == TRS_S_SUB) return a[0] - s;
-        else if constexpr (OP == TRS_S_MUL) return a[0] * s;
-        else if constexpr (OP == TRS_S_DIV) return a[0] / s;
-        else if constexpr (OP == TRS_S_RSUB) return s - a[0];
-        else return s * (1.0f / a[0]);  // scalar_div: reciprocal multiplication
-    }
-};
-
-template <int OP>
-struct UnaryF {
-    static constexpr int NIN = 1;
-    __device__ __forceinline__ float operator()(const float *a) const {
-        if constexpr (OP == TRS_EXP) return exp_value(a[0]);
-        else if constexpr (OP == TRS_RELU) return relu_value(a[0]);
-        else if constexpr (OP == TRS_NEG) return negate_value(a[0]);
-        else return a[0];
-    }
-};
-
-// (h * mask) * scale with the mask read as uint8 (input 1).
-struct MaskApplyF {
-    static constexpr int NIN = 2;
-    float scale;
-    __device__ __forceinline__ float operator()(const float *a) const {
-        const float t = a[0] * a[1];
-        return t * scale;
-    }
-};
-
-// Backward of dropout-apply (h * mask) * scale, in the order the reference's
-// graph runs it: the MultiplyScalar VJP (up * scale) and then the Multiply VJP
-// (* mask) -- two roundings, one pass.
-struct MaskBackwardF {
-    static constexpr int NIN = 2;  // (upstream, mask as u8)
-    float scale;
-    __device__ __forceinline__ float operator()(const float *a) const {
-        const float t = a[0] * scale;
-        return t * a[1];
-    }
-};
-
-struct ReluBackwardF {
-    static constexpr int NIN = 2;  // (saved input, upstream)
-    __device__ __forceinline__ float operator()(const float *a) const {
-        return relu_backward_value(a[0], a[1]);
-    }
-};
-
-// ---- AOT wrappers -----------------------------------------------------------
-// S: inputs read once (loaded non-temporally), a compile-time mask.
-
-// The geometry is every wrapper's first argument: the bodies read it in place
-// (kernarg_geom); the functor, which may carry a scalar, comes last.
-template <class F, unsigned M, bool V, unsigned S>
-__global__ void __launch_bounds__(kFlatBlock) k_flat(PwGeom, PwPtrs p, F f) {
-    pw_flat_body<F, M, V, S>(f, kernarg_geom(), p);
-}
-template <class F, unsigned M>
-__global__ void __launch_bounds__(kFlatBlock) k_flat_contig(PwGeom, PwPtrs p, F f) {
-    pw_flat_contig_body<F, M>(f, kernarg_geom(), p);
-}
-template <class F, unsigned M, bool V, unsigned S, int RK = 0>
-__global__ void __launch_bounds__(256) k_rows(PwGeom, PwPtrs p, F f) {
-    pw_rows_body<F, M, V, S, RK>(f, kernarg_geom(), p);
-}
-template <class F, unsigned M, bool V, unsigned TR, unsigned S>
-__global__ void __launch_bounds__(64 * kXposeWT * kXposeWX) k_xpose(PwGeom, PwPtrs p, F f) {
-    pw_xpose_body<F, M, V, kXposeWT, kXposeWX, TR, 0u, 0u, 1, S>(f, kernarg_geom(), p);
-}
-template <class F, unsigned M>
-__global__ void __launch_bounds__(256) k_generic(PwGeom, PwPtrs p, F f) { pw_generic_body<F, M>(f, kernarg_geom(), p); }
-
-// Calls fn.template operator()<K>() with K the compile-time value of the
-// run-time mask `m` over NIN bits (NIN is 1 or 2 here).
-template <int NIN, class Fn>
-void with_mask(unsigned m, Fn &&fn) {
-    static_assert(NIN >= 1 && NIN <= 2, "AOT functors take one or two inputs");
-    if constexpr (NIN == 1) {
-        if (m & 1u) fn.template operator()<1u>();
-        else fn.template operator()<0u>();
-    } else {
-        switch (m & 3u) {
-        case 0u: fn.template operator()<0u>(); break;
-        case 1u: fn.template operator()<1u>(); break;
-        case 2u: fn.template operator()<2u>(); break;
-        default: fn.template operator()<3u>(); break;
-        }
-    }
-}
-
-template <class F, unsigned M>
-int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
-    constexpr int NIN = F::NIN;
-    const dim3 grid((unsigned)pl.grid), block((unsigned)pl.block);
-    const unsigned sm = pl.g.streamed & ((1u << NIN) - 1u);
-    switch (pl.variant) {
-    case PwVariant::Empty:
-        return TRS_OK;
-    case PwVariant::Flat:
-        if (pl.contig) hipLaunchKernelGGL((k_flat_contig<F, M>), grid, block, 0, s, pl.g, pl.p, f);
-        else if (pl.vec)
-            with_mask<NIN>(sm, [&]<unsigned S>() { hipLaunchKernelGGL((k_flat<F, M, true, S>), grid, block, 0, s, pl.g, pl.p, f); });
-        else hipLaunchKernelGGL((k_flat<F, M, false, 0u>), grid, block, 0, s, pl.g, pl.p, f);
-        break;
-    case PwVariant::Rows:
-        if (pl.vec)
-            with_mask<NIN>(sm, [&]<unsigned S>() {
-                if (pl.rk == 2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, pl.g, pl.p, f);
-                else if (pl.rk == 3) hipLaunchKernelGGL((k_rows<F, M, true, S, 3>), grid, block, 0, s, pl.g, pl.p, f);
-                else if (pl.rk == 4) hipLaunchKernelGGL((k_rows<F, M, true, S, 4>), grid, block, 0, s, pl.g, pl.p, f);
-                else hipLaunchKernelGGL((k_rows<F, M, true, S, 0>), grid, block, 0, s, pl.g, pl.p, f);
-            });
-        else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, pl.g, pl.p, f);
-        break;
-    case PwVariant::Xpose:
-        // One outer tuple per block (no roles): every transposed-operand mask.
-        with_mask<NIN>(pl.trans, [&]<unsigned TR>() {
-            if constexpr (TR != 0u) {
-                if (pl.vec)
-                    with_mask<NIN>(sm, [&]<unsigned S>() {
-                        hipLaunchKernelGGL((k_xpose<F, M, true, TR, S>), grid, block, 0, s, pl.g, pl.p, f);
-                    });
-                else hipLaunchKernelGGL((k_xpose<F, M, false, TR, 0u>), grid, block, 0, s, pl.g, pl.p, f);
-            }
-        });
-        break;
-    case PwVariant::Generic:
-        hipLaunchKernelGGL((k_generic<F, M>), grid, block, 0, s, pl.g, pl.p, f);
-        break;
-    }
-    TRS_LAUNCH_CHECK("pointwise kernel launch");
-    return TRS_OK;
-}
-
-template <class F, unsigned M = 0u>
-int run_pointwise(const F &f, const trs_layout *lo, float *out, int nin, const void *const *bases,
-                  const trs_layout *const *lins, const int *eb) {
-    DeviceState *dev = device_state();
-    if (!dev) return TRS_E_NO_DEVICE;
-    PwPlan pl;
-    int rc = plan_pointwise(lo, out, nin, bases, lins, eb, dev->cu_count, &pl);
-    if (rc) return rc;
-    return launch_planned<F, M>(f, pl, dev->stream);
-}
 
 // ---- reductions -------------------------------------------------------------
 
@@ -769,108 +605,18 @@ int sum_launch(DeviceState *dev, const float *x, const trs_layout *lx, float *ou
     return rc;
 }
 
-// Contiguous layout of `shape` (for gradients, which are logical-order).
-trs_layout contiguous_like(const trs_layout *l) {
-    trs_layout c{};
-    c.rank = l->rank;
-    int64_t s = 1;
-    for (int d = l->rank - 1; d >= 0; d--) {
-        c.shape[d] = l->shape[d];
-        c.stride[d] = s;
-        s *= l->shape[d];
-    }
-    c.offset = 0;
-    return c;
-}
-
 }  // namespace trs
 
 using namespace trs;
 
 extern "C" {
 
-int trs_binary_f32(int op, const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
-                   float *out, const trs_layout *lo) {
-    const void *bases[2] = {a, b};
-    const trs_layout *ls[2] = {la, lb};
-    const int eb[2] = {4, 4};
-    switch (op) {
-    case TRS_ADD: return run_pointwise(BinaryF<TRS_ADD>{}, lo, out, 2, bases, ls, eb);
-    case TRS_SUB: return run_pointwise(BinaryF<TRS_SUB>{}, lo, out, 2, bases, ls, eb);
-    case TRS_MUL: return run_pointwise(BinaryF<TRS_MUL>{}, lo, out, 2, bases, ls, eb);
-    case TRS_DIV: return run_pointwise(BinaryF<TRS_DIV>{}, lo, out, 2, bases, ls, eb);
-    default: return set_error(TRS_E_INVALID_ARGUMENT, "unknown binary op %d", op);
-    }
-}
-
-int trs_binary_scalar_f32(int op, const float *a, const trs_layout *la, float s, float *out,
-                          const trs_layout *lo) {
-    const void *bases[1] = {a};
-    const trs_layout *ls[1] = {la};
-    const int eb[1] = {4};
-    if (la && lo && la->rank != lo->rank)
-        return set_error(TRS_E_SHAPE_MISMATCH, "scalar op output rank differs from input rank");
-    switch (op) {
-    case TRS_S_ADD: return run_pointwise(ScalarF<TRS_S_ADD>{s}, lo, out, 1, bases, ls, eb);
-    case TRS_S_SUB: return run_pointwise(ScalarF<TRS_S_SUB>{s}, lo, out, 1, bases, ls, eb);
-    case TRS_S_MUL: return run_pointwise(ScalarF<TRS_S_MUL>{s}, lo, out, 1, bases, ls, eb);
-    case TRS_S_DIV: return run_pointwise(ScalarF<TRS_S_DIV>{s}, lo, out, 1, bases, ls, eb);
-    case TRS_S_RSUB: return run_pointwise(ScalarF<TRS_S_RSUB>{s}, lo, out, 1, bases, ls, eb);
-    case TRS_S_RDIV: return run_pointwise(ScalarF<TRS_S_RDIV>{s}, lo, out, 1, bases, ls, eb);
-    default: return set_error(TRS_E_INVALID_ARGUMENT, "unknown scalar op %d", op);
-    }
-}
-
-int trs_unary_f32(int op, const float *a, const trs_layout *la, float *out, const trs_layout *lo) {
-    const void *bases[1] = {a};
-    const trs_layout *ls[1] = {la};
-    const int eb[1] = {4};
-    if (la && lo && la->rank != lo->rank)
-        return set_error(TRS_E_SHAPE_MISMATCH, "unary op output rank differs from input rank");
-    switch (op) {
-    case TRS_EXP: return run_pointwise(UnaryF<TRS_EXP>{}, lo, out, 1, bases, ls, eb);
-    case TRS_RELU: return run_pointwise(UnaryF<TRS_RELU>{}, lo, out, 1, bases, ls, eb);
-    case TRS_NEG: return run_pointwise(UnaryF<TRS_NEG>{}, lo, out, 1, bases, ls, eb);
-    case TRS_COPY: return run_pointwise(UnaryF<TRS_COPY>{}, lo, out, 1, bases, ls, eb);
-    default: return set_error(TRS_E_INVALID_ARGUMENT, "unknown unary op %d", op);
-    }
-}
-
-int trs_mask_apply_f32(const float *h, const trs_layout *lh, const uint8_t *mask, const trs_layout *lm,
-                       float scale, float *out, const trs_layout *lo) {
-    const void *bases[2] = {h, mask};
-    const trs_layout *ls[2] = {lh, lm};
-    const int eb[2] = {4, 1};
-    return run_pointwise<MaskApplyF, 2u>(MaskApplyF{scale}, lo, out, 2, bases, ls, eb);
-}
-
-int trs_mask_backward_f32(const float *up, const trs_layout *lu, const uint8_t *mask, const trs_layout *lm,
-                          float scale, float *grad, const trs_layout *lg) {
-    const void *bases[2] = {up, mask};
-    const trs_layout *ls[2] = {lu, lm};
-    const int eb[2] = {4, 1};
-    return run_pointwise<MaskBackwardF, 2u>(MaskBackwardF{scale}, lg, grad, 2, bases, ls, eb);
-}
-
-int trs_relu_backward_f32(const float *input, const trs_layout *li, const float *up, float *grad) {
-    int rc = check_layout(li, "input");
-    if (rc) return rc;
-    const trs_layout lc = contiguous_like(li);
-    const void *bases[2] = {input, up};
-    const trs_layout *ls[2] = {li, &lc};
-    const int eb[2] = {4, 4};
-    return run_pointwise(ReluBackwardF{}, &lc, grad, 2, bases, ls, eb);
-}
-
 int trs_accumulate_f32(float *dst, const float *src, size_t n) {
     trs_layout l{};
     l.rank = 1;
     l.shape[0] = (int64_t)n;
     l.stride[0] = 1;
-    const void *bases[2] = {dst, src};
-    const trs_layout *ls[2] = {&l, &l};
-    const int eb[2] = {4, 4};
-    return run_pointwise(BinaryF<TRS_ADD>{}, &l, dst, 2, bases, ls, eb);
+    return trs_binary_f32(TRS_ADD, dst, &l, src, &l, dst, &l);  // in place: the same view
 }
 
 int trs_fill_f32(float *out, size_t n, float value) {
@@ -906,10 +652,7 @@ int trs_mul_backward_f32(const float *up, const trs_layout *lout, const float *o
     if (layout_numel(lself) == layout_numel(lout)) {
         // No broadcast: one contribution per element, stored as is.
         const trs_layout lc = contiguous_like(lout);
-        const void *bases[2] = {up, other};
-        const trs_layout *ls[2] = {&lc, lother};
-        const int eb[2] = {4, 4};
-        return run_pointwise(BinaryF<TRS_MUL>{}, &lc, grad, 2, bases, ls, eb);
+        return trs_binary_f32(TRS_MUL, up, &lc, other, lother, grad, &lc);
     }
     return reduce_to_operand(up, lout, other, lother, lself, grad);
 }

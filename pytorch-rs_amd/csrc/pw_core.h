@@ -1,6 +1,6 @@
 // pw_core.h -- device-side pointwise engine for gfx950 (CDNA4).
 //
-// Shared verbatim by the ahead-of-time kernels (pointwise.hip) and by the
+// Shared verbatim by the ahead-of-time kernels (pw_ops.h) and by the
 // runtime fusion compiler (fusion.hip embeds this file and compiles it with
 // hipRTC), so an eager op and a fused chain run the same index machinery.
 //

@@ -81,6 +81,20 @@ int check_layout(const trs_layout *l, const char *what);
 int64_t layout_numel(const trs_layout *l);
 bool layout_is_contiguous(const trs_layout *l);
 
+// Contiguous layout of `l`'s shape (for gradients, which are logical-order).
+inline trs_layout contiguous_like(const trs_layout *l) {
+    trs_layout c{};
+    c.rank = l->rank;
+    int64_t s = 1;
+    for (int d = l->rank - 1; d >= 0; d--) {
+        c.shape[d] = l->shape[d];
+        c.stride[d] = s;
+        s *= l->shape[d];
+    }
+    c.offset = 0;
+    return c;
+}
+
 // The bytes a non-empty view can touch: [begin, end) from its base pointer.
 struct ByteRange {
     uintptr_t begin = 0, end = 0;
