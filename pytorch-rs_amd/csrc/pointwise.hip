@@ -37,18 +37,30 @@ __global__ void __launch_bounds__(256) sum_pass1(const float *x, PwGeom g, int64
     __shared__ float red[256];
     const int64_t begin = (int64_t)blockIdx.x * chunk;
     const int64_t end = begin + chunk < g.numel ? begin + chunk : g.numel;
-    float acc = -0.0f;
-    for (int64_t e = begin + threadIdx.x; e < end; e += 256) {
-        int64_t off;
+    auto offset_of = [&](int64_t e) -> int64_t {
         if constexpr (CONTIG) {
-            off = g.ioff[0] + e;
+            return g.ioff[0] + e;
         } else {
             int64_t oo, io[1];
             decode_outer<1>(g, g.rank, e, oo, io);
-            off = io[0];
+            return io[0];
         }
-        acc += x[off];
+    };
+    // The lane's elements are added one by one in index order; only the
+    // loads run ahead: U of them are issued before their U additions, so a
+    // lane waits for memory once per U elements instead of once per element
+    // (the additions, and so the bits, are those of the plain loop).
+    constexpr int U = 8;
+    float acc = -0.0f;
+    int64_t e = begin + threadIdx.x;
+    for (; e + (U - 1) * 256 < end; e += U * 256) {
+        float v[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) v[k] = x[offset_of(e + k * 256)];
+#pragma unroll
+        for (int k = 0; k < U; k++) acc += v[k];
     }
+    for (; e < end; e += 256) acc += x[offset_of(e)];
     red[threadIdx.x] = acc;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {

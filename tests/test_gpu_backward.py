@@ -232,6 +232,47 @@ def test_sum_within_its_tree_bound(n, dist):
     assert abs(got - want) <= (gamma(d) + gamma(n - 1)) * abs_sum
 
 
+def device_tree_sum(x: np.ndarray) -> np.float32:
+    """trs_sum_f32's documented order in float32 numpy (one rounding per add):
+    a block over a contiguous range has 256 lanes; lane l adds elements l,
+    l+256, ... of the range in order from -0.0, then the lanes meet in a tree
+    (lane i += lane i+w for w = 128, 64, ..., 1).  Up to 32768 elements one
+    block covers all; above, block b covers [b*chunk, (b+1)*chunk) with chunk =
+    ceil(n/1024), and one more block sums the partials the same way."""
+    def block(vals):
+        acc = np.full(256, -0.0, np.float32)
+        for s in range(0, vals.size, 256):
+            seg = vals[s:s + 256]
+            acc[:seg.size] = acc[:seg.size] + seg
+        w = 128
+        while w:
+            acc[:w] = acc[:w] + acc[w:2 * w]
+            w >>= 1
+        return acc[0]
+
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    if x.size <= 32768:
+        return block(x)
+    chunk = -(-x.size // 1024)
+    partial = np.array([block(x[b:b + chunk]) for b in range(0, x.size, chunk)], np.float32)
+    return block(partial)
+
+
+@pytest.mark.parametrize("n", [1, 255, 32768, 32769, 1 << 20, (1 << 23) + 5])
+def test_sum_follows_its_documented_tree_bit_for_bit(n):
+    """The device sum is the fixed tree its header documents, exactly: the
+    kernel may reorder loads for speed but never additions."""
+    rng = np.random.default_rng(n + 11)
+    x = rng.standard_normal(n).astype(np.float32) * np.float32(1000.0)
+    got = np.float32(gpu_sum(x, (n,)))
+    assert got.view(np.uint32) == device_tree_sum(x).view(np.uint32)
+    if n >= 1000:  # a transposed view sums in logical order
+        r = n // 37
+        m = x[: r * 37].reshape(37, r)
+        got = np.float32(gpu_sum(np.ascontiguousarray(m), (r, 37), (1, r)))
+        assert got.view(np.uint32) == device_tree_sum(m.T).view(np.uint32)
+
+
 @pytest.mark.parametrize("n", [1, 2, 257, 32768, 40000, 1 << 20])
 def test_sum_of_negative_zeros_is_negative_zero(n):
     """Rust's f32 Sum starts from -0.0 (the oracle's fold does too): an
