@@ -218,8 +218,11 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
 /* C = A @ B in fp32 on CDNA4 FP32 MFMA.  Rank 2 ([M,K] @ [K,N]) or rank 3
  * ([b,M,K] @ [b,K,N], the batch the reference spells as rank-2 calls).
  * Operands may be transposed views (unit stride in either matrix dim,
- * e.g. `.mT`); other strides run a one-thread-per-output kernel in the
- * reference's own k order.  `lc` must be contiguous.
+ * e.g. `.mT`).  An operand with no unit stride is first copied into a
+ * contiguous buffer from the library's block cache (as large as the operand,
+ * returned at the end of the call); if that memory cannot be allocated, a
+ * one-thread-per-output kernel runs in the reference's own k order.  `lc`
+ * must be contiguous.
  * Tolerance versus the reference's sequential order: |dC| <= 1e-5*sqrt(K) *
  * (|A||B|) elementwise.  A single 16-byte-aligned matrix whose M and N are
  * multiples of 256, with fewer 256x256 tiles than the device has CUs and a
@@ -239,8 +242,9 @@ int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const t
 /* Diagnostic (no counterpart in the reference): the kernel trs_matmul_f32
  * would run for these operands on the current device, without launching or
  * allocating.  Pointers are used only for their alignment and may be null.
- * *tile_m x *tile_n x *tile_k is one block's C tile and k depth (all 0 for
- * the one-thread-per-output strided kernel, or when nothing is launched),
+ * *tile_m x *tile_n x *tile_k is one block's C tile and k depth (all 0
+ * when nothing is launched; operands with no unit stride report the tile
+ * their contiguous copies run on),
  * *splits the number of K slices (1 = unsplit), *blocks the blocks of the
  * main launch.  Any out pointer may be null. */
 int trs_matmul_plan_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,

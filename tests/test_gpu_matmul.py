@@ -86,17 +86,34 @@ def test_batched_against_per_matrix_reference():
         _check_tol(got[t], want[t], _abs_bound(a[t], b[t]), k)
 
 
-def test_general_strides_use_the_strided_path():
-    rng = np.random.default_rng(4)
-    m, k, n = 20, 30, 10
-    buf_a = rng.standard_normal(m * k * 2).astype(np.float32)
-    buf_b = rng.standard_normal(k * n * 3).astype(np.float32)
+@pytest.mark.parametrize("m,k,n", [(20, 30, 10), (256, 512, 384), (1024, 1024, 1024)])
+def test_general_strides_are_gathered_onto_the_mfma_tiles(m, k, n):
+    """Operands with no unit stride are copied contiguous and multiplied on
+    the MFMA tiles: exact on small integers, within the tolerance on normal
+    data, and the plan reports an MFMA tile."""
+    rng = np.random.default_rng(4 + m)
     la = ((m, k), (2 * k, 2), 1)   # no unit stride
     lb = ((k, n), (3 * n, 3), 2)
+    ints_a = rng.integers(-3, 4, m * k * 2).astype(np.float32)
+    ints_b = rng.integers(-3, 4, k * n * 3).astype(np.float32)
+    got = U.matmul(ints_a, *la, ints_b, *lb)
+    want = O.matmul(ints_a, *la, ints_b, *lb).reshape(m, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    buf_a = rng.standard_normal(m * k * 2).astype(np.float32)
+    buf_b = rng.standard_normal(k * n * 3).astype(np.float32)
     got = U.matmul(buf_a, *la, buf_b, *lb)
     want = O.matmul(buf_a, *la, buf_b, *lb).reshape(m, n)
-    # The strided fallback keeps the reference order (one rounding per op).
-    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    a = np.lib.stride_tricks.as_strided(buf_a[1:], (m, k), (8 * k, 8))
+    b = np.lib.stride_tricks.as_strided(buf_b[2:], (k, n), (12 * n, 12))
+    _check_tol(got, want, _abs_bound(a, b), k)
+    import ctypes
+    from trs_backend import abi
+    tm, tn, tk, sp, bl = (ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64())
+    abi.check(abi.lib.trs_matmul_plan_f32(None, ctypes.byref(abi.layout_of(*la)), None,
+                                          ctypes.byref(abi.layout_of(*lb)), None, ctypes.byref(abi.layout_of((m, n))),
+                                          ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk), ctypes.byref(sp),
+                                          ctypes.byref(bl)))
+    assert tm.value > 0 and tn.value > 0 and tk.value > 0
 
 
 def _oracle_threads():
