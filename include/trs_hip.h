@@ -251,6 +251,31 @@ int trs_matmul_plan_f32(const float *a, const trs_layout *la, const float *b, co
                         const float *c, const trs_layout *lc, int *tile_m, int *tile_n, int *tile_k,
                         int64_t *splits, int64_t *blocks);
 
+/* Diagnostic (no counterpart in the reference): the launch plan the
+ * pointwise entry points would use for these layouts (or, with roles = 1, a
+ * fused program, which also specialises on held and once-per-tuple operands),
+ * without launching anything or touching a device.  `inputs` and `out` are
+ * used only for their alignment and the overlap checks and may be any
+ * addresses; `elem_bytes` gives each input's element size (4 for f32, 1 for
+ * a u8 mask; null means all 4); `cu_count` is the compute-unit count the plan
+ * assumes.  Errors are those of the pointwise entry points. */
+typedef struct trs_pw_plan_info {
+    int32_t variant;    /* 0 nothing to do, 1 flat, 2 rows, 3 transposing, 4 generic */
+    int32_t rank;       /* rank after dropping size-1 dims and merging contiguous ones */
+    int32_t vec;        /* 16-byte vector accesses */
+    int32_t fixed_rank; /* rank the kernel is compiled for (32-bit offsets), 0 = decoded at run time */
+    int32_t skew;       /* transposing: a tuple's tiles taken in diagonal order */
+    int32_t walk;       /* transposing: outer tuples per block */
+    uint32_t trans;     /* transposing: inputs read transposed (bit i = input i) */
+    uint32_t held;      /* transposing with roles: inputs loaded once per block */
+    uint32_t once;      /* transposing with roles: inputs loaded once per outer tuple */
+    int32_t block;      /* lanes per block */
+    int64_t grid;       /* blocks */
+} trs_pw_plan_info;
+int trs_pointwise_plan(int n_inputs, const void *const *inputs, const trs_layout *const *layouts,
+                       const int *elem_bytes, const float *out, const trs_layout *lo, int cu_count, int roles,
+                       trs_pw_plan_info *info);
+
 /* ---- pointwise fusion compiler (new; no counterpart in the reference) */
 
 /* Compile a pointwise IR program to a gfx950 kernel with hipRTC (-O3,

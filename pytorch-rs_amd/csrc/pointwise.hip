@@ -680,6 +680,36 @@ int trs_reduce_to_shape_f32(const float *up, const trs_layout *lout, const trs_l
     return reduce_to_operand(up, lout, nullptr, nullptr, lself, grad);
 }
 
+int trs_pointwise_plan(int n_inputs, const void *const *inputs, const trs_layout *const *layouts,
+                       const int *elem_bytes, const float *out, const trs_layout *lo, int cu_count, int roles,
+                       trs_pw_plan_info *info) {
+    if (!info) return set_error(TRS_E_INVALID_ARGUMENT, "null plan info");
+    if (n_inputs < 1 || n_inputs > kMaxIn)
+        return set_error(TRS_E_INVALID_ARGUMENT, "pointwise plans take 1 to %d inputs, got %d", kMaxIn, n_inputs);
+    if (!inputs || !layouts) return set_error(TRS_E_INVALID_ARGUMENT, "null input arrays");
+    if (cu_count < 1) return set_error(TRS_E_INVALID_ARGUMENT, "cu_count must be positive, got %d", cu_count);
+    int eb[kMaxIn];
+    for (int i = 0; i < n_inputs; i++) eb[i] = elem_bytes ? elem_bytes[i] : 4;
+    PwPlan pl;
+    const int rc = plan_pointwise(lo, const_cast<float *>(out), n_inputs, inputs, layouts, eb, cu_count, &pl, 1,
+                                  nullptr, roles != 0);
+    if (rc) return rc;
+    *info = trs_pw_plan_info{};
+    info->variant = (int32_t)pl.variant;
+    if (pl.variant == PwVariant::Empty) return TRS_OK;
+    info->rank = pl.g.rank;
+    info->vec = pl.vec;
+    info->fixed_rank = pl.rk;
+    info->skew = pl.g.skew;
+    info->walk = pl.walk;
+    info->trans = pl.trans;
+    info->held = pl.held;
+    info->once = pl.once;
+    info->block = pl.block;
+    info->grid = pl.grid;
+    return TRS_OK;
+}
+
 int trs_sum_f32(const float *x, const trs_layout *lx, float *out) {
     DeviceState *dev = device_state();
     if (!dev) return TRS_E_NO_DEVICE;

@@ -74,6 +74,23 @@ def layout_of(shape, strides=None, offset: int = 0) -> Layout:
     return lay
 
 
+class PwPlanInfo(ctypes.Structure):
+    """trs_pw_plan_info: the launch plan trs_pointwise_plan reports."""
+    _fields_ = [
+        ("variant", c_int32),     # 0 nothing to do, 1 flat, 2 rows, 3 transposing, 4 generic
+        ("rank", c_int32),
+        ("vec", c_int32),
+        ("fixed_rank", c_int32),
+        ("skew", c_int32),
+        ("walk", c_int32),
+        ("trans", c_uint32),
+        ("held", c_uint32),
+        ("once", c_uint32),
+        ("block", c_int32),
+        ("grid", ctypes.c_int64),
+    ]
+
+
 _LP = POINTER(Layout)
 _FP = POINTER(c_float)
 
@@ -112,6 +129,8 @@ _SIGNATURES = {
     "trs_matmul_f32": ([c_void_p, _LP, c_void_p, _LP, c_void_p, _LP], c_int),
     "trs_matmul_plan_f32": ([c_void_p, _LP, c_void_p, _LP, c_void_p, _LP, POINTER(c_int), POINTER(c_int),
                              POINTER(c_int), POINTER(ctypes.c_int64), POINTER(ctypes.c_int64)], c_int),
+    "trs_pointwise_plan": ([c_int, POINTER(c_void_p), POINTER(_LP), POINTER(c_int), c_void_p, _LP, c_int, c_int,
+                            POINTER(PwPlanInfo)], c_int),
     "trs_fusion_compile": ([c_char_p, c_size_t, POINTER(c_uint64)], c_int),
     "trs_fusion_launch": ([c_uint64, c_int, POINTER(c_void_p), _LP, c_void_p, _LP], c_int),
     "trs_fusion_launch_multi": ([c_uint64, c_int, POINTER(c_void_p), _LP, c_int, POINTER(c_void_p), _LP], c_int),
@@ -149,6 +168,23 @@ def check(rc: int) -> None:
     if rc != 0:
         msg = lib.trs_last_error()
         raise TrsError(rc, msg.decode() if msg else "")
+
+
+def pointwise_plan(layouts, out_layout, bases=None, out=0x10000000000, elem_bytes=None, cu_count=256,
+                   roles=False) -> PwPlanInfo:
+    """trs_pointwise_plan for input `layouts` and `out_layout` (no device
+    needed).  `bases` and `out` are addresses, used only for alignment and
+    the overlap checks: by default far apart and 256-byte aligned."""
+    n = len(layouts)
+    if bases is None:
+        bases = [0x20000000000 + i * 0x10000000000 for i in range(n)]
+    ptrs = (c_void_p * n)(*bases)
+    lays = (_LP * n)(*[ctypes.pointer(l) for l in layouts])
+    eb = (c_int * n)(*(elem_bytes or [4] * n))
+    info = PwPlanInfo()
+    check(lib.trs_pointwise_plan(n, ptrs, lays, eb, c_void_p(out), ctypes.byref(out_layout), cu_count,
+                                 1 if roles else 0, ctypes.byref(info)))
+    return info
 
 
 def device_count() -> int:
