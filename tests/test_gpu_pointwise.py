@@ -282,6 +282,55 @@ def test_random_layouts_unary_bit_exact(op):
             raise AssertionError(f"case {case}: {sh} {st} +{off}: {e}") from None
 
 
+def _random_big_view(rng, shape, perm):
+    """A view of `shape` whose dims lie in memory in the order `perm`
+    (outermost first), unit inner stride, sometimes a padded row, and an
+    offset of 0, 4 (aligned) or 1 (unaligned)."""
+    r = len(shape)
+    strides = [0] * r
+    step = 1
+    for d in reversed(perm):
+        strides[d] = step
+        step *= max(shape[d], 1) + (4 if rng.random() < 0.2 else 0)
+    return _view(rng, shape, strides, int(rng.choice([0, 0, 4, 1])))
+
+
+@pytest.mark.parametrize("op", [O.ADD, O.MUL])
+def test_random_large_layouts_binary_bit_exact(op):
+    """40 random layouts per op at sizes the kernels' fast cases and edge
+    paths need (rank 2-4, dims up to 4100, up to 16M elements): transposed
+    and permuted operands, broadcasts, padded rows, aligned and unaligned
+    offsets, so the fixed-rank rows kernels, the transposing kernel in both
+    tile orders and the ragged tiles are all checked against the oracle."""
+    rng = np.random.default_rng(90210 + op)
+    dims = [1, 2, 5, 64, 129, 1024, 2048, 4096, 4100]
+    for case in range(40):
+        rank = int(rng.integers(2, 5))
+        while True:
+            oshape = tuple(int(rng.choice(dims)) for _ in range(rank))
+            if 1 << 16 <= int(np.prod(oshape)) <= 1 << 24:
+                break
+        ash, bsh = _random_broadcast_shape(rng, oshape), _random_broadcast_shape(rng, oshape)
+        if rng.random() < 0.6:
+            ash = oshape
+        # operand dims in memory order: b's reverses a's half the time (a
+        # transpose between them), else each is plain or randomly permuted
+        pa = rng.permutation(len(ash)) if rng.random() < 0.3 else np.arange(len(ash))
+        if rng.random() < 0.5 and len(bsh) == len(ash):
+            pb = pa[::-1]
+        else:
+            pb = rng.permutation(len(bsh)) if rng.random() < 0.3 else np.arange(len(bsh))
+        a, ash, ast, aoff = _random_big_view(rng, ash, pa)
+        b, bsh, bst, boff = _random_big_view(rng, bsh, pb)
+        osh, ostr = O.binary_output_layout(ash, ast, bsh, bst)
+        want = O.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ostr)
+        got = U.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ostr)
+        try:
+            assert_bitwise_equal(got, want)
+        except AssertionError as e:
+            raise AssertionError(f"case {case}: a {ash} {ast} +{aoff}, b {bsh} {bst} +{boff}: {e}") from None
+
+
 def test_reference_fast_path_vectors_on_gpu():
     """The operands of src/tensor.rs:4887-5024 (signalling NaNs, infinities,
     signed zeros and denormals; an offset transposed view, a rank-mixing
