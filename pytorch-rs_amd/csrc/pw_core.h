@@ -761,19 +761,41 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
 }
 
 // ---- pw_generic -----------------------------------------------------------
+// Any strides: every element decoded on its own by magic-number division.  A
+// block takes kGenericUnroll * blockDim consecutive elements per step, lane t
+// the elements t, t + blockDim, ... of them, so each load instruction still
+// covers consecutive elements; the lane issues all its loads before any
+// arithmetic.  With one element per lane, x[::2] + y[::2] over 2^25 elements
+// took 171 us, each lane waiting for its loads before the next element.
+constexpr int kGenericUnroll = 4;
+
 template <class F, unsigned U8MASK>
 __device__ __forceinline__ void pw_generic_body(const F &f, const PwGeom &g, const PwPtrs &p) {
     constexpr int NIN = F::NIN;
+    constexpr int NIN1 = NIN > 0 ? NIN : 1;
     constexpr int NOUT = nout_of<F>();
-    const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < g.numel; e += nthreads) {
-        int64_t oo, io[NIN > 0 ? NIN : 1];
-        decode_outer<NIN>(g, g.rank, e, oo, io);
-        float a[NIN > 0 ? NIN : 1];
-        static_for<NIN>([&]<int I>() { a[I] = ld1<U8MASK, I>(p, io[I]); });
-        float o[NOUT];
-        eval1(f, a, o);
-        store1<NOUT>(p, oo, o);
+    constexpr int U = kGenericUnroll;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x * U;
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x * U; base < g.numel; base += step) {
+        int64_t oo[U], io[U][NIN1];
+        float a[U][NIN1];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t e = base + (int64_t)u * blockDim.x + threadIdx.x;
+            if (e < g.numel) {
+                decode_outer<NIN>(g, g.rank, e, oo[u], io[u]);
+                static_for<NIN>([&]<int I>() { a[u][I] = ld1<U8MASK, I>(p, io[u][I]); });
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t e = base + (int64_t)u * blockDim.x + threadIdx.x;
+            if (e < g.numel) {
+                float o[NOUT];
+                eval1(f, a[u], o);
+                store1<NOUT>(p, oo[u], o);
+            }
+        }
     }
 }
 
