@@ -232,7 +232,12 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
  * memory from the library's block cache for the duration of the call
  * (S <= 8, and S*M*N is at most 65,536 floats per CU: 64 MiB on a 256-CU
  * device).  If that memory cannot be allocated the call runs the unsplit
- * tile instead.  The order of summation, and so the low bits of a result,
+ * tile instead.  An output with at most 32 rows or columns (a matrix-vector
+ * product, a small-batch linear layer) runs a kernel that streams the long
+ * operand once; it splits K to fill the device when the partial products
+ * (splits * M * N * batch floats, from the block cache) move at most 1/8 of
+ * the long operand's bytes, and runs unsplit when that memory cannot be had.
+ * The order of summation, and so the low bits of a result,
  * depends on the shape, the layout, the device's CU count and the operands'
  * 16-byte alignment; for fixed values of these the result is deterministic.
  * Empty outputs launch nothing; K = 0 writes +0.0 and then the operands may
@@ -244,7 +249,8 @@ int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const t
  * allocating.  Pointers are used only for their alignment and may be null.
  * *tile_m x *tile_n x *tile_k is one block's C tile and k depth (all 0
  * when nothing is launched; operands with no unit stride report the tile
- * their contiguous copies run on),
+ * their contiguous copies run on; a short output side reports its padded
+ * rows, 16 or 32, by 64 and the k per slice),
  * *splits the number of K slices (1 = unsplit), *blocks the blocks of the
  * main launch.  Any out pointer may be null. */
 int trs_matmul_plan_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,

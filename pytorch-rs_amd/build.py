@@ -40,7 +40,7 @@ HIP_FLAGS = [
 # The pointwise op families are separate translation units so they compile in
 # parallel (one file held every instantiation and took about 3 minutes).
 HIP_SOURCES = ["pw_binary.hip", "pw_binary_muldiv.hip", "pw_scalar.hip", "pw_unary.hip", "pw_mask.hip",
-               "pointwise.hip", "runtime.hip", "transfer.hip", "gemm.hip", "fusion.hip"]
+               "pointwise.hip", "runtime.hip", "transfer.hip", "gemm.hip", "gemm_skinny.hip", "fusion.hip"]
 ENGINE_SOURCES = ["engine.cpp", "py_module.cpp"]
 
 
@@ -81,7 +81,7 @@ def build_hip(jobs: int, if_stale: bool) -> Path:
     BUILD.mkdir(parents=True, exist_ok=True)
     LIB.mkdir(parents=True, exist_ok=True)
     gen_embedded_source()
-    headers = [CSRC / h for h in ("pw_core.h", "pw_host.h", "pw_ops.h", "trs_internal.h")] + [INCLUDE / "trs_hip.h",
+    headers = [CSRC / h for h in ("pw_core.h", "pw_host.h", "pw_ops.h", "trs_internal.h", "gemm_skinny.h")] + [INCLUDE / "trs_hip.h",
                                                                                  GEN / "pw_core_src.inc"]
     objs = []
     todo = []

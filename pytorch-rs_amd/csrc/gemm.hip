@@ -29,6 +29,7 @@
 
 #include <algorithm>
 
+#include "gemm_skinny.h"
 #include "trs_internal.h"
 
 namespace trs {
@@ -47,6 +48,9 @@ struct GemmArgs {
     int64_t ldc;
     int64_t bsa, bsb, bsc;  // batch strides (elements)
     int64_t batch;
+    // Split K (batches are K slices of depth K): the full depth, so the last
+    // slice stops at ktotal; 0 when every batch has depth K.
+    int64_t ktotal;
     int32_t tiles_m, tiles_n;
     int32_t xcd_remap;
 };
@@ -137,6 +141,7 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
     const int64_t tile_m = first_m + within % gm;
     const int64_t tile_n = within / gm;
 
+    const int64_t Kb = args.ktotal ? std::min<int64_t>(args.K, args.ktotal - batch_idx * args.K) : args.K;
     const float *A = args.a + batch_idx * args.bsa;
     const float *B = args.b + batch_idx * args.bsb;
     float *Cp = args.c + batch_idx * args.bsc;
@@ -157,13 +162,13 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
         for (int j = 0; j < TN; j++) acc[i][j] = (vf4acc){0.f, 0.f, 0.f, 0.f};
 
     auto load_slice = [&](int64_t k0) {
-        if constexpr (TA) la.load(A, args.lda, k0, m0, args.K, args.M);
-        else la.load(A, args.lda, m0, k0, args.M, args.K);
-        if constexpr (TB) lb.load(B, args.ldb, n0, k0, args.N, args.K);
-        else lb.load(B, args.ldb, k0, n0, args.K, args.N);
+        if constexpr (TA) la.load(A, args.lda, k0, m0, Kb, args.M);
+        else la.load(A, args.lda, m0, k0, args.M, Kb);
+        if constexpr (TB) lb.load(B, args.ldb, n0, k0, args.N, Kb);
+        else lb.load(B, args.ldb, k0, n0, Kb, args.N);
     };
 
-    const int64_t kslices = (args.K + BK - 1) / BK;
+    const int64_t kslices = (Kb + BK - 1) / BK;
     load_slice(0);
     la.template store<APITCH>(lds);
     lb.template store<BPITCH>(lds + ASIZE);
@@ -363,48 +368,32 @@ int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
     return launch_tiled<LargeTilesK16, true, true>(g, true, s);
 }
 
-// Split K: an output with fewer 256x256 tiles than CUs (the MLP's 8192x1024
-// and 4096x1024 GEMMs) runs its K in S slices as S batches of the large tile,
-// into a workspace of S partial products that one more pass sums in slice
-// order.  The workspace comes from the block cache and returns to it in
-// stream order.  `sak`/`sbk` are the operands' k strides.
+// Split K: an output with fewer tiles than CUs runs its K in S slices as S
+// batches of its tile, into a workspace of S partial products that one more
+// pass sums in slice order.  The workspace comes from the block cache and
+// returns to it in stream order.
+//   - The large tile (the MLP's 8192x1024 and 4096x1024 GEMMs): S a power of
+//     two up to 8 dividing K into slices of at least 1,024.
+//   - The 128x128 and 64x128 tiles, when they give at most one block per CU
+//     (1000^3 ran as 64 blocks, a 64x4096x4096 product as 32): S up to 16,
+//     for about two blocks per CU, slices of at least 256 k (the last one
+//     may be shorter), and at most 65,536 floats of partial products per CU.
 constexpr int64_t kMaxSplitK = 8;
 constexpr int64_t kMinSplitDepth = 1024;
-
-// Runs the split; returns TRS_E_ALLOCATION_FAILED without launching anything
-// when the workspace cannot be had (the caller then runs the unsplit tile).
-int launch_split_k(GemmArgs g, bool a_plain, bool b_plain, int64_t sak, int64_t sbk, int64_t S, hipStream_t s) {
-    float *const C = g.c;
-    const int64_t mn = g.M * g.N, Ks = g.K / S;
-    void *ws = nullptr;
-    int rc = trs_alloc((size_t)(S * mn) * sizeof(float), &ws);
-    if (rc) return rc;
-    g.c = (float *)ws;
-    g.K = Ks;
-    g.bsa = Ks * sak;
-    g.bsb = Ks * sbk;
-    g.bsc = mn;
-    g.batch = S;
-    rc = launch_large(g, a_plain, b_plain, s);
-    if (rc == TRS_OK) {
-        const int64_t n4 = mn / 4;
-        hipLaunchKernelGGL(splitk_sum, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, (const float4 *)ws,
-                           (float4 *)C, n4, (int)S);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) rc = hip_fail(e, "split-k sum launch");
-    }
-    const int frc = trs_free(ws);
-    return rc ? rc : frc;
-}
+constexpr int64_t kMaxTileSplit = 16;
+constexpr int64_t kMinTileSplitDepth = 256;
+constexpr int64_t kSplitFloatsPerCu = 65536;
 
 // Which kernel a product runs.  Tile choice:
 //   - the 256x256 tile when it divides M, N and K and gives every CU a block;
 //   - else, for an aligned single matrix with M, N multiples of 256 and a long
 //     K, the 256x256 tile over S K-slices, when S*tiles reaches half the CUs
 //     or at least the block count of the tile it replaces;
-//   - else 64x128 when 128x128 would give fewer than two blocks per CU (76%
-//     against 69% of peak measured at 4096x1024x8192), else 128x128 (full or
-//     edge-guarded).
+//   - else 64x128 when 128x128 would give fewer than two blocks per CU and
+//     64x128 divides the shape (76% against 69% of peak measured at
+//     4096x1024x8192), else 128x128 (full or edge-guarded);
+//   - a single matrix whose tile gives at most one block per CU splits K
+//     over that tile (above).
 enum class GemmKind { Strided, Large, SplitK, Medium, Small };
 struct GemmPlan {
     GemmKind kind = GemmKind::Strided;
@@ -412,7 +401,10 @@ struct GemmPlan {
     int64_t splits = 1;
     int64_t blocks = 0;
     bool full = false;
-    // SplitK only: the unsplit tile, run when no workspace can be allocated.
+    // SplitK only: the tile each slice runs on, the k per slice, and the
+    // unsplit plan, run when no workspace can be allocated.
+    GemmKind split_tile = GemmKind::Large;
+    int64_t ks = 0;
     GemmKind fallback = GemmKind::Small;
     bool fallback_full = false;
 };
@@ -437,17 +429,20 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
         return p;
     }
     const bool full = aligned && M % SmallTiles::BM == 0 && N % SmallTiles::BN == 0 && K % SmallTiles::BK == 0;
+    const bool medium_full =
+        aligned && M % MediumTiles::BM == 0 && N % MediumTiles::BN == 0 && K % MediumTiles::BK == 0;
     const int64_t small_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batch;
-    if (full && small_tiles < 2 * (int64_t)cu_count) {
+    if (medium_full && small_tiles < 2 * (int64_t)cu_count) {
         p.kind = GemmKind::Medium;
         p.bm = MediumTiles::BM, p.bn = MediumTiles::BN, p.bk = MediumTiles::BK;
-        p.blocks = ((M + 63) / 64) * ((N + 127) / 128) * batch;
+        p.blocks = (M / 64) * (N / 128) * batch;
+        p.full = true;
     } else {
         p.kind = GemmKind::Small;
         p.bm = SmallTiles::BM, p.bn = SmallTiles::BN, p.bk = SmallTiles::BK;
         p.blocks = small_tiles;
+        p.full = full;
     }
-    p.full = full;
     if (batch == 1 && large_fits && large_tiles > 0 && large_tiles < cu_count) {
         int64_t S = 1;
         while (S < kMaxSplitK && large_tiles * S * 2 <= cu_count && K % (S * 2 * large_bk) == 0 &&
@@ -457,13 +452,71 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
             p.fallback = p.kind;
             p.fallback_full = p.full;
             p.kind = GemmKind::SplitK;
+            p.split_tile = GemmKind::Large;
             p.bm = LargeTiles::BM, p.bn = LargeTiles::BN, p.bk = (int)large_bk;
             p.splits = S;
+            p.ks = K / S;
             p.blocks = large_tiles * S;
             p.full = true;
+            return p;
+        }
+    }
+    if (batch == 1 && p.blocks <= cu_count) {
+        int64_t S = std::min<int64_t>(kMaxTileSplit, 2 * (int64_t)cu_count / p.blocks);
+        S = std::min<int64_t>(S, K / kMinTileSplitDepth);
+        S = std::min<int64_t>(S, kSplitFloatsPerCu * cu_count / (M * N));
+        if (S >= 2) {
+            const int64_t ks = ((K + S - 1) / S + p.bk - 1) / p.bk * p.bk;
+            S = (K + ks - 1) / ks;
+            if (S >= 2) {
+                p.fallback = p.kind;
+                p.fallback_full = p.full;
+                p.split_tile = p.kind;
+                p.kind = GemmKind::SplitK;
+                p.splits = S;
+                p.ks = ks;
+                p.blocks *= S;
+            }
         }
     }
     return p;
+}
+
+// Runs a split plan; returns TRS_E_ALLOCATION_FAILED without launching
+// anything when the workspace cannot be had (the caller then runs the
+// unsplit tile).  `sak`/`sbk` are the operands' k strides.
+int launch_split_k(const GemmPlan &p, GemmArgs g, bool a_plain, bool b_plain, int64_t sak, int64_t sbk,
+                   hipStream_t s) {
+    float *const C = g.c;
+    const int64_t mn = g.M * g.N, S = p.splits, Ks = p.ks;
+    void *ws = nullptr;
+    int rc = trs_alloc((size_t)(S * mn) * sizeof(float), &ws);
+    if (rc) return rc;
+    g.c = (float *)ws;
+    g.ktotal = g.K;
+    g.K = Ks;
+    g.bsa = Ks * sak;
+    g.bsb = Ks * sbk;
+    g.bsc = mn;
+    g.batch = S;
+    switch (p.split_tile) {
+    case GemmKind::Large: rc = launch_large(g, a_plain, b_plain, s); break;
+    case GemmKind::Medium: rc = launch_layout<MediumTiles>(g, a_plain, b_plain, true, s); break;
+    default: rc = launch_layout<SmallTiles>(g, a_plain, b_plain, p.full, s); break;
+    }
+    if (rc == TRS_OK) {
+        if (mn % 4 == 0 && (uintptr_t)C % 16 == 0) {
+            const int64_t n4 = mn / 4;
+            hipLaunchKernelGGL(splitk_sum, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, (const float4 *)ws,
+                               (float4 *)C, n4, (int)S);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) rc = hip_fail(e, "split-k sum launch");
+        } else {
+            rc = launch_slice_sum((const float *)ws, C, mn, 1, S, s);
+        }
+    }
+    const int frc = trs_free(ws);
+    return rc ? rc : frc;
 }
 
 // Operand analysis shared by trs_matmul_f32 and trs_matmul_plan_f32: checks
@@ -537,6 +590,44 @@ int setup_gemm(const float *a, const trs_layout *la, const float *b, const trs_l
     return TRS_OK;
 }
 
+// The skinny form of a product whose operands each have a unit stride and
+// whose output has at most kSkinnyMaxRows rows or columns: the short side
+// is X's rows (A's rows, or B's columns read as B^T) and the other operand
+// is Y.  Returns false otherwise.
+bool skinny_problem(const GemmSetup &st, SkinnyProblem *sp) {
+    const GemmArgs &g = st.g;
+    if (!(st.a_plain || st.a_trans) || !(st.b_plain || st.b_trans)) return false;
+    const bool short_m = g.M <= g.N;
+    if ((short_m ? g.M : g.N) > kSkinnyMaxRows) return false;
+    SkinnyProblem p;
+    p.K = g.K;
+    p.batch = g.batch;
+    p.out = g.c;
+    if (short_m) {
+        // X(i, k) = A(i, k); Y(k, j) = B(k, j); C(i, j) at i*N + j.
+        p.x = g.a, p.y = g.b;
+        p.R = g.M, p.L = g.N;
+        p.xi = st.a_plain ? g.lda : 1;
+        p.xk = st.a_plain ? 1 : g.lda;
+        p.dot = !st.b_plain;
+        p.yl = g.ldb;
+        p.oi = g.N, p.oj = 1;
+        p.bx = g.bsa, p.by = g.bsb;
+    } else {
+        // X(i, k) = B(k, i); Y(k, j) = A(j, k); C(j, i) at j*N + i.
+        p.x = g.b, p.y = g.a;
+        p.R = g.N, p.L = g.M;
+        p.xi = st.b_plain ? 1 : g.ldb;
+        p.xk = st.b_plain ? g.ldb : 1;
+        p.dot = st.a_plain;
+        p.yl = g.lda;
+        p.oi = 1, p.oj = g.N;
+        p.bx = g.bsb, p.by = g.bsa;
+    }
+    *sp = p;
+    return true;
+}
+
 int run_unsplit(const GemmPlan &p, const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
     switch (p.kind) {
     case GemmKind::Large:
@@ -561,6 +652,9 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
     if (rc || st.empty_output) return rc;
     const GemmArgs &g = st.g;
     if (st.zero_k) return trs_memset_zero(g.c, (size_t)(g.M * g.N * g.batch) * sizeof(float));
+    SkinnyProblem sp;
+    SkinnyPlan spl;
+    if (skinny_problem(st, &sp) && plan_skinny(sp, dev->cu_count, &spl)) return run_skinny(sp, spl, dev->stream);
     const GemmPlan p = plan_gemm(g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, st.aligned, dev->cu_count);
     if (p.kind == GemmKind::Strided) {
         // An operand with no unit stride is gathered into a contiguous buffer
@@ -589,7 +683,7 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
         return TRS_OK;
     }
     if (p.kind == GemmKind::SplitK) {
-        rc = launch_split_k(g, st.a_plain, st.b_plain, st.sak, st.sbk, p.splits, dev->stream);
+        rc = launch_split_k(p, g, st.a_plain, st.b_plain, st.sak, st.sbk, dev->stream);
         if (rc != TRS_E_ALLOCATION_FAILED) return rc;
         // No workspace: the split is only an optimisation, so run the tile the
         // plan would otherwise have chosen (nothing was launched).
@@ -610,18 +704,31 @@ extern "C" int trs_matmul_plan_f32(const float *a, const trs_layout *la, const f
     int rc = setup_gemm(a, la, b, lb, const_cast<float *>(c), lc, false, &st);
     if (rc) return rc;
     GemmPlan p;
-    if (!st.empty_output && !st.zero_k)
-        p = plan_gemm(st.g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, st.aligned, dev->cu_count);
+    const bool work = !st.empty_output && !st.zero_k;
+    if (work) p = plan_gemm(st.g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, st.aligned, dev->cu_count);
+    GemmSetup sg;
+    const GemmSetup *ran = &st;
     if (p.kind == GemmKind::Strided) {
         // What trs_matmul_f32 runs: the plan of the gathered, contiguous
         // operands (their buffers come from the block cache, 256-byte aligned).
         const bool ga = !(st.a_plain || st.a_trans), gb = !(st.b_plain || st.b_trans);
         const trs_layout ca = contiguous_like(la), cb = contiguous_like(lb);
-        GemmSetup sg;
         rc = setup_gemm(ga ? nullptr : a, ga ? &ca : la, gb ? nullptr : b, gb ? &cb : lb, const_cast<float *>(c), lc,
                         false, &sg);
         if (rc) return rc;
         p = plan_gemm(sg.g, sg.a_plain, sg.a_trans, sg.b_plain, sg.b_trans, sg.aligned, dev->cu_count);
+        ran = &sg;
+    }
+    SkinnyProblem sp;
+    SkinnyPlan spl;
+    if (work && skinny_problem(*ran, &sp) && plan_skinny(sp, dev->cu_count, &spl)) {
+        // The short side's padded MFMA rows by the 64 columns of a block.
+        const bool short_m = ran->g.M <= ran->g.N;
+        p.bm = short_m ? 16 * spl.row_groups : kSkinnyCols;
+        p.bn = short_m ? kSkinnyCols : 16 * spl.row_groups;
+        p.bk = (int)spl.kc;
+        p.splits = spl.splits;
+        p.blocks = spl.blocks;
     }
     if (tile_m) *tile_m = p.bm;
     if (tile_n) *tile_n = p.bn;

@@ -1,0 +1,56 @@
+// gemm_skinny.h -- products with a short output side (at most 32 rows or
+// columns), shared by gemm.hip (which chooses them) and gemm_skinny.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace trs {
+
+// out(i, j) = sum_k X(i, k) * Y(k, j) for i < R, j < L, k < K, per batch.
+// X is the short operand, Y the long one.  Y has a unit stride along k
+// (`dot`, element (k, j) at y + j*yl + k) or along j (element at
+// y + k*yl + j).  The output is contiguous per batch (element (i, j) at
+// out + i*oi + j*oj, batch stride R*L), so either (oi, oj) = (L, 1) or
+// (1, R).
+struct SkinnyProblem {
+    const float *x = nullptr;
+    const float *y = nullptr;
+    float *out = nullptr;
+    int64_t xi = 0, xk = 0;
+    int64_t yl = 0;
+    bool dot = false;
+    int64_t oi = 0, oj = 0;
+    int64_t bx = 0, by = 0;
+    int64_t R = 0, L = 0, K = 0, batch = 1;
+};
+
+struct SkinnyPlan {
+    int row_groups = 1;   // 16-row MFMA groups covering R
+    bool yvec = false;    // Y read as float4 (else four scalar loads)
+    bool xvec = false;    // X rows read as float4 along k
+    int64_t kc = 0;       // k per split (a multiple of 16)
+    int64_t splits = 1;   // K split into this many slices, summed in slice order
+    int64_t blocks = 0;
+};
+
+constexpr int64_t kSkinnyMaxRows = 32;
+constexpr int kSkinnyCols = 64;  // output columns per block
+
+// Fills `plan` and returns true when the kernel takes the problem (R at
+// most kSkinnyMaxRows).  Y is read as float4 when 16-byte aligned with yl
+// and by multiples of 4; X likewise when xk is 1.
+bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan);
+
+// c[b*mn + e] = ((p0 + p1) + p2) + ... over S partial products in slice
+// order, slice s of batch b at ws[(b*S + s)*mn + e]; one float per lane, so
+// any mn and alignment.
+int launch_slice_sum(const float *ws, float *c, int64_t mn, int64_t batch, int64_t S, hipStream_t s);
+
+// Runs the plan on stream `s`.  A split plan takes a workspace of
+// splits * R * L * batch floats from the block cache; without one it runs
+// unsplit.
+int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s);
+
+}  // namespace trs

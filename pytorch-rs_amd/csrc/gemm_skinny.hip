@@ -1,0 +1,328 @@
+// gemm_skinny.hip -- fp32 products with a short output side on FP32 MFMA.
+//
+// Replaces Tensor::matmul (src/tensor.rs:2453-2533, 3872-3994) for outputs
+// of at most 32 rows or columns: matrix-vector products and small-batch
+// linear layers.  These read one long operand Y once and do little
+// arithmetic per byte, so the bound is HBM.  On the square-tile kernel
+// (gemm.hip) a [1, 4096] x [4096, 4096] product ran as 32 blocks, each
+// walking all of K, and took ~350 us for 64 MiB.
+//
+// Layout of the work: the short operand X (R <= 32 rows) is the MFMA's A
+// operand, padded with zero rows to 16 or 32; Y supplies the B operand.  A
+// block owns 64 output columns and one slice of K; its 4 waves take
+// alternate 32-k steps of that slice and their accumulators are added in
+// wave order through LDS at the end.  K is split into slices so the grid
+// holds ~4 blocks per CU; the slices' partial products go to a workspace
+// and one more pass adds them in slice order.
+//
+// Fragments straight from global memory, no LDS staging (each Y element is
+// used by one lane of one MFMA):
+//   - Y unit-stride along k ("dot" form, e.g. W.mT): lane (fi, fk) loads
+//     float4 k = kg + 4fk .. +3 of row j = 16t + fi, and MFMA step e of the
+//     16-k group takes its component e (the MFMA sums k in any order);
+//   - Y unit-stride along j: lane (fi, fk) loads float4 columns 4fi .. 4fi+3
+//     of row k = kg + 4fk + e, and component c feeds column sub-tile c, so
+//     output column 4fi + c comes from lane fi of sub-tile c.
+// Either way one float4 of Y feeds four MFMAs per 16-row group of X.
+//
+// The sum is fp32 in MFMA order, then wave order, then slice order; like
+// gemm.hip it is checked against the reference's sequential sum within
+// |dC| <= 1e-5*sqrt(K)*(|A||B|).  Zero padding (rows of X past R, columns
+// of Y past L, k past the slice) only meets outputs that are not stored, so
+// an infinity in X or Y cannot turn a stored output into NaN through it.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "gemm_skinny.h"
+#include "trs_internal.h"
+
+namespace trs {
+
+namespace {
+
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
+struct SkinnyArgs {
+    const float *x;
+    const float *y;
+    float *o;
+    int64_t xi, xk, yl;
+    int64_t oi, oj, bo, os;  // output strides: (i, j), batch, slice
+    int64_t bx, by;
+    int64_t R, L, K, kc;
+    int32_t S, jblocks;
+};
+
+constexpr int kWaves = 4;
+constexpr int kStepK = 32;  // k per wave step
+
+template <bool VEC>
+__device__ __forceinline__ vf4 load4(const float *p) {
+    if constexpr (VEC) return *(const vf4 *)p;
+    else return (vf4){p[0], p[1], p[2], p[3]};
+}
+
+template <bool DOT, bool YVEC, bool XVEC, int RG>
+__global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
+    // 16-k groups a wave loads before its MFMAs: two where they fit in the
+    // 128 registers of 4 waves per SIMD without spilling, else one (then
+    // a step is two load-then-MFMA rounds).
+    constexpr int kGroups = (RG == 1 && YVEC) ? 2 : 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int fi = lane & 15, fk = lane >> 4;
+    int64_t bid = blockIdx.x;
+    const int64_t jb = bid % g.jblocks;
+    bid /= g.jblocks;
+    const int64_t s = bid % g.S, b = bid / g.S;
+    const int64_t j0 = jb * kSkinnyCols;
+    const int64_t kbeg = s * g.kc, kend = std::min(g.K, kbeg + g.kc);
+    const float *X = g.x + b * g.bx;
+    const float *Y = g.y + b * g.by;
+
+    // This lane's X row in each 16-row group (zero past R).
+    const float *xrow[RG];
+    bool xin[RG];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++) {
+        const int64_t i = 16 * rg + fi;
+        xin[rg] = i < g.R;
+        xrow[rg] = X + (xin[rg] ? i : 0) * g.xi;
+    }
+    // Dot form: this lane's Y row in each column sub-tile.  Otherwise: how
+    // many of its four columns lie below L.
+    const float *yrow[4];
+    bool yin[4];
+    int ncols = 0;
+    if constexpr (DOT) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int64_t j = j0 + 16 * t + fi;
+            yin[t] = j < g.L;
+            yrow[t] = Y + (yin[t] ? j : 0) * g.yl;
+        }
+    } else {
+        ncols = (int)std::max<int64_t>(0, std::min<int64_t>(4, g.L - (j0 + 4 * fi)));
+    }
+
+    vf4 acc[RG][4];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[rg][t] = (vf4){0.f, 0.f, 0.f, 0.f};
+
+    // Loads one 16-k group starting at kg.  GUARD: k may reach kend.
+    auto load_group = [&]<bool GUARD>(int64_t kg, vf4 (&ya)[4], vf4 (&xa)[RG]) {
+        const int64_t k4 = kg + 4 * fk;
+        if constexpr (DOT) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                if (!GUARD) {
+                    ya[t] = yin[t] ? load4<YVEC>(yrow[t] + k4) : (vf4){0.f, 0.f, 0.f, 0.f};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) ya[t][e] = (yin[t] && k4 + e < kend) ? yrow[t][k4 + e] : 0.f;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int64_t k = k4 + e;
+                const float *p = Y + k * g.yl + j0 + 4 * fi;
+                const bool kin = !GUARD || k < kend;
+                if (YVEC && kin && ncols == 4) {
+                    ya[e] = load4<true>(p);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; c++) ya[e][c] = (kin && c < ncols) ? p[c] : 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int rg = 0; rg < RG; rg++) {
+            if (!GUARD && XVEC) {
+                xa[rg] = xin[rg] ? load4<true>(xrow[rg] + k4) : (vf4){0.f, 0.f, 0.f, 0.f};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    xa[rg][e] = (xin[rg] && (!GUARD || k4 + e < kend)) ? xrow[rg][(k4 + e) * g.xk] : 0.f;
+            }
+        }
+    };
+
+    auto mma_group = [&](const vf4 (&ya)[4], const vf4 (&xa)[RG]) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    acc[rg][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[rg][e], DOT ? ya[t][e] : ya[e][t],
+                                                                      acc[rg][t], 0, 0, 0);
+    };
+
+    for (int64_t k0 = kbeg + (int64_t)kStepK * wave; k0 < kend; k0 += (int64_t)kStepK * kWaves) {
+        const bool whole = k0 + kStepK <= kend;
+#pragma unroll
+        for (int h = 0; h < kStepK / 16; h += kGroups) {
+            vf4 ya[kGroups][4], xa[kGroups][RG];
+            if (whole) {
+#pragma unroll
+                for (int u = 0; u < kGroups; u++)
+                    load_group.template operator()<false>(k0 + 16 * (h + u), ya[u], xa[u]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < kGroups; u++)
+                    load_group.template operator()<true>(k0 + 16 * (h + u), ya[u], xa[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < kGroups; u++) mma_group(ya[u], xa[u]);
+        }
+    }
+
+    // Waves' accumulators added in wave order; wave w finishes sub-tile w.
+    // Lane (fi, fk) holds output rows 16rg + 4fk + r of sub-tile t's column
+    // for lane slot fi.
+    __shared__ float red[kWaves][RG * 16][64];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[wave][rg * 16 + t * 4 + r][lane] = acc[rg][t][r];
+    __syncthreads();
+    const int t = wave;
+    const int64_t j = DOT ? j0 + 16 * t + fi : j0 + 4 * fi + t;
+    float *O = g.o + b * g.bo + s * g.os;
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int q = rg * 16 + t * 4 + r;
+            float v = red[0][q][lane];
+#pragma unroll
+            for (int w = 1; w < kWaves; w++) v += red[w][q][lane];
+            const int64_t i = 16 * rg + 4 * fk + r;
+            if (i < g.R && j < g.L) O[i * g.oi + j * g.oj] = v;
+        }
+    }
+}
+
+// c[e] = ((p0 + p1) + p2) + ... over the S slices of e's batch, in slice
+// order.  Slice s of batch b starts at ws + (b*S + s)*mn.
+__global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, float *__restrict__ c, int64_t mn,
+                                                  int64_t total, int S) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= total) return;
+    const int64_t b = e / mn, r = e - b * mn;
+    const float *p = ws + b * S * mn + r;
+    float v = p[0];
+    int s = 1;
+    for (; s + 7 < S; s += 8) {
+        float part[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) part[q] = p[(int64_t)(s + q) * mn];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v += part[q];
+    }
+    for (; s < S; s++) v += p[(int64_t)s * mn];
+    c[e] = v;
+}
+
+template <bool DOT, bool YVEC, bool XVEC>
+int launch_rg(int rg, dim3 grid, hipStream_t s, const SkinnyArgs &g) {
+    if (rg == 1) hipLaunchKernelGGL((gemm_f32_skinny<DOT, YVEC, XVEC, 1>), grid, dim3(256), 0, s, g);
+    else hipLaunchKernelGGL((gemm_f32_skinny<DOT, YVEC, XVEC, 2>), grid, dim3(256), 0, s, g);
+    TRS_LAUNCH_CHECK("skinny gemm launch");
+    return TRS_OK;
+}
+
+// With Y read as scalars, X is too (a float4 X there only adds registers).
+template <bool DOT>
+int launch_form(bool yvec, bool xvec, int rg, dim3 grid, hipStream_t s, const SkinnyArgs &g) {
+    if (yvec) return xvec ? launch_rg<DOT, true, true>(rg, grid, s, g) : launch_rg<DOT, true, false>(rg, grid, s, g);
+    return launch_rg<DOT, false, false>(rg, grid, s, g);
+}
+
+bool aligned16(const void *p) { return (uintptr_t)p % 16 == 0; }
+
+}  // namespace
+
+bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
+    if (p.R < 1 || p.R > kSkinnyMaxRows || p.L < 1 || p.K < 1 || p.batch < 1 || cu_count < 1) return false;
+    SkinnyPlan pl;
+    pl.row_groups = p.R <= 16 ? 1 : 2;
+    pl.yvec = aligned16(p.y) && p.yl % 4 == 0 && (p.batch == 1 || p.by % 4 == 0);
+    pl.xvec = p.xk == 1 && aligned16(p.x) && (p.R == 1 || p.xi % 4 == 0) && (p.batch == 1 || p.bx % 4 == 0);
+    const int64_t jblocks = (p.L + kSkinnyCols - 1) / kSkinnyCols;
+    const int64_t base = jblocks * p.batch;
+    // ~4 blocks per CU; each slice at least 128 deep (one step per wave), and
+    // the partial products' traffic (written and read back) at most 1/8 of Y's.
+    const int64_t want = (4 * (int64_t)cu_count + base - 1) / base;
+    const int64_t cap = std::max<int64_t>(1, std::min(p.K / 128, p.K / (16 * p.R)));
+    int64_t S = std::clamp<int64_t>(want, 1, cap);
+    int64_t kc = (p.K + S - 1) / S;
+    kc = (kc + 127) / 128 * 128;
+    S = (p.K + kc - 1) / kc;
+    if (base * S > INT32_MAX || jblocks > INT32_MAX) return false;
+    pl.kc = kc;
+    pl.splits = S;
+    pl.blocks = base * S;
+    *plan = pl;
+    return true;
+}
+
+int launch_slice_sum(const float *ws, float *c, int64_t mn, int64_t batch, int64_t S, hipStream_t s) {
+    const int64_t total = mn * batch;
+    hipLaunchKernelGGL(slice_sum, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws, c, mn, total, (int)S);
+    TRS_LAUNCH_CHECK("gemm slice sum launch");
+    return TRS_OK;
+}
+
+int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
+    SkinnyArgs g{};
+    g.x = p.x;
+    g.y = p.y;
+    g.xi = p.xi;
+    g.xk = p.xk;
+    g.yl = p.yl;
+    g.oi = p.oi;
+    g.oj = p.oj;
+    g.bx = p.bx;
+    g.by = p.by;
+    g.R = p.R;
+    g.L = p.L;
+    g.K = p.K;
+    g.jblocks = (int32_t)((p.L + kSkinnyCols - 1) / kSkinnyCols);
+    const int64_t mn = p.R * p.L;
+    int64_t S = plan.splits, kc = plan.kc;
+    void *ws = nullptr;
+    // The split only adds blocks: without a workspace the product runs unsplit.
+    if (S > 1 && trs_alloc((size_t)(S * mn * p.batch) * sizeof(float), &ws) != TRS_OK) {
+        ws = nullptr;
+        S = 1;
+    }
+    if (S == 1) kc = p.K;
+    g.S = (int32_t)S;
+    g.kc = kc;
+    if (ws) {
+        g.o = (float *)ws;
+        g.os = mn;
+        g.bo = S * mn;
+    } else {
+        g.o = p.out;
+        g.os = 0;
+        g.bo = mn;
+    }
+    const dim3 grid((unsigned)((int64_t)g.jblocks * S * p.batch));
+    int rc = p.dot ? launch_form<true>(plan.yvec, plan.xvec, plan.row_groups, grid, s, g)
+                   : launch_form<false>(plan.yvec, plan.xvec, plan.row_groups, grid, s, g);
+    if (rc == TRS_OK && ws) rc = launch_slice_sum((const float *)ws, p.out, mn, p.batch, S, s);
+    if (ws) {
+        const int frc = trs_free(ws);
+        if (!rc) rc = frc;
+    }
+    return rc;
+}
+
+}  // namespace trs

@@ -234,19 +234,43 @@ def test_split_k_all_layouts_exact_on_small_integers(m, k, n, s, ta, tb):
     assert np.array_equal(U.matmul(sa, *la, sb, *lb), want)
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 2048, 256), (1024, 4096, 1024), (512, 4096, 1024)])
-def test_split_k_not_taken_where_it_gives_fewer_blocks(m, k, n):
-    """Splitting these into 256x256 slices would give fewer blocks than the
-    64x128 tile (and fill less than half the CUs), so they run unsplit on it;
+# Outputs whose 128x128 or 64x128 tile gives at most one block per CU: K is
+# split over that tile for about two blocks per CU, in slices of at least 256
+# k rounded up to the tile's depth (the last slice may be shorter).  The
+# first three would give fewer blocks split over the 256x256 tile.  Values
+# are the (tile_m, tile_n, splits) of a 256-CU device.
+TILE_SPLIT = [((256, 2048, 256), (64, 128, 8)), ((1024, 4096, 1024), (64, 128, 4)), ((512, 4096, 1024), (64, 128, 8)),
+              ((64, 4096, 4096), (64, 128, 16)), ((1000, 1000, 1000), (128, 128, 3)),
+              ((2047, 2047, 2047), (128, 128, 2)), ((33, 1000, 65), (128, 128, 3))]
+
+
+@pytest.mark.parametrize("mkn,plan", TILE_SPLIT)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_tile_split_all_layouts_exact_on_small_integers(mkn, plan, ta, tb):
+    """The plan splits as listed; slices of ragged K (1000, 2047) end short,
+    and outputs of any element count (33 x 65) are summed one float per lane;
     the products are exact on small integers."""
+    m, k, n = mkn
     if _cu_count() != 256:
         pytest.skip("plan expectations are those of a 256-CU device")
-    assert _plan(m, k, n)[:4] == (64, 128, 32, 1)
-    rng = np.random.default_rng(m + n)
+    got_plan = _plan(m, k, n, ta, tb)
+    assert (got_plan[0], got_plan[1], got_plan[3]) == plan, got_plan
+    rng = np.random.default_rng(m + n + 2 * ta + tb)
     a = rng.integers(-3, 4, (m, k)).astype(np.float32)
     b = rng.integers(-3, 4, (k, n)).astype(np.float32)
     want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
-    assert np.array_equal(U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0), want)
+    sa, la, sb, lb = _layouts(a, b, ta, tb)
+    assert np.array_equal(U.matmul(sa, *la, sb, *lb), want)
+
+
+@pytest.mark.parametrize("m,k,n", [(1000, 1000, 1000), (64, 4096, 4096)])
+def test_tile_split_normal_inputs_within_tolerance(m, k, n):
+    rng = np.random.default_rng(31 + m)
+    a = (rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    got = U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0)
+    want = O.matmul_threads(a, b, threads=_oracle_threads())
+    _check_tol(got, want, _abs_bound(a, b), k)
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])

@@ -1,0 +1,146 @@
+"""GPU parity of trs_matmul_f32 on outputs with a short side (at most 32 rows
+or columns: matrix-vector products, small-batch linear layers), which run the
+streaming skinny kernel with K split over slices.
+
+Bar (north_star), as for every matmul: exact on small integers (every partial
+sum exact, so any summation order gives the integer product), and
+|C_gpu - C_ref| <= 1e-5 * sqrt(K) * (|A| |B|) elementwise against the
+oracle's sequential sum (src/tensor.rs:3919-3966) on normal data.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import gpu_util as U
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _plan(ashape, astr, aoff, bshape, bstr, boff):
+    from trs_backend import abi
+    la, lb = abi.layout_of(ashape, astr, aoff), abi.layout_of(bshape, bstr, boff)
+    oshape = tuple(ashape[:-1]) + (bshape[-1],)
+    lc = abi.layout_of(oshape)
+    tm, tn, tk = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    sp, bl = ctypes.c_int64(), ctypes.c_int64()
+    # 256-byte-aligned stand-in addresses shifted by the offsets, as the
+    # device buffers of gpu_util.matmul are.
+    abi.check(abi.lib.trs_matmul_plan_f32(0x10000000000, ctypes.byref(la), 0x20000000000, ctypes.byref(lb),
+                                          0x30000000000, ctypes.byref(lc), ctypes.byref(tm), ctypes.byref(tn),
+                                          ctypes.byref(tk), ctypes.byref(sp), ctypes.byref(bl)))
+    return tm.value, tn.value, tk.value, sp.value, bl.value
+
+
+def _operands(rng, m, k, n, ta, tb, batch=0, aoff=0, boff=0, ints=True):
+    nb = max(batch, 1)
+    if ints:
+        a = rng.integers(-3, 4, size=(nb, m, k)).astype(np.float32)
+        b = rng.integers(-3, 4, size=(nb, k, n)).astype(np.float32)
+    else:
+        a = (rng.standard_normal((nb, m, k)) / np.sqrt(k)).astype(np.float32)
+        b = rng.standard_normal((nb, k, n)).astype(np.float32)
+    sa = np.concatenate([np.zeros(aoff, np.float32), (np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a).ravel()])
+    sb = np.concatenate([np.zeros(boff, np.float32), (np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b).ravel()])
+    ast = (1, m) if ta else (k, 1)
+    bst = (1, k) if tb else (n, 1)
+    if batch:
+        la = ((batch, m, k), (m * k,) + ast, aoff)
+        lb = ((batch, k, n), (k * n,) + bst, boff)
+    else:
+        la, lb = ((m, k), ast, aoff), ((k, n), bst, boff)
+        a, b = a[0], b[0]
+    return a, b, sa, la, sb, lb
+
+
+LAYOUTS = [(False, False), (False, True), (True, False), (True, True)]
+
+# (M, K, N): short side M or N from 1 to 32, K below one slice, ragged, and
+# long enough to split; the long side ragged against the 64-column blocks.
+SHAPES = [
+    (1, 4096, 4096), (4096, 4096, 1), (8, 1000, 300), (300, 1000, 8), (16, 2048, 1000), (1000, 2048, 16),
+    (17, 777, 513), (513, 777, 17), (32, 4096, 96), (96, 4096, 32), (3, 5, 7), (1, 1, 1), (31, 130, 2),
+    (2, 130, 31), (1, 100003, 3), (5, 64, 4099), (24, 24, 24),
+]
+
+
+def test_short_sides_plan_the_skinny_kernel():
+    """Rows of the short side are padded to 16 or 32 by 64 columns a block;
+    33 rows go to the square tiles; K is split to fill the device."""
+    plain = lambda m, k, n: _plan((m, k), (k, 1), 0, (k, n), (n, 1), 0)
+    assert plain(1, 4096, 4096)[:2] == (16, 64) and plain(1, 4096, 4096)[3] > 1
+    assert plain(4096, 4096, 1)[:2] == (64, 16)
+    assert plain(16, 512, 4096)[:2] == (16, 64) and plain(17, 512, 4096)[:2] == (32, 64)
+    assert plain(32, 512, 4096)[:2] == (32, 64) and plain(33, 512, 4096)[:2] != (32, 64)
+    assert plain(4096, 512, 32)[:2] == (64, 32)
+    tm, tn, tk, s, blocks = plain(1, 4096, 4096)
+    assert tk % 128 == 0 and s * tk >= 4096 and blocks == (4096 // 64) * s
+    assert plain(1, 100, 4096)[3] == 1  # K shorter than one slice
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_skinny_small_integers_exact(m, k, n, ta, tb):
+    rng = np.random.default_rng(m + 3 * k + 7 * n + 11 * ta + 13 * tb)
+    a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb)
+    got = U.matmul(sa, *la, sb, *lb)
+    assert np.array_equal(got, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 4096), (4096, 4096, 1), (16, 3000, 700), (700, 3000, 32)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_skinny_normal_inputs_within_tolerance(m, k, n, ta, tb):
+    rng = np.random.default_rng(91 + m + n + 2 * ta + tb)
+    a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, ints=False)
+    got = U.matmul(sa, *la, sb, *lb)
+    want = O.matmul(sa, *la, sb, *lb).reshape(m, n)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    tol = 1e-5 * np.sqrt(k) * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+    assert (err <= tol).all(), err.max()
+
+
+@pytest.mark.parametrize("aoff,boff", [(1, 0), (0, 3), (2, 2)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_skinny_misaligned_and_odd_strides_exact(aoff, boff, ta, tb):
+    """Operands at offsets that break 16-byte alignment, and a row length of
+    1,001 floats, take the scalar-load variants; still exact."""
+    rng = np.random.default_rng(5 + aoff + 7 * boff + 2 * ta + tb)
+    for m, k, n in [(7, 1001, 1001), (1001, 1001, 7), (1, 517, 2050)]:
+        a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, aoff=aoff, boff=boff)
+        got = U.matmul(sa, *la, sb, *lb)
+        assert np.array_equal(got, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)), (m, k, n)
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_skinny_batched_exact(ta, tb):
+    rng = np.random.default_rng(17 + 2 * ta + tb)
+    for batch, m, k, n in [(5, 4, 300, 700), (3, 700, 1500, 20), (64, 1, 512, 512), (2, 32, 8192, 64)]:
+        a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, batch=batch)
+        got = U.matmul(sa, *la, sb, *lb)
+        want = np.matmul(a.astype(np.int64), b.astype(np.int64)).astype(np.float32)
+        assert np.array_equal(got.reshape(want.shape), want), (batch, m, k, n)
+
+
+def test_skinny_special_values_across_slices():
+    """Infinities and a NaN in different K slices of a split matrix-vector
+    product and of a 20-row product: NaN and signed-infinity positions equal
+    the oracle's; finite elements within tolerance.  Zero padding never meets
+    a stored output, so an infinity does not spread NaN to other rows."""
+    rng = np.random.default_rng(23)
+    for m, k, n in [(1, 8192, 2048), (20, 8192, 300), (2048, 8192, 3)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        a[0, 100] = np.inf
+        a[m - 1, 6000] = -np.inf
+        b[4000, n - 1] = np.nan
+        b[7000, 0] = np.inf
+        got = U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0)
+        want = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+        for pred in (np.isnan, np.isposinf, np.isneginf):
+            assert np.array_equal(pred(got), pred(want)), (m, k, n, pred.__name__)
+        fin = np.isfinite(want)
+        with np.errstate(invalid="ignore", over="ignore"):
+            bound = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+        err = np.abs(got[fin].astype(np.float64) - want[fin].astype(np.float64))
+        assert (err <= 1e-5 * np.sqrt(k) * bound[fin]).all()
