@@ -52,6 +52,10 @@ struct GemmArgs {
     // slice stops at ktotal; 0 when every batch has depth K.
     int64_t ktotal;
     int32_t tiles_m, tiles_n;
+    // Operands 16-byte aligned with row strides (and batch strides) that
+    // are multiples of 4 floats: interior tiles of the edge-guarded kernel
+    // then load as float4.
+    int32_t vec_ok;
     int32_t xcd_remap;
 };
 
@@ -60,14 +64,16 @@ constexpr int kXcds = 8;
 
 // Load an R x C tile whose C dim is contiguous in memory (row stride ld),
 // starting at (r0, c0) of an Rv x Cv matrix, into registers: NT lanes, one
-// float4 each per step.
-template <int R, int C, int NT, bool FULL>
+// float4 each per step.  FULL: the tile lies inside the matrix and rows are
+// 16-byte aligned; otherwise each element is bounds-checked.
+template <int R, int C, int NT>
 struct TileLoader {
     static constexpr int kVec = R * C / 4;          // float4 per tile
     static constexpr int kPerThread = kVec / NT;    // float4 per lane
     static_assert(kVec % NT == 0 && kPerThread >= 1, "tile must split evenly over the block");
     vf4 v[kPerThread];
 
+    template <bool FULL>
     __device__ __forceinline__ void load(const float *src, int64_t ld, int64_t r0, int64_t c0, int64_t Rv,
                                          int64_t Cv) {
 #pragma unroll
@@ -79,13 +85,17 @@ struct TileLoader {
             if constexpr (FULL) {
                 v[i] = *(const vf4 *)(src + gr * ld + gc);
             } else {
-                vf4 t = {0.f, 0.f, 0.f, 0.f};
-                if (gr < Rv) {
-                    const float *p = src + gr * ld;
-                    if (gc + 0 < Cv) t.x = p[gc + 0];
-                    if (gc + 1 < Cv) t.y = p[gc + 1];
-                    if (gc + 2 < Cv) t.z = p[gc + 2];
-                    if (gc + 3 < Cv) t.w = p[gc + 3];
+                // Branch-free: an element outside the matrix loads the
+                // matrix's first element instead and is replaced by 0, so
+                // every load of the slice is issued before any is waited for.
+                const bool rin = gr < Rv;
+                const float *p = src + (rin ? gr : 0) * ld;
+                vf4 t;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const bool in = rin && gc + e < Cv;
+                    const float x = p[in ? gc + e : 0];
+                    t[e] = in ? x : 0.f;
                 }
                 v[i] = t;
             }
@@ -151,8 +161,8 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
     const int wave = threadIdx.x >> 6;
     const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
 
-    TileLoader<AR, AC, NT, FULL> la;
-    TileLoader<BR, BC, NT, FULL> lb;
+    TileLoader<AR, AC, NT> la;
+    TileLoader<BR, BC, NT> lb;
 
     typedef float vf4acc __attribute__((ext_vector_type(4)));
     vf4acc acc[TM][TN];
@@ -161,15 +171,20 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = (vf4acc){0.f, 0.f, 0.f, 0.f};
 
-    auto load_slice = [&](int64_t k0) {
-        if constexpr (TA) la.load(A, args.lda, k0, m0, Kb, args.M);
-        else la.load(A, args.lda, m0, k0, args.M, Kb);
-        if constexpr (TB) lb.load(B, args.ldb, n0, k0, args.N, Kb);
-        else lb.load(B, args.ldb, k0, n0, Kb, args.N);
+    auto load_tiles = [&]<bool F>(int64_t k0) {
+        if constexpr (TA) la.template load<F>(A, args.lda, k0, m0, Kb, args.M);
+        else la.template load<F>(A, args.lda, m0, k0, args.M, Kb);
+        if constexpr (TB) lb.template load<F>(B, args.ldb, n0, k0, args.N, Kb);
+        else lb.template load<F>(B, args.ldb, k0, n0, Kb, args.N);
     };
-
+    // The edge-guarded kernel checks bounds only in tiles that cross the
+    // matrix's edge (or when rows are not 16-byte aligned): an interior tile's
+    // first kvec slices, all but a ragged last one, load as float4.
     const int64_t kslices = (Kb + BK - 1) / BK;
-    load_slice(0);
+    const bool inner = args.vec_ok && m0 + BM <= args.M && n0 + BN <= args.N;
+    const int64_t kvec = FULL ? kslices : (inner ? Kb / BK : 0);
+    if (FULL || kvec > 0) load_tiles.template operator()<true>(0);
+    else load_tiles.template operator()<false>(0);
     la.template store<APITCH>(lds);
     lb.template store<BPITCH>(lds + ASIZE);
     __syncthreads();
@@ -183,12 +198,14 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
     const int fi = lane & 15;
     const int fk = lane >> 4;
 
-    for (int64_t s = 0; s < kslices; s++) {
+    // One slice: prefetch slice s+1 (as float4 when F) into registers, run
+    // slice s's MFMAs from LDS, then store the prefetch to the other buffer.
+    auto step = [&]<bool F>(int64_t s) {
         const int cur = (int)(s & 1);
         const float *As = lds + cur * (ASIZE + BSIZE);
         const float *Bs = As + ASIZE;
         const bool more = s + 1 < kslices;
-        if (more) load_slice((s + 1) * BK);
+        if (more) load_tiles.template operator()<F>((s + 1) * BK);
         if constexpr (VK) {
             // Kept rolled: unrolled, the groups' fragment reads are all
             // hoisted and BK=32 spills at 16 waves; rolled, one barrier per
@@ -252,6 +269,16 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
             lb.template store<BPITCH>(An + ASIZE);
         }
         __syncthreads();
+    };
+    // Two loops, each with one kind of load: a load under a per-slice
+    // condition makes the compiler wait for it before the MFMAs, which
+    // undoes the prefetch.
+    if constexpr (FULL) {
+        for (int64_t s = 0; s < kslices; s++) step.template operator()<true>(s);
+    } else {
+        int64_t s = 0;
+        for (; s + 1 < kvec; s++) step.template operator()<true>(s);
+        for (; s < kslices; s++) step.template operator()<false>(s);
     }
 
     // ---- epilogue: lane holds C[4*(lane/16)+r][lane%16] of each 16x16 tile ----
@@ -376,12 +403,12 @@ int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
 //     two up to 8 dividing K into slices of at least 1,024.
 //   - The 128x128 and 64x128 tiles, when they give at most one block per CU
 //     (1000^3 ran as 64 blocks, a 64x4096x4096 product as 32): S up to 16,
-//     for about two blocks per CU, slices of at least 256 k (the last one
+//     for about two blocks per CU, slices of at least 128 k (the last one
 //     may be shorter), and at most 65,536 floats of partial products per CU.
 constexpr int64_t kMaxSplitK = 8;
 constexpr int64_t kMinSplitDepth = 1024;
 constexpr int64_t kMaxTileSplit = 16;
-constexpr int64_t kMinTileSplitDepth = 256;
+constexpr int64_t kMinTileSplitDepth = 128;
 constexpr int64_t kSplitFloatsPerCu = 65536;
 
 // Which kernel a product runs.  Tile choice:
@@ -587,6 +614,7 @@ int setup_gemm(const float *a, const trs_layout *la, const float *b, const trs_l
     auto al16 = [](const float *p) { return ((uintptr_t)p % 16) == 0; };
     st->aligned = al16(g.a) && al16(g.b) && al16(g.c) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                   (batch == 1 || (bsa % 4 == 0 && bsb % 4 == 0));
+    g.vec_ok = st->aligned ? 1 : 0;
     return TRS_OK;
 }
 

@@ -10,7 +10,7 @@
 // Layout of the work: the short operand X (R <= 32 rows) is the MFMA's A
 // operand, padded with zero rows to 16 or 32; Y supplies the B operand.  A
 // block owns 64 output columns and one slice of K; its 4 waves take
-// alternate 32-k steps of that slice and their accumulators are added in
+// consecutive quarters of that slice and their accumulators are added in
 // wave order through LDS at the end.  K is split into slices so the grid
 // holds ~4 blocks per CU; the slices' partial products go to a workspace
 // and one more pass adds them in slice order.
@@ -63,8 +63,10 @@ __device__ __forceinline__ vf4 load4(const float *p) {
     else return (vf4){p[0], p[1], p[2], p[3]};
 }
 
+// Four waves per SIMD (128 registers), except the unaligned, scalar-load
+// form with 32 rows, which needs a few more and runs three.
 template <bool DOT, bool YVEC, bool XVEC, int RG>
-__global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
+__global__ void __launch_bounds__(256, (!DOT && !YVEC && RG == 2) ? 3 : 4) gemm_f32_skinny(SkinnyArgs g) {
     // 16-k groups a wave loads before its MFMAs: two where they fit in the
     // 128 registers of 4 waves per SIMD without spilling, else one (then
     // a step is two load-then-MFMA rounds).
@@ -77,6 +79,10 @@ __global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
     const int64_t s = bid % g.S, b = bid / g.S;
     const int64_t j0 = jb * kSkinnyCols;
     const int64_t kbeg = s * g.kc, kend = std::min(g.K, kbeg + g.kc);
+    // Wave w takes the w-th quarter of the slice, in 32-k steps, so each of
+    // its rows is read as one contiguous run.
+    const int64_t kw = ((kend - kbeg + kWaves - 1) / kWaves + kStepK - 1) / kStepK * kStepK;
+    const int64_t wbeg = kbeg + wave * kw, wend = std::min(kend, wbeg + kw);
     const float *X = g.x + b * g.bx;
     const float *Y = g.y + b * g.by;
 
@@ -111,7 +117,7 @@ __global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
 #pragma unroll
         for (int t = 0; t < 4; t++) acc[rg][t] = (vf4){0.f, 0.f, 0.f, 0.f};
 
-    // Loads one 16-k group starting at kg.  GUARD: k may reach kend.
+    // Loads one 16-k group starting at kg.  GUARD: k may reach wend.
     auto load_group = [&]<bool GUARD>(int64_t kg, vf4 (&ya)[4], vf4 (&xa)[RG]) {
         const int64_t k4 = kg + 4 * fk;
         if constexpr (DOT) {
@@ -121,7 +127,7 @@ __global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
                     ya[t] = yin[t] ? load4<YVEC>(yrow[t] + k4) : (vf4){0.f, 0.f, 0.f, 0.f};
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) ya[t][e] = (yin[t] && k4 + e < kend) ? yrow[t][k4 + e] : 0.f;
+                    for (int e = 0; e < 4; e++) ya[t][e] = (yin[t] && k4 + e < wend) ? yrow[t][k4 + e] : 0.f;
                 }
             }
         } else {
@@ -129,7 +135,7 @@ __global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
             for (int e = 0; e < 4; e++) {
                 const int64_t k = k4 + e;
                 const float *p = Y + k * g.yl + j0 + 4 * fi;
-                const bool kin = !GUARD || k < kend;
+                const bool kin = !GUARD || k < wend;
                 if (YVEC && kin && ncols == 4) {
                     ya[e] = load4<true>(p);
                 } else {
@@ -145,7 +151,7 @@ __global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++)
-                    xa[rg][e] = (xin[rg] && (!GUARD || k4 + e < kend)) ? xrow[rg][(k4 + e) * g.xk] : 0.f;
+                    xa[rg][e] = (xin[rg] && (!GUARD || k4 + e < wend)) ? xrow[rg][(k4 + e) * g.xk] : 0.f;
             }
         }
     };
@@ -161,8 +167,8 @@ __global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
                                                                       acc[rg][t], 0, 0, 0);
     };
 
-    for (int64_t k0 = kbeg + (int64_t)kStepK * wave; k0 < kend; k0 += (int64_t)kStepK * kWaves) {
-        const bool whole = k0 + kStepK <= kend;
+    for (int64_t k0 = wbeg; k0 < wend; k0 += kStepK) {
+        const bool whole = k0 + kStepK <= wend;
 #pragma unroll
         for (int h = 0; h < kStepK / 16; h += kGroups) {
             vf4 ya[kGroups][4], xa[kGroups][RG];
@@ -216,16 +222,16 @@ __global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, f
     if (e >= total) return;
     const int64_t b = e / mn, r = e - b * mn;
     const float *p = ws + b * S * mn + r;
-    float v = p[0];
-    int s = 1;
-    for (; s + 7 < S; s += 8) {
-        float part[8];
+    // All of up to 16 slices' loads issued before the adds: the sum is a
+    // few KB for a matrix-vector product, so its time is load latency.
+    float part[16];
 #pragma unroll
-        for (int q = 0; q < 8; q++) part[q] = p[(int64_t)(s + q) * mn];
+    for (int q = 0; q < 16; q++) part[q] = q < S ? p[(int64_t)q * mn] : 0.f;
+    float v = part[0];
 #pragma unroll
-        for (int q = 0; q < 8; q++) v += part[q];
-    }
-    for (; s < S; s++) v += p[(int64_t)s * mn];
+    for (int q = 1; q < 16; q++)
+        if (q < S) v += part[q];
+    for (int s = 16; s < S; s++) v += p[(int64_t)s * mn];
     c[e] = v;
 }
 

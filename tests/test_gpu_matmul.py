@@ -235,13 +235,13 @@ def test_split_k_all_layouts_exact_on_small_integers(m, k, n, s, ta, tb):
 
 
 # Outputs whose 128x128 or 64x128 tile gives at most one block per CU: K is
-# split over that tile for about two blocks per CU, in slices of at least 256
+# split over that tile for about two blocks per CU, in slices of at least 128
 # k rounded up to the tile's depth (the last slice may be shorter).  The
 # first three would give fewer blocks split over the 256x256 tile.  Values
 # are the (tile_m, tile_n, splits) of a 256-CU device.
-TILE_SPLIT = [((256, 2048, 256), (64, 128, 8)), ((1024, 4096, 1024), (64, 128, 4)), ((512, 4096, 1024), (64, 128, 8)),
-              ((64, 4096, 4096), (64, 128, 16)), ((1000, 1000, 1000), (128, 128, 3)),
-              ((2047, 2047, 2047), (128, 128, 2)), ((33, 1000, 65), (128, 128, 3))]
+TILE_SPLIT = [((256, 2048, 256), (64, 128, 16)), ((1024, 4096, 1024), (64, 128, 4)),
+              ((512, 4096, 1024), (64, 128, 8)), ((64, 4096, 4096), (64, 128, 16)),
+              ((1000, 1000, 1000), (128, 128, 7)), ((2047, 2047, 2047), (128, 128, 2)), ((33, 1000, 65), (128, 128, 7))]
 
 
 @pytest.mark.parametrize("mkn,plan", TILE_SPLIT)
