@@ -68,7 +68,8 @@ def main() -> int:
                          "transfer: host<->device copy rates (pageable and page-locked host memory); "
                          "matmul: the 4096^3 fp32 GEMM alone, for rocprofv3 MFMA counters; "
                          "config: one of the extra configs alone (--config), for per-kernel profiles")
-    ap.add_argument("--config", choices=("relu_bias", "broadcast_strided", "reduce_vjp", "matmul", "mlp"),
+    ap.add_argument("--config", choices=("relu_bias", "broadcast_strided", "reduce_vjp", "matmul", "matmul_shapes",
+                                         "mlp"),
                     default="broadcast_strided", help="the extra config --workload config runs")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -224,15 +224,16 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
  * one-thread-per-output kernel runs in the reference's own k order.  `lc`
  * must be contiguous.
  * Tolerance versus the reference's sequential order: |dC| <= 1e-5*sqrt(K) *
- * (|A||B|) elementwise.  A single 16-byte-aligned matrix whose M and N are
- * multiples of 256, with fewer 256x256 tiles than the device has CUs and a
- * long K, may split K into S slices summed in slice order (when S slices
- * fill at least half the CUs, or give at least as many blocks as the
- * unsplit tile); the partial products then take S*M*N floats of device
- * memory from the library's block cache for the duration of the call
- * (S <= 8, and S*M*N is at most 65,536 floats per CU: 64 MiB on a 256-CU
- * device).  If that memory cannot be allocated the call runs the unsplit
- * tile instead.  An output with at most 32 rows or columns (a matrix-vector
+ * (|A||B|) elementwise.  A single matrix whose tiles would leave CUs idle
+ * may split K into S slices summed in slice order: a 16-byte-aligned one
+ * with M and N multiples of 256, fewer 256x256 tiles than CUs and a long K
+ * (S <= 8, when S slices fill at least half the CUs or give at least as
+ * many blocks as the unsplit tile), else one whose 128x128 or 64x128 tile
+ * gives at most one block per CU (S <= 16, slices of at least 128 k).  The
+ * partial products then take S*M*N floats of device memory from the
+ * library's block cache for the duration of the call (at most 65,536
+ * floats per CU: 64 MiB on a 256-CU device).  If that memory cannot be
+ * allocated the call runs the unsplit tile instead.  An output with at most 32 rows or columns (a matrix-vector
  * product, a small-batch linear layer) runs a kernel that streams the long
  * operand once; it splits K to fill the device when the partial products
  * (splits * M * N * batch floats, from the block cache) move at most 1/8 of

@@ -210,6 +210,73 @@ def matmul(log, reps: int = 20) -> dict:
     return out
 
 
+# (name, M, K, N, A transposed, B transposed, bound): outputs with a short
+# side (matrix-vector products and small-batch linear layers, x @ W or
+# x @ W.mT), which stream the long operand once and are HBM-bound, and
+# shapes whose square tiles alone would leave CUs idle (K split over them).
+MATMUL_SHAPES = [
+    ("matvec [1,4096]@[4096,4096]", 1, 4096, 4096, False, False, "hbm"),
+    ("matvec [1,4096]@W.mT", 1, 4096, 4096, False, True, "hbm"),
+    ("[8,4096]@[4096,4096]", 8, 4096, 4096, False, False, "hbm"),
+    ("[32,4096]@W.mT", 32, 4096, 4096, False, True, "hbm"),
+    ("[4096,4096]@[4096,1]", 4096, 4096, 1, False, False, "hbm"),
+    ("matvec [1,16384]@W.mT", 1, 16384, 16384, False, True, "hbm"),
+    ("[64,4096]@[4096,4096]", 64, 4096, 4096, False, False, "mfma"),
+    ("1000^3", 1000, 1000, 1000, False, False, "mfma"),
+    ("2047^3", 2047, 2047, 2047, False, False, "mfma"),
+]
+
+
+def matmul_shapes(log, reps: int = 100) -> dict:
+    """The matmul beyond the square configs: each shape of MATMUL_SHAPES with
+    its operands filled with constants (fp32 MFMA timing does not depend on
+    the values) and rotated over enough sets that they total at least 512 MiB.
+    Reports the average per call over a back-to-back region (the kernel and,
+    for a split K, the pass that sums the slices), the rate against the
+    shape's bound (algorithmic bytes, every operand read once and C written
+    once, for HBM; 2*M*N*K for MFMA) and the plan trs_matmul_plan_f32 gives."""
+    out = {}
+    for name, M, K, N, ta, tb, bound in MATMUL_SHAPES:
+        per_set = (M * K + K * N) * 4
+        nsets = max(1, min(8, -(-(512 << 20) // per_set)))
+        la = layout_of((M, K), (1, M) if ta else (K, 1))
+        lb = layout_of((K, N), (1, K) if tb else (N, 1))
+        lc = layout_of((M, N))
+        sets = []
+        for _ in range(nsets):
+            a, b, c = DeviceArray(M * K * 4), DeviceArray(K * N * 4), DeviceArray(M * N * 4)
+            check(abi.lib.trs_fill_f32(a.ptr, M * K, 0.5))
+            check(abi.lib.trs_fill_f32(b.ptr, K * N, 0.25))
+            sets.append((a.ptr, ctypes.byref(la), b.ptr, ctypes.byref(lb), c.ptr, ctypes.byref(lc), (a, b, c)))
+        tm, tn, tk, sp, bl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64()
+        check(abi.lib.trs_matmul_plan_f32(*sets[0][:6], ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk),
+                                          ctypes.byref(sp), ctypes.byref(bl)))
+        i = [0]
+
+        def call():
+            s = sets[i[0] % nsets]
+            i[0] += 1
+            check(abi.lib.trs_matmul_f32(*s[:6]))
+
+        ms = time_region(call, reps, warmup=10)
+        us = ms * 1e3
+        entry = {"M": M, "K": K, "N": N, "a_transposed": ta, "b_transposed": tb, "us_avg": us,
+                 "plan": {"tile": [tm.value, tn.value, tk.value], "splits": sp.value, "blocks": bl.value},
+                 "input_sets": nsets, "bound": bound}
+        if bound == "hbm":
+            gbs = (M * K + K * N + M * N) * 4 / (us * 1e-6) / 1e9
+            entry.update({"GBs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS})
+            rate = f"{gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.2f})"
+        else:
+            tf = 2 * M * N * K / (us * 1e-6) / 1e12
+            entry.update({"TFLOPS": tf, "frac_mfma_peak": tf / FP32_MFMA_PEAK_TFLOPS})
+            rate = f"{tf:.1f} TFLOPS ({tf / FP32_MFMA_PEAK_TFLOPS:.2f})"
+        out[name] = entry
+        log(f"matmul {name}: {us:.1f} us, {rate}, tile {tm.value}x{tn.value}x{tk.value} splits {sp.value}")
+        del sets
+    return out
+
+
 def mlp(log, reps: int = 20) -> dict:
     """Config 4: 2-layer MLP forward+backward through the torch_rs API on the device."""
     from . import mlp_bench
@@ -265,9 +332,10 @@ def reduce_vjp(log, reps: int = 50) -> dict:
 
 def run_all(log) -> dict:
     res = {}
-    for fn in (relu_bias, broadcast_strided, reduce_vjp, matmul, mlp):
+    for fn in (relu_bias, broadcast_strided, reduce_vjp, matmul, matmul_shapes, mlp):
         try:
-            res.update(fn(log))
+            r = fn(log)
+            res.update({fn.__name__: r} if fn is matmul_shapes else r)
         except Exception as exc:
             res[fn.__name__] = {"error": repr(exc)}
             log(f"{fn.__name__} failed: {exc!r}")

@@ -144,3 +144,20 @@ def test_skinny_special_values_across_slices():
             bound = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
         err = np.abs(got[fin].astype(np.float64) - want[fin].astype(np.float64))
         assert (err <= 1e-5 * np.sqrt(k) * bound[fin]).all()
+
+
+def test_split_products_repeated_back_to_back():
+    """Split products of different shapes, each repeated three times back to
+    back (their workspaces come from, and return to, the block cache in
+    stream order): every call exact."""
+    rng = np.random.default_rng(71)
+    cases = []
+    for m, k, n, ta, tb in [(1, 4096, 4096, False, True), (3, 8192, 1000, False, False), (1, 4096, 4096, False, True),
+                            (2000, 6000, 5, True, False), (16, 2048, 64, False, True)]:
+        a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb)
+        want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+        assert _plan(*la, *lb)[3] > 1, (m, k, n)
+        cases.append((sa, la, sb, lb, want))
+    for _ in range(3):
+        for sa, la, sb, lb, want in cases:
+            assert np.array_equal(U.matmul(sa, *la, sb, *lb), want)
