@@ -750,10 +750,14 @@ extern "C" int trs_matmul_plan_f32(const float *a, const trs_layout *la, const f
     SkinnyProblem sp;
     SkinnyPlan spl;
     if (work && skinny_problem(*ran, &sp) && plan_skinny(sp, dev->cu_count, &spl)) {
-        // The short side's padded MFMA rows by the 64 columns of a block.
+        // The short side's padded MFMA rows by the 64 columns of a block, or
+        // for the matrix-vector kernel its 1, 2 or 4 rows by the 4 rows of
+        // the long operand a block takes.
         const bool short_m = ran->g.M <= ran->g.N;
-        p.bm = short_m ? 16 * spl.row_groups : kSkinnyCols;
-        p.bn = short_m ? kSkinnyCols : 16 * spl.row_groups;
+        const int rows = spl.gemv ? spl.row_groups : 16 * spl.row_groups;
+        const int cols = spl.gemv ? 4 : kSkinnyCols;
+        p.bm = short_m ? rows : cols;
+        p.bn = short_m ? cols : rows;
         p.bk = (int)spl.kc;
         p.splits = spl.splits;
         p.blocks = spl.blocks;

@@ -27,6 +27,9 @@ struct SkinnyProblem {
 };
 
 struct SkinnyPlan {
+    // The VALU matrix-vector kernel (dot form, R <= 4): row_groups is then
+    // the short rows it is compiled for (1, 2 or 4) and kc the k per wave.
+    bool gemv = false;
     int row_groups = 1;   // 16-row MFMA groups covering R
     bool yvec = false;    // Y read as float4 (else four scalar loads)
     bool xvec = false;    // X rows read as float4 along k

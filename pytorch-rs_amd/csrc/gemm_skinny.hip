@@ -63,6 +63,10 @@ __device__ __forceinline__ vf4 load4(const float *p) {
     else return (vf4){p[0], p[1], p[2], p[3]};
 }
 
+// The long operand, read once: a non-temporal load, so it does not displace
+// the short operand, which every block re-reads, from the caches.
+__device__ __forceinline__ vf4 load4_stream(const float *p) { return __builtin_nontemporal_load((const vf4 *)p); }
+
 // Four waves per SIMD (128 registers), except the unaligned, scalar-load
 // form with 32 rows, which needs a few more and runs three.
 template <bool DOT, bool YVEC, bool XVEC, int RG>
@@ -124,6 +128,8 @@ __global__ void __launch_bounds__(256, (!DOT && !YVEC && RG == 2) ? 3 : 4) gemm_
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 if (!GUARD) {
+                    // Plain loads: non-temporal ones measured 7% slower here
+                    // (32 rows), against 4% faster in the other form.
                     ya[t] = yin[t] ? load4<YVEC>(yrow[t] + k4) : (vf4){0.f, 0.f, 0.f, 0.f};
                 } else {
 #pragma unroll
@@ -137,7 +143,7 @@ __global__ void __launch_bounds__(256, (!DOT && !YVEC && RG == 2) ? 3 : 4) gemm_
                 const float *p = Y + k * g.yl + j0 + 4 * fi;
                 const bool kin = !GUARD || k < wend;
                 if (YVEC && kin && ncols == 4) {
-                    ya[e] = load4<true>(p);
+                    ya[e] = load4_stream(p);
                 } else {
 #pragma unroll
                     for (int c = 0; c < 4; c++) ya[e][c] = (kin && c < ncols) ? p[c] : 0.f;
@@ -214,6 +220,115 @@ __global__ void __launch_bounds__(256, (!DOT && !YVEC && RG == 2) ? 3 : 4) gemm_
     }
 }
 
+// Dot-form products with at most 4 short rows, on the VALU: padded to 16
+// rows, each float4 of Y would cost four 32-cycle MFMAs, and the MFMA
+// fragments read each row of Y in 64-byte pieces.  Here a block owns
+// kGemvRows rows of Y (output columns) over the whole of K, its 4 waves take
+// consecutive quarters of K, and a lane reads 16 bytes of a row per
+// instruction, so one instruction reads 1 KiB of one row.  Each lane sums its
+// k in order, the lanes' sums are added by a fixed shuffle tree and the
+// waves' in wave order.  No split of K across blocks, so no slice pass.
+constexpr int kGemvRows = 4;
+
+template <int RR, bool XVEC>
+__global__ void __launch_bounds__(256) gemv_f32_dot(SkinnyArgs g) {
+    constexpr int U = (RR == 4 || !XVEC) ? 2 : 4;  // 256-k steps loaded before the FMAs
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t nb = (g.L + kGemvRows - 1) / kGemvRows;
+    const int64_t b = blockIdx.x / nb, j0 = (blockIdx.x - b * nb) * kGemvRows;
+    const float *X = g.x + b * g.bx;
+    const float *Y = g.y + b * g.by;
+    const int64_t kq = (g.K + 4 * 256 - 1) / (4 * 256) * 256;
+    const int64_t kb = wave * kq, ke = std::min(g.K, kb + kq);
+
+    const float *yrow[kGemvRows];
+    bool yin[kGemvRows];
+#pragma unroll
+    for (int t = 0; t < kGemvRows; t++) {
+        yin[t] = j0 + t < g.L;
+        yrow[t] = Y + (yin[t] ? j0 + t : 0) * g.yl;
+    }
+    const float *xrow[RR];
+    bool xin[RR];
+#pragma unroll
+    for (int i = 0; i < RR; i++) {
+        xin[i] = i < g.R;
+        xrow[i] = X + (xin[i] ? i : 0) * g.xi;
+    }
+    float acc[kGemvRows][RR];
+#pragma unroll
+    for (int t = 0; t < kGemvRows; t++)
+#pragma unroll
+        for (int i = 0; i < RR; i++) acc[t][i] = 0.f;
+
+    auto fma4 = [&](const vf4 (&y)[kGemvRows], const vf4 (&x)[RR]) {
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int t = 0; t < kGemvRows; t++)
+#pragma unroll
+                for (int i = 0; i < RR; i++) acc[t][i] += x[i][c] * y[t][c];
+    };
+    auto load_step = [&](int64_t k, vf4 (&y)[kGemvRows], vf4 (&x)[RR]) {
+#pragma unroll
+        for (int t = 0; t < kGemvRows; t++) y[t] = yin[t] ? load4_stream(yrow[t] + k) : (vf4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < RR; i++) {
+            if (!xin[i]) x[i] = (vf4){0.f, 0.f, 0.f, 0.f};
+            else if (XVEC) x[i] = load4<true>(xrow[i] + k);
+            else x[i] = (vf4){xrow[i][k * g.xk], xrow[i][(k + 1) * g.xk], xrow[i][(k + 2) * g.xk], xrow[i][(k + 3) * g.xk]};
+        }
+    };
+
+    int64_t k0 = kb;
+    for (; k0 + 256 * U <= ke; k0 += 256 * U) {
+        vf4 y[U][kGemvRows], x[U][RR];
+#pragma unroll
+        for (int u = 0; u < U; u++) load_step(k0 + 256 * u + 4 * lane, y[u], x[u]);
+#pragma unroll
+        for (int u = 0; u < U; u++) fma4(y[u], x[u]);
+    }
+    for (; k0 + 256 <= ke; k0 += 256) {
+        vf4 y[kGemvRows], x[RR];
+        load_step(k0 + 4 * lane, y, x);
+        fma4(y, x);
+    }
+    if (k0 < ke) {  // ragged end of the wave's range: element by element
+        vf4 y[kGemvRows], x[RR];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int64_t k = k0 + 4 * lane + c;
+            const bool kin = k < ke;
+#pragma unroll
+            for (int t = 0; t < kGemvRows; t++) y[t][c] = (kin && yin[t]) ? yrow[t][k] : 0.f;
+#pragma unroll
+            for (int i = 0; i < RR; i++) x[i][c] = (kin && xin[i]) ? xrow[i][k * g.xk] : 0.f;
+        }
+        fma4(y, x);
+    }
+
+    __shared__ float red[4][kGemvRows * RR];
+#pragma unroll
+    for (int t = 0; t < kGemvRows; t++)
+#pragma unroll
+        for (int i = 0; i < RR; i++) {
+            float v = acc[t][i];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0) red[wave][t * RR + i] = v;
+        }
+    __syncthreads();
+    if (threadIdx.x < kGemvRows * RR) {
+        const int q = threadIdx.x, t = q / RR, i = q % RR;
+        if (j0 + t < g.L && i < g.R) {
+            float v = red[0][q];
+#pragma unroll
+            for (int w = 1; w < 4; w++) v += red[w][q];
+            g.o[b * g.bo + i * g.oi + (j0 + t) * g.oj] = v;
+        }
+    }
+}
+
 // c[e] = ((p0 + p1) + p2) + ... over the S slices of e's batch, in slice
 // order.  Slice s of batch b starts at ws + (b*S + s)*mn.
 __global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, float *__restrict__ c, int64_t mn,
@@ -260,6 +375,20 @@ bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
     pl.row_groups = p.R <= 16 ? 1 : 2;
     pl.yvec = aligned16(p.y) && p.yl % 4 == 0 && (p.batch == 1 || p.by % 4 == 0);
     pl.xvec = p.xk == 1 && aligned16(p.x) && (p.R == 1 || p.xi % 4 == 0) && (p.batch == 1 || p.bx % 4 == 0);
+    // The VALU matrix-vector kernel: dot form, at most 4 short rows, a K long
+    // enough that each wave's quarter covers its 64 lanes, and enough rows
+    // for two blocks per CU.
+    const int64_t gemv_blocks = (p.L + kGemvRows - 1) / kGemvRows * p.batch;
+    if (p.dot && pl.yvec && p.R <= 4 && p.K >= 1024 && gemv_blocks >= 2 * (int64_t)cu_count &&
+        gemv_blocks <= INT32_MAX) {
+        pl.gemv = true;
+        pl.row_groups = p.R == 1 ? 1 : p.R == 2 ? 2 : 4;
+        pl.kc = (p.K + 4 * 256 - 1) / (4 * 256) * 256;
+        pl.splits = 1;
+        pl.blocks = gemv_blocks;
+        *plan = pl;
+        return true;
+    }
     const int64_t jblocks = (p.L + kSkinnyCols - 1) / kSkinnyCols;
     const int64_t base = jblocks * p.batch;
     // ~4 blocks per CU; each slice at least 128 deep (one step per wave), and
@@ -287,6 +416,26 @@ int launch_slice_sum(const float *ws, float *c, int64_t mn, int64_t batch, int64
 
 int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
     SkinnyArgs g{};
+    if (plan.gemv) {
+        g.x = p.x, g.y = p.y, g.o = p.out;
+        g.xi = p.xi, g.xk = p.xk, g.yl = p.yl;
+        g.oi = p.oi, g.oj = p.oj, g.bo = p.R * p.L;
+        g.bx = p.bx, g.by = p.by;
+        g.R = p.R, g.L = p.L, g.K = p.K;
+        const dim3 grid((unsigned)plan.blocks);
+        const int rr = plan.row_groups;
+        if (plan.xvec) {
+            if (rr == 1) hipLaunchKernelGGL((gemv_f32_dot<1, true>), grid, dim3(256), 0, s, g);
+            else if (rr == 2) hipLaunchKernelGGL((gemv_f32_dot<2, true>), grid, dim3(256), 0, s, g);
+            else hipLaunchKernelGGL((gemv_f32_dot<4, true>), grid, dim3(256), 0, s, g);
+        } else {
+            if (rr == 1) hipLaunchKernelGGL((gemv_f32_dot<1, false>), grid, dim3(256), 0, s, g);
+            else if (rr == 2) hipLaunchKernelGGL((gemv_f32_dot<2, false>), grid, dim3(256), 0, s, g);
+            else hipLaunchKernelGGL((gemv_f32_dot<4, false>), grid, dim3(256), 0, s, g);
+        }
+        TRS_LAUNCH_CHECK("gemv launch");
+        return TRS_OK;
+    }
     g.x = p.x;
     g.y = p.y;
     g.xi = p.xi;

@@ -70,7 +70,7 @@ def test_short_sides_plan_the_skinny_kernel():
     33 rows go to the square tiles; K is split to fill the device."""
     plain = lambda m, k, n: _plan((m, k), (k, 1), 0, (k, n), (n, 1), 0)
     assert plain(1, 4096, 4096)[:2] == (16, 64) and plain(1, 4096, 4096)[3] > 1
-    assert plain(4096, 4096, 1)[:2] == (64, 16)
+    assert plain(4096, 100, 1)[:2] == (64, 16)
     assert plain(16, 512, 4096)[:2] == (16, 64) and plain(17, 512, 4096)[:2] == (32, 64)
     assert plain(32, 512, 4096)[:2] == (32, 64) and plain(33, 512, 4096)[:2] != (32, 64)
     assert plain(4096, 512, 32)[:2] == (64, 32)
@@ -152,7 +152,7 @@ def test_split_products_repeated_back_to_back():
     stream order): every call exact."""
     rng = np.random.default_rng(71)
     cases = []
-    for m, k, n, ta, tb in [(1, 4096, 4096, False, True), (3, 8192, 1000, False, False), (1, 4096, 4096, False, True),
+    for m, k, n, ta, tb in [(1, 4096, 4096, False, False), (3, 8192, 1000, False, False), (1, 4096, 4096, False, False),
                             (2000, 6000, 5, True, False), (16, 2048, 64, False, True)]:
         a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb)
         want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
@@ -161,3 +161,47 @@ def test_split_products_repeated_back_to_back():
     for _ in range(3):
         for sa, la, sb, lb, want in cases:
             assert np.array_equal(U.matmul(sa, *la, sb, *lb), want)
+
+
+def test_dot_form_with_four_rows_or_fewer_plans_the_matrix_vector_kernel():
+    """x @ W.mT (and W @ x) with at most 4 short rows, K >= 1024 and enough
+    rows of W for two blocks per CU run the VALU matrix-vector kernel: the
+    plan reports its 1, 2 or 4 rows by the 4 rows of W a block takes, over
+    the whole of K (no split)."""
+    dot = lambda m, k, n: _plan((m, k), (k, 1), 0, (k, n), (1, k), 0)
+    assert dot(1, 4096, 4096)[:4] == (1, 4, 1024, 1)
+    assert dot(2, 4096, 4096)[:2] == (2, 4) and dot(3, 4096, 4096)[:2] == (4, 4)
+    assert dot(5, 4096, 4096)[:2] == (16, 64)       # five rows: the MFMA kernel
+    assert dot(1, 512, 4096)[:2] == (16, 64)        # short K
+    assert dot(1, 4096, 1024)[:2] == (16, 64)       # too few rows of W
+    assert _plan((4096, 4096), (4096, 1), 0, (4096, 1), (1, 1), 0)[:2] == (4, 1)  # W @ x
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb,aoff,boff", [
+    (1, 1024, 2048, False, True, 0, 0), (2, 3000, 2050, False, True, 0, 0), (3, 4100, 2048, False, True, 0, 0),
+    (4, 5000, 3001, False, True, 0, 0), (1, 70000, 2048, False, True, 0, 0),
+    (2050, 3000, 2, False, False, 0, 0),   # W @ x: X = x^T with a k stride of 2 (scalar X loads)
+    (3001, 1027, 4, False, True, 0, 0), (2048, 4096, 1, False, True, 0, 0),
+    (1, 4096, 4096, False, True, 1, 0),    # x misaligned: scalar X loads
+    (1, 4096, 4096, False, True, 0, 1),    # W misaligned: the MFMA kernel
+])
+def test_matrix_vector_kernel_exact(m, k, n, ta, tb, aoff, boff):
+    rng = np.random.default_rng(m + k + n + aoff + 3 * boff)
+    a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, aoff=aoff, boff=boff)
+    got = U.matmul(sa, *la, sb, *lb)
+    assert np.array_equal(got, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32))
+
+
+def test_matrix_vector_kernel_batched_and_normal_inputs():
+    rng = np.random.default_rng(9)
+    a, b, sa, la, sb, lb = _operands(rng, 1, 2048, 2048, False, True, batch=3)
+    got = U.matmul(sa, *la, sb, *lb)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(got.reshape(want.shape), want)
+    for m, k, n in [(1, 4096, 4096), (4, 3000, 2048)]:
+        a, b, sa, la, sb, lb = _operands(rng, m, k, n, False, True, ints=False)
+        got = U.matmul(sa, *la, sb, *lb)
+        want = O.matmul(sa, *la, sb, *lb).reshape(m, n)
+        err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+        tol = 1e-5 * np.sqrt(k) * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+        assert (err <= tol).all(), err.max()
