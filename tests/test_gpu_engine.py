@@ -237,6 +237,24 @@ def test_matmul_vjp_exact_on_small_integers():
         assert np.array_equal(B.grad.numpy(), (a.T.astype(np.int64) @ w.astype(np.int64)).astype(np.float32))
 
 
+def test_small_batch_linear_layer_forward_and_backward_exact():
+    """x @ W.mT with 1 or 3 rows of x and W [4096, 4096] (the layout of a
+    linear layer's weight): the forward is a matrix-vector product, dX = up @ W
+    a skinny product with K split, and dW = up^T @ x an outer product of depth
+    1 or 3.  Small integers make every order exact."""
+    rng = np.random.default_rng(6)
+    for m in (1, 3):
+        x = rng.integers(-3, 4, (m, 4096)).astype(np.float32)
+        wt = rng.integers(-3, 4, (4096, 4096)).astype(np.float32)
+        up = rng.integers(-2, 3, (m, 4096)).astype(np.float32)
+        X, W = cuda(x, True), cuda(wt, True)
+        out = X @ W.mT
+        assert np.array_equal(out.numpy(), (x.astype(np.float64) @ wt.T.astype(np.float64)).astype(np.float32))
+        (out * cuda(up)).sum().backward()
+        assert np.array_equal(X.grad.numpy(), (up.astype(np.float64) @ wt.astype(np.float64)).astype(np.float32))
+        assert np.array_equal(W.grad.numpy(), (up.T.astype(np.float64) @ x.astype(np.float64)).astype(np.float32))
+
+
 def test_batched_matmul_vjp_exact_on_small_integers():
     rng = np.random.default_rng(4)
     a = rng.integers(-3, 4, (4, 20, 12)).astype(np.float32)
