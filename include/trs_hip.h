@@ -46,7 +46,11 @@
 extern "C" {
 #endif
 
-#define TRS_MAX_RANK 8
+/* Views of up to TRS_MAX_RANK dims (the reference's shapes are vectors of
+ * any length).  Kernels index at most 8 dims after size-1 dims are dropped
+ * and contiguous dims merged; a pointwise view with more than that is run as
+ * one launch per index tuple of its outermost dims. */
+#define TRS_MAX_RANK 25
 
 /* Status codes (TensorError variants, src/tensor_error.rs:7-108). */
 #define TRS_OK 0
@@ -56,12 +60,12 @@ extern "C" {
 #define TRS_E_SHAPE_MISMATCH (-4)         /* ShapeMismatch */
 #define TRS_E_MATMUL_INNER_MISMATCH (-5)  /* MatmulInnerDimensionMismatch */
 #define TRS_E_MATMUL_REQUIRES_MATRICES (-6) /* MatmulRequiresMatrices */
-#define TRS_E_INVALID_ARGUMENT (-7)       /* bad op code, rank > 8, null pointer */
+#define TRS_E_INVALID_ARGUMENT (-7)       /* bad op code, rank > TRS_MAX_RANK, null pointer */
 #define TRS_E_HIP (-8)                    /* HIP runtime failure */
 #define TRS_E_FUSION (-9)                 /* fusion IR parse or hipRTC failure */
 #define TRS_E_NO_DEVICE (-10)             /* no usable gfx950 device */
 
-/* A strided view: rank <= 8, shape/stride/offset in elements (the Tensor
+/* A strided view: rank <= TRS_MAX_RANK, shape/stride/offset in elements (the Tensor
  * metadata of src/tensor.rs:212-221). */
 typedef struct trs_layout {
     int32_t rank;
@@ -277,7 +281,10 @@ typedef struct trs_pw_plan_info {
     uint32_t held;      /* transposing with roles: inputs loaded once per block */
     uint32_t once;      /* transposing with roles: inputs loaded once per outer tuple */
     int32_t block;      /* lanes per block */
-    int64_t grid;       /* blocks */
+    int64_t grid;       /* blocks per launch */
+    int32_t split;      /* outer dims walked on the host, one launch per index
+                         * tuple, when more than 8 dims remain after merging */
+    int32_t reserved;
 } trs_pw_plan_info;
 int trs_pointwise_plan(int n_inputs, const void *const *inputs, const trs_layout *const *layouts,
                        const int *elem_bytes, const float *out, const trs_layout *lo, int cu_count, int roles,

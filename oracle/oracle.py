@@ -13,7 +13,7 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-MAX_RANK = 8
+MAX_RANK = 25
 
 
 class OLayout(ctypes.Structure):

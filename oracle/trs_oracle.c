@@ -25,7 +25,7 @@
 #include <gnu/libc-version.h>
 #include <pthread.h>
 
-#define ORC_MAX_RANK 8
+#define ORC_MAX_RANK 25
 
 /* Error codes; the same numbering as the product ABI (include/trs_hip.h). */
 enum {

@@ -459,7 +459,7 @@ AutogradMeta::~AutogradMeta() {
 // ---- tensor basics -----------------------------------------------------------
 
 trs_layout Tensor::abi_layout() const {
-    if (shape.size() > TRS_MAX_RANK) throw TensorError("tensors above rank 8 are not supported on the device");
+    if (shape.size() > TRS_MAX_RANK) throw TensorError("tensors above rank " + std::to_string(TRS_MAX_RANK) + " are not supported on the device");
     trs_layout l{};
     l.rank = (int32_t)shape.size();
     for (size_t i = 0; i < shape.size(); i++) {
@@ -471,7 +471,7 @@ trs_layout Tensor::abi_layout() const {
 }
 
 static trs_layout abi_layout_of(const Dims &shape, const Dims &strides, int64_t offset) {
-    if (shape.size() > TRS_MAX_RANK) throw TensorError("tensors above rank 8 are not supported on the device");
+    if (shape.size() > TRS_MAX_RANK) throw TensorError("tensors above rank " + std::to_string(TRS_MAX_RANK) + " are not supported on the device");
     trs_layout l{};
     l.rank = (int32_t)shape.size();
     for (size_t i = 0; i < shape.size(); i++) {

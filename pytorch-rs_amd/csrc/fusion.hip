@@ -520,11 +520,15 @@ int trs_fusion_launch_multi(uint64_t kernel_id, int n_inputs, const void *const 
         hipFunction_t fn;
         rc = get_plan_function(prog, dev, pl, &fn);
         if (rc) return rc;
-        void *args[] = {(void *)&pl.g, (void *)&pl.p};
-        TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, (unsigned)pl.block, 1, 1, 0, dev->stream, args,
-                                            nullptr),
-                      "hipModuleLaunchKernel");
-        return TRS_OK;
+        return for_each_part(pl, [&](const PwGeom &g) -> int {
+            PwGeom gp = g;
+            PwPtrs pp = pl.p;
+            void *args[] = {(void *)&gp, (void *)&pp};
+            TRS_HIP_CHECK(hipModuleLaunchKernel(fn, (unsigned)pl.grid, 1, 1, (unsigned)pl.block, 1, 1, 0, dev->stream,
+                                                args, nullptr),
+                          "hipModuleLaunchKernel");
+            return TRS_OK;
+        });
     });
 }
 

@@ -457,7 +457,7 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
     ReduceGeom rg{};
     const int lead = lout->rank - lself->rank;
     const int olead = other ? lout->rank - lother->rank : 0;
-    int64_t ustride[kMaxRank];
+    int64_t ustride[TRS_MAX_RANK];
     {
         int64_t s = 1;
         for (int d = lout->rank - 1; d >= 0; d--) {
@@ -465,6 +465,27 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
             s *= lout->shape[d];
         }
     }
+    // Kept dims (the operand's own) and reduced dims (broadcast along), each
+    // in output order.  Size-1 dims index nothing and are dropped; a dim that
+    // continues the previous one of its kind in both up and other (stride =
+    // next stride * next size) is merged into it.  Either way the operand's
+    // row-major index and the row-major order of each chain are unchanged.
+    struct DimList {
+        int n = 0;
+        int64_t size[TRS_MAX_RANK], up[TRS_MAX_RANK], ot[TRS_MAX_RANK];
+        void add(int64_t sz, int64_t u, int64_t o) {
+            if (n > 0 && up[n - 1] == u * sz && ot[n - 1] == o * sz) {
+                size[n - 1] *= sz;
+                up[n - 1] = u;
+                ot[n - 1] = o;
+                return;
+            }
+            size[n] = sz;
+            up[n] = u;
+            ot[n] = o;
+            n++;
+        }
+    } kept, red;
     for (int d = 0; d < lout->rank; d++) {
         const int64_t osz = lout->shape[d];
         const bool self_bcast = d < lead || (lself->shape[d - lead] == 1 && osz != 1);
@@ -476,18 +497,25 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
             if (s != osz && s != 1) return set_error(TRS_E_SHAPE_MISMATCH, "other does not broadcast");
             ost = (s == 1) ? 0 : lother->stride[d - olead];
         }
-        if (self_bcast) {
-            if (osz == 1) continue;
-            rg.red_size[rg.nred] = osz;
-            rg.red_up[rg.nred] = ustride[d];
-            rg.red_other[rg.nred] = ost;
-            rg.nred++;
-        } else {
-            rg.kept_size[rg.nkept] = osz;
-            rg.kept_up[rg.nkept] = ustride[d];
-            rg.kept_other[rg.nkept] = ost;
-            rg.nkept++;
-        }
+        if (osz == 1) continue;
+        if (self_bcast) red.add(osz, ustride[d], ost);
+        else kept.add(osz, ustride[d], ost);
+    }
+    if (kept.n > kMaxRank || red.n > kMaxRank)
+        return set_error(TRS_E_INVALID_ARGUMENT,
+                         "broadcast reduction: the operand's dims merge to %d kept and %d reduced dims, above %d",
+                         kept.n, red.n, kMaxRank);
+    rg.nkept = kept.n;
+    rg.nred = red.n;
+    for (int d = 0; d < kept.n; d++) {
+        rg.kept_size[d] = kept.size[d];
+        rg.kept_up[d] = kept.up[d];
+        rg.kept_other[d] = kept.ot[d];
+    }
+    for (int d = 0; d < red.n; d++) {
+        rg.red_size[d] = red.size[d];
+        rg.red_up[d] = red.up[d];
+        rg.red_other[d] = red.ot[d];
     }
     rg.nself = layout_numel(lself);
     rg.nred_total = 1;
@@ -563,19 +591,52 @@ int sum_launch(DeviceState *dev, const float *x, const trs_layout *lx, float *ou
     const int64_t n = layout_numel(lx);
     if (n == 0) return trs_fill_f32(out, 1, -0.0f);
     if (!x) return set_error(TRS_E_INVALID_ARGUMENT, "null input");
+    // The tree adds elements by their position in row-major logical order.
+    // Dropping size-1 dims and merging contiguous ones keeps every position,
+    // so the merged view gives the same bits.
+    trs_layout lm;
+    merge_layout_dims(lx, &lm);
+    if (lm.rank > kMaxRank) {
+        // More dims than the kernel decodes: copy the view to a contiguous
+        // buffer of this call's own (the same elements in the same order)
+        // and sum that.
+        if (partial)
+            return set_error(TRS_E_INVALID_ARGUMENT,
+                             "the no-allocation sum takes views that merge to at most %d dims; this one keeps %d",
+                             kMaxRank, lm.rank);
+        void *tmp = nullptr;
+        rc = trs_alloc((size_t)n * sizeof(float), &tmp);
+        if (rc) return rc;
+        trs_layout lc{};
+        lc.rank = lx->rank;
+        int64_t s = 1;
+        for (int d = lx->rank - 1; d >= 0; d--) {
+            lc.shape[d] = lx->shape[d];
+            lc.stride[d] = s;
+            s *= lx->shape[d];
+        }
+        rc = trs_unary_f32(TRS_COPY, x, lx, (float *)tmp, &lc);
+        trs_layout l1{};
+        l1.rank = 1;
+        l1.shape[0] = n;
+        l1.stride[0] = 1;
+        if (!rc) rc = sum_launch(dev, (const float *)tmp, &l1, out, nullptr);
+        const int frc = trs_free(tmp);
+        return rc ? rc : frc;
+    }
     // Geometry for logical-order decode of a strided input.
     PwGeom g;
     std::memset(&g, 0, sizeof g);
     g.numel = n;
-    g.rank = lx->rank;
-    g.ioff[0] = lx->offset;
-    for (int d = 0; d < lx->rank; d++) {
-        g.size[d] = lx->shape[d];
-        g.istride[0][d] = lx->stride[d];
-        if (lx->shape[d] > (int64_t)UINT32_MAX) g.wide = 1;
-        g.fd[d] = make_fast_div(lx->shape[d] > (int64_t)UINT32_MAX ? 1u : (uint32_t)lx->shape[d]);
+    g.rank = lm.rank;
+    g.ioff[0] = lm.offset;
+    for (int d = 0; d < lm.rank; d++) {
+        g.size[d] = lm.shape[d];
+        g.istride[0][d] = lm.stride[d];
+        if (lm.shape[d] > (int64_t)UINT32_MAX) g.wide = 1;
+        g.fd[d] = make_fast_div(lm.shape[d] > (int64_t)UINT32_MAX ? 1u : (uint32_t)lm.shape[d]);
     }
-    const bool contig = layout_is_contiguous(lx);
+    const bool contig = layout_is_contiguous(&lm);
     // Up to kSumOneBlock elements: pass 1 alone, one block writing the result
     // (one launch and no partials; the order is still fixed by n).
     if (n <= kSumOneBlock) {
@@ -707,6 +768,7 @@ int trs_pointwise_plan(int n_inputs, const void *const *inputs, const trs_layout
     info->once = pl.once;
     info->block = pl.block;
     info->grid = pl.grid;
+    info->split = pl.nsplit;
     return TRS_OK;
 }
 

@@ -241,10 +241,12 @@ __device__ __forceinline__ void decode_outer(const PwGeom &g, int ndims, int64_t
     if (!g.wide && outer < 0x100000000LL) {
         // Unrolled over every possible dim so each geometry field has a
         // constant index (loads the compiler can issue up front); dims at or
-        // above ndims are skipped by a uniform branch.
+        // above ndims are skipped by a uniform branch.  The rows kernels
+        // decode at most kMaxRank - 1 outer dims, the generic kernel and the
+        // strided sum all kMaxRank.
         uint32_t rem = (uint32_t)outer;
 #pragma unroll
-        for (int d = kMaxRank - 2; d >= 0; d--) {
+        for (int d = kMaxRank - 1; d >= 0; d--) {
             if (d >= ndims) continue;
             uint32_t q = fast_div(rem, g.fd[d]);
             uint32_t c = rem - q * g.fd[d].div;

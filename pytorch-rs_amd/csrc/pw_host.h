@@ -21,6 +21,9 @@ namespace trs {
 
 enum class PwVariant { Empty, Flat, Rows, Xpose, Generic };
 
+// Dims a plan can walk on the host beyond the kernel geometry's kMaxRank.
+constexpr int kMaxSplit = TRS_MAX_RANK - kMaxRank;
+
 // pw_xpose tile: 4 x 2 waves = 128 (t) x 64 (x).  On (a + b) * c.mT over
 // [64, 512, 1024] this shape's access pattern measured fastest of 64-256 x
 // 32-256 (its reads of c are 512 B runs); walking 8 outer tuples per block
@@ -50,7 +53,39 @@ struct PwPlan {
     int64_t grid = 0;
     PwGeom g;
     PwPtrs p;
+    // Views that keep more than kMaxRank dims after merging: the outermost
+    // nsplit dims (largest output strides) are walked on the host, one launch
+    // of the inner kMaxRank dims per index tuple, each with the base offsets
+    // moved by that tuple (for_each_part).
+    int nsplit = 0;
+    int64_t ssize[kMaxSplit];
+    int64_t sos[kMaxSplit];
+    int64_t sis[kMaxIn][kMaxSplit];
 };
+
+// Calls launch(g) once per part of the plan: with no split, on the plan's
+// geometry; otherwise on a copy whose output and input offsets are moved to
+// each index tuple of the split dims, in row-major order.  The parts write
+// disjoint output elements, so their order does not change any result.
+template <class L>
+int for_each_part(const PwPlan &pl, L &&launch) {
+    if (pl.nsplit == 0) return launch(pl.g);
+    PwGeom g = pl.g;
+    int64_t idx[kMaxSplit] = {};
+    for (;;) {
+        g.ooff = pl.g.ooff;
+        for (int i = 0; i < kMaxIn; i++) g.ioff[i] = pl.g.ioff[i];
+        for (int d = 0; d < pl.nsplit; d++) {
+            g.ooff += idx[d] * pl.sos[d];
+            for (int i = 0; i < kMaxIn; i++) g.ioff[i] += idx[d] * pl.sis[i][d];
+        }
+        const int rc = launch(g);
+        if (rc) return rc;
+        int d = pl.nsplit - 1;
+        while (d >= 0 && ++idx[d] == pl.ssize[d]) idx[d--] = 0;
+        if (d < 0) return TRS_OK;
+    }
+}
 
 inline FastDiv make_fast_div(uint32_t d) {
     FastDiv f{};
@@ -133,7 +168,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
 
     // 1-2. align, drop singleton dims.
     int rank = 0;
-    int64_t size[kMaxRank], os[kMaxRank], is[kMaxIn][kMaxRank];
+    int64_t size[TRS_MAX_RANK], os[TRS_MAX_RANK], is[kMaxIn][TRS_MAX_RANK];
     for (int d = 0; d < lo->rank; d++) {
         if (lo->shape[d] == 1) continue;
         size[rank] = lo->shape[d];
@@ -161,7 +196,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         return set_error(TRS_E_INVALID_ARGUMENT, "output layout overlaps itself");
     // Merge dims that are contiguous for every operand.
     {
-        int64_t nsize[kMaxRank], nos[kMaxRank], nis[kMaxIn][kMaxRank];
+        int64_t nsize[TRS_MAX_RANK], nos[TRS_MAX_RANK], nis[kMaxIn][TRS_MAX_RANK];
         int nr = 0;
         // Walk from innermost to outermost, building reversed list.
         for (int d = rank - 1; d >= 0; d--) {
@@ -192,6 +227,23 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         os[0] = 1;
         for (int i = 0; i < nin; i++) is[i][0] = 0;
     }
+    // More dims than a kernel's geometry holds: split off the outermost.
+    if (rank > kMaxRank) {
+        const int ns = rank - kMaxRank;
+        plan->nsplit = ns;
+        for (int d = 0; d < ns; d++) {
+            plan->ssize[d] = size[d];
+            plan->sos[d] = os[d];
+            for (int i = 0; i < nin; i++) plan->sis[i][d] = is[i][d];
+            numel /= size[d];
+        }
+        for (int d = 0; d < kMaxRank; d++) {
+            size[d] = size[d + ns];
+            os[d] = os[d + ns];
+            for (int i = 0; i < nin; i++) is[i][d] = is[i][d + ns];
+        }
+        rank = kMaxRank;
+    }
 
     g.rank = rank;
     g.numel = numel;
@@ -209,34 +261,40 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             g.istride[i][d] = is[i][d];
             bcast |= is[i][d] == 0;
         }
+        for (int d = 0; d < plan->nsplit; d++) bcast |= plan->sis[i][d] == 0;
         if (!bcast) g.streamed |= 1u << i;
     }
 
-    // Alignment of a unit-stride access along dim `ud` for operand bytes.
-    auto aligned = [&](const void *base, int64_t off, const int64_t *strides, int ud, int eb) {
+    // Alignment of a unit-stride access along dim `ud` for operand bytes, in
+    // every part of a split launch (`sst`: the operand's split-dim strides).
+    auto aligned = [&](const void *base, int64_t off, const int64_t *strides, const int64_t *sst, int ud, int eb) {
         const uint64_t addr = (uint64_t)(uintptr_t)base + (uint64_t)off * (uint64_t)eb;
         if (addr % (uint64_t)(4 * eb) != 0) return false;
         for (int d = 0; d < rank; d++)
             if (d != ud && strides[d] % 4 != 0) return false;
+        for (int d = 0; d < plan->nsplit; d++)
+            if (sst[d] % 4 != 0) return false;
         return true;
     };
 
     const int inner = rank - 1;
     auto outputs_aligned = [&]() {
-        bool ok = aligned(out, lo->offset, os, inner, 4);
-        for (int o = 1; o < nout; o++) ok = ok && aligned(more[o - 1], lo->offset, os, inner, 4);
+        bool ok = aligned(out, lo->offset, os, plan->sos, inner, 4);
+        for (int o = 1; o < nout; o++) ok = ok && aligned(more[o - 1], lo->offset, os, plan->sos, inner, 4);
         return ok;
     };
-    // Every element offset the launch forms is below 2^32: strides are
-    // non-negative, so the largest is offset + sum (size - 1) * stride.
+    // Every element offset the launch forms (in any part) is below 2^32:
+    // strides are non-negative, so the largest is offset + sum (size - 1) *
+    // stride over the inner and the split dims.
     auto offsets_fit32 = [&]() {
-        auto last = [&](int64_t off, const int64_t *st) {
+        auto last = [&](int64_t off, const int64_t *st, const int64_t *sst) {
             for (int d = 0; d < rank; d++) off += (size[d] - 1) * st[d];
+            for (int d = 0; d < plan->nsplit; d++) off += (plan->ssize[d] - 1) * sst[d];
             return off;
         };
-        if (last(g.ooff, os) > (int64_t)UINT32_MAX) return false;
+        if (last(g.ooff, os, plan->sos) > (int64_t)UINT32_MAX) return false;
         for (int i = 0; i < nin; i++)
-            if (last(g.ioff[i], is[i]) > (int64_t)UINT32_MAX) return false;
+            if (last(g.ioff[i], is[i], plan->sis[i]) > (int64_t)UINT32_MAX) return false;
         return true;
     };
     bool unit_or_bcast = os[inner] == 1;
@@ -246,7 +304,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
     if (unit_or_bcast) {
         bool vec = outputs_aligned();
         for (int i = 0; i < nin; i++)
-            if (is[i][inner] == 1) vec &= aligned(bases[i], g.ioff[i], is[i], inner, elem_bytes[i]);
+            if (is[i][inner] == 1) vec &= aligned(bases[i], g.ioff[i], is[i], plan->sis[i], inner, elem_bytes[i]);
         if (rank == 1) {
             plan->variant = PwVariant::Flat;
             plan->vec = vec;
@@ -291,9 +349,9 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             bool vec = outputs_aligned();
             for (int i = 0; i < nin; i++) {
                 if ((tmask >> i) & 1u) {
-                    vec &= aligned(bases[i], g.ioff[i], is[i], tdim, elem_bytes[i]);
+                    vec &= aligned(bases[i], g.ioff[i], is[i], plan->sis[i], tdim, elem_bytes[i]);
                 } else if (is[i][inner] == 1) {
-                    vec &= aligned(bases[i], g.ioff[i], is[i], inner, elem_bytes[i]);
+                    vec &= aligned(bases[i], g.ioff[i], is[i], plan->sis[i], inner, elem_bytes[i]);
                 }
             }
             plan->vec = vec;

@@ -125,29 +125,31 @@ void with_mask(unsigned m, Fn &&fn) {
     }
 }
 
+// One launch of the plan's kernel on geometry `g` (the plan's own, or one
+// part of a split plan).
 template <class F, unsigned M>
-int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
+int launch_part(const F &f, const PwPlan &pl, const PwGeom &g, hipStream_t s) {
     constexpr int NIN = F::NIN;
     const dim3 grid((unsigned)pl.grid), block((unsigned)pl.block);
-    const unsigned sm = pl.g.streamed & ((1u << NIN) - 1u);
+    const unsigned sm = g.streamed & ((1u << NIN) - 1u);
     switch (pl.variant) {
     case PwVariant::Empty:
         return TRS_OK;
     case PwVariant::Flat:
-        if (pl.contig) hipLaunchKernelGGL((k_flat_contig<F, M>), grid, block, 0, s, pl.g, pl.p, f);
+        if (pl.contig) hipLaunchKernelGGL((k_flat_contig<F, M>), grid, block, 0, s, g, pl.p, f);
         else if (pl.vec)
-            with_mask<NIN>(sm, [&]<unsigned S>() { hipLaunchKernelGGL((k_flat<F, M, true, S>), grid, block, 0, s, pl.g, pl.p, f); });
-        else hipLaunchKernelGGL((k_flat<F, M, false, 0u>), grid, block, 0, s, pl.g, pl.p, f);
+            with_mask<NIN>(sm, [&]<unsigned S>() { hipLaunchKernelGGL((k_flat<F, M, true, S>), grid, block, 0, s, g, pl.p, f); });
+        else hipLaunchKernelGGL((k_flat<F, M, false, 0u>), grid, block, 0, s, g, pl.p, f);
         break;
     case PwVariant::Rows:
         if (pl.vec)
             with_mask<NIN>(sm, [&]<unsigned S>() {
-                if (pl.rk == 2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, pl.g, pl.p, f);
-                else if (pl.rk == 3) hipLaunchKernelGGL((k_rows<F, M, true, S, 3>), grid, block, 0, s, pl.g, pl.p, f);
-                else if (pl.rk == 4) hipLaunchKernelGGL((k_rows<F, M, true, S, 4>), grid, block, 0, s, pl.g, pl.p, f);
-                else hipLaunchKernelGGL((k_rows<F, M, true, S, 0>), grid, block, 0, s, pl.g, pl.p, f);
+                if (pl.rk == 2) hipLaunchKernelGGL((k_rows<F, M, true, S, 2>), grid, block, 0, s, g, pl.p, f);
+                else if (pl.rk == 3) hipLaunchKernelGGL((k_rows<F, M, true, S, 3>), grid, block, 0, s, g, pl.p, f);
+                else if (pl.rk == 4) hipLaunchKernelGGL((k_rows<F, M, true, S, 4>), grid, block, 0, s, g, pl.p, f);
+                else hipLaunchKernelGGL((k_rows<F, M, true, S, 0>), grid, block, 0, s, g, pl.p, f);
             });
-        else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, pl.g, pl.p, f);
+        else hipLaunchKernelGGL((k_rows<F, M, false, 0u>), grid, block, 0, s, g, pl.p, f);
         break;
     case PwVariant::Xpose:
         // One outer tuple per block (no roles): every transposed-operand mask.
@@ -155,18 +157,24 @@ int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
             if constexpr (TR != 0u) {
                 if (pl.vec)
                     with_mask<NIN>(sm, [&]<unsigned S>() {
-                        hipLaunchKernelGGL((k_xpose<F, M, true, TR, S>), grid, block, 0, s, pl.g, pl.p, f);
+                        hipLaunchKernelGGL((k_xpose<F, M, true, TR, S>), grid, block, 0, s, g, pl.p, f);
                     });
-                else hipLaunchKernelGGL((k_xpose<F, M, false, TR, 0u>), grid, block, 0, s, pl.g, pl.p, f);
+                else hipLaunchKernelGGL((k_xpose<F, M, false, TR, 0u>), grid, block, 0, s, g, pl.p, f);
             }
         });
         break;
     case PwVariant::Generic:
-        hipLaunchKernelGGL((k_generic<F, M>), grid, block, 0, s, pl.g, pl.p, f);
+        hipLaunchKernelGGL((k_generic<F, M>), grid, block, 0, s, g, pl.p, f);
         break;
     }
     TRS_LAUNCH_CHECK("pointwise kernel launch");
     return TRS_OK;
+}
+
+template <class F, unsigned M>
+int launch_planned(const F &f, const PwPlan &pl, hipStream_t s) {
+    if (pl.variant == PwVariant::Empty) return TRS_OK;
+    return for_each_part(pl, [&](const PwGeom &g) { return launch_part<F, M>(f, pl, g, s); });
 }
 
 template <class F, unsigned M = 0u>

@@ -89,7 +89,7 @@ int hip_fail(hipError_t e, const char *what) {
 int check_layout(const trs_layout *l, const char *what) {
     if (l == nullptr) return set_error(TRS_E_INVALID_ARGUMENT, "%s layout is null", what);
     if (l->rank < 0 || l->rank > TRS_MAX_RANK)
-        return set_error(TRS_E_INVALID_ARGUMENT, "%s rank %d outside [0, 8]", what, l->rank);
+        return set_error(TRS_E_INVALID_ARGUMENT, "%s rank %d outside [0, %d]", what, l->rank, TRS_MAX_RANK);
     if (l->offset < 0) return set_error(TRS_E_INVALID_ARGUMENT, "%s offset is negative", what);
     int64_t numel = 1;
     for (int d = 0; d < l->rank; d++) {
@@ -126,6 +126,30 @@ bool layout_is_contiguous(const trs_layout *l) {
         expected *= l->shape[d];
     }
     return true;
+}
+
+void merge_layout_dims(const trs_layout *in, trs_layout *out) {
+    trs_layout m{};
+    m.offset = in->offset;
+    int r = 0;
+    for (int d = 0; d < in->rank; d++) {
+        if (in->shape[d] == 1) continue;
+        if (r > 0 && m.stride[r - 1] == in->stride[d] * in->shape[d]) {
+            m.shape[r - 1] *= in->shape[d];
+            m.stride[r - 1] = in->stride[d];
+            continue;
+        }
+        m.shape[r] = in->shape[d];
+        m.stride[r] = in->stride[d];
+        r++;
+    }
+    if (r == 0) {
+        m.shape[0] = 1;
+        m.stride[0] = 1;
+        r = 1;
+    }
+    m.rank = r;
+    *out = m;
 }
 
 DeviceState *device_state() {

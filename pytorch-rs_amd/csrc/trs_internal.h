@@ -76,10 +76,14 @@ int abi_guard(Fn &&fn) noexcept {
 // Maps a HIP failure to TRS_E_HIP with the runtime's message.
 int hip_fail(hipError_t e, const char *what);
 
-// Validates rank (0..8), non-negative shape/stride/offset.
+// Validates rank (0..TRS_MAX_RANK), non-negative shape/stride/offset.
 int check_layout(const trs_layout *l, const char *what);
 int64_t layout_numel(const trs_layout *l);
 bool layout_is_contiguous(const trs_layout *l);
+// Drops size-1 dims and merges each dim into its inner neighbour where
+// stride[d] == stride[d+1] * shape[d+1]: the same elements in the same
+// row-major order, in as few dims as the view allows (at least one).
+void merge_layout_dims(const trs_layout *in, trs_layout *out);
 
 // Contiguous layout of `l`'s shape (for gradients, which are logical-order).
 inline trs_layout contiguous_like(const trs_layout *l) {

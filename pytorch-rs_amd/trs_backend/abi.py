@@ -14,7 +14,7 @@ import numpy as np
 
 PKG = Path(__file__).resolve().parent.parent
 LIB_DIR = PKG / "lib"
-MAX_RANK = 8
+MAX_RANK = 25
 
 TRS_ADD, TRS_SUB, TRS_MUL, TRS_DIV = 0, 1, 2, 3
 TRS_S_ADD, TRS_S_SUB, TRS_S_MUL, TRS_S_DIV, TRS_S_RSUB, TRS_S_RDIV = range(6)
@@ -62,7 +62,7 @@ def contiguous_strides(shape) -> tuple:
 def layout_of(shape, strides=None, offset: int = 0) -> Layout:
     shape = tuple(int(d) for d in shape)
     if len(shape) > MAX_RANK:
-        raise ValueError("rank above 8")
+        raise ValueError(f"rank above {MAX_RANK}")
     if strides is None:
         strides = contiguous_strides(shape)
     lay = Layout()
@@ -88,6 +88,8 @@ class PwPlanInfo(ctypes.Structure):
         ("once", c_uint32),
         ("block", c_int32),
         ("grid", ctypes.c_int64),
+        ("split", c_int32),       # outer dims walked on the host, one launch each
+        ("reserved", c_int32),
     ]
 
 

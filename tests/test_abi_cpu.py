@@ -33,8 +33,16 @@ def test_binding_declares_nothing_the_header_lacks():
 
 
 def test_layout_struct_matches_header_size():
-    # int32 rank, int32 reserved, int64 shape[8], int64 stride[8], int64 offset
-    assert ctypes.sizeof(abi.Layout) == 4 + 4 + 8 * 8 + 8 * 8 + 8
+    # int32 rank, int32 reserved, int64 shape[R], int64 stride[R], int64 offset
+    # with R = TRS_MAX_RANK; the oracle's layout has the same binary form
+    import oracle as O
+    text = (ROOT / "include" / "trs_hip.h").read_text()
+    max_rank = int(re.search(r"^#define TRS_MAX_RANK (\d+)", text, flags=re.M).group(1))
+    assert max_rank == abi.MAX_RANK == O.MAX_RANK == 25
+    assert ctypes.sizeof(abi.Layout) == 4 + 4 + 8 * max_rank + 8 * max_rank + 8
+    assert ctypes.sizeof(O.OLayout) == ctypes.sizeof(abi.Layout)
+    # trs_pw_plan_info: 10 int32 fields, an int64, then split and a reserved int32
+    assert ctypes.sizeof(abi.PwPlanInfo) == 10 * 4 + 8 + 4 + 4
 
 
 def test_philox_known_answer_vectors():

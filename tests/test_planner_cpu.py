@@ -102,6 +102,60 @@ def test_strided_and_empty_layouts():
     assert plan(layout_of((0, 5)), layout_of((5,)), out=layout_of((0, 5))).variant == 0
 
 
+def reversed_strides(shape):
+    """A view transposed in every dim: no two of its dims merge with a
+    contiguous operand's."""
+    st, s = [], 1
+    for d in shape:  # dim d of the view is dim rank-1-d of the reversed buffer
+        st.append(s)
+        s *= d
+    return tuple(st)
+
+
+def test_views_above_eight_dims_split_their_outer_dims_onto_the_host():
+    """The kernels index at most 8 dims; a view keeping more after merging is
+    launched once per index tuple of its outermost dims."""
+    for shape in [(2, 3) * 5, (2,) * 12 + (1,) * 10 + (3, 1, 2), (2,) * 25]:
+        nonunit = sum(1 for d in shape if d != 1)
+        p = plan(layout_of(shape), layout_of(shape, reversed_strides(shape)), out=layout_of(shape))
+        assert (p.rank, p.split) == (8, nonunit - 8)
+        assert p.variant == GENERIC  # the reversed operand's unit stride is on a split dim
+
+
+def test_views_above_eight_dims_that_merge_need_no_split():
+    shape = (2, 3) * 6
+    p = plan(layout_of(shape), layout_of(shape), out=layout_of(shape))
+    assert (p.variant, p.rank, p.split, p.vec) == (FLAT, 1, 0, 1)
+    # broadcast along the 11 outer dims: the rows kernel over [prod, 3]
+    p = plan(layout_of(shape), layout_of((3,)), out=layout_of(shape))
+    assert (p.variant, p.rank, p.split) == (ROWS, 2, 0)
+    assert plan(layout_of((2, 3)), out=layout_of((2, 3))).split == 0
+
+
+def test_split_launches_vectorise_only_when_every_part_is_aligned():
+    shape = (2,) * 9 + (8,)
+    x = layout_of(shape)
+    yst = tuple(8 * 2 ** d for d in range(9)) + (1,)  # dims 0-8 reversed, rows of 8 contiguous
+    p = plan(x, layout_of(shape, yst), out=layout_of(shape))
+    assert (p.variant, p.rank, p.split, p.vec) == (ROWS, 8, 2, 1)
+    p = plan(x, layout_of(shape, yst, offset=1), out=layout_of(shape))  # y's base one float off
+    assert (p.split, p.vec) == (2, 0)
+    # the outermost split dim moves y by 10 floats: the second part of the
+    # launch would start 8 bytes off a 16-byte boundary
+    p = plan(x, layout_of(shape, (10,) + yst[1:]), out=layout_of(shape))
+    assert (p.split, p.vec) == (2, 0)
+
+
+def test_views_above_the_abi_rank_are_errors():
+    lay = abi.Layout()
+    lay.rank = abi.MAX_RANK + 1  # refused before any shape entry is read
+    with pytest.raises(abi.TrsError) as e:
+        plan(layout_of((2,)), out=lay)
+    assert e.value.code == abi.TRS_E_INVALID_ARGUMENT
+    with pytest.raises(ValueError):
+        layout_of((1,) * (abi.MAX_RANK + 1))
+
+
 def test_shape_mismatch_and_bad_arguments_are_errors():
     with pytest.raises(abi.TrsError) as e:
         plan(layout_of((3, 4)), layout_of((5,)), out=layout_of((3, 4)))
