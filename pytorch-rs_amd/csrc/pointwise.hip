@@ -102,12 +102,12 @@ __global__ void __launch_bounds__(256) fill_kernel(float *out, size_t n, float v
 struct ReduceGeom {
     int32_t nkept;
     int32_t nred;
-    int64_t kept_size[kMaxRank];
-    int64_t kept_up[kMaxRank];     // strides of up (output-contiguous) per kept dim
-    int64_t kept_other[kMaxRank];  // strides of other per kept dim
-    int64_t red_size[kMaxRank];
-    int64_t red_up[kMaxRank];
-    int64_t red_other[kMaxRank];
+    int64_t kept_size[TRS_MAX_RANK];
+    int64_t kept_up[TRS_MAX_RANK];     // strides of up (output-contiguous) per kept dim
+    int64_t kept_other[TRS_MAX_RANK];  // strides of other per kept dim
+    int64_t red_size[TRS_MAX_RANK];
+    int64_t red_up[TRS_MAX_RANK];
+    int64_t red_other[TRS_MAX_RANK];
     int64_t nself;
     int64_t nred_total;
     int64_t other_off;
@@ -132,9 +132,24 @@ __global__ void __launch_bounds__(256) reduce_bcast_kernel(const float *up, cons
             ob += c * rg.kept_other[d];
         }
         float acc = 0.0f;
-        int64_t cnt[kMaxRank];
-        for (int d = 0; d < rg.nred; d++) cnt[d] = 0;
-        int64_t uo = ub, oo = ob;
+        // The reduced positions in row-major order: the innermost reduced dim
+        // is stepped by its strides, and where it wraps the next position is
+        // decoded afresh (no per-dim counters, so no local array at any rank).
+        const int last = rg.nred - 1;
+        const int64_t isz = rg.nred ? rg.red_size[last] : 1;
+        const int64_t iup = rg.nred ? rg.red_up[last] : 0, iot = rg.nred ? rg.red_other[last] : 0;
+        auto position = [&](int64_t r, int64_t &u, int64_t &o) {
+            u = ub;
+            o = ob;
+            for (int d = last; d >= 0; d--) {
+                const int64_t q = r / rg.red_size[d];
+                const int64_t cd = r - q * rg.red_size[d];
+                r = q;
+                u += cd * rg.red_up[d];
+                o += cd * rg.red_other[d];
+            }
+        };
+        int64_t uo = ub, oo = ob, ci = 0;
         for (int64_t r0 = 0; r0 < rg.nred_total; r0 += kRedUnroll) {
             float c[kRedUnroll];
 #pragma unroll
@@ -142,16 +157,12 @@ __global__ void __launch_bounds__(256) reduce_bcast_kernel(const float *up, cons
                 if (r0 + i < rg.nred_total) {
                     c[i] = up[uo];
                     if constexpr (HAS_OTHER) c[i] = c[i] * other[oo];
-                    // odometer over reduced dims, innermost last
-                    for (int d = rg.nred - 1; d >= 0; d--) {
-                        if (++cnt[d] < rg.red_size[d]) {
-                            uo += rg.red_up[d];
-                            oo += rg.red_other[d];
-                            break;
-                        }
-                        cnt[d] = 0;
-                        uo -= rg.red_up[d] * (rg.red_size[d] - 1);
-                        oo -= rg.red_other[d] * (rg.red_size[d] - 1);
+                    if (++ci < isz) {
+                        uo += iup;
+                        oo += iot;
+                    } else {
+                        ci = 0;
+                        position(r0 + i + 1, uo, oo);
                     }
                 }
             }
@@ -501,10 +512,6 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
         if (self_bcast) red.add(osz, ustride[d], ost);
         else kept.add(osz, ustride[d], ost);
     }
-    if (kept.n > kMaxRank || red.n > kMaxRank)
-        return set_error(TRS_E_INVALID_ARGUMENT,
-                         "broadcast reduction: the operand's dims merge to %d kept and %d reduced dims, above %d",
-                         kept.n, red.n, kMaxRank);
     rg.nkept = kept.n;
     rg.nred = red.n;
     for (int d = 0; d < kept.n; d++) {

@@ -5,7 +5,8 @@ The ABI takes up to TRS_MAX_RANK (25) dims; a kernel's geometry indexes at
 most 8 after size-1 dims are dropped and contiguous dims merged.  A
 pointwise view that keeps more is run as one launch per index tuple of its
 outermost dims, sum copies such a view to a contiguous buffer first, and the
-broadcast reduction merges its kept and reduced dims.
+broadcast reduction merges its kept and reduced dims, walking any number that
+remain.
 
 The views here are built so that nothing merges: an operand transposed in
 every dim (a contiguous buffer of the reversed shape, read in reverse dim
@@ -213,14 +214,20 @@ def test_broadcast_reduction_above_eight_dims(rank):
     assert_bitwise_equal(got, want)
 
 
-def test_broadcast_reduction_that_does_not_merge_to_eight_dims_is_refused():
-    """Kept and reduced dims alternating 9 times each cannot merge to 8."""
-    shape = (2, 2) * 9
-    self_shape = (2, 1) * 9
-    n = int(np.prod(shape))
-    up = np.ones(n, np.float32)
-    rc, _ = gpu_mul_backward(up, shape, up, shape, O.contiguous_strides(shape), self_shape)
-    assert rc == abi.TRS_E_INVALID_ARGUMENT
+def test_broadcast_reduction_whose_dims_do_not_merge():
+    """Kept and reduced dims alternating 9 times each (rank 18), and a
+    reversed other operand at rank 12 that merges nothing: the per-element
+    reduction walks any number of dims in the reference's order."""
+    rng = rng_for("alternating")
+    for shape, self_shape, ost in [((2, 2) * 9, (2, 1) * 9, None),
+                                   ((2, 3) * 6, (1, 3) + (2, 3) * 5, reversed_strides((2, 3) * 6))]:
+        n = int(np.prod(shape))
+        ost = ost or O.contiguous_strides(shape)
+        up = rng.standard_normal(n).astype(np.float32)
+        other = U.special_mix(rng, n)
+        rc, got = gpu_mul_backward(up, shape, other, shape, ost, self_shape)
+        check(rc)
+        assert_bitwise_equal(got, O.mul_backward(up, shape, other, shape, ost, 0, self_shape))
 
 
 def test_torch_rs_autograd_on_rank_ten_tensors():
@@ -248,3 +255,91 @@ def test_torch_rs_autograd_on_rank_ten_tensors():
     gw = np.transpose(g * x_np, perm)
     assert_bitwise_equal(w.grad.numpy().reshape(-1), gw.reshape(-1))
     assert tuple(x.grad.shape) == shape
+
+
+# ---- random layouts at ranks 6-14 -----------------------------------------
+
+def _rand_shape(rng, rank, cap=200_000):
+    while True:
+        shape = tuple(int(rng.choice([1, 2, 2, 3])) for _ in range(rank))
+        if np.prod(shape) <= cap:
+            return shape
+
+
+def _rand_strides(rng, shape):
+    """A random physical dim order, inner stride 1 or 2, gaps between dims."""
+    perm = rng.permutation(len(shape))
+    strides = [0] * len(shape)
+    step = int(rng.integers(1, 3))
+    for d in reversed(perm):
+        strides[d] = step
+        step *= max(shape[d], 1) + int(rng.integers(0, 2))
+    return tuple(strides)
+
+
+def _rand_bshape(rng, oshape):
+    rank = int(rng.integers(0, len(oshape) + 1))
+    return tuple(1 if rng.random() < 0.3 else d for d in oshape[len(oshape) - rank:])
+
+
+def _rand_view(rng, shape):
+    st = _rand_strides(rng, shape)
+    off = int(rng.integers(0, 3))
+    return U.special_mix(rng, max(O.storage_size(shape, st, off), 1)), shape, st, off
+
+
+@pytest.mark.parametrize("op", [O.ADD, O.MUL])
+def test_random_high_rank_layouts_binary(op):
+    """60 random layouts per op at ranks 6-14 (permuted dims with gaps,
+    offsets, size-1 and broadcast dims): with or without a split, every
+    kernel variant agrees with the oracle bit for bit."""
+    rng = np.random.default_rng(9100 + op)
+    for case in range(60):
+        oshape = _rand_shape(rng, int(rng.integers(6, 15)))
+        ash = oshape if rng.random() < 0.5 else _rand_bshape(rng, oshape)
+        bsh = _rand_bshape(rng, oshape)
+        a, ash, ast, aoff = _rand_view(rng, ash)
+        b, bsh, bst, boff = _rand_view(rng, bsh)
+        osh, ostr = O.binary_output_layout(ash, ast, bsh, bst)
+        want = O.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ostr)
+        got = U.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ostr)
+        try:
+            assert_bitwise_equal(got, want)
+        except AssertionError as e:
+            raise AssertionError(f"case {case}: a {ash} {ast} +{aoff}, b {bsh} {bst} +{boff}: {e}") from None
+
+
+def test_random_high_rank_layouts_unary():
+    rng = np.random.default_rng(9200)
+    for case in range(60):
+        shape = _rand_shape(rng, int(rng.integers(6, 15)))
+        a, sh, st, off = _rand_view(rng, shape)
+        ostr = O.unary_output_strides(sh, st)
+        for op in (O.RELU, O.COPY):
+            try:
+                assert_bitwise_equal(U.unary(op, a, sh, st, off, ostr), O.unary(op, a, sh, st, off, ostr),
+                                     nan_equal=False)
+            except AssertionError as e:
+                raise AssertionError(f"case {case} op {op}: {sh} {st} +{off}: {e}") from None
+
+
+def test_random_high_rank_broadcast_reduction():
+    """60 random (output, other, self) shapes at ranks 6-12: the multiply VJP
+    accumulates in the reference's order bit for bit."""
+    rng = np.random.default_rng(9300)
+    for case in range(60):
+        oshape = _rand_shape(rng, int(rng.integers(6, 13)), cap=100_000)
+        self_shape = _rand_bshape(rng, oshape)
+        oth_shape = _rand_bshape(rng, oshape) if rng.random() < 0.6 else oshape
+        oth_strides = _rand_strides(rng, oth_shape)
+        n = int(np.prod(oshape))
+        up = U.special_mix(rng, n)
+        other = U.special_mix(rng, max(O.storage_size(oth_shape, oth_strides, 0), 1))
+        rc, got = gpu_mul_backward(up, oshape, other, oth_shape, oth_strides, self_shape)
+        check(rc)
+        want = O.mul_backward(up, oshape, other, oth_shape, oth_strides, 0, self_shape)
+        try:
+            assert_bitwise_equal(got, want)
+        except AssertionError as e:
+            raise AssertionError(f"case {case}: out {oshape}, other {oth_shape} {oth_strides}, "
+                                 f"self {self_shape}: {e}") from None
