@@ -19,7 +19,7 @@ MAX_RANK = 25
 TRS_ADD, TRS_SUB, TRS_MUL, TRS_DIV = 0, 1, 2, 3
 TRS_S_ADD, TRS_S_SUB, TRS_S_MUL, TRS_S_DIV, TRS_S_RSUB, TRS_S_RDIV = range(6)
 TRS_EXP, TRS_RELU, TRS_NEG, TRS_COPY = 0, 1, 2, 3
-TRS_E_SHAPE_MISMATCH, TRS_E_INVALID_ARGUMENT = -4, -7
+TRS_E_SHAPE_MISMATCH, TRS_E_INVALID_ARGUMENT, TRS_E_FUSION = -4, -7, -9
 
 ERROR_NAMES = {
     -1: "ALLOCATION_FAILED", -2: "INDEX_OVERFLOW", -3: "STRIDE_OVERFLOW", -4: "SHAPE_MISMATCH",

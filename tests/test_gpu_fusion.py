@@ -509,3 +509,75 @@ def test_fused_backward_input_with_two_uses_equals_eager():
     sq_f = run(torch_rs.fuse(lambda x, y: x * x))
     assert sq_f[0]._grad_fn_name == "FusedBackward0" and sq_f[2].grad is None
     assert_bitwise_equal(sq_f[1].grad.numpy().ravel(), sq_e[1].grad.numpy().ravel())
+
+
+# ---- the program limits: 8 inputs, 8 outputs ----------------------------------
+
+_EIGHT_IR = ("in f32\n" * 8 + "add %0 %1\nmul %8 %2\nsub %9 %3\nadd %10 %4\nmul %11 %5\ndiv %12 %6\nadd %13 %7\n"
+             "relu %14\n" + "".join(f"out %{v}\n" for v in range(8, 16)))
+_EIGHT_OPS = [O.ADD, O.MUL, O.SUB, O.ADD, O.MUL, O.DIV, O.ADD]
+
+
+def _eight_views(rng, oshape):
+    """Eight operands of oshape (rank >= 2) in different layouts: contiguous,
+    a row broadcast, transposed in its last two dims, a broadcast along the
+    second-to-last dim, an offset view transposed in every dim (so no dims
+    merge), a scalar, a strided gather and a column broadcast."""
+    r = len(oshape)
+    lead, (m, k) = oshape[:-2], oshape[-2:]
+    views = []
+
+    def add(shape, strides=None, off=0, extra=0):
+        strides = O.contiguous_strides(shape) if strides is None else strides
+        n = O.storage_size(shape, strides, off) + extra
+        views.append((U.special_mix(rng, max(n, 1)), tuple(shape), tuple(strides), off))
+
+    add(oshape)
+    add((k,))
+    t = O.contiguous_strides(lead + (k, m))
+    add(oshape, t[:-2] + (1, m))
+    add(lead + (1, k))
+    add(oshape, tuple(reversed(O.contiguous_strides(tuple(reversed(oshape))))), off=5)
+    add(())
+    add(oshape, tuple(2 * s for s in O.contiguous_strides(oshape)))
+    add((m, 1))
+    assert all(len(v[1]) <= r for v in views)
+    return views
+
+
+@pytest.mark.parametrize("oshape", [(4, 33, 70), (2, 3, 2, 3, 2, 3, 2, 3, 5, 6)])
+def test_program_with_eight_inputs_and_eight_outputs(oshape):
+    """The most inputs and outputs a program takes, at rank 3 and at rank 10
+    (launched in parts): every output equals the eager oracle composition
+    bit for bit."""
+    from trs_backend import abi
+    rng = np.random.default_rng(len(oshape))
+    views = _eight_views(rng, oshape)
+    lays = [layout_of(*v[1:3], v[3]) for v in views]
+    assert abi.pointwise_plan(lays, layout_of(oshape)).split == max(0, len(oshape) - 8)
+    n = int(np.prod(oshape))
+    ostr = O.contiguous_strides(oshape)
+    kid = U.fusion_compile(_EIGHT_IR)
+    outs = [U.out_buffer(n) for _ in range(8)]
+    rc = U.fusion_launch_multi(kid, [U.dev(v[0]) for v in views], lays, outs, layout_of(oshape))
+    assert rc == 0
+    buf, sh, st, off = views[0]
+    want = []
+    for i, op in enumerate(_EIGHT_OPS, start=1):
+        b = views[i]
+        buf = O.binary(op, buf, sh, st, off, b[0], b[1], b[2], b[3], oshape, ostr)
+        sh, st, off = oshape, ostr, 0
+        want.append(buf)
+    want.append(O.unary(O.RELU, buf, oshape, ostr, 0, ostr))
+    for i in range(8):
+        assert_bitwise_equal(outs[i].to_numpy(count=n), want[i])
+
+
+def test_program_limits_are_errors():
+    import ctypes
+    from trs_backend import abi
+    kid = ctypes.c_uint64()
+    nine = "in f32\n" * 9 + "add %0 %1\nout %9\n"
+    assert abi.lib.trs_fusion_compile(nine.encode(), len(nine), ctypes.byref(kid)) == abi.TRS_E_FUSION
+    nine_out = "in f32\n" + "".join(f"neg %{v}\n" for v in range(9)) + "".join(f"out %{v}\n" for v in range(1, 10))
+    assert abi.lib.trs_fusion_compile(nine_out.encode(), len(nine_out), ctypes.byref(kid)) == abi.TRS_E_FUSION
