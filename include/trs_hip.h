@@ -171,7 +171,10 @@ int trs_mask_apply_f32(const float *h, const trs_layout *lh, const uint8_t *mask
  * u = 2^-24 and d = ceil(n/256) + 8 up to 32,768 elements, else
  * ceil(ceil(n/1024)/256) + 20.  Every partial sum starts from -0.0, as
  * Rust's f32 Sum does, so an all-(-0.0) input gives -0.0; an empty one gives
- * -0.0 too. */
+ * -0.0 too.  Elements are added by their row-major logical position: a view
+ * that keeps more than 8 dims after size-1 dims are dropped and contiguous
+ * dims merged is first copied to a contiguous buffer of the call's own, which
+ * gives the same bits. */
 int trs_sum_f32(const float *x, const trs_layout *lx, float *out);
 /* trs_sum_f32 that allocates nothing: no counterpart in the reference; for
  * callers that cannot allocate device memory (code under HIP graph capture,
@@ -183,7 +186,9 @@ int trs_sum_f32(const float *x, const trs_layout *lx, float *out);
  * device's library stream, and calls that ran on different streams of one
  * GPU at once would race on it.  Nothing needs clearing between calls (pass
  * 1 writes every partial pass 2 reads).  Its device address is looked up
- * once per device when the library sets the device up (trs_init). */
+ * once per device when the library sets the device up (trs_init).  It cannot
+ * copy, so a view that keeps more than 8 dims after merging is refused
+ * (TRS_E_INVALID_ARGUMENT). */
 int trs_sum_f32_noalloc(const float *x, const trs_layout *lx, float *out);
 /* out[0..n) = *value (a device float): the Sum VJP fill (src/tensor.rs:3008-3013). */
 int trs_fill_from_device_f32(float *out, size_t n, const float *value);
