@@ -206,6 +206,13 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
         const float *Bs = As + ASIZE;
         const bool more = s + 1 < kslices;
         if (more) load_tiles.template operator()<F>((s + 1) * BK);
+        // The next slice goes to the other buffer, which no wave reads in this
+        // slice (the barrier ending the previous slice saw its last reads).
+        auto store_next = [&]() {
+            float *An = lds + (cur ^ 1) * (ASIZE + BSIZE);
+            la.template store<APITCH>(An);
+            lb.template store<BPITCH>(An + ASIZE);
+        };
         if constexpr (VK) {
             // Kept rolled: unrolled, the groups' fragment reads are all
             // hoisted and BK=32 spills at 16 waves; rolled, one barrier per
@@ -235,6 +242,9 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
                         for (int j = 0; j < TN; j++)
                             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
                 }
+                // After the first 16 k: the stores' LDS writes then complete
+                // under the next group's MFMAs instead of before the barrier.
+                if (kg == 0 && more) store_next();
             }
         } else {
             // The slice's MFMAs at raised wave priority: with two blocks per
@@ -262,11 +272,7 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
             __builtin_amdgcn_s_setprio(0);
-        }
-        if (more) {
-            float *An = lds + (cur ^ 1) * (ASIZE + BSIZE);
-            la.template store<APITCH>(An);
-            lb.template store<BPITCH>(An + ASIZE);
+            if (more) store_next();
         }
         __syncthreads();
     };
