@@ -89,6 +89,35 @@ def test_exp_exhaustive_over_all_bit_patterns():
     assert worst <= 2
 
 
+def test_relu_neg_and_relu_vjp_exhaustive_over_all_bit_patterns():
+    """relu (src/tensor.rs:4392-4400), neg (:4388-4390) and relu's VJP
+    (:4422-4432) on the device at every one of the 2^32 float bit patterns,
+    bit for bit against the oracle (NaN payloads included: all three only
+    pass bits through, flip the sign or return +0.0)."""
+    import ctypes
+    from trs_backend import abi
+    from trs_backend.abi import check, layout_of
+    chunk = 1 << 28
+    lay = layout_of((chunk,))
+    up = np.full(chunk, 1.25, np.float32)
+    dup = U.dev(up)
+    out = U.out_buffer(chunk)
+    want_vjp_pass = np.float32(1.25)
+    for k in range(16):
+        first = k * chunk
+        x = np.arange(first, first + chunk, dtype=np.uint64).astype(np.uint32).view(np.float32)
+        dx = U.dev(x)
+        for op in (O.RELU, O.NEG):
+            check(abi.lib.trs_unary_f32(op, dx.ptr, ctypes.byref(lay), out.ptr, ctypes.byref(lay)))
+            assert_bitwise_equal(out.to_numpy(count=chunk), O.unary_contig(op, x), nan_equal=False)
+        check(abi.lib.trs_relu_backward_f32(dx.ptr, ctypes.byref(lay), dup.ptr, out.ptr))
+        got = out.to_numpy(count=chunk)
+        want = O.relu_backward(x, (chunk,), (1,), 0, up)
+        assert_bitwise_equal(got, want, nan_equal=False)
+        assert set(np.unique(got.view(np.uint32)).tolist()) <= {0, int(want_vjp_pass.view(np.uint32))}
+        del x, dx
+
+
 def _threads():
     import os
     return max(1, min(16, len(os.sched_getaffinity(0))))
