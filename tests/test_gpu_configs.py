@@ -89,11 +89,14 @@ def test_exp_exhaustive_over_all_bit_patterns():
     assert worst <= 2
 
 
-def test_relu_neg_and_relu_vjp_exhaustive_over_all_bit_patterns():
+def test_relu_neg_relu_vjp_and_scalar_ops_exhaustive_over_all_bit_patterns():
     """relu (src/tensor.rs:4392-4400), neg (:4388-4390) and relu's VJP
     (:4422-4432) on the device at every one of the 2^32 float bit patterns,
     bit for bit against the oracle (NaN payloads included: all three only
-    pass bits through, flip the sign or return +0.0)."""
+    pass bits through, flip the sign or return +0.0).  The configs' scalar
+    ops, x - 1.0 (sub_scalar) and x * f32(1/0.9) (the dropout scale), too:
+    one IEEE rounding each, so subnormal inputs and results pin the
+    device's denormal mode (NaNs compared as NaN)."""
     import ctypes
     from trs_backend import abi
     from trs_backend.abi import check, layout_of
@@ -110,6 +113,10 @@ def test_relu_neg_and_relu_vjp_exhaustive_over_all_bit_patterns():
         for op in (O.RELU, O.NEG):
             check(abi.lib.trs_unary_f32(op, dx.ptr, ctypes.byref(lay), out.ptr, ctypes.byref(lay)))
             assert_bitwise_equal(out.to_numpy(count=chunk), O.unary_contig(op, x), nan_equal=False)
+        for op, s in ((O.S_SUB, 1.0), (O.S_MUL, float(np.float32(1.0 / 0.9)))):
+            check(abi.lib.trs_binary_scalar_f32(op, dx.ptr, ctypes.byref(lay), ctypes.c_float(s), out.ptr,
+                                                ctypes.byref(lay)))
+            assert_bitwise_equal(out.to_numpy(count=chunk), O.scalar_contig(op, x, s))
         check(abi.lib.trs_relu_backward_f32(dx.ptr, ctypes.byref(lay), dup.ptr, out.ptr))
         got = out.to_numpy(count=chunk)
         want = O.relu_backward(x, (chunk,), (1,), 0, up)
