@@ -343,3 +343,40 @@ def test_random_high_rank_broadcast_reduction():
         except AssertionError as e:
             raise AssertionError(f"case {case}: out {oshape}, other {oth_shape} {oth_strides}, "
                                  f"self {self_shape}: {e}") from None
+
+
+def test_fused_transposing_roles_inside_a_split_launch():
+    """(a + b) * c at rank 9 with c transposed in its last two dims and
+    reversed in the outer ones, b broadcast over every outer dim (held in
+    registers across a walk) and a constant along the transposed dim (loaded
+    once per tuple): the inner 8 dims run the transposing kernel with its
+    roles, once per index of the split dim, bit-exact against the oracle."""
+    outer = (2, 3, 2, 3, 2, 3, 2)
+    m, k = 64, 128
+    shape = outer + (m, k)
+    rng = rng_for("xpose_split")
+    ashape = outer + (1, k)
+    bshape = (1,) * len(outer) + (m, k)
+    n = int(np.prod(shape))
+    a = U.special_mix(rng, int(np.prod(ashape)))
+    b = U.special_mix(rng, m * k)
+    c = U.special_mix(rng, n)
+    ast, bst = O.contiguous_strides(ashape), O.contiguous_strides(bshape)
+    # c: a contiguous buffer laid out as reversed(outer) + (k, m), viewed in
+    # outer + (m, k) order
+    base = O.contiguous_strides(tuple(reversed(outer)) + (k, m))
+    cst = tuple(reversed(base[:len(outer)])) + (1, m)
+    lays = [layout_of(ashape, ast), layout_of(bshape, bst), layout_of(shape, cst)]
+    info = abi.pointwise_plan(lays, layout_of(shape), roles=True)
+    assert (info.variant, info.split, info.rank) == (3, 1, 8)  # transposing kernel, one split dim
+    assert (info.trans, info.held, info.once) == (0b100, 0b010, 0b001)
+    kid = U.fusion_compile("in f32\nin f32\nin f32\nadd %0 %1\nmul %3 %2\nout %4\n")
+    out = U.out_buffer(n)
+    U.fusion_launch(kid, [U.dev(a), U.dev(b), U.dev(c)], lays, out, layout_of(shape))
+    ost = O.contiguous_strides(shape)
+    t = O.binary(O.ADD, a, ashape, ast, 0, b, bshape, bst, 0, shape, ost)
+    want = O.binary(O.MUL, t, shape, ost, 0, c, shape, cst, 0, shape, ost)
+    assert_bitwise_equal(out.to_numpy(count=n), want)
+    # the eager launcher plans the same layout without roles
+    got = U.binary(O.MUL, t, shape, ost, 0, c, shape, cst, 0, shape, ost)
+    assert_bitwise_equal(got, want)
