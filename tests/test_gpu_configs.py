@@ -94,7 +94,8 @@ def test_relu_neg_relu_vjp_and_scalar_ops_exhaustive_over_all_bit_patterns():
     (:4422-4432) on the device at every one of the 2^32 float bit patterns,
     bit for bit against the oracle (NaN payloads included: all three only
     pass bits through, flip the sign or return +0.0).  The configs' scalar
-    ops, x - 1.0 (sub_scalar) and x * f32(1/0.9) (the dropout scale), too:
+    ops, x - 1.0 (sub_scalar) and x * f32(1/0.9), and dropout-apply
+    (h * f32(mask)) * f32(1/0.9) with each mask value, too:
     one IEEE rounding each, so subnormal inputs and results pin the
     device's denormal mode (NaNs compared as NaN)."""
     import ctypes
@@ -106,6 +107,10 @@ def test_relu_neg_relu_vjp_and_scalar_ops_exhaustive_over_all_bit_patterns():
     dup = U.dev(up)
     out = U.out_buffer(chunk)
     want_vjp_pass = np.float32(1.25)
+    scale = float(np.float32(1.0 / 0.9))
+    m0 = (np.arange(chunk) & 1).astype(np.uint8)
+    m1 = (1 - m0).astype(np.uint8)
+    dmask0, dmask1 = (U.dev(m0), m0), (U.dev(m1), m1)
     for k in range(16):
         first = k * chunk
         x = np.arange(first, first + chunk, dtype=np.uint64).astype(np.uint32).view(np.float32)
@@ -113,6 +118,12 @@ def test_relu_neg_relu_vjp_and_scalar_ops_exhaustive_over_all_bit_patterns():
         for op in (O.RELU, O.NEG):
             check(abi.lib.trs_unary_f32(op, dx.ptr, ctypes.byref(lay), out.ptr, ctypes.byref(lay)))
             assert_bitwise_equal(out.to_numpy(count=chunk), O.unary_contig(op, x), nan_equal=False)
+        # dropout-apply (h * f32(m)) * s with complementary masks, so both mask
+        # values meet every h
+        for mask in (dmask0, dmask1):
+            check(abi.lib.trs_mask_apply_f32(dx.ptr, ctypes.byref(lay), mask[0].ptr, ctypes.byref(lay),
+                                             ctypes.c_float(scale), out.ptr, ctypes.byref(lay)))
+            assert_bitwise_equal(out.to_numpy(count=chunk), O.mask_apply(x, mask[1], scale))
         for op, s in ((O.S_SUB, 1.0), (O.S_MUL, float(np.float32(1.0 / 0.9)))):
             check(abi.lib.trs_binary_scalar_f32(op, dx.ptr, ctypes.byref(lay), ctypes.c_float(s), out.ptr,
                                                 ctypes.byref(lay)))
