@@ -198,7 +198,6 @@ constexpr int kStRows = 256;
 constexpr int kStChains = 32;                    // chains per block (adder lanes 0..31)
 constexpr int kStProducers = 8;                  // producer waves; wave 8 adds
 constexpr int kStLanes = (kStProducers + 1) * 64;
-constexpr int kStQuads = kStProducers * 8;       // row quads per producer pass (256 rows)
 
 struct RedColsGeom {
     int64_t KO, R, KI;
@@ -242,27 +241,38 @@ __device__ __forceinline__ float stage_copy(float x) {
     return y;
 }
 
-template <int OT, int AHEAD, int SR>
+// CH = 32 or 16 chains per block.  A producer wave covers CH/4 chain quads
+// by RQ = 256/CH row quads.  With 16, a block reads 64 B of each row, and
+// blocks b and b + 8 (one XCD) take the two halves of each 128 B line, so
+// the line is fetched once into that XCD's L2; the launcher uses it when
+// 32-chain blocks would leave CUs idle.
+template <int OT, int AHEAD, int SR, int CH = kStChains>
 __global__ void __launch_bounds__(kStLanes) reduce_stage_kernel(const float *up, const float *other, RedColsGeom g,
                                                                  float *grad) {
-    constexpr int NQ = SR / (4 * kStQuads);  // 4x4 blocks per producer lane per stage
+    static_assert(CH == 32 || CH == 16, "chains per block");
+    constexpr int RQ = 256 / CH;                // row quads per producer wave
+    constexpr int QUADS = kStProducers * RQ;    // row quads per producer pass
+    constexpr int NQ = SR / (4 * QUADS);        // 4x4 blocks per producer lane per stage
     // Floats per chain in a stage: (SR + 4) / 4 is 1 mod 16, so the b128
     // accesses of 8 consecutive lanes (chain-strided for the adder,
     // row-strided for the producers) fall on distinct 4-bank groups.
     constexpr int PITCH = SR + 4;
-    static_assert(NQ >= 1 && NQ * 4 * kStQuads == SR && (PITCH / 4) % 16 == 1, "stage shape");
-    __shared__ __attribute__((aligned(16))) float stage[2][kStChains][PITCH];
+    static_assert(NQ >= 1 && NQ * 4 * QUADS == SR && (PITCH / 4) % 16 == 1, "stage shape");
+    __shared__ __attribute__((aligned(16))) float stage[2][CH][PITCH];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int64_t groups = g.KI / kStChains;
+    const int64_t groups = g.KI / CH;
     const int64_t ko = blockIdx.x / groups;
-    const int64_t ki0 = (blockIdx.x % groups) * kStChains;
+    int64_t gi = blockIdx.x % groups;
+    if (CH == 16 && groups % 16 == 0)  // blocks b, b + 8: the two halves of one 128 B line
+        gi = (gi / 16) * 16 + 2 * (gi % 8) + (gi / 8) % 2;
+    const int64_t ki0 = gi * CH;
     const int64_t nst = (g.R + SR - 1) / SR;
     const int64_t nit = (nst + AHEAD - 1) / AHEAD * AHEAD;  // stages run, padded to whole rings
     if (wave < kStProducers) {
-        const int cq = lane >> 3;  // chains cq*4 .. cq*4+3
-        // row quads j*64 + wave*8 + (lane&7) of a stage, j < NQ
-        const int quad0 = wave * 8 + (lane & 7);
+        const int cq = lane / RQ;  // chains cq*4 .. cq*4+3
+        // row quads j*QUADS + wave*RQ + lane%RQ of a stage, j < NQ
+        const int quad0 = wave * RQ + lane % RQ;
         // Loads go through a buffer descriptor per stage, built in scalar
         // registers from the block's base and the stage index: a lane's byte
         // offsets within a stage never change, and the descriptor's extent
@@ -275,11 +285,11 @@ __global__ void __launch_bounds__(kStLanes) reduce_stage_kernel(const float *up,
         for (int j = 0; j < NQ; j++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int64_t row = (j * kStQuads + quad0) * 4 + i;
+                const int64_t row = (j * QUADS + quad0) * 4 + i;
                 vu[j][i] = (int)((row * g.up_r + cq * 4) * 4);
                 if constexpr (OT == kOtVecKi) vo[j][i] = (int)((row * g.ot_r + cq * 4) * 4);
                 else if constexpr (OT == kOtVecR)
-                    vo[j][i] = (int)(((int64_t)(cq * 4 + i) * g.ot_ki + (j * kStQuads + quad0) * 4) * 4);
+                    vo[j][i] = (int)(((int64_t)(cq * 4 + i) * g.ot_ki + (j * QUADS + quad0) * 4) * 4);
                 else vo[j][i] = 0;
             }
         // ru[s][j][i]: row i's 4 chains; ro[s][j][i]: the same for kOtVecKi
@@ -288,20 +298,20 @@ __global__ void __launch_bounds__(kStLanes) reduce_stage_kernel(const float *up,
         auto issue = [&](int slot, int64_t st) {
             const int64_t sc = st < nst ? st : nst - 1;  // past the end: no rows, base kept in range
             const int64_t rem = g.R - st * SR;            // rows from this stage's first on
-            const auto rs = stage_rsrc(ub + sc * SR * g.up_r, stage_span(rem, g.up_r, kStChains));
+            const auto rs = stage_rsrc(ub + sc * SR * g.up_r, stage_span(rem, g.up_r, CH));
 #pragma unroll
             for (int j = 0; j < NQ; j++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) ru[slot][j][i] = buffer_vf4(rs, vu[j][i]);
             if constexpr (OT == kOtVecKi) {
-                const auto os = stage_rsrc(ob + sc * SR * g.ot_r, stage_span(rem, g.ot_r, kStChains));
+                const auto os = stage_rsrc(ob + sc * SR * g.ot_r, stage_span(rem, g.ot_r, CH));
 #pragma unroll
                 for (int j = 0; j < NQ; j++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) ro[slot][j][i] = buffer_vf4(os, vo[j][i]);
             } else if constexpr (OT == kOtVecR) {
-                // chain 31's remaining rows end the extent
-                const auto os = stage_rsrc(ob + sc * SR, stage_span(rem, 1, (kStChains - 1) * g.ot_ki + 1));
+                // the last chain's remaining rows end the extent
+                const auto os = stage_rsrc(ob + sc * SR, stage_span(rem, 1, (CH - 1) * g.ot_ki + 1));
 #pragma unroll
                 for (int j = 0; j < NQ; j++)
 #pragma unroll
@@ -312,7 +322,7 @@ __global__ void __launch_bounds__(kStLanes) reduce_stage_kernel(const float *up,
                 for (int j = 0; j < NQ; j++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        const int64_t r = st * SR + (j * kStQuads + quad0) * 4 + i;
+                        const int64_t r = st * SR + (j * QUADS + quad0) * 4 + i;
                         const float *op = oc + (r < g.R ? r : g.R - 1) * g.ot_r;
                         ro[slot][j][i] = vf4{op[0], op[g.ot_ki], op[2 * g.ot_ki], op[3 * g.ot_ki]};
                     }
@@ -351,7 +361,7 @@ __global__ void __launch_bounds__(kStLanes) reduce_stage_kernel(const float *up,
                         }
 #pragma unroll
                     for (int c = 0; c < 4; c++)
-                        *(vf4 *)&stage[st & 1][cq * 4 + c][(j * kStQuads + quad0) * 4] = w[c];
+                        *(vf4 *)&stage[st & 1][cq * 4 + c][(j * QUADS + quad0) * 4] = w[c];
                 }
                 issue(k, st + AHEAD);
                 __syncthreads();
@@ -359,9 +369,9 @@ __global__ void __launch_bounds__(kStLanes) reduce_stage_kernel(const float *up,
         }
     } else {
         float acc = 0.0f;
-        const bool active = lane < kStChains;
+        const bool active = lane < CH;
         auto add_stage = [&](int64_t st) {
-            const float *row = &stage[st & 1][lane & (kStChains - 1)][0];
+            const float *row = &stage[st & 1][lane & (CH - 1)][0];
             const int64_t left = g.R - st * SR;
             if (left >= SR) {
                 // SR/4 quads in groups of 8, the next group read before the
@@ -547,20 +557,31 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
         cg.KO * (cg.KI / kStChains) <= INT32_MAX && (uintptr_t)up % 16 == 0 && cg.up_ko % 4 == 0 &&
         cg.up_r % 4 == 0 && fits(kStRows * cg.up_r + kStChains) &&
         (!other || (cg.ot_ko >= 0 && cg.ot_r >= 0 && cg.ot_ki >= 0))) {
-        const int64_t grid = cg.KO * (cg.KI / kStChains);
-        const dim3 gd((unsigned)grid), bd(kStLanes);
-        constexpr int SR = kStRows;
-        if (!other) {
-            hipLaunchKernelGGL((reduce_stage_kernel<kOtNone, 2, SR>), gd, bd, 0, dev->stream, up, other, cg, grad);
-        } else {
-            const bool base16 = (uintptr_t)(other + cg.other_off) % 16 == 0 && cg.ot_ko % 4 == 0;
-            if (base16 && cg.ot_ki == 1 && cg.ot_r % 4 == 0 && fits(SR * cg.ot_r + kStChains))
-                hipLaunchKernelGGL((reduce_stage_kernel<kOtVecKi, 2, SR>), gd, bd, 0, dev->stream, up, other, cg, grad);
-            else if (base16 && cg.ot_r == 1 && cg.ot_ki % 4 == 0 && cg.R % 4 == 0 && fits(kStChains * cg.ot_ki + SR))
-                hipLaunchKernelGGL((reduce_stage_kernel<kOtVecR, 2, SR>), gd, bd, 0, dev->stream, up, other, cg, grad);
-            else
-                hipLaunchKernelGGL((reduce_stage_kernel<kOtScalar, 2, SR>), gd, bd, 0, dev->stream, up, other, cg, grad);
-        }
+        auto launch = [&]<int CH, int SR>() {
+            const int64_t grid = cg.KO * (cg.KI / CH);
+            const dim3 gd((unsigned)grid), bd(kStLanes);
+            if (!other) {
+                hipLaunchKernelGGL((reduce_stage_kernel<kOtNone, 2, SR, CH>), gd, bd, 0, dev->stream, up, other, cg,
+                                   grad);
+            } else {
+                const bool base16 = (uintptr_t)(other + cg.other_off) % 16 == 0 && cg.ot_ko % 4 == 0;
+                if (base16 && cg.ot_ki == 1 && cg.ot_r % 4 == 0 && fits(SR * cg.ot_r + CH))
+                    hipLaunchKernelGGL((reduce_stage_kernel<kOtVecKi, 2, SR, CH>), gd, bd, 0, dev->stream, up, other,
+                                       cg, grad);
+                else if (base16 && cg.ot_r == 1 && cg.ot_ki % 4 == 0 && cg.R % 4 == 0 && fits(CH * cg.ot_ki + SR))
+                    hipLaunchKernelGGL((reduce_stage_kernel<kOtVecR, 2, SR, CH>), gd, bd, 0, dev->stream, up, other,
+                                       cg, grad);
+                else
+                    hipLaunchKernelGGL((reduce_stage_kernel<kOtScalar, 2, SR, CH>), gd, bd, 0, dev->stream, up, other,
+                                       cg, grad);
+            }
+        };
+        // 16-chain blocks with 512-row stages when 32-chain blocks would
+        // leave CUs idle (a bias gradient over [8192, 4096]: 128 blocks).
+        if (cg.KO * (cg.KI / kStChains) < dev->cu_count && cg.R >= 2 * kStRows && fits(2 * kStRows * cg.up_r + 16))
+            launch.template operator()<16, 2 * kStRows>();
+        else
+            launch.template operator()<kStChains, kStRows>();
         TRS_LAUNCH_CHECK("staged broadcast reduction kernel");
         return TRS_OK;
     }

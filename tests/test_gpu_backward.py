@@ -362,3 +362,19 @@ def test_random_broadcast_mul_vjp_and_reduce_bit_exact():
         except AssertionError as e:
             raise AssertionError(f"case {case}: out {oshape}, other {oth_shape} {oth_strides} +{oth_off}, "
                                  f"self {self_shape}: {e}") from None
+
+
+@pytest.mark.parametrize("oshape,self_shape", [((4099, 32), (32,)), ((1030, 64), (64,)), ((2, 700, 96), (2, 1, 96))])
+def test_staged_mul_vjp_scalar_other_reads_on_16_chain_blocks(oshape, self_shape):
+    """Few chains over at least 512 rows take 16-chain blocks; `other`
+    transposed with a row count that is not a multiple of 4 is read one
+    float at a time.  Bit for bit against the oracle."""
+    rng = np.random.default_rng(sum(oshape))
+    n = int(np.prod(oshape))
+    up = rng.standard_normal(n).astype(np.float32)
+    other = rng.standard_normal(n).astype(np.float32)
+    *lead, m, k = oshape
+    base = O.contiguous_strides(tuple(lead) + (k, m))
+    ostr = tuple(base[:-2]) + (base[-1], base[-2])
+    got = gpu_mul_backward(up, oshape, other, oshape, ostr, 0, self_shape)
+    assert_bitwise_equal(got, O.mul_backward(up, oshape, other, oshape, ostr, 0, self_shape))
