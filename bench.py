@@ -62,12 +62,14 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-configs", action="store_true",
                     help="time the reference's CPU path (oracle, one thread) on every BASELINE config and exit")
-    ap.add_argument("--workload", choices=("fused_chain", "copy", "transfer", "matmul", "config"),
+    ap.add_argument("--workload", choices=("fused_chain", "copy", "transfer", "matmul", "config", "torch_ceilings"),
                     default="fused_chain",
                     help="copy: a plain 2^28-float copy kernel, the calibration run for rocprofv3 byte counters; "
                          "transfer: host<->device copy rates (pageable and page-locked host memory); "
                          "matmul: the 4096^3 fp32 GEMM alone, for rocprofv3 MFMA counters; "
-                         "config: one of the extra configs alone (--config), for per-kernel profiles")
+                         "config: one of the extra configs alone (--config), for per-kernel profiles; "
+                         "torch_ceilings: ROCm PyTorch's own kernels on configs 1 and 3's shapes, in a process "
+                         "that never loads this library (independent same-box ceilings)")
     ap.add_argument("--config", choices=("relu_bias", "broadcast_strided", "reduce_vjp", "matmul", "matmul_shapes",
                                          "mlp"),
                     default="broadcast_strided", help="the extra config --workload config runs")
@@ -77,6 +79,14 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    if args.workload == "torch_ceilings":
+        # Loaded by path: importing the trs_backend package would load libtrs_hip.so.
+        import importlib.util
+        spec = importlib.util.spec_from_file_location(
+            "torch_ceilings", ROOT / "pytorch-rs_amd" / "trs_backend" / "torch_ceilings.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        return mod.main()
     ensure_built()
     if args.cpu_configs:
         return cpu_configs()

@@ -103,16 +103,26 @@ def relu_bias(log, reps: int = SHORT_KERNEL_REPS, sets: int = 8) -> dict:
         i[0] += 1
         check(abi.lib.trs_unary_f32(3, xs[k].ptr, ctypes.byref(ln), tmp[k].ptr, ctypes.byref(ln)))
 
+    # The runtime's own device-to-device copy (hipMemcpyAsync) of the same bytes.
+    def d2d():
+        k = i[0] % sets
+        i[0] += 1
+        check(abi.lib.trs_memcpy_d2d(tmp[k].ptr, xs[k].ptr, R * C * 4))
+
     e = time_region(eager, reps)
     f = time_region(fused, reps)
     cp = time_region(copy, reps)
+    dd = time_region(d2d, reps)
     spread = _spread(time_launches(fused, 20))
-    log(f"relu_bias: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us, same-shape copy {cp * 1e3:.1f} us")
+    log(f"relu_bias: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us, same-shape copy {cp * 1e3:.1f} us, "
+        f"hipMemcpyAsync d2d {dd * 1e3:.1f} us")
     return {"relu_bias": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
                           "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
                           "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS, "fused_spread": spread,
                           "copy_same_shape_us": cp * 1e3, "copy_same_shape_frac_hbm": 2 * R * C * 4 / (cp * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                          "fused_time_over_copy": f / cp, "buffer_sets": sets,
+                          "fused_time_over_copy": f / cp, "memcpy_d2d_same_shape_us": dd * 1e3,
+                          "memcpy_d2d_same_shape_frac_hbm": 2 * R * C * 4 / (dd * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                          "buffer_sets": sets,
                           "output_checksum": _checksum(outs[(i[0] - 1) % sets], R * C)}}
 
 
@@ -155,16 +165,37 @@ def broadcast_strided(log, reps: int = SHORT_KERNEL_REPS, sets: int = 4) -> dict
         i[0] += 1
         check(abi.lib.trs_unary_f32(3, dcs[k].ptr, ctypes.byref(lc), tmps[k].ptr, ctypes.byref(lo)))
 
+    # The same 128 MiB read and written in order: c copied flat (the COPY op
+    # on contiguous layouts), and through the runtime's hipMemcpyAsync.
+    lflat = layout_of((B * M * N,))
+
+    def flat_copy():
+        k = i[0] % sets
+        i[0] += 1
+        check(abi.lib.trs_unary_f32(3, dcs[k].ptr, ctypes.byref(lflat), tmps[k].ptr, ctypes.byref(lflat)))
+
+    def d2d():
+        k = i[0] % sets
+        i[0] += 1
+        check(abi.lib.trs_memcpy_d2d(tmps[k].ptr, dcs[k].ptr, B * M * N * 4))
+
     e = time_region(eager, reps)
     f = time_region(fused, reps)
     tc = time_region(transpose_copy, reps)
+    fc = time_region(flat_copy, reps)
+    dd = time_region(d2d, reps)
     spread = _spread(time_launches(fused, 20))
-    log(f"broadcast_strided: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us, c.mT copy {tc * 1e3:.1f} us")
+    log(f"broadcast_strided: eager {e * 1e3:.1f} us, fused {f * 1e3:.1f} us, c.mT copy {tc * 1e3:.1f} us, "
+        f"flat copy {fc * 1e3:.1f} us, hipMemcpyAsync d2d {dd * 1e3:.1f} us")
     return {"broadcast_strided": {"algorithmic_bytes": algo, "eager_us": e * 1e3, "fused_us": f * 1e3,
                                   "eager_GBps": algo / (e * 1e-3) / 1e9, "fused_GBps": algo / (f * 1e-3) / 1e9,
                                   "fused_frac_hbm": algo / (f * 1e-3) / 1e9 / HBM_PEAK_GBS, "fused_spread": spread,
                                   "transpose_copy_us": tc * 1e3,
                                   "transpose_copy_frac_hbm": 2 * B * M * N * 4 / (tc * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                  "flat_copy_us": fc * 1e3,
+                                  "flat_copy_frac_hbm": 2 * B * M * N * 4 / (fc * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                  "memcpy_d2d_us": dd * 1e3,
+                                  "memcpy_d2d_frac_hbm": 2 * B * M * N * 4 / (dd * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                   "buffer_sets": sets, "output_checksum": _checksum(outs[(i[0] - 1) % sets], B * M * N)}}
 
 
