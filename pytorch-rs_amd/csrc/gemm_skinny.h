@@ -30,6 +30,9 @@ struct SkinnyPlan {
     // The VALU matrix-vector kernel (dot form, R <= 4): row_groups is then
     // the short rows it is compiled for (1, 2 or 4) and kc the k per wave.
     bool gemv = false;
+    // The VALU kernel for the other form (Y unit-stride along j, R <= 2):
+    // row_groups is then R and kc the rows of Y per slice.
+    bool axpy = false;
     int row_groups = 1;   // 16-row MFMA groups covering R
     bool yvec = false;    // Y read as float4 (else four scalar loads)
     bool xvec = false;    // X rows read as float4 along k
@@ -40,6 +43,7 @@ struct SkinnyPlan {
 
 constexpr int64_t kSkinnyMaxRows = 32;
 constexpr int kSkinnyCols = 64;  // output columns per block
+constexpr int kAxpyCols = 128;   // output columns per block of the VALU axpy kernel
 
 // Fills `plan` and returns true when the kernel takes the problem (R at
 // most kSkinnyMaxRows).  Y is read as float4 when 16-byte aligned with yl

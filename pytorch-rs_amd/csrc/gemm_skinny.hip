@@ -13,7 +13,12 @@
 // consecutive quarters of that slice and their accumulators are added in
 // wave order through LDS at the end.  K is split into slices so the grid
 // holds ~4 blocks per CU; the slices' partial products go to a workspace
-// and one more pass adds them in slice order.
+// and one more pass adds them in slice order (slice_sum).  Adding them in
+// the kernel instead, the last block of each column group to arrive summing
+// its group's partials (stored and reloaded as tagged relaxed agent-scope
+// atomics, so no release fence is needed), measured slower on the box:
+// 20.3 against 16.6 us for x[1,4096] @ W, 43.7 against 24.8 us for
+// x[32,4096] @ W.mT.
 //
 // Fragments straight from global memory, no LDS staging (each Y element is
 // used by one lane of one MFMA):
@@ -329,6 +334,83 @@ __global__ void __launch_bounds__(256) gemv_f32_dot(SkinnyArgs g) {
     }
 }
 
+// The other form (Y unit-stride along the output columns j, e.g. x @ W)
+// with one or two short rows, on the VALU: padded to 16 MFMA rows it does 8
+// to 16 times the arithmetic it needs, and its fragments read each row of Y
+// in 256-byte pieces.  A block owns kAxpyCols columns and one slice of kc
+// rows of Y: 32 lanes read one 512-byte run of a row (a float4 each) and the
+// block's 8 such lane groups take every 8th row of the slice, eight rows in
+// flight per lane, each with its X elements (read per row: the 32 lanes of
+// a group load the same address).  Each lane adds its rows in increasing k
+// with one fused multiply-add per element, the 8 lane groups' sums are added
+// in group order through LDS, and the slices in slice order.
+// Measured on the box for x[1,4096] @ W[4096,4096] with the slices added by
+// slice_sum: 16.7 us per call against 18.5 us for the MFMA form's 16 x 64
+// tiles; staging X in LDS (17.2 us), or that with the next rows' loads
+// issued before the current rows' FMAs (18.8 us), was slower.  With 8 short
+// rows this kernel took 21.9 us (X in LDS) or 32 us (X per row) against
+// 19.5 us on the MFMA tiles, so it takes at most 2.
+constexpr int kAxpyMaxRows = 2;
+constexpr int kAxpyRowGroups = 8;    // lane groups of 32 lanes, one row each
+constexpr int kAxpyInFlight = 8;     // rows of Y loaded before their FMAs per lane
+
+template <int RR>
+__global__ void __launch_bounds__(256) gemv_f32_axpy(SkinnyArgs g) {
+    constexpr int U = kAxpyInFlight;
+    constexpr int BR = kAxpyRowGroups * U;  // rows of a batch: U per lane group
+    const int lc = threadIdx.x & 31, lr = threadIdx.x >> 5;
+    int64_t bid = blockIdx.x;
+    const int64_t jb = bid % g.jblocks;
+    bid /= g.jblocks;
+    const int64_t s = bid % g.S, b = bid / g.S;
+    const int64_t j0 = jb * kAxpyCols;
+    const int64_t kbeg = s * g.kc, kend = std::min(g.K, kbeg + g.kc);
+    const int64_t nrows = kend - kbeg;
+    const int64_t j = j0 + 4 * lc;
+    const bool jin = j < g.L;  // L is a multiple of 4: a lane's float4 is all in or all out
+    const float *yp = g.y + b * g.by + kbeg * g.yl + (jin ? j : 0);
+    // This lane's X elements: row i's at xp[i] + r * xk for slice row r.
+    const float *xp[RR];
+#pragma unroll
+    for (int i = 0; i < RR; i++) xp[i] = g.x + b * g.bx + (i < g.R ? i : 0) * g.xi + kbeg * g.xk;
+
+    __shared__ float red[kAxpyRowGroups][RR][kAxpyCols];
+    vf4 acc[RR];
+#pragma unroll
+    for (int i = 0; i < RR; i++) acc[i] = (vf4){0.f, 0.f, 0.f, 0.f};
+    for (int64_t r0 = lr; r0 < nrows; r0 += BR) {
+        vf4 v[U];
+        float xv[U][RR];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t r = r0 + kAxpyRowGroups * u;
+            const bool in = r < nrows;
+            v[u] = (jin && in) ? load4_stream(yp + r * g.yl) : (vf4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < RR; i++) xv[u][i] = (in && i < g.R) ? xp[i][r * g.xk] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int i = 0; i < RR; i++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[i][c] = __builtin_fmaf(xv[u][i], v[u][c], acc[i][c]);
+    }
+#pragma unroll
+    for (int i = 0; i < RR; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) red[lr][i][4 * lc + c] = acc[i][c];
+    __syncthreads();
+    float *O = g.o + b * g.bo + s * g.os;
+    for (int q = threadIdx.x; q < RR * kAxpyCols; q += 256) {
+        const int i = q / kAxpyCols, cc = q - i * kAxpyCols;
+        float r = red[0][i][cc];
+#pragma unroll
+        for (int w = 1; w < kAxpyRowGroups; w++) r += red[w][i][cc];
+        if (i < g.R && j0 + cc < g.L) O[i * g.oi + (j0 + cc) * g.oj] = r;
+    }
+}
+
 // c[e] = ((p0 + p1) + p2) + ... over the S slices of e's batch, in slice
 // order.  Slice s of batch b starts at ws + (b*S + s)*mn.
 __global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, float *__restrict__ c, int64_t mn,
@@ -389,6 +471,32 @@ bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
         *plan = pl;
         return true;
     }
+    // The VALU axpy kernel: Y unit-stride along j and read as float4, at most
+    // kAxpyMaxRows short rows, and K deep enough for a 64-row slice per
+    // block.  About 2
+    // blocks per CU (the probe's fastest grid: 512 blocks of 512 KiB-slices
+    // of 4 KiB rows ran 12.0 us where 256 blocks ran 16.3 us), slices of a
+    // multiple of 64 rows, and the partial products' traffic (written and
+    // read back) at most 1/8 of Y's.
+    if (!p.dot && pl.yvec && p.R <= kAxpyMaxRows && p.L % 4 == 0 && p.K >= 64) {
+        const int64_t jb = (p.L + kAxpyCols - 1) / kAxpyCols;
+        const int64_t ab = jb * p.batch;
+        const int64_t want = (2 * (int64_t)cu_count + ab - 1) / ab;
+        const int64_t cap = std::max<int64_t>(1, std::min(p.K / 64, p.K / (16 * p.R)));
+        int64_t S = std::clamp<int64_t>(want, 1, cap);
+        int64_t kc = (p.K + S - 1) / S;
+        kc = (kc + 63) / 64 * 64;
+        S = (p.K + kc - 1) / kc;
+        if (ab * S <= INT32_MAX && jb <= INT32_MAX) {
+            pl.axpy = true;
+            pl.row_groups = (int)p.R;
+            pl.kc = kc;
+            pl.splits = S;
+            pl.blocks = ab * S;
+            *plan = pl;
+            return true;
+        }
+    }
     const int64_t jblocks = (p.L + kSkinnyCols - 1) / kSkinnyCols;
     const int64_t base = jblocks * p.batch;
     // ~4 blocks per CU; each slice at least 128 deep (one step per wave), and
@@ -448,7 +556,7 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
     g.R = p.R;
     g.L = p.L;
     g.K = p.K;
-    g.jblocks = (int32_t)((p.L + kSkinnyCols - 1) / kSkinnyCols);
+    g.jblocks = (int32_t)((p.L + (plan.axpy ? kAxpyCols : kSkinnyCols) - 1) / (plan.axpy ? kAxpyCols : kSkinnyCols));
     const int64_t mn = p.R * p.L;
     int64_t S = plan.splits, kc = plan.kc;
     void *ws = nullptr;
@@ -470,8 +578,15 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
         g.bo = mn;
     }
     const dim3 grid((unsigned)((int64_t)g.jblocks * S * p.batch));
-    int rc = p.dot ? launch_form<true>(plan.yvec, plan.xvec, plan.row_groups, grid, s, g)
+    int rc = TRS_OK;
+    if (plan.axpy) {
+        if (plan.row_groups == 1) hipLaunchKernelGGL((gemv_f32_axpy<1>), grid, dim3(256), 0, s, g);
+        else hipLaunchKernelGGL((gemv_f32_axpy<2>), grid, dim3(256), 0, s, g);
+        TRS_LAUNCH_CHECK("axpy gemv launch");
+    } else {
+        rc = p.dot ? launch_form<true>(plan.yvec, plan.xvec, plan.row_groups, grid, s, g)
                    : launch_form<false>(plan.yvec, plan.xvec, plan.row_groups, grid, s, g);
+    }
     if (rc == TRS_OK && ws) rc = launch_slice_sum((const float *)ws, p.out, mn, p.batch, S, s);
     if (ws) {
         const int frc = trs_free(ws);
