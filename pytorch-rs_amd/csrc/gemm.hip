@@ -9,9 +9,10 @@
 //
 // Tiling: a block of WGM x WGN waves owns a BM x BN tile of C; each wave owns
 // (BM/WGM) x (BN/WGN) as a grid of 16x16 MFMA tiles held in accumulators.
-// Three shapes are used: 256x256x32 with 16 waves (one block per CU, 4 waves
+// Three shapes are used: 256x256 with 16 waves (one block per CU, 4 waves
 // per SIMD, 140 KB of LDS) when the output has at least one such tile per CU
-// and K is a multiple of 32; else
+// (ragged M, N and K included: edge tiles clamp their loads, and rims of at
+// most 32 rows or columns run as skinny products); else
 // 128x128x32 with 8 waves (two blocks per CU), or 64x128x32 when 128x128
 // would give fewer than two blocks per CU.  Measured on the MI355X at 4096^3:
 // 84-88% of the FP32 MFMA peak for the large shape in every operand layout,
@@ -37,6 +38,9 @@ namespace trs {
 namespace {
 
 typedef float vf4 __attribute__((ext_vector_type(4)));
+// A float4 that may start at any float: global_load_dwordx4 needs only dword
+// alignment, so rows of any length (4095, 2047 floats) load as vectors.
+typedef float vf4u __attribute__((ext_vector_type(4), aligned(4)));
 
 struct GemmArgs {
     const float *a;
@@ -52,10 +56,6 @@ struct GemmArgs {
     // slice stops at ktotal; 0 when every batch has depth K.
     int64_t ktotal;
     int32_t tiles_m, tiles_n;
-    // Operands 16-byte aligned with row strides (and batch strides) that
-    // are multiples of 4 floats: interior tiles of the edge-guarded kernel
-    // then load as float4.
-    int32_t vec_ok;
     int32_t xcd_remap;
 };
 
@@ -64,8 +64,18 @@ constexpr int kXcds = 8;
 
 // Load an R x C tile whose C dim is contiguous in memory (row stride ld),
 // starting at (r0, c0) of an Rv x Cv matrix, into registers: NT lanes, one
-// float4 each per step.  FULL: the tile lies inside the matrix and rows are
-// 16-byte aligned; otherwise each element is bounds-checked.
+// float4 each per step.  The float4 need only be dword-aligned.
+//   kLoadFull: the tile lies inside the matrix.
+//   kLoadClamp: the tile may cross the matrix's edge in its M or N dim
+//     (never in k): rows past the edge read the last row, and a float4 that
+//     crosses or passes the last column reads the row's last four floats,
+//     shifted so that its columns inside the matrix hold their own values.
+//     The values past the edge are real elements of the matrix: they meet
+//     only outputs past M or N, which are not stored.  Needs Cv >= 4.
+//   kLoadChecked: every element bounds-checked and zero outside (the ragged
+//     k tail, where zeros are needed, and matrices narrower than 4).
+constexpr int kLoadFull = 0, kLoadClamp = 1, kLoadChecked = 2;
+
 template <int R, int C, int NT>
 struct TileLoader {
     static constexpr int kVec = R * C / 4;          // float4 per tile
@@ -73,7 +83,7 @@ struct TileLoader {
     static_assert(kVec % NT == 0 && kPerThread >= 1, "tile must split evenly over the block");
     vf4 v[kPerThread];
 
-    template <bool FULL>
+    template <int MODE>
     __device__ __forceinline__ void load(const float *src, int64_t ld, int64_t r0, int64_t c0, int64_t Rv,
                                          int64_t Cv) {
 #pragma unroll
@@ -82,8 +92,14 @@ struct TileLoader {
             const int r = q / (C / 4);
             const int c = (q % (C / 4)) * 4;
             const int64_t gr = r0 + r, gc = c0 + c;
-            if constexpr (FULL) {
-                v[i] = *(const vf4 *)(src + gr * ld + gc);
+            if constexpr (MODE == kLoadFull) {
+                v[i] = *(const vf4u *)(src + gr * ld + gc);
+            } else if constexpr (MODE == kLoadClamp) {
+                // The shift of a float4 that crosses the edge is applied when
+                // storing (store_shifted): selecting on the loaded values here
+                // would wait for the prefetch before the slice's MFMAs.
+                const int64_t cb = gc < Cv - 4 ? gc : Cv - 4;
+                v[i] = *(const vf4u *)(src + (gr < Rv ? gr : Rv - 1) * ld + cb);
             } else {
                 // Branch-free: an element outside the matrix loads the
                 // matrix's first element instead and is replaced by 0, so
@@ -110,6 +126,34 @@ struct TileLoader {
             const int r = q / (C / 4);
             const int c = (q % (C / 4)) * 4;
             *(vf4 *)(lds + r * PITCH + c) = v[i];
+        }
+    }
+
+    // store() of a kLoadClamp tile whose contiguous dim is M or N, starting
+    // at c0 of Cv columns: a float4 that crossed the last column was read
+    // from the row's last four floats, so its element e is that read's
+    // element e + (column - (Cv - 4)) (capped at 3; the elements past the
+    // edge meet no stored output).
+    template <int PITCH>
+    __device__ __forceinline__ void store_shifted(float *lds, int64_t c0, int64_t Cv) const {
+#pragma unroll
+        for (int i = 0; i < kPerThread; i++) {
+            const int q = threadIdx.x + NT * i;
+            const int r = q / (C / 4);
+            const int c = (q % (C / 4)) * 4;
+            const int64_t d = c0 + c - (Cv - 4);
+            const int sh = d <= 0 ? 0 : d < 3 ? (int)d : 3;
+            // Shift down by 1, then by 2, each a per-element select (nested
+            // selects on a computed index compiled to branches).
+            const bool s1 = (sh & 1) != 0, s2 = (sh & 2) != 0;
+            const vf4 x = v[i];
+            const float y0 = s1 ? x[1] : x[0], y1 = s1 ? x[2] : x[1], y2 = s1 ? x[3] : x[2], y3 = x[3];
+            vf4 t;
+            t[0] = s2 ? y2 : y0;
+            t[1] = s2 ? y3 : y1;
+            t[2] = s2 ? y3 : y2;
+            t[3] = y3;
+            *(vf4 *)(lds + r * PITCH + c) = t;
         }
     }
 };
@@ -171,22 +215,41 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = (vf4acc){0.f, 0.f, 0.f, 0.f};
 
-    auto load_tiles = [&]<bool F>(int64_t k0) {
-        if constexpr (TA) la.template load<F>(A, args.lda, k0, m0, Kb, args.M);
-        else la.template load<F>(A, args.lda, m0, k0, args.M, Kb);
-        if constexpr (TB) lb.template load<F>(B, args.ldb, n0, k0, args.N, Kb);
-        else lb.template load<F>(B, args.ldb, k0, n0, Kb, args.N);
+    // MODE: how a slice loads (kLoadFull, kLoadClamp, kLoadChecked above).
+    auto load_tiles = [&]<int MODE>(int64_t k0) {
+        if constexpr (TA) la.template load<MODE>(A, args.lda, k0, m0, Kb, args.M);
+        else la.template load<MODE>(A, args.lda, m0, k0, args.M, Kb);
+        if constexpr (TB) lb.template load<MODE>(B, args.ldb, n0, k0, args.N, Kb);
+        else lb.template load<MODE>(B, args.ldb, k0, n0, Kb, args.N);
     };
-    // The edge-guarded kernel checks bounds only in tiles that cross the
-    // matrix's edge (or when rows are not 16-byte aligned): an interior tile's
-    // first kvec slices, all but a ragged last one, load as float4.
+    // The edge-guarded kernel loads every slice of whole k as float4,
+    // clamped at M and N (kLoadClamp: inside the matrix it reads exactly what
+    // kLoadFull does), and checks bounds only in the ragged last slice -- or
+    // in every slice when a contiguous dim is shorter than 4 (no float4
+    // fits).  With every element of an edge tile bounds-checked, 4095^3 took
+    // 1.26 ms (all its blocks run at once, so the edge tiles set the pace);
+    // clamped, 1.02 ms, and 2047^3 on the 128x128 tile 195 -> 154 us.
     const int64_t kslices = (Kb + BK - 1) / BK;
-    const bool inner = args.vec_ok && m0 + BM <= args.M && n0 + BN <= args.N;
-    const int64_t kvec = FULL ? kslices : (inner ? Kb / BK : 0);
-    if (FULL || kvec > 0) load_tiles.template operator()<true>(0);
-    else load_tiles.template operator()<false>(0);
-    la.template store<APITCH>(lds);
-    lb.template store<BPITCH>(lds + ASIZE);
+    const bool clampable = (TA ? args.M : Kb) >= 4 && (TB ? Kb : args.N) >= 4;
+    const int64_t kvec = FULL ? kslices : (clampable ? Kb / BK : 0);
+    // Only a tile that crosses M (A read as [k][m]) or N (B as [k][n]) has
+    // float4 to shift; the test is block-uniform (the shifts' selects cost
+    // the 4096 x 4096 x 4097 product 10% when every tile ran them).
+    const bool a_edge = TA && m0 + BM > args.M, b_edge = !TB && n0 + BN > args.N;
+    auto store_tiles = [&]<int MODE>(float *dst) {
+        if (MODE == kLoadClamp && a_edge) la.template store_shifted<APITCH>(dst, m0, args.M);
+        else la.template store<APITCH>(dst);
+        if (MODE == kLoadClamp && b_edge) lb.template store_shifted<BPITCH>(dst + ASIZE, n0, args.N);
+        else lb.template store<BPITCH>(dst + ASIZE);
+    };
+    constexpr int kWhole = FULL ? kLoadFull : kLoadClamp;  // slices of whole k
+    if (FULL || kvec > 0) {
+        load_tiles.template operator()<kWhole>(0);
+        store_tiles.template operator()<kWhole>(lds);
+    } else {
+        load_tiles.template operator()<kLoadChecked>(0);
+        store_tiles.template operator()<kLoadChecked>(lds);
+    }
     __syncthreads();
 
     // Fragments: lane (fi, fk) supplies row/col fi of its 16x16 tile.  With
@@ -198,21 +261,17 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
     const int fi = lane & 15;
     const int fk = lane >> 4;
 
-    // One slice: prefetch slice s+1 (as float4 when F) into registers, run
+    // One slice: prefetch slice s+1 (loaded in MODE) into registers, run
     // slice s's MFMAs from LDS, then store the prefetch to the other buffer.
-    auto step = [&]<bool F>(int64_t s) {
+    auto step = [&]<int MODE>(int64_t s) {
         const int cur = (int)(s & 1);
         const float *As = lds + cur * (ASIZE + BSIZE);
         const float *Bs = As + ASIZE;
         const bool more = s + 1 < kslices;
-        if (more) load_tiles.template operator()<F>((s + 1) * BK);
+        if (more) load_tiles.template operator()<MODE>((s + 1) * BK);
         // The next slice goes to the other buffer, which no wave reads in this
         // slice (the barrier ending the previous slice saw its last reads).
-        auto store_next = [&]() {
-            float *An = lds + (cur ^ 1) * (ASIZE + BSIZE);
-            la.template store<APITCH>(An);
-            lb.template store<BPITCH>(An + ASIZE);
-        };
+        auto store_next = [&]() { store_tiles.template operator()<MODE>(lds + (cur ^ 1) * (ASIZE + BSIZE)); };
         if constexpr (VK) {
             // Kept rolled: unrolled, the groups' fragment reads are all
             // hoisted and BK=32 spills at 16 waves; rolled, one barrier per
@@ -280,11 +339,11 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
     // condition makes the compiler wait for it before the MFMAs, which
     // undoes the prefetch.
     if constexpr (FULL) {
-        for (int64_t s = 0; s < kslices; s++) step.template operator()<true>(s);
+        for (int64_t s = 0; s < kslices; s++) step.template operator()<kLoadFull>(s);
     } else {
         int64_t s = 0;
-        for (; s + 1 < kvec; s++) step.template operator()<true>(s);
-        for (; s < kslices; s++) step.template operator()<false>(s);
+        for (; s + 1 < kvec; s++) step.template operator()<kLoadClamp>(s);
+        for (; s < kslices; s++) step.template operator()<kLoadChecked>(s);
     }
 
     // ---- epilogue: lane holds C[4*(lane/16)+r][lane%16] of each 16x16 tile ----
@@ -349,16 +408,19 @@ struct Tiles {
     static constexpr bool VK = VK_, EDGE = EDGE_;
     static constexpr int NT = WGM * WGN * 64;
 };
-// The large and medium tiles run only on shapes they divide.  Float4
-// fragment reads measured +0.9% (NT) to -0.1% on the large tile and -2 to -3%
+// The medium tile runs only on shapes it divides; the large and small tiles
+// also on ragged ones (the large one since 4095^3 and 2047^3 ran 0.55 of
+// peak on the small tile).  Float4 fragment reads measured +0.9% (NT) to -0.1% on the large tile and -2 to -3%
 // on the 4-wave tiles, so only the large tile uses them.
 // BK=32 pays only in the plain layout: 138.8 against 137.3 TFLOP/s at
 // 8192x4096x4096, while a transposed A runs 1.6-1.9% slower at BK=32 than at
 // BK=16 (134.6 against 137.2 TFLOP/s at 4096x4096x8192) and a transposed B
 // holds more fragment registers and spills at BK=32 with 16 waves.  The k
 // order, and so every result bit, is the same at both depths.
+// Shapes the large tile does not divide run its BK=16 form in every layout:
+// the BK=32 plain form's edge-guarded variant spills at 16 waves.
 using LargeTiles = Tiles<256, 256, 32, 4, 4, 1, true, false>;
-using LargeTilesK16 = Tiles<256, 256, 16, 4, 4, 1, true, false>;
+using LargeTilesK16 = Tiles<256, 256, 16, 4, 4, 1, true, true>;
 // The 128x128 tile runs 8 waves of 32x64 each (4 per SIMD with two blocks per
 // CU): batched 32x512^3 117.3 -> 121 TFLOP/s, 2047^3 214 -> 199 us against 4
 // waves of 64x64; 8 waves of 64x32 and 16 waves of 32x32 measured between.
@@ -396,35 +458,48 @@ int launch_layout(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipS
     return launch_tiled<T, true, true>(g, full, s);
 }
 
-// The large tile in each layout (full tiles only).
-int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
-    if (a_plain && b_plain) return launch_tiled<LargeTiles, false, false>(g, true, s);
-    if (a_plain) return launch_tiled<LargeTilesK16, false, true>(g, true, s);
-    if (b_plain) return launch_tiled<LargeTilesK16, true, false>(g, true, s);
-    return launch_tiled<LargeTilesK16, true, true>(g, true, s);
+// The large tile in each layout; `full` when it divides M, N and K.
+int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipStream_t s) {
+    if (a_plain && b_plain)
+        return full ? launch_tiled<LargeTiles, false, false>(g, true, s)
+                    : launch_tiled<LargeTilesK16, false, false>(g, false, s);
+    if (a_plain) return launch_tiled<LargeTilesK16, false, true>(g, full, s);
+    if (b_plain) return launch_tiled<LargeTilesK16, true, false>(g, full, s);
+    return launch_tiled<LargeTilesK16, true, true>(g, full, s);
 }
 
 // Split K: an output with fewer tiles than CUs runs its K in S slices as S
 // batches of its tile, into a workspace of S partial products that one more
 // pass sums in slice order.  The workspace comes from the block cache and
-// returns to it in stream order.
+// returns to it in stream order.  The last slice may be shorter (the kernel
+// bounds each batch's k by the full depth).
 //   - The large tile (the MLP's 8192x1024 and 4096x1024 GEMMs): S a power of
-//     two up to 8 dividing K into slices of at least 1,024.
+//     two up to 8, slices of at least kMinSplitDepth.
 //   - The 128x128 and 64x128 tiles, when they give at most one block per CU
 //     (1000^3 ran as 64 blocks, a 64x4096x4096 product as 32): S up to 16,
-//     for about two blocks per CU, slices of at least 128 k (the last one
-//     may be shorter), and at most 65,536 floats of partial products per CU.
+//     for about two blocks per CU, slices of at least 128 k, and at most
+//     65,536 floats of partial products per CU.
 constexpr int64_t kMaxSplitK = 8;
 constexpr int64_t kMinSplitDepth = 1024;
 constexpr int64_t kMaxTileSplit = 16;
 constexpr int64_t kMinTileSplitDepth = 128;
 constexpr int64_t kSplitFloatsPerCu = 65536;
+// Time of two 128x128 blocks sharing a CU against one 256x256 block on it,
+// from the measured rates (0.77 and 0.887 of peak): a ragged output takes the
+// large tile when its rounds of blocks, so weighted, are no more.
+constexpr double kSmallPairOverLarge = 0.575;
 
 // Which kernel a product runs.  Tile choice:
-//   - the 256x256 tile when it divides M, N and K and gives every CU a block;
-//   - else, for an aligned single matrix with M, N multiples of 256 and a long
-//     K, the 256x256 tile over S K-slices, when S*tiles reaches half the CUs
-//     or at least the block count of the tile it replaces;
+//   - the 256x256 tile when it divides M and N and gives every CU a block;
+//     on ragged M or N (edge tiles bounds-checked, interior ones not) when
+//     its rounds of blocks take no longer than the 128x128 tile's;
+//   - a single matrix whose M or N exceeds such an output by at most 32 rows
+//     or columns: the 256x256 tile on the rest, and the thin rims as skinny
+//     products (4097^3 would otherwise run 17 x 17 large tiles, two rounds);
+//   - else, for a single matrix with fewer large tiles than CUs, those
+//     tiles at least 90% covered, and a long K, the 256x256 tile over S
+//     K-slices, when S*tiles reaches half the CUs or at least the block
+//     count of the tile it replaces;
 //   - else 64x128 when 128x128 would give fewer than two blocks per CU and
 //     64x128 divides the shape (76% against 69% of peak measured at
 //     4096x1024x8192), else 128x128 (full or edge-guarded);
@@ -443,10 +518,12 @@ struct GemmPlan {
     int64_t ks = 0;
     GemmKind fallback = GemmKind::Small;
     bool fallback_full = false;
+    // Large with rims: the tile runs on rows [0, main_m) and columns
+    // [0, main_n); the rest is peeled off as skinny products (0: nothing).
+    int64_t main_m = 0, main_n = 0;
 };
 
-GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, bool b_trans, bool aligned,
-                   int cu_count) {
+GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, bool b_trans, int cu_count) {
     GemmPlan p;
     const int64_t M = g.M, N = g.N, K = g.K, batch = g.batch;
     if (!(a_plain || a_trans) || !(b_plain || b_trans)) {
@@ -454,20 +531,44 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
         p.blocks = std::min<int64_t>((M * N * batch + 255) / 256, (int64_t)cu_count * 16);
         return p;
     }
-    const int64_t large_tiles = (M / LargeTiles::BM) * (N / LargeTiles::BN) * batch;
+    constexpr int64_t L = LargeTiles::BM;  // 256, both dims
     const int64_t large_bk = (a_plain && b_plain) ? LargeTiles::BK : LargeTilesK16::BK;
-    const bool large_fits = aligned && M % LargeTiles::BM == 0 && N % LargeTiles::BN == 0;
-    if (large_fits && K % large_bk == 0 && large_tiles >= cu_count) {
+    const auto ceil_div = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+    const int64_t large_tiles = ceil_div(M, L) * ceil_div(N, L) * batch;
+    const int64_t small_tiles = ceil_div(M, 128) * ceil_div(N, 128) * batch;
+    const bool large_div = M % L == 0 && N % L == 0;
+    const auto use_large = [&](int64_t mm, int64_t nn, int64_t tiles) {
         p.kind = GemmKind::Large;
-        p.bm = LargeTiles::BM, p.bn = LargeTiles::BN, p.bk = (int)large_bk;
-        p.blocks = large_tiles;
-        p.full = true;
+        p.bm = L, p.bn = L;
+        p.blocks = tiles;
+        p.full = mm % L == 0 && nn % L == 0 && K % large_bk == 0;
+        p.bk = p.full ? (int)large_bk : LargeTilesK16::BK;
+    };
+    if (large_div && large_tiles >= cu_count) {
+        use_large(M, N, large_tiles);
         return p;
     }
-    const bool full = aligned && M % SmallTiles::BM == 0 && N % SmallTiles::BN == 0 && K % SmallTiles::BK == 0;
-    const bool medium_full =
-        aligned && M % MediumTiles::BM == 0 && N % MediumTiles::BN == 0 && K % MediumTiles::BK == 0;
-    const int64_t small_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+    // Thin rims peeled off a single matrix.
+    if (batch == 1) {
+        const int64_t mr = M % L, nr = N % L;
+        const bool pm = M > L && mr >= 1 && mr <= kSkinnyMaxRows;
+        const bool pn = N > L && nr >= 1 && nr <= kSkinnyMaxRows;
+        const int64_t mm = pm ? M - mr : M, nn = pn ? N - nr : N;
+        const int64_t tiles = ceil_div(mm, L) * ceil_div(nn, L);
+        if ((pm || pn) && tiles >= cu_count) {
+            use_large(mm, nn, tiles);
+            p.main_m = mm;
+            p.main_n = nn;
+            return p;
+        }
+    }
+    if (!large_div && large_tiles >= cu_count &&
+        (double)ceil_div(large_tiles, cu_count) <= kSmallPairOverLarge * (double)ceil_div(small_tiles, 2 * cu_count)) {
+        use_large(M, N, large_tiles);
+        return p;
+    }
+    const bool full = M % SmallTiles::BM == 0 && N % SmallTiles::BN == 0 && K % SmallTiles::BK == 0;
+    const bool medium_full = M % MediumTiles::BM == 0 && N % MediumTiles::BN == 0 && K % MediumTiles::BK == 0;
     if (medium_full && small_tiles < 2 * (int64_t)cu_count) {
         p.kind = GemmKind::Medium;
         p.bm = MediumTiles::BM, p.bn = MediumTiles::BN, p.bk = MediumTiles::BK;
@@ -479,21 +580,24 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
         p.blocks = small_tiles;
         p.full = full;
     }
-    if (batch == 1 && large_fits && large_tiles > 0 && large_tiles < cu_count) {
+    // The large split needs the 256x256 tiles nearly full (a 64-row output
+    // would compute four times its rows): at least 90% of their area.
+    const bool large_dense = (double)(M * N * batch) >= 0.9 * (double)(large_tiles * L * L);
+    if (batch == 1 && large_dense && large_tiles > 0 && large_tiles < cu_count) {
         int64_t S = 1;
-        while (S < kMaxSplitK && large_tiles * S * 2 <= cu_count && K % (S * 2 * large_bk) == 0 &&
-               K / (S * 2) >= kMinSplitDepth)
-            S *= 2;
+        while (S < kMaxSplitK && large_tiles * S * 2 <= cu_count && K / (S * 2) >= kMinSplitDepth) S *= 2;
         if (S > 1 && (2 * large_tiles * S >= cu_count || large_tiles * S >= p.blocks)) {
+            const int64_t ks = ceil_div(ceil_div(K, S), large_bk) * large_bk;
             p.fallback = p.kind;
             p.fallback_full = p.full;
             p.kind = GemmKind::SplitK;
             p.split_tile = GemmKind::Large;
-            p.bm = LargeTiles::BM, p.bn = LargeTiles::BN, p.bk = (int)large_bk;
-            p.splits = S;
-            p.ks = K / S;
-            p.blocks = large_tiles * S;
-            p.full = true;
+            p.bm = L, p.bn = L;
+            p.splits = ceil_div(K, ks);
+            p.ks = ks;
+            p.blocks = large_tiles * p.splits;
+            p.full = large_div && K % ks == 0;
+            p.bk = p.full ? (int)large_bk : LargeTilesK16::BK;
             return p;
         }
     }
@@ -536,7 +640,7 @@ int launch_split_k(const GemmPlan &p, GemmArgs g, bool a_plain, bool b_plain, in
     g.bsc = mn;
     g.batch = S;
     switch (p.split_tile) {
-    case GemmKind::Large: rc = launch_large(g, a_plain, b_plain, s); break;
+    case GemmKind::Large: rc = launch_large(g, a_plain, b_plain, p.full, s); break;
     case GemmKind::Medium: rc = launch_layout<MediumTiles>(g, a_plain, b_plain, true, s); break;
     default: rc = launch_layout<SmallTiles>(g, a_plain, b_plain, p.full, s); break;
     }
@@ -560,7 +664,7 @@ int launch_split_k(const GemmPlan &p, GemmArgs g, bool a_plain, bool b_plain, in
 // to be computed (an empty output, or K = 0).
 struct GemmSetup {
     GemmArgs g{};
-    bool a_plain = false, a_trans = false, b_plain = false, b_trans = false, aligned = false;
+    bool a_plain = false, a_trans = false, b_plain = false, b_trans = false;
     int64_t sam = 0, sak = 0, sbk = 0, sbn = 0;
     bool empty_output = false, zero_k = false;
 };
@@ -620,10 +724,6 @@ int setup_gemm(const float *a, const trs_layout *la, const float *b, const trs_l
     g.bsb = bsb;
     g.bsc = M * N;
     g.batch = batch;
-    auto al16 = [](const float *p) { return ((uintptr_t)p % 16) == 0; };
-    st->aligned = al16(g.a) && al16(g.b) && al16(g.c) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
-                  (batch == 1 || (bsa % 4 == 0 && bsb % 4 == 0));
-    g.vec_ok = st->aligned ? 1 : 0;
     return TRS_OK;
 }
 
@@ -668,10 +768,48 @@ bool skinny_problem(const GemmSetup &st, SkinnyProblem *sp) {
 int run_unsplit(const GemmPlan &p, const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
     switch (p.kind) {
     case GemmKind::Large:
-    case GemmKind::SplitK: return launch_large(g, a_plain, b_plain, s);
+    case GemmKind::SplitK: return launch_large(g, a_plain, b_plain, p.full, s);
     case GemmKind::Medium: return launch_layout<MediumTiles>(g, a_plain, b_plain, true, s);
     default: return launch_layout<SmallTiles>(g, a_plain, b_plain, p.full, s);
     }
+}
+
+// A Large plan with rims: the tile on C[0:main_m, 0:main_n], then the rows
+// below as one skinny product (X = those rows of A, Y = B, full width) and
+// the columns to the right of the tile's rows as another (X = those columns
+// of B read as B^T, Y = A's first main_m rows), each writing its part of C
+// in place.
+int run_peeled(const GemmPlan &p, const GemmSetup &st, int cu_count, hipStream_t s) {
+    const GemmArgs &g = st.g;
+    GemmArgs gm = g;
+    gm.M = p.main_m;
+    gm.N = p.main_n;
+    TRS_CHECK(launch_large(gm, st.a_plain, st.b_plain, p.full, s));
+    if (p.main_m < g.M) {
+        SkinnyProblem r;
+        r.R = g.M - p.main_m, r.L = g.N, r.K = g.K, r.batch = 1;
+        r.x = st.a_plain ? g.a + p.main_m * g.lda : g.a + p.main_m;
+        r.xi = st.a_plain ? g.lda : 1;
+        r.xk = st.a_plain ? 1 : g.lda;
+        r.y = g.b, r.dot = !st.b_plain, r.yl = g.ldb;
+        r.out = g.c + p.main_m * g.ldc, r.oi = g.ldc, r.oj = 1;
+        SkinnyPlan rp;
+        if (!plan_skinny(r, cu_count, &rp)) return set_error(TRS_E_INVALID_ARGUMENT, "gemm row rim has no plan");
+        TRS_CHECK(run_skinny(r, rp, s));
+    }
+    if (p.main_n < g.N) {
+        SkinnyProblem c;
+        c.R = g.N - p.main_n, c.L = p.main_m, c.K = g.K, c.batch = 1;
+        c.x = st.b_plain ? g.b + p.main_n : g.b + p.main_n * g.ldb;
+        c.xi = st.b_plain ? 1 : g.ldb;
+        c.xk = st.b_plain ? g.ldb : 1;
+        c.y = g.a, c.dot = st.a_plain, c.yl = g.lda;
+        c.out = g.c + p.main_n, c.oi = 1, c.oj = g.ldc;
+        SkinnyPlan cp;
+        if (!plan_skinny(c, cu_count, &cp)) return set_error(TRS_E_INVALID_ARGUMENT, "gemm column rim has no plan");
+        TRS_CHECK(run_skinny(c, cp, s));
+    }
+    return TRS_OK;
 }
 
 }  // namespace
@@ -692,7 +830,8 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
     SkinnyProblem sp;
     SkinnyPlan spl;
     if (skinny_problem(st, &sp) && plan_skinny(sp, dev->cu_count, &spl)) return run_skinny(sp, spl, dev->stream);
-    const GemmPlan p = plan_gemm(g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, st.aligned, dev->cu_count);
+    const GemmPlan p = plan_gemm(g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, dev->cu_count);
+    if (p.main_m) return run_peeled(p, st, dev->cu_count, dev->stream);
     if (p.kind == GemmKind::Strided) {
         // An operand with no unit stride is gathered into a contiguous buffer
         // from the block cache (the library's copy kernel, bit for bit), and
@@ -742,7 +881,7 @@ extern "C" int trs_matmul_plan_f32(const float *a, const trs_layout *la, const f
     if (rc) return rc;
     GemmPlan p;
     const bool work = !st.empty_output && !st.zero_k;
-    if (work) p = plan_gemm(st.g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, st.aligned, dev->cu_count);
+    if (work) p = plan_gemm(st.g, st.a_plain, st.a_trans, st.b_plain, st.b_trans, dev->cu_count);
     GemmSetup sg;
     const GemmSetup *ran = &st;
     if (p.kind == GemmKind::Strided) {
@@ -753,7 +892,7 @@ extern "C" int trs_matmul_plan_f32(const float *a, const trs_layout *la, const f
         rc = setup_gemm(ga ? nullptr : a, ga ? &ca : la, gb ? nullptr : b, gb ? &cb : lb, const_cast<float *>(c), lc,
                         false, &sg);
         if (rc) return rc;
-        p = plan_gemm(sg.g, sg.a_plain, sg.a_trans, sg.b_plain, sg.b_trans, sg.aligned, dev->cu_count);
+        p = plan_gemm(sg.g, sg.a_plain, sg.a_trans, sg.b_plain, sg.b_trans, dev->cu_count);
         ran = &sg;
     }
     SkinnyProblem sp;

@@ -11,9 +11,10 @@ namespace trs {
 // out(i, j) = sum_k X(i, k) * Y(k, j) for i < R, j < L, k < K, per batch.
 // X is the short operand, Y the long one.  Y has a unit stride along k
 // (`dot`, element (k, j) at y + j*yl + k) or along j (element at
-// y + k*yl + j).  The output is contiguous per batch (element (i, j) at
-// out + i*oi + j*oj, batch stride R*L), so either (oi, oj) = (L, 1) or
-// (1, R).
+// y + k*yl + j).  Output element (i, j) of batch b is at
+// out + b*bo + i*oi + j*oj, with bo = R*L when left 0; a whole contiguous
+// product has (oi, oj) = (L, 1) or (1, R), a block of columns or rows of a
+// larger output (a GEMM's rim) its row stride in oi or oj.
 struct SkinnyProblem {
     const float *x = nullptr;
     const float *y = nullptr;
@@ -21,7 +22,7 @@ struct SkinnyProblem {
     int64_t xi = 0, xk = 0;
     int64_t yl = 0;
     bool dot = false;
-    int64_t oi = 0, oj = 0;
+    int64_t oi = 0, oj = 0, bo = 0;
     int64_t bx = 0, by = 0;
     int64_t R = 0, L = 0, K = 0, batch = 1;
 };
@@ -50,10 +51,16 @@ constexpr int kAxpyCols = 128;   // output columns per block of the VALU axpy ke
 // and by multiples of 4; X likewise when xk is 1.
 bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan);
 
-// c[b*mn + e] = ((p0 + p1) + p2) + ... over S partial products in slice
-// order, slice s of batch b at ws[(b*S + s)*mn + e]; one float per lane, so
-// any mn and alignment.
-int launch_slice_sum(const float *ws, float *c, int64_t mn, int64_t batch, int64_t S, hipStream_t s);
+// ((p0 + p1) + p2) + ... over S partial products in slice order, slice s of
+// batch b at ws[(b*S + s)*mn + e]; one float per lane, so any mn and
+// alignment.  The sum of element e goes to c[b*mn + e], or with `scatter`
+// (e = i*L + j) to c[b*bo + i*oi + j*oj].
+struct SliceOut {
+    bool scatter = false;
+    int64_t L = 0, oi = 0, oj = 0, bo = 0;
+};
+int launch_slice_sum(const float *ws, float *c, int64_t mn, int64_t batch, int64_t S, hipStream_t s,
+                     const SliceOut &out = SliceOut{});
 
 // Runs the plan on stream `s`.  A split plan takes a workspace of
 // splits * R * L * batch floats from the block cache; without one it runs

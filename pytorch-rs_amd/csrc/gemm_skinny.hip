@@ -414,7 +414,7 @@ __global__ void __launch_bounds__(256) gemv_f32_axpy(SkinnyArgs g) {
 // c[e] = ((p0 + p1) + p2) + ... over the S slices of e's batch, in slice
 // order.  Slice s of batch b starts at ws + (b*S + s)*mn.
 __global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, float *__restrict__ c, int64_t mn,
-                                                  int64_t total, int S) {
+                                                  int64_t total, int S, SliceOut out) {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= total) return;
     const int64_t b = e / mn, r = e - b * mn;
@@ -429,7 +429,12 @@ __global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, f
     for (int q = 1; q < 16; q++)
         if (q < S) v += part[q];
     for (int s = 16; s < S; s++) v += p[(int64_t)s * mn];
-    c[e] = v;
+    if (!out.scatter) {
+        c[e] = v;
+    } else {
+        const int64_t i = r / out.L, j = r - i * out.L;
+        c[b * out.bo + i * out.oi + j * out.oj] = v;
+    }
 }
 
 template <bool DOT, bool YVEC, bool XVEC>
@@ -515,9 +520,11 @@ bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
     return true;
 }
 
-int launch_slice_sum(const float *ws, float *c, int64_t mn, int64_t batch, int64_t S, hipStream_t s) {
+int launch_slice_sum(const float *ws, float *c, int64_t mn, int64_t batch, int64_t S, hipStream_t s,
+                     const SliceOut &out) {
     const int64_t total = mn * batch;
-    hipLaunchKernelGGL(slice_sum, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws, c, mn, total, (int)S);
+    hipLaunchKernelGGL(slice_sum, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws, c, mn, total, (int)S,
+                       out);
     TRS_LAUNCH_CHECK("gemm slice sum launch");
     return TRS_OK;
 }
@@ -527,7 +534,7 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
     if (plan.gemv) {
         g.x = p.x, g.y = p.y, g.o = p.out;
         g.xi = p.xi, g.xk = p.xk, g.yl = p.yl;
-        g.oi = p.oi, g.oj = p.oj, g.bo = p.R * p.L;
+        g.oi = p.oi, g.oj = p.oj, g.bo = p.bo ? p.bo : p.R * p.L;
         g.bx = p.bx, g.by = p.by;
         g.R = p.R, g.L = p.L, g.K = p.K;
         const dim3 grid((unsigned)plan.blocks);
@@ -568,14 +575,26 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
     if (S == 1) kc = p.K;
     g.S = (int32_t)S;
     g.kc = kc;
+    // The workspace holds each slice in the output's own element order when
+    // the output is one contiguous product, else row-major (i, j), and the
+    // slice pass scatters the sums to the output's strides.
+    const int64_t bo = p.bo ? p.bo : mn;
+    const bool compact = bo == mn && ((p.oi == p.L && p.oj == 1) || (p.oi == 1 && p.oj == p.R));
+    SliceOut so;
     if (ws) {
         g.o = (float *)ws;
         g.os = mn;
         g.bo = S * mn;
+        if (!compact) {
+            g.oi = p.L;
+            g.oj = 1;
+            so.scatter = true;
+            so.L = p.L, so.oi = p.oi, so.oj = p.oj, so.bo = bo;
+        }
     } else {
         g.o = p.out;
         g.os = 0;
-        g.bo = mn;
+        g.bo = bo;
     }
     const dim3 grid((unsigned)((int64_t)g.jblocks * S * p.batch));
     int rc = TRS_OK;
@@ -587,7 +606,7 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
         rc = p.dot ? launch_form<true>(plan.yvec, plan.xvec, plan.row_groups, grid, s, g)
                    : launch_form<false>(plan.yvec, plan.xvec, plan.row_groups, grid, s, g);
     }
-    if (rc == TRS_OK && ws) rc = launch_slice_sum((const float *)ws, p.out, mn, p.batch, S, s);
+    if (rc == TRS_OK && ws) rc = launch_slice_sum((const float *)ws, p.out, mn, p.batch, S, s, so);
     if (ws) {
         const int frc = trs_free(ws);
         if (!rc) rc = frc;

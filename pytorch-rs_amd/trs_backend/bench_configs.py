@@ -255,6 +255,8 @@ MATMUL_SHAPES = [
     ("[64,4096]@[4096,4096]", 64, 4096, 4096, False, False, "mfma"),
     ("1000^3", 1000, 1000, 1000, False, False, "mfma"),
     ("2047^3", 2047, 2047, 2047, False, False, "mfma"),
+    ("4095^3", 4095, 4095, 4095, False, False, "mfma"),
+    ("4097^3", 4097, 4097, 4097, False, False, "mfma"),
 ]
 
 

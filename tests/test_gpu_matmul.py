@@ -379,3 +379,54 @@ def test_empty_dimensions_on_the_device():
     no_inner = torch_rs.ones((2, 0), device="cuda") @ torch_rs.zeros((0, 4), device="cuda")
     assert no_inner.shape == (2, 4)
     assert (no_inner.numpy().view(np.uint32) == 0).all()
+
+
+# Ragged products on the 256x256 tile (BK=16 form, edge tiles bounds-checked,
+# interior tiles loading dword-aligned float4 from rows of any length), and
+# single matrices that exceed a multiple of 256 by at most 32 rows or columns,
+# whose rims run as skinny products.  Plans are those of a 256-CU device.
+RAGGED_LARGE = [
+    ((4095, 300, 4095), 0, (256, 256, 16, 1, 256)),     # 255-wide rim tiles, K tail of 12
+    ((1000, 50, 1000), 16, (256, 256, 16, 1, 256)),     # a batch of ragged outputs
+    ((4096, 4097, 4096), 0, (256, 256, 16, 1, 256)),    # ragged K only: one 1-deep tail slice
+    ((4097, 300, 4097), 0, (256, 256, 16, 1, 256)),     # one-row and one-column rims
+    ((4096 + 31, 129, 4096), 0, (256, 256, 16, 1, 256)),   # a 31-row rim, full-width tile
+    ((4096, 77, 4096 + 5), 0, (256, 256, 16, 1, 256)),     # a 5-column rim
+    ((4352 + 3, 65, 4096 + 32), 0, (256, 256, 16, 1, 272)),  # both rims, 17 x 16 main tiles
+]
+
+
+@pytest.mark.parametrize("mkn,batch,plan", RAGGED_LARGE)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_ragged_large_tile_and_rims_exact_on_small_integers(mkn, batch, plan, ta, tb):
+    m, k, n = mkn
+    if _cu_count() != 256:
+        pytest.skip("plan expectations are those of a 256-CU device")
+    rng = np.random.default_rng(m + 3 * k + 7 * n + batch + 2 * ta + tb)
+    nb = max(batch, 1)
+    a = rng.integers(-3, 4, (nb, m, k)).astype(np.float32)
+    b = rng.integers(-3, 4, (nb, k, n)).astype(np.float32)
+    sa = (np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a).ravel()
+    sb = (np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b).ravel()
+    ast, bst = ((1, m) if ta else (k, 1)), ((1, k) if tb else (n, 1))
+    if batch:
+        la, lb = ((batch, m, k), (m * k,) + ast, 0), ((batch, k, n), (k * n,) + bst, 0)
+    else:
+        la, lb = ((m, k), ast, 0), ((k, n), bst, 0)
+        assert _plan(m, k, n, ta, tb) == plan
+    got = U.matmul(sa, *la, sb, *lb).reshape(nb, m, n)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("s", [4095, 4097])
+def test_ragged_cubes_normal_inputs_within_tolerance(s):
+    """4095^3 (edge tiles) and 4097^3 (a 4096^3 tile product and two rims)
+    with N(0, 1/sqrt(K)) entries: every element against the reference-order
+    oracle within 1e-5*sqrt(K)*(|A||B|)."""
+    rng = np.random.default_rng(s)
+    a = (rng.standard_normal((s, s)) / np.sqrt(s)).astype(np.float32)
+    b = (rng.standard_normal((s, s)) / np.sqrt(s)).astype(np.float32)
+    got = U.matmul(a.ravel(), (s, s), (s, 1), 0, b.ravel(), (s, s), (s, 1), 0)
+    want = O.matmul_threads(a, b, threads=_oracle_threads())
+    _check_tol(got, want, _abs_bound(a, b), s)
