@@ -233,12 +233,24 @@ __device__ __forceinline__ void store1(const PwPtrs &p, int64_t off, const float
 // Offsets of output and inputs for a logical index tuple given by the first
 // `ndims` dims of the decomposition of `outer` (row-major over dims
 // [0, ndims)).  Uses 32-bit magic division when `outer` fits in 32 bits.
-template <int NIN>
+// ROLLED: the 32-bit path loops over the ndims dims at run time instead of
+// unrolling over every possible one (fewer geometry fields live in scalar
+// registers at once, for bodies that would otherwise spill them).
+template <int NIN, bool ROLLED = false>
 __device__ __forceinline__ void decode_outer(const PwGeom &g, int ndims, int64_t outer,
                                              int64_t &oo, int64_t *io) {
     oo = g.ooff;
     for (int i = 0; i < NIN; i++) io[i] = g.ioff[i];
-    if (!g.wide && outer < 0x100000000LL) {
+    if (ROLLED && !g.wide && outer < 0x100000000LL) {
+        uint32_t rem = (uint32_t)outer;
+        for (int d = ndims - 1; d >= 0; d--) {
+            const uint32_t q = fast_div(rem, g.fd[d]);
+            const uint32_t c = rem - q * g.fd[d].div;
+            rem = q;
+            oo += (int64_t)c * g.ostride[d];
+            for (int i = 0; i < NIN; i++) io[i] += (int64_t)c * g.istride[i][d];
+        }
+    } else if (!g.wide && outer < 0x100000000LL) {
         // Unrolled over every possible dim so each geometry field has a
         // constant index (loads the compiler can issue up front); dims at or
         // above ndims are skipped by a uniform branch.  The rows kernels
@@ -424,7 +436,10 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
             oo = (int64_t)o;
             for (int i = 0; i < NIN; i++) io[i] = (int64_t)ii[i];
         } else {
-            decode_outer<NIN>(g, inner, row, oo, io);
+            // The scalar fallback (rows not float4-aligned) decodes in a
+            // rolled loop: unrolled, this body spilled 46 scalar registers
+            // and reserved a private segment.
+            decode_outer<NIN, !VEC>(g, inner, row, oo, io);
         }
         if constexpr (VEC) {
             constexpr int RV = kRowChunkVec / 1024;  // float4 per lane

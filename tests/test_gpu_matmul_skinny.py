@@ -80,6 +80,104 @@ def test_short_sides_plan_the_skinny_kernel():
     assert plain(9, 100, 4096)[3] == 1  # K shorter than one slice
 
 
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_skinny_small_integers_exact(m, k, n, ta, tb):
+    rng = np.random.default_rng(m + 3 * k + 7 * n + 11 * ta + 13 * tb)
+    a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb)
+    got = U.matmul(sa, *la, sb, *lb)
+    assert np.array_equal(got, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 4096), (4096, 4096, 1), (16, 3000, 700), (700, 3000, 32)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_skinny_normal_inputs_within_tolerance(m, k, n, ta, tb):
+    rng = np.random.default_rng(91 + m + n + 2 * ta + tb)
+    a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, ints=False)
+    got = U.matmul(sa, *la, sb, *lb)
+    want = O.matmul(sa, *la, sb, *lb).reshape(m, n)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    tol = 1e-5 * np.sqrt(k) * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+    assert (err <= tol).all(), err.max()
+
+
+@pytest.mark.parametrize("aoff,boff", [(1, 0), (0, 3), (2, 2)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_skinny_misaligned_and_odd_strides_exact(aoff, boff, ta, tb):
+    """Operands at offsets that break 16-byte alignment, and a row length of
+    1,001 floats, take the scalar-load variants; still exact."""
+    rng = np.random.default_rng(5 + aoff + 7 * boff + 2 * ta + tb)
+    for m, k, n in [(7, 1001, 1001), (1001, 1001, 7), (1, 517, 2050)]:
+        a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, aoff=aoff, boff=boff)
+        got = U.matmul(sa, *la, sb, *lb)
+        assert np.array_equal(got, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)), (m, k, n)
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_skinny_batched_exact(ta, tb):
+    rng = np.random.default_rng(17 + 2 * ta + tb)
+    for batch, m, k, n in [(5, 4, 300, 700), (3, 700, 1500, 20), (64, 1, 512, 512), (2, 32, 8192, 64)]:
+        a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, batch=batch)
+        got = U.matmul(sa, *la, sb, *lb)
+        want = np.matmul(a.astype(np.int64), b.astype(np.int64)).astype(np.float32)
+        assert np.array_equal(got.reshape(want.shape), want), (batch, m, k, n)
+
+
+def test_skinny_special_values_across_slices():
+    """Infinities and a NaN in different K slices of a split matrix-vector
+    product and of a 20-row product: NaN and signed-infinity positions equal
+    the oracle's; finite elements within tolerance.  Zero padding never meets
+    a stored output, so an infinity does not spread NaN to other rows."""
+    rng = np.random.default_rng(23)
+    for m, k, n in [(1, 8192, 2048), (20, 8192, 300), (2048, 8192, 3)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        a[0, 100] = np.inf
+        a[m - 1, 6000] = -np.inf
+        b[4000, n - 1] = np.nan
+        b[7000, 0] = np.inf
+        got = U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0)
+        want = O.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0).reshape(m, n)
+        for pred in (np.isnan, np.isposinf, np.isneginf):
+            assert np.array_equal(pred(got), pred(want)), (m, k, n, pred.__name__)
+        fin = np.isfinite(want)
+        with np.errstate(invalid="ignore", over="ignore"):
+            bound = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+        err = np.abs(got[fin].astype(np.float64) - want[fin].astype(np.float64))
+        assert (err <= 1e-5 * np.sqrt(k) * bound[fin]).all()
+
+
+def test_split_products_repeated_back_to_back():
+    """Split products of different shapes, each repeated three times back to
+    back (their workspaces come from, and return to, the block cache in
+    stream order): every call exact."""
+    rng = np.random.default_rng(71)
+    cases = []
+    for m, k, n, ta, tb in [(1, 4096, 4096, False, False), (3, 8192, 1000, False, False), (1, 4096, 4096, False, False),
+                            (2000, 6000, 5, True, False), (16, 2048, 64, False, True)]:
+        a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb)
+        want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+        assert _plan(*la, *lb)[3] > 1, (m, k, n)
+        cases.append((sa, la, sb, lb, want))
+    for _ in range(3):
+        for sa, la, sb, lb, want in cases:
+            assert np.array_equal(U.matmul(sa, *la, sb, *lb), want)
+
+
+def test_dot_form_with_four_rows_or_fewer_plans_the_matrix_vector_kernel():
+    """x @ W.mT (and W @ x) with at most 4 short rows, K >= 1024 and enough
+    rows of W for two blocks per CU run the VALU matrix-vector kernel: the
+    plan reports its 1, 2 or 4 rows by the 4 rows of W a block takes, over
+    the whole of K (no split)."""
+    dot = lambda m, k, n: _plan((m, k), (k, 1), 0, (k, n), (1, k), 0)
+    assert dot(1, 4096, 4096)[:4] == (1, 4, 1024, 1)
+    assert dot(2, 4096, 4096)[:2] == (2, 4) and dot(3, 4096, 4096)[:2] == (4, 4)
+    assert dot(5, 4096, 4096)[:2] == (16, 64)       # five rows: the MFMA kernel
+    assert dot(1, 512, 4096)[:2] == (16, 64)        # short K
+    assert dot(1, 4096, 1024)[:2] == (16, 64)       # too few rows of W
+    assert _plan((4096, 4096), (4096, 1), 0, (4096, 1), (1, 1), 0)[:2] == (4, 1)  # W @ x
+
+
 def test_axpy_form_with_two_rows_or_fewer_plans_the_valu_kernel():
     """x @ W (W unit-stride along the output columns) with one or two short
     rows, the long side a multiple of 4 and K >= 64 runs the VALU axpy
