@@ -91,6 +91,14 @@ int trs_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz);
  * library's stream after it is freed.  Pointers not from trs_alloc are
  * released with a stream sync and hipFree. */
 int trs_alloc(size_t bytes, void **ptr);
+/* Test hook (no counterpart in the reference; for the tests of this
+ * library's fallbacks, which nothing else can reach): after `n` more
+ * successful trs_alloc calls in this process, every trs_alloc fails with
+ * TRS_E_ALLOCATION_FAILED until the hook is called again; n < 0 removes the
+ * limit.  The fallbacks it reaches: a matmul whose gather buffers for
+ * operands with no unit stride cannot be had runs the one-lane-per-output
+ * kernel; a split K whose workspace cannot be had runs unsplit. */
+int trs_debug_fail_allocs_after(int64_t n);
 int trs_free(void *ptr);
 /* Return every cached block to HIP (after draining the device stream). */
 int trs_empty_cache(void);
@@ -287,9 +295,10 @@ typedef struct trs_pw_plan_info {
     uint32_t once;      /* transposing with roles: inputs loaded once per outer tuple */
     int32_t block;      /* lanes per block */
     int64_t grid;       /* blocks per launch */
-    int32_t split;      /* outer dims walked on the host, one launch per index
-                         * tuple, when more than 8 dims remain after merging */
-    int32_t reserved;
+    int32_t split;      /* dims walked on the host, one launch per index tuple,
+                         * when more than 8 dims remain after merging (those
+                         * with the fewest indices, never the innermost) */
+    int32_t launches;   /* kernel launches per call (saturates at INT32_MAX) */
 } trs_pw_plan_info;
 int trs_pointwise_plan(int n_inputs, const void *const *inputs, const trs_layout *const *layouts,
                        const int *elem_bytes, const float *out, const trs_layout *lo, int cu_count, int roles,

@@ -59,8 +59,12 @@ struct Program {
     bool from_disk = false;
     CodeObject base;
     // pw_xpose kernels specialised on operand roles, built on first launch
-    // of each role signature (kernel name -> code object).
+    // of each role signature (kernel name -> code object).  spec_mu guards
+    // the maps and is held only for lookups and inserts; compile_mu is held
+    // over a specialisation's hipRTC compile, so launches of kernels already
+    // built never wait for one.
     std::mutex spec_mu;
+    std::mutex compile_mu;
     std::map<std::string, std::unique_ptr<CodeObject>> specs;
     // Launch-plan signature -> function, per device: a repeated launch looks
     // its kernel up here without building names or sources.
@@ -371,20 +375,28 @@ int get_function(CodeObject *co, DeviceState *dev, const std::string &name, hipF
 // specialisation; `body` is the kernel body call.
 int get_spec_function(Program *prog, DeviceState *dev, const std::string &name, const std::string &body,
                       int lanes, hipFunction_t *fn) {
-    CodeObject *co = nullptr;
-    {
+    auto find = [&]() -> CodeObject * {
         std::lock_guard<std::mutex> lock(prog->spec_mu);
         auto it = prog->specs.find(name);
-        if (it == prog->specs.end()) {
+        return it == prog->specs.end() ? nullptr : it->second.get();
+    };
+    CodeObject *co = find();
+    if (!co) {
+        // One compile at a time per program; a thread that waited here finds
+        // the specialisation another one built meanwhile.
+        std::lock_guard<std::mutex> compile_lock(prog->compile_mu);
+        co = find();
+        if (!co) {
             std::ostringstream w;
             w << prog->functor << "extern \"C\" __global__ void __launch_bounds__(" << lanes << ") " << name
               << "(trs::PwGeom, trs::PwPtrs p) { " << body << "(TrsFused{}, trs::kernarg_geom(), p); }\n";
             auto spec = std::make_unique<CodeObject>();
             const int rc = compile_source(w.str(), spec.get(), nullptr, nullptr);
             if (rc) return rc;
-            it = prog->specs.emplace(name, std::move(spec)).first;
+            co = spec.get();
+            std::lock_guard<std::mutex> lock(prog->spec_mu);
+            prog->specs.emplace(name, std::move(spec));
         }
-        co = it->second.get();
     }
     return get_function(co, dev, name, fn);
 }
@@ -412,8 +424,10 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
                                  256, fn);
     }
     case PwVariant::Xpose: {
+        // The scalar form reads every input plainly, so the streamed mask is
+        // not part of its name (one kernel for every mask).
         std::snprintf(name, sizeof name, "trs_fused_xpose_%c%d_%u_%u_%u_%u_%d_%u", pl.vec ? 'v' : 's', pl.rk,
-                      pl.trans, pl.held, pl.once, pl.xbc, pl.walk, strm);
+                      pl.trans, pl.held, pl.once, pl.xbc, pl.walk, pl.vec ? strm : 0u);
         std::ostringstream b;
         b << "trs::pw_xpose_body<TrsFused, " << mask << ", " << (pl.vec ? "true" : "false") << ", " << kXposeWT << ", "
           << kXposeWX << ", " << pl.trans << "u, " << pl.held << "u, " << pl.once << "u, " << pl.walk << ", "
@@ -430,7 +444,10 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
 // vector access, role masks, walk, streamed inputs, fixed rank), resolved on
 // a miss.
 int get_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunction_t *fn) {
-    const uint64_t strm = pl.g.streamed & ((1u << prog->nin) - 1u);
+    // The streamed mask selects among vector kernels only (the scalar
+    // transposing kernel ignores it).
+    const uint64_t strm =
+        (pl.variant == PwVariant::Xpose && !pl.vec) ? 0 : pl.g.streamed & ((1u << prog->nin) - 1u);
     const uint64_t key = (uint64_t)pl.variant | (uint64_t)pl.vec << 3 | (uint64_t)pl.contig << 4 |
                          (uint64_t)pl.walk << 5 | strm << 9 | (uint64_t)pl.trans << 17 | (uint64_t)pl.held << 25 |
                          (uint64_t)pl.once << 33 | (uint64_t)pl.xbc << 41 | (uint64_t)pl.rk << 49;

@@ -797,6 +797,9 @@ int trs_pointwise_plan(int n_inputs, const void *const *inputs, const trs_layout
     info->block = pl.block;
     info->grid = pl.grid;
     info->split = pl.nsplit;
+    int64_t launches = pl.variant == PwVariant::Empty ? 0 : 1;
+    for (int d = 0; d < pl.nsplit; d++) launches = std::min<int64_t>(launches * pl.ssize[d], INT32_MAX);
+    info->launches = (int32_t)launches;
     return TRS_OK;
 }
 

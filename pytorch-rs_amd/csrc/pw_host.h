@@ -53,9 +53,9 @@ struct PwPlan {
     int64_t grid = 0;
     PwGeom g;
     PwPtrs p;
-    // Views that keep more than kMaxRank dims after merging: the outermost
-    // nsplit dims (largest output strides) are walked on the host, one launch
-    // of the inner kMaxRank dims per index tuple, each with the base offsets
+    // Views that keep more than kMaxRank dims after merging: nsplit dims
+    // (those with the fewest indices) are walked on the host, one launch of
+    // the other kMaxRank dims per index tuple, each with the base offsets
     // moved by that tuple (for_each_part).
     int nsplit = 0;
     int64_t ssize[kMaxSplit];
@@ -227,20 +227,35 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         os[0] = 1;
         for (int i = 0; i < nin; i++) is[i][0] = 0;
     }
-    // More dims than a kernel's geometry holds: split off the outermost.
+    // More dims than a kernel's geometry holds: split off, onto the host, the
+    // dims with the fewest indices (never the innermost; the outermost of
+    // equal sizes), so the launches number the product of the smallest
+    // sizes: [100000, 2, 2, ...] runs as 2 launches, not 100,000.  Both the
+    // split and the kept dims stay in stride order.
     if (rank > kMaxRank) {
         const int ns = rank - kMaxRank;
-        plan->nsplit = ns;
-        for (int d = 0; d < ns; d++) {
-            plan->ssize[d] = size[d];
-            plan->sos[d] = os[d];
-            for (int i = 0; i < nin; i++) plan->sis[i][d] = is[i][d];
-            numel /= size[d];
+        bool split[TRS_MAX_RANK] = {};
+        for (int n = 0; n < ns; n++) {
+            int best = -1;
+            for (int d = 0; d < rank - 1; d++)
+                if (!split[d] && (best < 0 || size[d] < size[best])) best = d;
+            split[best] = true;
         }
-        for (int d = 0; d < kMaxRank; d++) {
-            size[d] = size[d + ns];
-            os[d] = os[d + ns];
-            for (int i = 0; i < nin; i++) is[i][d] = is[i][d + ns];
+        plan->nsplit = ns;
+        int w = 0, k = 0;
+        for (int d = 0; d < rank; d++) {
+            if (split[d]) {
+                plan->ssize[w] = size[d];
+                plan->sos[w] = os[d];
+                for (int i = 0; i < nin; i++) plan->sis[i][w] = is[i][d];
+                numel /= size[d];
+                w++;
+            } else {
+                size[k] = size[d];
+                os[k] = os[d];
+                for (int i = 0; i < nin; i++) is[i][k] = is[i][d];
+                k++;
+            }
         }
         rank = kMaxRank;
     }

@@ -6,6 +6,7 @@
 // one stream per device.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -206,6 +207,11 @@ DeviceState *device_state() {
 
 using namespace trs;
 
+namespace trs {
+// Allocations trs_alloc grants before it refuses every one (-1: no limit).
+std::atomic<int64_t> g_allocs_before_failure{-1};
+}  // namespace trs
+
 extern "C" {
 
 const char *trs_last_error(void) { return g_last_error; }
@@ -252,6 +258,11 @@ int trs_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz) 
     });
 }
 
+int trs_debug_fail_allocs_after(int64_t n) {
+    trs::g_allocs_before_failure.store(n < 0 ? -1 : n);
+    return TRS_OK;
+}
+
 int trs_alloc(size_t bytes, void **ptr) {
     return abi_guard([&]() -> int {
         if (!ptr) return set_error(TRS_E_INVALID_ARGUMENT, "null out pointer");
@@ -259,6 +270,12 @@ int trs_alloc(size_t bytes, void **ptr) {
         DeviceState *dev = device_state();
         if (!dev) return TRS_E_NO_DEVICE;
         if (bytes == 0) return TRS_OK;
+        // The test hook (trs_debug_fail_allocs_after): count down, then refuse.
+        for (int64_t left = trs::g_allocs_before_failure.load(); left >= 0;) {
+            if (left == 0)
+                return set_error(TRS_E_ALLOCATION_FAILED, "allocation refused (trs_debug_fail_allocs_after)");
+            if (trs::g_allocs_before_failure.compare_exchange_weak(left, left - 1)) break;
+        }
         const size_t rounded = round_block(bytes);
         {
             std::lock_guard<std::mutex> lock(dev->cache_mu);

@@ -88,8 +88,8 @@ class PwPlanInfo(ctypes.Structure):
         ("once", c_uint32),
         ("block", c_int32),
         ("grid", ctypes.c_int64),
-        ("split", c_int32),       # outer dims walked on the host, one launch each
-        ("reserved", c_int32),
+        ("split", c_int32),       # dims walked on the host (the fewest indices), one launch each
+        ("launches", c_int32),    # kernel launches per call (saturates at INT32_MAX)
     ]
 
 
@@ -110,6 +110,7 @@ _SIGNATURES = {
     "trs_memory_stats": ([POINTER(c_size_t), POINTER(c_size_t)], c_int),
     "trs_memcpy_h2d": ([c_void_p, c_void_p, c_size_t], c_int),
     "trs_memcpy_d2h": ([c_void_p, c_void_p, c_size_t], c_int),
+    "trs_debug_fail_allocs_after": ([c_int64], c_int),
     "trs_memcpy_d2d": ([c_void_p, c_void_p, c_size_t], c_int),
     "trs_memset_zero": ([c_void_p, c_size_t], c_int),
     "trs_synchronize": ([], c_int),

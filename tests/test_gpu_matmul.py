@@ -430,3 +430,55 @@ def test_ragged_cubes_normal_inputs_within_tolerance(s):
     got = U.matmul(a.ravel(), (s, s), (s, 1), 0, b.ravel(), (s, s), (s, 1), 0)
     want = O.matmul_threads(a, b, threads=_oracle_threads())
     _check_tol(got, want, _abs_bound(a, b), s)
+
+
+def _matmul_without_allocations(a, ashape, astr, aoff, b, bshape, bstr, boff):
+    """U.matmul with trs_alloc refusing every request while the product runs
+    (the operands and output are allocated before the hook is set)."""
+    import ctypes
+    from trs_backend import abi
+    da, db = U.dev(a), U.dev(b)
+    oshape = tuple(ashape[:-1]) + (bshape[-1],)
+    n = int(np.prod(oshape))
+    do = U.out_buffer(n)
+    abi.check(abi.lib.trs_debug_fail_allocs_after(0))
+    try:
+        abi.check(abi.lib.trs_matmul_f32(da.ptr, ctypes.byref(abi.layout_of(ashape, astr, aoff)), db.ptr,
+                                         ctypes.byref(abi.layout_of(bshape, bstr, boff)), do.ptr,
+                                         ctypes.byref(abi.layout_of(oshape))))
+    finally:
+        abi.check(abi.lib.trs_debug_fail_allocs_after(-1))
+    return do.to_numpy(count=n).reshape(oshape)
+
+
+def test_fallbacks_when_no_workspace_can_be_allocated():
+    """With every allocation refused (trs_debug_fail_allocs_after(0)):
+    operands with no unit stride run the one-lane-per-output kernel, which
+    adds k in the reference's order from +0.0, so it equals the oracle bit
+    for bit on normal data; products whose plan splits K (over the large
+    tile, the small tile, a skinny kernel, and the rims of a peeled product)
+    run unsplit, exact on small integers."""
+    import ctypes
+    from trs_backend import abi
+    rng = np.random.default_rng(2024)
+    # a[::2, ::2] and b[::3, ::2]: no unit stride in either operand.
+    m, k, n = 70, 90, 50
+    ab = rng.standard_normal((2 * m, 2 * k)).astype(np.float32)
+    bb = rng.standard_normal((3 * k, 2 * n)).astype(np.float32)
+    la, lb = ((m, k), (4 * k, 2), 0), ((k, n), (6 * n, 2), 0)
+    got = _matmul_without_allocations(ab.ravel(), *la, bb.ravel(), *lb)
+    want = O.matmul(ab.ravel(), *la, bb.ravel(), *lb).reshape(m, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    cases = [(1024, 8192, 1024, False, False), (1000, 1000, 1000, False, False), (1, 4096, 4096, False, False),
+             (32, 4096, 4096, False, True), (4097, 300, 4097, False, False)]
+    for m, k, n, ta, tb in cases:
+        assert _plan(m, k, n, ta, tb)[3] > 1 or m == 4097, (m, k, n)
+        a = rng.integers(-3, 4, (m, k)).astype(np.float32)
+        b = rng.integers(-3, 4, (k, n)).astype(np.float32)
+        sa, la, sb, lb = _layouts(a, b, ta, tb)
+        got = _matmul_without_allocations(sa, *la, sb, *lb)
+        assert np.array_equal(got, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)), (m, k, n)
+    # the hook is off again: an allocation succeeds
+    p = ctypes.c_void_p()
+    abi.check(abi.lib.trs_alloc(64, ctypes.byref(p)))
+    abi.check(abi.lib.trs_free(p))

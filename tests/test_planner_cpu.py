@@ -112,14 +112,22 @@ def reversed_strides(shape):
     return tuple(st)
 
 
-def test_views_above_eight_dims_split_their_outer_dims_onto_the_host():
+def test_views_above_eight_dims_split_their_smallest_dims_onto_the_host():
     """The kernels index at most 8 dims; a view keeping more after merging is
-    launched once per index tuple of its outermost dims."""
-    for shape in [(2, 3) * 5, (2,) * 12 + (1,) * 10 + (3, 1, 2), (2,) * 25]:
+    launched once per index tuple of its dims with the fewest indices (never
+    the innermost), so the launch count is the product of the smallest
+    sizes."""
+    for shape, launches in [((2, 3) * 5, 2 ** 2), ((2,) * 12 + (1,) * 10 + (3, 1, 2), 2 ** 6), ((2,) * 25, 2 ** 17)]:
         nonunit = sum(1 for d in shape if d != 1)
         p = plan(layout_of(shape), layout_of(shape, reversed_strides(shape)), out=layout_of(shape))
-        assert (p.rank, p.split) == (8, nonunit - 8)
+        assert (p.rank, p.split, p.launches) == (8, nonunit - 8, launches)
         assert p.variant == GENERIC  # the reversed operand's unit stride is on a split dim
+    # [100000, 2 x 8]: one small dim goes to the host, not the 100,000
+    shape = (100000,) + (2,) * 8
+    p = plan(layout_of(shape), layout_of(shape, reversed_strides(shape)), out=layout_of(shape))
+    assert (p.rank, p.split, p.launches) == (8, 1, 2)
+    assert plan(layout_of((4, 5)), out=layout_of((4, 5))).launches == 1
+    assert plan(layout_of((0, 5)), out=layout_of((0, 5))).launches == 0
 
 
 def test_views_above_eight_dims_that_merge_need_no_split():
