@@ -47,8 +47,8 @@ constexpr int kSkinnyCols = 64;  // output columns per block
 constexpr int kAxpyCols = 128;   // output columns per block of the VALU axpy kernel
 
 // Fills `plan` and returns true when the kernel takes the problem (R at
-// most kSkinnyMaxRows).  Y is read as float4 when 16-byte aligned with yl
-// and by multiples of 4; X likewise when xk is 1.
+// most kSkinnyMaxRows).  Y is read as float4 wherever a whole float4 lies in
+// its row (dword alignment suffices); X likewise when xk is 1.
 bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan);
 
 // ((p0 + p1) + p2) + ... over S partial products in slice order, slice s of

@@ -68,7 +68,7 @@ SHAPES = [
 def test_short_sides_plan_the_skinny_kernel():
     """Rows of the short side are padded to 16 or 32 by 64 columns a block;
     33 rows go to the square tiles; K is split to fill the device.  x @ W
-    with at most 8 short rows runs the VALU axpy kernel instead (below)."""
+    with at most 2 short rows runs the VALU axpy kernel instead (below)."""
     plain = lambda m, k, n: _plan((m, k), (k, 1), 0, (k, n), (n, 1), 0)
     assert plain(9, 4096, 4096)[:2] == (16, 64) and plain(9, 4096, 4096)[3] > 1
     assert plain(4096, 100, 1)[:2] == (64, 16)
@@ -231,8 +231,10 @@ def test_axpy_kernel_normal_inputs_within_tolerance():
     (4, 5000, 3001, False, True, 0, 0), (1, 70000, 2048, False, True, 0, 0),
     (2050, 3000, 2, False, False, 0, 0),   # W @ x: X = x^T with a k stride of 2 (scalar X loads)
     (3001, 1027, 4, False, True, 0, 0), (2048, 4096, 1, False, True, 0, 0),
-    (1, 4096, 4096, False, True, 1, 0),    # x misaligned: scalar X loads
-    (1, 4096, 4096, False, True, 0, 1),    # W misaligned: the MFMA kernel
+    (1, 4096, 4096, False, True, 1, 0),    # x misaligned: float4 loads at dword alignment
+    (1, 4096, 4096, False, True, 0, 1),    # W misaligned, likewise
+    (1, 4097, 4096, False, True, 0, 0),    # rows of W 4097 floats apart: every other row misaligned
+    (3, 4097, 4097, False, False, 0, 0),   # the axpy form's fallback (L not a multiple of 4)
 ])
 def test_matrix_vector_kernel_exact(m, k, n, ta, tb, aoff, boff):
     rng = np.random.default_rng(m + k + n + aoff + 3 * boff)
