@@ -256,8 +256,9 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
  * (splits * M * N * batch floats, from the block cache) move at most 1/8 of
  * the long operand's bytes, and runs unsplit when that memory cannot be had.
  * The order of summation, and so the low bits of a result,
- * depends on the shape, the layout, the device's CU count and the operands'
- * 16-byte alignment; for fixed values of these the result is deterministic.
+ * depends on the shape, the layout and the device's CU count (not on the
+ * operands' alignment); for fixed values of these the result is
+ * deterministic.
  * Empty outputs launch nothing; K = 0 writes +0.0 and then the operands may
  * be null (src/tensor.rs:4817-4839). */
 int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,

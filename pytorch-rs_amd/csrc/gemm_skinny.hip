@@ -18,7 +18,7 @@
 // its group's partials (stored and reloaded as tagged relaxed agent-scope
 // atomics, so no release fence is needed), measured slower on the box:
 // 20.3 against 16.6 us for x[1,4096] @ W, 43.7 against 24.8 us for
-// x[32,4096] @ W.mT.
+// x[32,4096] @ W.mT (and the separate pass has since become faster).
 //
 // Fragments straight from global memory, no LDS staging (each Y element is
 // used by one lane of one MFMA):
@@ -38,6 +38,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "gemm_skinny.h"
 #include "trs_internal.h"
@@ -63,6 +64,18 @@ struct SkinnyArgs {
     int32_t S, jblocks;
 };
 
+// A block's column block, slice and batch: block = (b*S + s)*jblocks + jb.
+// In 32 bits (the planner keeps the grid below 2^31): a 64-bit division is a
+// long VALU sequence, and these kernels run a few microseconds.
+struct BlockCoords {
+    uint32_t jb, s, b;
+};
+__device__ __forceinline__ BlockCoords block_coords(const SkinnyArgs &g) {
+    const uint32_t bid = blockIdx.x, jbs = (uint32_t)g.jblocks, ss = (uint32_t)g.S;
+    const uint32_t q = bid / jbs;
+    return {bid - q * jbs, q % ss, q / ss};
+}
+
 constexpr int kWaves = 4;
 constexpr int kStepK = 32;  // k per wave step
 
@@ -87,10 +100,8 @@ __global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
     constexpr int kGroups = (RG == 1 && YVEC) ? 2 : 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int fi = lane & 15, fk = lane >> 4;
-    int64_t bid = blockIdx.x;
-    const int64_t jb = bid % g.jblocks;
-    bid /= g.jblocks;
-    const int64_t s = bid % g.S, b = bid / g.S;
+    const BlockCoords bc = block_coords(g);
+    const int64_t jb = bc.jb, s = bc.s, b = bc.b;
     const int64_t j0 = jb * kSkinnyCols;
     const int64_t kbeg = s * g.kc, kend = std::min(g.K, kbeg + g.kc);
     // Wave w takes the w-th quarter of the slice, in 32-k steps, so each of
@@ -244,8 +255,9 @@ template <int RR, bool XVEC>
 __global__ void __launch_bounds__(256) gemv_f32_dot(SkinnyArgs g) {
     constexpr int U = (RR == 4 || !XVEC) ? 2 : 4;  // 256-k steps loaded before the FMAs
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t nb = (g.L + kGemvRows - 1) / kGemvRows;
-    const int64_t b = blockIdx.x / nb, j0 = (blockIdx.x - b * nb) * kGemvRows;
+    const uint32_t nb = (uint32_t)((g.L + kGemvRows - 1) / kGemvRows);  // blocks <= INT32_MAX: 32-bit division
+    const uint32_t bq = blockIdx.x / nb;
+    const int64_t b = bq, j0 = (int64_t)(blockIdx.x - bq * nb) * kGemvRows;
     const float *X = g.x + b * g.bx;
     const float *Y = g.y + b * g.by;
     const int64_t kq = (g.K + 4 * 256 - 1) / (4 * 256) * 256;
@@ -350,8 +362,8 @@ __global__ void __launch_bounds__(256) gemv_f32_dot(SkinnyArgs g) {
 // with one fused multiply-add per element, the 8 lane groups' sums are added
 // in group order through LDS, and the slices in slice order.
 // Measured on the box for x[1,4096] @ W[4096,4096] with the slices added by
-// slice_sum: 16.7 us per call against 18.5 us for the MFMA form's 16 x 64
-// tiles; staging X in LDS (17.2 us), or that with the next rows' loads
+// slice_sum: 16.7 us per call (14.8 us once the slice pass issued all its
+// loads at once) against 18.5 us for the MFMA form's 16 x 64 tiles; staging X in LDS (17.2 us), or that with the next rows' loads
 // issued before the current rows' FMAs (18.8 us), was slower.  With 8 short
 // rows this kernel took 21.9 us (X in LDS) or 32 us (X per row) against
 // 19.5 us on the MFMA tiles, so it takes at most 2.
@@ -364,10 +376,8 @@ __global__ void __launch_bounds__(256) gemv_f32_axpy(SkinnyArgs g) {
     constexpr int U = kAxpyInFlight;
     constexpr int BR = kAxpyRowGroups * U;  // rows of a batch: U per lane group
     const int lc = threadIdx.x & 31, lr = threadIdx.x >> 5;
-    int64_t bid = blockIdx.x;
-    const int64_t jb = bid % g.jblocks;
-    bid /= g.jblocks;
-    const int64_t s = bid % g.S, b = bid / g.S;
+    const BlockCoords bc = block_coords(g);
+    const int64_t jb = bc.jb, s = bc.s, b = bc.b;
     const int64_t j0 = jb * kAxpyCols;
     const int64_t kbeg = s * g.kc, kend = std::min(g.K, kbeg + g.kc);
     const int64_t nrows = kend - kbeg;
@@ -417,29 +427,55 @@ __global__ void __launch_bounds__(256) gemv_f32_axpy(SkinnyArgs g) {
 }
 
 // c[e] = ((p0 + p1) + p2) + ... over the S slices of e's batch, in slice
-// order.  Slice s of batch b starts at ws + (b*S + s)*mn.
+// order.  Slice s of batch b starts at ws + (b*S + s)*mn.  The element
+// index e = b*mn + r (and r = i*L + j when scattering) is split in 32-bit
+// arithmetic unless WIDE (outputs of 2^32 elements or more): one 64-bit
+// division per lane, a long VALU sequence ahead of the loads, made this pass
+// 1.4 us slower, and both widths in one kernel compile to both divisions.
+// NS is S when 2 <= S <= 16, else 0 (S read at run time).  The sum of a
+// matrix-vector product is a few KB, so its time is load latency: with NS
+// all loads go out before the first add, with no branch between them (a
+// copy at a branch join waits for every load issued before it; conditional
+// loads made this pass 1.2 us slower).
+template <bool WIDE, int NS>
 __global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, float *__restrict__ c, int64_t mn,
                                                   int64_t total, int S, SliceOut out) {
+    typedef std::conditional_t<WIDE, int64_t, uint32_t> Index;
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= total) return;
-    const int64_t b = e / mn, r = e - b * mn;
-    const float *p = ws + b * S * mn + r;
-    // All of up to 16 slices' loads issued before the adds: the sum is a
-    // few KB for a matrix-vector product, so its time is load latency.
-    float part[16];
+    const Index b = total > mn ? (Index)e / (Index)mn : 0;
+    const Index r = (Index)e - b * (Index)mn;
+    const float *p = ws + (int64_t)b * S * mn + (int64_t)r;
+    float v;
+    if constexpr (NS > 0) {
+        float part[NS];
+        const float *pq = p;
 #pragma unroll
-    for (int q = 0; q < 16; q++) part[q] = q < S ? p[(int64_t)q * mn] : 0.f;
-    float v = part[0];
+        for (int q = 0; q < NS; q++) {
+            part[q] = *pq;
+            if (q + 1 < NS) pq += mn;
+        }
+        v = part[0];
 #pragma unroll
-    for (int q = 1; q < 16; q++)
-        if (q < S) v += part[q];
-    for (int s = 16; s < S; s++) v += p[(int64_t)s * mn];
+        for (int q = 1; q < NS; q++) v += part[q];
+    } else {
+        v = p[0];
+        for (int q = 1; q < S; q++) v += p[(int64_t)q * mn];
+    }
     if (!out.scatter) {
         c[e] = v;
     } else {
-        const int64_t i = r / out.L, j = r - i * out.L;
-        c[b * out.bo + i * out.oi + j * out.oj] = v;
+        const Index i = r / (Index)out.L, j = r - i * (Index)out.L;
+        c[(int64_t)b * out.bo + (int64_t)i * out.oi + (int64_t)j * out.oj] = v;
     }
+}
+
+template <bool WIDE, int NS = 2>
+void launch_slices(int S, dim3 grid, hipStream_t s, const float *ws, float *c, int64_t mn, int64_t total,
+                   const SliceOut &out) {
+    if constexpr (NS > 16) hipLaunchKernelGGL((slice_sum<WIDE, 0>), grid, dim3(256), 0, s, ws, c, mn, total, S, out);
+    else if (S == NS) hipLaunchKernelGGL((slice_sum<WIDE, NS>), grid, dim3(256), 0, s, ws, c, mn, total, S, out);
+    else launch_slices<WIDE, NS + 1>(S, grid, s, ws, c, mn, total, out);
 }
 
 template <bool DOT, bool YVEC, bool XVEC>
@@ -530,8 +566,9 @@ bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
 int launch_slice_sum(const float *ws, float *c, int64_t mn, int64_t batch, int64_t S, hipStream_t s,
                      const SliceOut &out) {
     const int64_t total = mn * batch;
-    hipLaunchKernelGGL(slice_sum, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws, c, mn, total, (int)S,
-                       out);
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (total > (int64_t)UINT32_MAX) launch_slices<true>((int)S, grid, s, ws, c, mn, total, out);
+    else launch_slices<false>((int)S, grid, s, ws, c, mn, total, out);
     TRS_LAUNCH_CHECK("gemm slice sum launch");
     return TRS_OK;
 }

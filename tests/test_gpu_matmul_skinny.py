@@ -243,6 +243,29 @@ def test_matrix_vector_kernel_exact(m, k, n, ta, tb, aoff, boff):
     assert np.array_equal(got, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32))
 
 
+@pytest.mark.parametrize("m,k,n,ta,tb", [
+    (1, 4096, 4096, False, False),    # VALU axpy kernel, K split
+    (1, 4096, 4096, False, True),     # VALU matrix-vector kernel
+    (8, 4096, 1000, False, False),    # MFMA skinny kernel, K split, slice sum
+    (32, 2048, 300, False, True),
+    (64, 4096, 512, False, False),    # K split over the small tiles, float4 split sum
+    (300, 1000, 500, True, False),    # edge-guarded small tiles
+    (2047, 2047, 2047, False, False),  # K split, one float per lane in the slice sum
+])
+def test_result_bits_do_not_depend_on_operand_alignment(m, k, n, ta, tb):
+    """Float4 loads need only dword alignment, so the plan, and with it every
+    result bit, is the same with the operands at any float offset."""
+    got, plans = [], []
+    for aoff, boff in [(0, 0), (1, 0), (0, 3), (2, 1)]:
+        rng = np.random.default_rng(m * 7 + k * 3 + n)
+        a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, aoff=aoff, boff=boff, ints=False)
+        got.append(U.matmul(sa, *la, sb, *lb))
+        plans.append(_plan(*la, *lb))
+    for g, p in zip(got[1:], plans[1:]):
+        assert p == plans[0]
+        assert np.array_equal(g.view(np.uint32), got[0].view(np.uint32))
+
+
 def test_matrix_vector_kernel_batched_and_normal_inputs():
     rng = np.random.default_rng(9)
     a, b, sa, la, sb, lb = _operands(rng, 1, 2048, 2048, False, True, batch=3)
