@@ -174,7 +174,7 @@ __global__ void __launch_bounds__(256, 4) gemm_f32_skinny(SkinnyArgs g) {
 #pragma unroll
         for (int rg = 0; rg < RG; rg++) {
             if (!GUARD && XVEC) {
-                xa[rg] = xin[rg] ? load4<true>(xrow[rg] + k4) : (vf4){0.f, 0.f, 0.f, 0.f};
+                xa[rg] = load4<true>(xrow[rg] + k4);  // rows past R: row 0, into rows never stored
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++)
