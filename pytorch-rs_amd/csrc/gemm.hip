@@ -361,6 +361,214 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
     }
 }
 
+// ---- The large tile with its slices loaded straight into LDS ----
+//
+// global_load_lds_dwordx4: each lane's 16 bytes go from global memory to
+// LDS at m0 + 16*lane, so a wave's load instruction fills one contiguous
+// KiB of LDS with no registers in between.  Against the register-staged
+// kernel above this drops the slice's four float4 LDS stores per lane and
+// the registers that hold the prefetch; the result bits are the same (each
+// lane's MFMA sequence is unchanged).  256x256 tile, 16 waves, whole tiles
+// only (FULL), row offsets within 2^31 bytes.
+//
+// LDS layouts, per operand and buffer:
+//   - a tile read along k (A not transposed, B transposed): 256 rows of BK
+//     floats, unpadded; a KiB segment holds 256/BK whole rows, and row r
+//     keeps its 16-byte chunk c at c ^ swz(r), which spreads the rows a
+//     fragment read touches over the banks as the +4 pitch does above;
+//   - a tile of k rows (A transposed, B plain): BK rows of 256 floats, one
+//     segment each, at a pitch of 260 floats (padding between segments is
+//     free).
+typedef __attribute__((address_space(3))) float lds_float;
+
+__device__ __forceinline__ uint32_t lds_address(const float *p) { return (uint32_t)(uintptr_t)(const lds_float *)p; }
+
+// 16 bytes per lane from sbase + voff (bytes) to LDS at m0 + 16 * lane.  As
+// asm the compiler adds no waits of its own around it: it cannot tell these
+// LDS bytes from the ones the current slice reads, and waited for the loads
+// before every LDS read.  The kernel waits for them itself before the
+// barrier that ends each slice.
+__device__ __forceinline__ void lds_dma16(const float *sbase, uint32_t voff, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
+                 : "memory", "m0");
+}
+
+constexpr int kLdsRowPitch = 260;  // floats per k row of 256 (+4: rows 4 apart sit 16 banks apart)
+
+template <int BK>
+__device__ __forceinline__ int lds_swizzle(int r) {
+    static_assert(BK == 16 || BK == 32, "two slice depths");
+    // 8 chunks of 16 B per row: chunk ^ (r & 7).  4 chunks per row (64-byte
+    // rows, two to a 128-byte bank line): chunk ^ ((r >> 1) & 3).
+    return BK == 32 ? (r & 7) : ((r >> 1) & 3);
+}
+
+// One operand's share of a slice: where each of this lane's loads reads
+// (bytes from the slice's base) and where its wave's segment goes (bytes
+// within the operand's LDS region).
+template <int BK, bool KROWS>
+struct LdsOperand {
+    static constexpr int kSegs = BK / 16;  // segments per wave per slice
+    static constexpr int kFloats = KROWS ? BK * kLdsRowPitch : 256 * BK;
+    uint32_t voff[kSegs], seg[kSegs];
+
+    // ld: the operand's row stride (elements).
+    __device__ __forceinline__ void plan(int64_t ld, int lane, int wave) {
+#pragma unroll
+        for (int q = 0; q < kSegs; q++) {
+            const int sg = wave + 16 * q;
+            if constexpr (KROWS) {
+                voff[q] = (uint32_t)((sg * ld + 4 * lane) * 4);
+                seg[q] = sg * kLdsRowPitch * 4;
+            } else {
+                constexpr int kChunks = BK / 4, kRowsPerSeg = 256 / BK;
+                const int r = sg * kRowsPerSeg + lane / kChunks;
+                const int c = (lane % kChunks) ^ lds_swizzle<BK>(r);
+                voff[q] = (uint32_t)((r * ld + 4 * c) * 4);
+                seg[q] = sg * 1024;
+            }
+        }
+    }
+    __device__ __forceinline__ void load(const float *base, const float *lds) const {
+        const uint32_t at = lds_address(lds);
+#pragma unroll
+        for (int q = 0; q < kSegs; q++) lds_dma16(base, voff[q], at + seg[q]);
+    }
+};
+
+// The slice depth gemm_f32_mfma_lds runs a whole-tile product at, or 0 when
+// it cannot: every 16-byte chunk it loads must be 16-byte aligned (operand
+// bases, row and batch strides), and the loads' byte offsets from a slice's
+// base (256 rows of the row stride) must stay below 2^31.  g.K is the depth
+// of one product (of one slice of a split K).  Measured at 4096^3: BK = 32
+// runs 0.925-0.934 of the FP32 MFMA peak with A not transposed, against
+// 0.919-0.924 at 16; with A transposed 16 is better (0.909-0.913 against
+// 0.904-0.911), and so it is at K = 1024 (0.889 against 0.864).
+inline int lds_tile_depth(const GemmArgs &g, bool a_trans) {
+    const bool aligned = (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                         (g.batch == 1 || (g.bsa % 4 == 0 && g.bsb % 4 == 0));
+    const bool fits = g.lda >= 0 && g.ldb >= 0 && 256 * g.lda * 4 < ((int64_t)1 << 31) &&
+                      256 * g.ldb * 4 < ((int64_t)1 << 31);
+    if (!aligned || !fits || g.K % 16 != 0) return 0;
+    return (!a_trans && g.K % 32 == 0 && g.K >= 2048) ? 32 : 16;
+}
+
+template <int BK, bool TA, bool TB>
+__global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
+    constexpr int BM = 256, BN = 256, WGN = 4, WM = 64, WN = 64, TM = WM / 16, TN = WN / 16;
+    using LA = LdsOperand<BK, TA>;
+    using LB = LdsOperand<BK, !TB>;
+    constexpr int ASIZE = LA::kFloats, BSIZE = LB::kFloats;
+    __shared__ __attribute__((aligned(16))) float lds[2 * (ASIZE + BSIZE)];
+
+    const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
+    int64_t bid = blockIdx.x;
+    if (args.xcd_remap) {
+        const int64_t total = tiles * args.batch;
+        const int64_t per_xcd = total / kXcds;
+        bid = (bid % kXcds) * per_xcd + bid / kXcds;
+    }
+    const int64_t batch_idx = bid / tiles;
+    int64_t t = bid - batch_idx * tiles;
+    const int64_t group_span = (int64_t)kGroupM * args.tiles_n;
+    const int64_t group = t / group_span;
+    const int64_t first_m = group * kGroupM;
+    const int64_t gm = std::min<int64_t>(args.tiles_m - first_m, kGroupM);
+    const int64_t within = t - group * group_span;
+    const int64_t tile_m = first_m + within % gm;
+    const int64_t tile_n = within / gm;
+
+    const int64_t Kb = args.ktotal ? std::min<int64_t>(args.K, args.ktotal - batch_idx * args.K) : args.K;
+    const float *A = args.a + batch_idx * args.bsa;
+    const float *B = args.b + batch_idx * args.bsb;
+    float *Cp = args.c + batch_idx * args.bsc;
+    const int64_t m0 = tile_m * BM, n0 = tile_n * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+    const int fi = lane & 15, fk = lane >> 4;
+
+    LA la;
+    LB lb;
+    la.plan(args.lda, lane, wave);
+    lb.plan(args.ldb, lane, wave);
+    // Slice s starts at abase + s * astep and bbase + s * bstep.
+    const float *abase = TA ? A + m0 : A + m0 * args.lda;
+    const float *bbase = TB ? B + n0 * args.ldb : B + n0;
+    const int64_t astep = TA ? BK * args.lda : BK, bstep = TB ? BK : BK * args.ldb;
+
+    typedef float vf4acc __attribute__((ext_vector_type(4)));
+    vf4acc acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = (vf4acc){0.f, 0.f, 0.f, 0.f};
+
+    // Row wm0 + 16i + fi (or wn0 + 16j + fi) has the swizzle of fi.
+    const int aswz = lds_swizzle<BK>(fi), bswz = aswz;
+    const int64_t kslices = Kb / BK;
+    la.load(abase, lds);
+    lb.load(bbase, lds + ASIZE);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int64_t s = 0; s < kslices; s++) {
+        const float *As = lds + (s & 1) * (ASIZE + BSIZE);
+        const float *Bs = As + ASIZE;
+        if (s + 1 < kslices) {
+            const float *nxt = lds + ((s + 1) & 1) * (ASIZE + BSIZE);
+            la.load(abase + (s + 1) * astep, nxt);
+            lb.load(bbase + (s + 1) * bstep, nxt + ASIZE);
+        }
+#pragma unroll 1
+        for (int kg = 0; kg < BK; kg += 16) {
+            const int k4 = kg + 4 * fk;
+            const int chunk = kg / 4 + fk;
+            vf4 a4[TM], b4[TN];
+            if constexpr (!TA) {
+                const float *ap = As + (wm0 + fi) * BK + ((chunk ^ aswz) << 2);
+#pragma unroll
+                for (int i = 0; i < TM; i++) a4[i] = *(const vf4 *)(ap + i * 16 * BK);
+            }
+            if constexpr (TB) {
+                const float *bp = Bs + (wn0 + fi) * BK + ((chunk ^ bswz) << 2);
+#pragma unroll
+                for (int j = 0; j < TN; j++) b4[j] = *(const vf4 *)(bp + j * 16 * BK);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float af[TM], bf[TN];
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    af[i] = TA ? As[(k4 + e) * kLdsRowPitch + wm0 + i * 16 + fi] : a4[i][e];
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    bf[j] = TB ? b4[j][e] : Bs[(k4 + e) * kLdsRowPitch + wn0 + j * 16 + fi];
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this slice's loads into the other buffer have landed
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int64_t n = n0 + wn0 + j * 16 + fi;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int64_t m = m0 + wm0 + i * 16 + 4 * fk + r;
+                Cp[m * args.ldc + n] = acc[i][j][r];
+            }
+        }
+    }
+}
+
 // Split-K epilogue: c = ((p0 + p1) + p2) + ... over the S partial products,
 // in slice order, four floats per lane.  NS is S when 2 <= S <= 16 (all S
 // loads issued before the first add: one memory latency instead of one per
@@ -483,8 +691,33 @@ int launch_layout(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipS
     return launch_tiled<T, true, true>(g, full, s);
 }
 
-// The large tile in each layout; `full` when it divides M, N and K.
+template <int BK, bool TA, bool TB>
+int launch_lds_tile(GemmArgs g, hipStream_t s) {
+    g.tiles_m = (int32_t)(g.M / 256);
+    g.tiles_n = (int32_t)(g.N / 256);
+    const int64_t blocks = (int64_t)g.tiles_m * g.tiles_n * g.batch;
+    g.xcd_remap = blocks % kXcds == 0 ? 1 : 0;
+    hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB>), dim3((unsigned)blocks), dim3(1024), 0, s, g);
+    TRS_LAUNCH_CHECK("gemm kernel launch");
+    return TRS_OK;
+}
+
+template <bool TA, bool TB>
+int launch_lds_layout(const GemmArgs &g, int bk, hipStream_t s) {
+    return bk == 32 ? launch_lds_tile<32, TA, TB>(g, s) : launch_lds_tile<16, TA, TB>(g, s);
+}
+
+// The large tile in each layout; `full` when it divides M, N and K.  Whole
+// tiles load their slices straight into LDS where lds_tile_depth allows.
 int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipStream_t s) {
+    if (full) {
+        if (const int bk = lds_tile_depth(g, !a_plain)) {
+            if (a_plain && b_plain) return launch_lds_layout<false, false>(g, bk, s);
+            if (a_plain) return launch_lds_layout<false, true>(g, bk, s);
+            if (b_plain) return launch_lds_layout<true, false>(g, bk, s);
+            return launch_lds_layout<true, true>(g, bk, s);
+        }
+    }
     if (a_plain && b_plain)
         return full ? launch_tiled<LargeTiles, false, false>(g, true, s)
                     : launch_tiled<LargeTilesK16, false, false>(g, false, s);
@@ -559,6 +792,15 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
     constexpr int64_t L = LargeTiles::BM;  // 256, both dims
     const int64_t large_bk = (a_plain && b_plain) ? LargeTiles::BK : LargeTilesK16::BK;
     const auto ceil_div = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+    // The depth a whole-tile product of depth k runs at (the LDS-loading
+    // kernel's where it applies; a split's slices share the operands'
+    // alignment, as their batch strides are ks times a k stride).
+    const auto large_depth = [&](int64_t k) -> int {
+        GemmArgs t = g;
+        t.K = k;
+        const int d = lds_tile_depth(t, !a_plain);
+        return d ? d : (int)large_bk;
+    };
     const int64_t large_tiles = ceil_div(M, L) * ceil_div(N, L) * batch;
     const int64_t small_tiles = ceil_div(M, 128) * ceil_div(N, 128) * batch;
     const bool large_div = M % L == 0 && N % L == 0;
@@ -567,7 +809,7 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
         p.bm = L, p.bn = L;
         p.blocks = tiles;
         p.full = mm % L == 0 && nn % L == 0 && K % large_bk == 0;
-        p.bk = p.full ? (int)large_bk : LargeTilesK16::BK;
+        p.bk = p.full ? large_depth(K) : LargeTilesK16::BK;
     };
     if (large_div && large_tiles >= cu_count) {
         use_large(M, N, large_tiles);
@@ -622,7 +864,7 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
             p.ks = ks;
             p.blocks = large_tiles * p.splits;
             p.full = large_div && K % ks == 0;
-            p.bk = p.full ? (int)large_bk : LargeTilesK16::BK;
+            p.bk = p.full ? large_depth(ks) : LargeTilesK16::BK;
             return p;
         }
     }
