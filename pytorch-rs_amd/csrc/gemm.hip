@@ -368,8 +368,9 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
 // KiB of LDS with no registers in between.  Against the register-staged
 // kernel above this drops the slice's four float4 LDS stores per lane and
 // the registers that hold the prefetch; the result bits are the same (each
-// lane's MFMA sequence is unchanged).  256x256 tile, 16 waves, whole tiles
-// only (FULL), row offsets within 2^31 bytes.
+// lane's MFMA sequence is unchanged).  256x256 tile, 16 waves, tiles whole
+// in M and N (a k that ends inside a slice ends with a partial slice loaded
+// through registers), row offsets within 2^31 bytes.
 //
 // LDS layouts, per operand and buffer:
 //   - a tile read along k (A not transposed, B transposed): 256 rows of BK
@@ -411,6 +412,7 @@ struct LdsOperand {
     static constexpr int kSegs = BK / 16;  // segments per wave per slice
     static constexpr int kFloats = KROWS ? BK * kLdsRowPitch : 256 * BK;
     uint32_t voff[kSegs], seg[kSegs];
+    int k0[kSegs];  // the slice k of this lane's first float in each segment
 
     // ld: the operand's row stride (elements).
     __device__ __forceinline__ void plan(int64_t ld, int lane, int wave) {
@@ -420,12 +422,14 @@ struct LdsOperand {
             if constexpr (KROWS) {
                 voff[q] = (uint32_t)((sg * ld + 4 * lane) * 4);
                 seg[q] = sg * kLdsRowPitch * 4;
+                k0[q] = sg;
             } else {
                 constexpr int kChunks = BK / 4, kRowsPerSeg = 256 / BK;
                 const int r = sg * kRowsPerSeg + lane / kChunks;
                 const int c = (lane % kChunks) ^ lds_swizzle<BK>(r);
                 voff[q] = (uint32_t)((r * ld + 4 * c) * 4);
                 seg[q] = sg * 1024;
+                k0[q] = 4 * c;
             }
         }
     }
@@ -434,23 +438,44 @@ struct LdsOperand {
 #pragma unroll
         for (int q = 0; q < kSegs; q++) lds_dma16(base, voff[q], at + seg[q]);
     }
+    // The last, partial slice (its first `tail` k only), through registers
+    // into the same LDS places, zero past the tail (so padded steps add
+    // 0 * 0, as the register-staged kernel's checked slice does).  Reads
+    // only elements inside the matrix.
+    __device__ __forceinline__ void load_tail(const float *base, float *lds, int tail, int lane) const {
+#pragma unroll
+        for (int q = 0; q < kSegs; q++) {
+            const float *p = base + voff[q] / 4;
+            vf4 v;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bool in = KROWS ? k0[q] < tail : k0[q] + e < tail;
+                v[e] = in ? p[e] : 0.f;
+            }
+            *(vf4 *)(lds + seg[q] / 4 + 4 * lane) = v;
+        }
+    }
 };
 
-// The slice depth gemm_f32_mfma_lds runs a whole-tile product at, or 0 when
-// it cannot: every 16-byte chunk it loads must be 16-byte aligned (operand
-// bases, row and batch strides), and the loads' byte offsets from a slice's
-// base (256 rows of the row stride) must stay below 2^31.  g.K is the depth
+// The slice depth gemm_f32_mfma_lds runs a product at, or 0 when it cannot:
+// the loads' byte offsets from a slice's base (256 rows of the row stride)
+// must stay below 2^31.  The 16-byte loads need only dword alignment (a
+// probe on the box read every float right at each of the four float offsets
+// within 16 bytes), so rows of any length qualify.  g.K is the depth
 // of one product (of one slice of a split K).  Measured at 4096^3: BK = 32
 // runs 0.925-0.934 of the FP32 MFMA peak with A not transposed, against
 // 0.919-0.924 at 16; with A transposed 16 is better (0.909-0.913 against
 // 0.904-0.911), and so it is at K = 1024 (0.889 against 0.864).
 inline int lds_tile_depth(const GemmArgs &g, bool a_trans) {
-    const bool aligned = (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
-                         (g.batch == 1 || (g.bsa % 4 == 0 && g.bsb % 4 == 0));
+    const bool aligned = (uintptr_t)g.a % 4 == 0 && (uintptr_t)g.b % 4 == 0;
     const bool fits = g.lda >= 0 && g.ldb >= 0 && 256 * g.lda * 4 < ((int64_t)1 << 31) &&
                       256 * g.ldb * 4 < ((int64_t)1 << 31);
-    if (!aligned || !fits || g.K % 16 != 0) return 0;
-    return (!a_trans && g.K % 32 == 0 && g.K >= 2048) ? 32 : 16;
+    if (!aligned || !fits) return 0;
+    // Depth 32 only where every product's k is whole slices of 32: where k
+    // ends inside a slice, the last slice is padded with zeros to 16, as in
+    // the register-staged kernel, so that the steps (and any -0.0 sum) match.
+    const bool whole32 = g.K % 32 == 0 && (g.ktotal == 0 || g.ktotal % 32 == 0);
+    return (!a_trans && whole32 && g.K >= 2048) ? 32 : 16;
 }
 
 template <int BK, bool TA, bool TB>
@@ -507,19 +532,27 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
 
     // Row wm0 + 16i + fi (or wn0 + 16j + fi) has the swizzle of fi.
     const int aswz = lds_swizzle<BK>(fi), bswz = aswz;
-    const int64_t kslices = Kb / BK;
-    la.load(abase, lds);
-    lb.load(bbase, lds + ASIZE);
+    // Whole slices load straight into LDS; a k that ends inside a slice
+    // ends with one more, partial slice loaded through registers.
+    const int64_t kwhole = Kb / BK;
+    const int tail = (int)(Kb - kwhole * BK);
+    const int64_t kslices = kwhole + (tail ? 1 : 0);
+    auto fetch = [&](int64_t s, float *dst) {
+        if (s < kwhole) {
+            la.load(abase + s * astep, dst);
+            lb.load(bbase + s * bstep, dst + ASIZE);
+        } else {
+            la.load_tail(abase + s * astep, dst, tail, lane);
+            lb.load_tail(bbase + s * bstep, dst + ASIZE, tail, lane);
+        }
+    };
+    fetch(0, lds);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int64_t s = 0; s < kslices; s++) {
         const float *As = lds + (s & 1) * (ASIZE + BSIZE);
         const float *Bs = As + ASIZE;
-        if (s + 1 < kslices) {
-            const float *nxt = lds + ((s + 1) & 1) * (ASIZE + BSIZE);
-            la.load(abase + (s + 1) * astep, nxt);
-            lb.load(bbase + (s + 1) * bstep, nxt + ASIZE);
-        }
+        if (s + 1 < kslices) fetch(s + 1, lds + ((s + 1) & 1) * (ASIZE + BSIZE));
 #pragma unroll 1
         for (int kg = 0; kg < BK; kg += 16) {
             const int k4 = kg + 4 * fk;
@@ -620,11 +653,10 @@ struct LdsOperandSmall {
     }
 };
 
-// The small tile qualifies when its 16-byte chunks are 16-byte aligned and
-// 128 rows of a row stride stay below 2^31 bytes.
+// The small tile qualifies when 128 rows of a row stride stay below 2^31
+// bytes (its loads need only dword alignment, as the large tile's).
 inline bool lds_small_ok(const GemmArgs &g) {
-    const bool aligned = (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
-                         (g.batch == 1 || (g.bsa % 4 == 0 && g.bsb % 4 == 0));
+    const bool aligned = (uintptr_t)g.a % 4 == 0 && (uintptr_t)g.b % 4 == 0;
     const bool fits = g.lda >= 0 && g.ldb >= 0 && 128 * g.lda * 4 < ((int64_t)1 << 31) &&
                       128 * g.ldb * 4 < ((int64_t)1 << 31);
     return aligned && fits && g.K % 32 == 0;
@@ -901,10 +933,11 @@ int launch_lds_layout(const GemmArgs &g, int bk, hipStream_t s) {
     return bk == 32 ? launch_lds_tile<32, TA, TB>(g, s) : launch_lds_tile<16, TA, TB>(g, s);
 }
 
-// The large tile in each layout; `full` when it divides M, N and K.  Whole
-// tiles load their slices straight into LDS where lds_tile_depth allows.
+// The large tile in each layout; `full` when it divides M, N and K.  Tiles
+// whole in M and N (any K) load their slices straight into LDS where
+// lds_tile_depth allows.
 int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipStream_t s) {
-    if (full) {
+    if (g.M % 256 == 0 && g.N % 256 == 0) {
         if (const int bk = lds_tile_depth(g, !a_plain)) {
             if (a_plain && b_plain) return launch_lds_layout<false, false>(g, bk, s);
             if (a_plain) return launch_lds_layout<false, true>(g, bk, s);
@@ -986,9 +1019,8 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
     constexpr int64_t L = LargeTiles::BM;  // 256, both dims
     const int64_t large_bk = (a_plain && b_plain) ? LargeTiles::BK : LargeTilesK16::BK;
     const auto ceil_div = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
-    // The depth a whole-tile product of depth k runs at (the LDS-loading
-    // kernel's where it applies; a split's slices share the operands'
-    // alignment, as their batch strides are ks times a k stride).
+    // The depth a whole-tile product of depth k runs at: the LDS-loading
+    // kernel's where its load offsets fit, else the register-staged tile's.
     const auto large_depth = [&](int64_t k) -> int {
         GemmArgs t = g;
         t.K = k;
