@@ -251,10 +251,13 @@ def test_matrix_vector_kernel_exact(m, k, n, ta, tb, aoff, boff):
     (64, 4096, 512, False, False),    # K split over the small tiles, float4 split sum
     (300, 1000, 500, True, False),    # edge-guarded small tiles
     (2047, 2047, 2047, False, False),  # K split, one float per lane in the slice sum
+    (4096, 80, 4096, False, True),    # 256x256 tiles loaded straight into LDS, a partial last slice
+    (1024, 512, 1024, True, False),   # 128x128 tiles loaded straight into LDS, K split
 ])
 def test_result_bits_do_not_depend_on_operand_alignment(m, k, n, ta, tb):
-    """Float4 loads need only dword alignment, so the plan, and with it every
-    result bit, is the same with the operands at any float offset."""
+    """Float4 loads, and the 16-byte loads straight into LDS, need only dword
+    alignment, so the plan, and with it every result bit, is the same with
+    the operands at any float offset."""
     got, plans = [], []
     for aoff, boff in [(0, 0), (1, 0), (0, 3), (2, 1)]:
         rng = np.random.default_rng(m * 7 + k * 3 + n)
