@@ -81,7 +81,7 @@ def build_hip(jobs: int, if_stale: bool) -> Path:
     BUILD.mkdir(parents=True, exist_ok=True)
     LIB.mkdir(parents=True, exist_ok=True)
     gen_embedded_source()
-    headers = [CSRC / h for h in ("pw_core.h", "pw_host.h", "pw_ops.h", "trs_internal.h", "gemm_skinny.h")] + [INCLUDE / "trs_hip.h",
+    headers = [CSRC / h for h in ("pw_core.h", "pw_host.h", "pw_ops.h", "trs_internal.h", "gemm_skinny.h", "lds_dma.h")] + [INCLUDE / "trs_hip.h",
                                                                                  GEN / "pw_core_src.inc"]
     objs = []
     todo = []

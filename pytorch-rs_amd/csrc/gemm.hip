@@ -31,6 +31,7 @@
 #include <algorithm>
 
 #include "gemm_skinny.h"
+#include "lds_dma.h"
 #include "trs_internal.h"
 
 namespace trs {
@@ -380,20 +381,6 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
 //   - a tile of k rows (A transposed, B plain): BK rows of 256 floats, one
 //     segment each, at a pitch of 260 floats (padding between segments is
 //     free).
-typedef __attribute__((address_space(3))) float lds_float;
-
-__device__ __forceinline__ uint32_t lds_address(const float *p) { return (uint32_t)(uintptr_t)(const lds_float *)p; }
-
-// 16 bytes per lane from sbase + voff (bytes) to LDS at m0 + 16 * lane.  As
-// asm the compiler adds no waits of its own around it: it cannot tell these
-// LDS bytes from the ones the current slice reads, and waited for the loads
-// before every LDS read.  The kernel waits for them itself before the
-// barrier that ends each slice.
-__device__ __forceinline__ void lds_dma16(const float *sbase, uint32_t voff, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
-                 : "memory", "m0");
-}
-
 constexpr int kLdsRowPitch = 260;  // floats per k row of 256 (+4: rows 4 apart sit 16 banks apart)
 
 template <int BK>
