@@ -1391,7 +1391,7 @@ extern "C" int trs_matmul_plan_f32(const float *a, const trs_layout *la, const f
         // the long operand a block takes.
         const bool short_m = ran->g.M <= ran->g.N;
         const int rows = (spl.gemv || spl.axpy) ? spl.row_groups : 16 * spl.row_groups;
-        const int cols = spl.gemv ? 4 : spl.axpy ? kAxpyCols : kSkinnyCols;
+        const int cols = spl.gemv ? 4 : spl.axpy ? kAxpyCols : spl.lds ? kLdsSkinnyCols : kSkinnyCols;
         p.bm = short_m ? rows : cols;
         p.bn = short_m ? cols : rows;
         p.bk = (int)spl.kc;

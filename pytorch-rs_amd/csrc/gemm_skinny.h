@@ -34,6 +34,9 @@ struct SkinnyPlan {
     // The VALU kernel for the other form (Y unit-stride along j, R <= 2):
     // row_groups is then R and kc the rows of Y per slice.
     bool axpy = false;
+    // The MFMA kernel that streams Y through LDS (dot form, 17..32 short
+    // rows): kLdsSkinnyCols columns per block, kc a multiple of 32.
+    bool lds = false;
     int row_groups = 1;   // 16-row MFMA groups covering R
     bool yvec = false;    // Y read as float4 (else four scalar loads)
     bool xvec = false;    // X rows read as float4 along k
@@ -45,6 +48,7 @@ struct SkinnyPlan {
 constexpr int64_t kSkinnyMaxRows = 32;
 constexpr int kSkinnyCols = 64;  // output columns per block
 constexpr int kAxpyCols = 128;   // output columns per block of the VALU axpy kernel
+constexpr int kLdsSkinnyCols = 64;  // output columns per block of the LDS-streaming kernel
 
 // Fills `plan` and returns true when the kernel takes the problem (R at
 // most kSkinnyMaxRows).  Y is read as float4 wherever a whole float4 lies in

@@ -41,6 +41,7 @@
 #include <type_traits>
 
 #include "gemm_skinny.h"
+#include "lds_dma.h"
 #include "trs_internal.h"
 
 namespace trs {
@@ -444,6 +445,98 @@ __global__ void __launch_bounds__(256) gemv_f32_axpy(SkinnyArgs g) {
     }
 }
 
+// Dot-form products with 17..32 short rows (x[32,K] @ W.mT): the same
+// MFMA arithmetic, with Y streamed through LDS.  Here X's fragment loads
+// (16 rows 16 KiB apart per instruction, twice Y's) set the time when each
+// lane reads its fragments from global memory; instead every slice of 32 k
+// -- 64 rows of Y and the 32 rows of X -- goes to LDS by
+// global_load_lds_dwordx4 through a 4-stage pipeline (three slices in
+// flight), and the fragments are read from LDS.  A block owns 64 output
+// columns and one K slice; its 4 waves own 16 columns each.  Rows of X past
+// R and of Y past L read row 0 / L-1 into sums that are never stored.  Tiles
+// in LDS keep their 16-byte chunks XOR-swizzled by row (chunk c of row r at
+// c ^ (r & 7)).  Measured on the box for x[32,4096] @ W.mT: 18.0-18.8 us per
+// call against 23.6 us for the register-fed kernel above; 8 waves, 128
+// columns per block, 2 or 6 stages, or 4 or 16 slices were slower.
+constexpr int kLdsSkinnyStages = 4;
+
+template <int RG>
+__global__ void __launch_bounds__(256) gemm_f32_skinny_lds(SkinnyArgs g) {
+    constexpr int BK = 32, NST = kLdsSkinnyStages, P = NST - 1;
+    constexpr int WSZ = kLdsSkinnyCols * BK, XSZ = 32 * BK, STG = WSZ + XSZ;
+    __shared__ __attribute__((aligned(16))) float lds[NST * STG];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int fi = lane & 15, fk = lane >> 4;
+    const BlockCoords bc = block_coords(g);
+    const int64_t jb = bc.jb, s = bc.s, b = bc.b;
+    const int64_t j0 = jb * kLdsSkinnyCols;
+    const int64_t kbeg = s * g.kc, kend = std::min(g.K, kbeg + g.kc);
+    const int nsl = (int)((kend - kbeg) / BK);  // K and kc are multiples of 32
+    const float *ybase = g.y + b * g.by + j0 * g.yl + kbeg;
+    const float *xbase = g.x + b * g.bx + kbeg;
+    // Y: 8 segments of 8 rows per slice, two per wave.  X: 4 segments, one
+    // for each wave.  Byte offsets from the slice bases.
+    uint32_t yoff[2], yseg[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int sg = wave + 4 * q;
+        const int r = sg * 8 + (lane >> 3);
+        const int64_t jr = std::min<int64_t>(r, g.L - 1 - j0);
+        const int c = (lane & 7) ^ (r & 7);
+        yoff[q] = (uint32_t)((jr * g.yl + 4 * c) * 4);
+        yseg[q] = sg * 1024;
+    }
+    const int xr = wave * 8 + (lane >> 3);
+    const uint32_t xoff = (uint32_t)(((xr < g.R ? xr : 0) * g.xi + 4 * ((lane & 7) ^ (xr & 7))) * 4);
+    const uint32_t xseg = WSZ * 4 + wave * 1024;
+    auto issue = [&](int sl) {
+        const uint32_t at = lds_address(lds + (sl % NST) * STG);
+#pragma unroll
+        for (int q = 0; q < 2; q++) lds_dma16(ybase + sl * BK, yoff[q], at + yseg[q]);
+        lds_dma16(xbase + sl * BK, xoff, at + xseg);
+    };
+    typedef float vf4acc __attribute__((ext_vector_type(4)));
+    vf4acc acc[RG];
+#pragma unroll
+    for (int i = 0; i < RG; i++) acc[i] = (vf4acc){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < P; q++)
+        if (q < nsl) issue(q);
+    const int sw = fi & 7;     // rows 16i + fi of X and wn0 + fi of Y
+    const int wn0 = wave * 16;
+    for (int sl = 0; sl < nsl; sl++) {
+        // Slice sl must have landed; slices sl+1 .. sl+P-1 (3 loads each) may
+        // still be in flight, except near the end, where fewer were issued.
+        if (sl + P <= nsl) __builtin_amdgcn_s_waitcnt(vmcnt_at_most((P - 1) * 3));
+        else __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // every wave's loads of slice sl; every read of slice sl-1
+        if (sl + P < nsl) issue(sl + P);  // into the buffer slice sl-1 used
+        const float *Ys = lds + (sl % NST) * STG, *Xs = Ys + WSZ;
+#pragma unroll
+        for (int kg = 0; kg < BK; kg += 16) {
+            const int c = ((kg / 4 + fk) ^ sw) << 2;
+            const vf4 w4 = *(const vf4 *)(Ys + (wn0 + fi) * BK + c);
+            vf4 x4[RG];
+#pragma unroll
+            for (int i = 0; i < RG; i++) x4[i] = *(const vf4 *)(Xs + (i * 16 + fi) * BK + c);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < RG; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(x4[i][e], w4[e], acc[i], 0, 0, 0);
+        }
+    }
+    float *O = g.o + b * g.bo + s * g.os;
+    const int64_t j = j0 + wn0 + fi;
+#pragma unroll
+    for (int i = 0; i < RG; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int64_t row = 16 * i + 4 * fk + r;
+            if (row < g.R && j < g.L) O[row * g.oi + j * g.oj] = acc[i][r];
+        }
+}
+
 // c[e] = ((p0 + p1) + p2) + ... over the S slices of e's batch, in slice
 // order.  Slice s of batch b starts at ws + (b*S + s)*mn.  The element
 // index e = b*mn + r (and r = i*L + j when scattering) is split in 32-bit
@@ -563,6 +656,30 @@ bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
             return true;
         }
     }
+    // The LDS-streaming kernel: dot form, 17..32 short rows, X unit-stride
+    // along k, K a multiple of 32, 64 rows of Y (and 32 of X) within 2^31
+    // bytes of a slice's base.  About 2 blocks per CU, slices of whole
+    // 32-k steps, and the partial products' traffic at most 1/8 of Y's.
+    if (p.dot && p.R > 16 && p.xk == 1 && p.K % 32 == 0 && 64 * p.yl * 4 < ((int64_t)1 << 31) &&
+        32 * p.xi * 4 < ((int64_t)1 << 31)) {
+        const int64_t jb = (p.L + kLdsSkinnyCols - 1) / kLdsSkinnyCols;
+        const int64_t ab = jb * p.batch;
+        const int64_t want = (2 * (int64_t)cu_count + ab - 1) / ab;
+        const int64_t cap = std::max<int64_t>(1, std::min(p.K / 256, p.K / (16 * p.R)));
+        int64_t S = std::clamp<int64_t>(want, 1, cap);
+        int64_t kc = (p.K + S - 1) / S;
+        kc = (kc + 31) / 32 * 32;
+        S = (p.K + kc - 1) / kc;
+        if (ab * S <= INT32_MAX && jb <= INT32_MAX) {
+            pl.lds = true;
+            pl.row_groups = 2;
+            pl.kc = kc;
+            pl.splits = S;
+            pl.blocks = ab * S;
+            *plan = pl;
+            return true;
+        }
+    }
     const int64_t jblocks = (p.L + kSkinnyCols - 1) / kSkinnyCols;
     const int64_t base = jblocks * p.batch;
     // ~4 blocks per CU; each slice at least 128 deep (one step per wave), and
@@ -625,7 +742,8 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
     g.R = p.R;
     g.L = p.L;
     g.K = p.K;
-    g.jblocks = (int32_t)((p.L + (plan.axpy ? kAxpyCols : kSkinnyCols) - 1) / (plan.axpy ? kAxpyCols : kSkinnyCols));
+    const int64_t cols = plan.axpy ? kAxpyCols : plan.lds ? kLdsSkinnyCols : kSkinnyCols;
+    g.jblocks = (int32_t)((p.L + cols - 1) / cols);
     const int64_t mn = p.R * p.L;
     int64_t S = plan.splits, kc = plan.kc;
     void *ws = nullptr;
@@ -664,6 +782,9 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
         if (plan.row_groups == 1) hipLaunchKernelGGL((gemv_f32_axpy<1>), grid, dim3(256), 0, s, g);
         else hipLaunchKernelGGL((gemv_f32_axpy<2>), grid, dim3(256), 0, s, g);
         TRS_LAUNCH_CHECK("axpy gemv launch");
+    } else if (plan.lds) {
+        hipLaunchKernelGGL((gemm_f32_skinny_lds<2>), grid, dim3(256), 0, s, g);
+        TRS_LAUNCH_CHECK("skinny lds launch");
     } else {
         rc = p.dot ? launch_form<true>(plan.xvec, plan.row_groups, grid, s, g)
                    : launch_form<false>(plan.xvec, plan.row_groups, grid, s, g);

@@ -56,6 +56,13 @@ def _operands(rng, m, k, n, ta, tb, batch=0, aoff=0, boff=0, ints=True):
 
 LAYOUTS = [(False, False), (False, True), (True, False), (True, True)]
 
+
+def _cu_count() -> int:
+    from trs_backend import abi
+    name, cus, clk = ctypes.create_string_buffer(256), ctypes.c_int(), ctypes.c_int()
+    abi.check(abi.lib.trs_device_info(name, 256, ctypes.byref(cus), ctypes.byref(clk)))
+    return cus.value
+
 # (M, K, N): short side M or N from 1 to 32, K below one slice, ragged, and
 # long enough to split; the long side ragged against the 64-column blocks.
 SHAPES = [
@@ -213,6 +220,41 @@ def test_axpy_kernel_exact(m, k, n, ta, tb, batch):
     got = U.matmul(sa, *la, sb, *lb)
     want = np.matmul(a.astype(np.int64), b.astype(np.int64)).astype(np.float32)
     assert np.array_equal(got.reshape(want.shape), want)
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb,batch,aoff", [
+    (32, 4096, 4096, False, True, 0, 0), (17, 1024, 1000, False, True, 0, 0), (24, 64, 65, False, True, 0, 1),
+    (32, 4128, 4097, False, True, 2, 0), (20, 96, 130, False, True, 3, 3), (32, 32, 64, False, True, 0, 0),
+    (4096, 512, 32, False, True, 0, 0), (1000, 2048, 25, False, True, 0, 2),
+])
+def test_lds_streaming_skinny_kernel_exact(m, k, n, ta, tb, batch, aoff):
+    """Dot-form products with 17..32 short rows and K a multiple of 32 stream
+    Y through LDS: long sides ragged against the 64-column blocks, one-slice
+    and split K, batches, operands at float offsets, and the W @ x form
+    (the short side N): exact on small integers."""
+    rng = np.random.default_rng(m + 3 * k + 7 * n + batch + aoff)
+    a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, batch=batch, aoff=aoff)
+    tm, tn, tk, s, blocks = _plan(*la, *lb)
+    assert (min(tm, tn), max(tm, tn)) == (32, 64) and tk % 32 == 0, (tm, tn, tk)
+    got = U.matmul(sa, *la, sb, *lb)
+    want = np.matmul(a.astype(np.int64), b.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(got.reshape(want.shape), want)
+
+
+def test_lds_streaming_skinny_kernel_plan_and_normal_inputs():
+    """[32,4096] @ W.mT splits K into 8 slices of 512 over 64 column blocks
+    (about 2 blocks per CU), and is within 1e-5 * sqrt(K) of the oracle on
+    normal data."""
+    if _cu_count() != 256:
+        pytest.skip("the split listed is that of a 256-CU device")
+    rng = np.random.default_rng(41)
+    a, b, sa, la, sb, lb = _operands(rng, 32, 4096, 4096, False, True, ints=False)
+    assert _plan(*la, *lb) == (32, 64, 512, 8, 512)
+    got = U.matmul(sa, *la, sb, *lb)
+    want = O.matmul(sa, *la, sb, *lb).reshape(32, 4096)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    tol = 1e-5 * np.sqrt(4096) * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+    assert (err <= tol).all(), err.max()
 
 
 def test_axpy_kernel_normal_inputs_within_tolerance():
