@@ -34,7 +34,7 @@ struct SkinnyPlan {
     // The VALU kernel for the other form (Y unit-stride along j, R <= 2):
     // row_groups is then R and kc the rows of Y per slice.
     bool axpy = false;
-    // The MFMA kernel that streams Y through LDS (dot form, 17..32 short
+    // The MFMA kernel that streams Y through LDS (dot form, 5..32 short
     // rows): kLdsSkinnyCols columns per block, kc a multiple of 32.
     bool lds = false;
     int row_groups = 1;   // 16-row MFMA groups covering R

@@ -445,8 +445,8 @@ __global__ void __launch_bounds__(256) gemv_f32_axpy(SkinnyArgs g) {
     }
 }
 
-// Dot-form products with 17..32 short rows (x[32,K] @ W.mT): the same
-// MFMA arithmetic, with Y streamed through LDS.  Here X's fragment loads
+// Dot-form products with 5..32 short rows (x[32,K] @ W.mT): the same MFMA
+// arithmetic, with Y streamed through LDS.  Here X's fragment loads
 // (16 rows 16 KiB apart per instruction, twice Y's) set the time when each
 // lane reads its fragments from global memory; instead every slice of 32 k
 // -- 64 rows of Y and the 32 rows of X -- goes to LDS by
@@ -456,8 +456,9 @@ __global__ void __launch_bounds__(256) gemv_f32_axpy(SkinnyArgs g) {
 // R and of Y past L read row 0 / L-1 into sums that are never stored.  Tiles
 // in LDS keep their 16-byte chunks XOR-swizzled by row (chunk c of row r at
 // c ^ (r & 7)).  Measured on the box for x[32,4096] @ W.mT: 18.0-18.8 us per
-// call against 23.6 us for the register-fed kernel above; 8 waves, 128
-// columns per block, 2 or 6 stages, or 4 or 16 slices were slower.
+// call against 23.6 us for the register-fed kernel above (8, 12 and 16
+// rows: 16.7-17.4 against 21.0-22.6 us); 8 waves, 128 columns per block, 2
+// or 6 stages, or 4 or 16 slices were slower.
 constexpr int kLdsSkinnyStages = 4;
 
 template <int RG>
@@ -656,11 +657,11 @@ bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
             return true;
         }
     }
-    // The LDS-streaming kernel: dot form, 17..32 short rows, X unit-stride
+    // The LDS-streaming kernel: dot form, 5..32 short rows, X unit-stride
     // along k, K a multiple of 32, 64 rows of Y (and 32 of X) within 2^31
     // bytes of a slice's base.  About 2 blocks per CU, slices of whole
     // 32-k steps, and the partial products' traffic at most 1/8 of Y's.
-    if (p.dot && p.R > 16 && p.xk == 1 && p.K % 32 == 0 && 64 * p.yl * 4 < ((int64_t)1 << 31) &&
+    if (p.dot && p.R > 4 && p.xk == 1 && p.K % 32 == 0 && 64 * p.yl * 4 < ((int64_t)1 << 31) &&
         32 * p.xi * 4 < ((int64_t)1 << 31)) {
         const int64_t jb = (p.L + kLdsSkinnyCols - 1) / kLdsSkinnyCols;
         const int64_t ab = jb * p.batch;
@@ -672,7 +673,7 @@ bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
         S = (p.K + kc - 1) / kc;
         if (ab * S <= INT32_MAX && jb <= INT32_MAX) {
             pl.lds = true;
-            pl.row_groups = 2;
+            pl.row_groups = p.R <= 16 ? 1 : 2;
             pl.kc = kc;
             pl.splits = S;
             pl.blocks = ab * S;
@@ -783,7 +784,8 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
         else hipLaunchKernelGGL((gemv_f32_axpy<2>), grid, dim3(256), 0, s, g);
         TRS_LAUNCH_CHECK("axpy gemv launch");
     } else if (plan.lds) {
-        hipLaunchKernelGGL((gemm_f32_skinny_lds<2>), grid, dim3(256), 0, s, g);
+        if (plan.row_groups == 1) hipLaunchKernelGGL((gemm_f32_skinny_lds<1>), grid, dim3(256), 0, s, g);
+        else hipLaunchKernelGGL((gemm_f32_skinny_lds<2>), grid, dim3(256), 0, s, g);
         TRS_LAUNCH_CHECK("skinny lds launch");
     } else {
         rc = p.dot ? launch_form<true>(plan.xvec, plan.row_groups, grid, s, g)

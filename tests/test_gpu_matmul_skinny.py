@@ -225,17 +225,18 @@ def test_axpy_kernel_exact(m, k, n, ta, tb, batch):
 @pytest.mark.parametrize("m,k,n,ta,tb,batch,aoff", [
     (32, 4096, 4096, False, True, 0, 0), (17, 1024, 1000, False, True, 0, 0), (24, 64, 65, False, True, 0, 1),
     (32, 4128, 4097, False, True, 2, 0), (20, 96, 130, False, True, 3, 3), (32, 32, 64, False, True, 0, 0),
-    (4096, 512, 32, False, True, 0, 0), (1000, 2048, 25, False, True, 0, 2),
+    (4096, 512, 32, False, True, 0, 0), (1000, 2048, 25, False, True, 0, 2), (8, 4096, 4096, False, True, 0, 0),
+    (5, 1024, 130, False, True, 2, 1), (16, 64, 65, False, True, 0, 0), (2000, 320, 12, False, True, 0, 0),
 ])
 def test_lds_streaming_skinny_kernel_exact(m, k, n, ta, tb, batch, aoff):
-    """Dot-form products with 17..32 short rows and K a multiple of 32 stream
+    """Dot-form products with 5..32 short rows and K a multiple of 32 stream
     Y through LDS: long sides ragged against the 64-column blocks, one-slice
     and split K, batches, operands at float offsets, and the W @ x form
     (the short side N): exact on small integers."""
     rng = np.random.default_rng(m + 3 * k + 7 * n + batch + aoff)
     a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, batch=batch, aoff=aoff)
     tm, tn, tk, s, blocks = _plan(*la, *lb)
-    assert (min(tm, tn), max(tm, tn)) == (32, 64) and tk % 32 == 0, (tm, tn, tk)
+    assert (min(tm, tn), max(tm, tn)) == (16 if min(m, n) <= 16 else 32, 64) and tk % 32 == 0, (tm, tn, tk)
     got = U.matmul(sa, *la, sb, *lb)
     want = np.matmul(a.astype(np.int64), b.astype(np.int64)).astype(np.float32)
     assert np.array_equal(got.reshape(want.shape), want)
