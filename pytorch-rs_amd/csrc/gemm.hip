@@ -603,15 +603,19 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
 // 0.081 -> 0.072 ms, 2048^3 0.144 -> 0.141 ms.
 constexpr int kSmallSegPitch = 272;
 
-template <bool KROWS>
+// ROWS: the tile's rows when read along k (128, or 64 for A of the 64x128
+// tile); a k-row tile is always 128 wide.  NW: the block's waves.
+template <bool KROWS, int ROWS, int NW>
 struct LdsOperandSmall {
-    static constexpr int kFloats = KROWS ? 16 * kSmallSegPitch : 128 * 32;
-    uint32_t voff[2], seg[2];
+    static_assert(!KROWS || ROWS == 128, "k rows of 128 floats only");
+    static constexpr int kFloats = KROWS ? 16 * kSmallSegPitch : ROWS * 32;
+    static constexpr int kSegs = (KROWS ? 16 : ROWS / 8) / NW;  // per wave
+    uint32_t voff[kSegs], seg[kSegs];
 
     __device__ __forceinline__ void plan(int64_t ld, int lane, int wave) {
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int sg = wave + 8 * q;
+        for (int q = 0; q < kSegs; q++) {
+            const int sg = wave + NW * q;
             if constexpr (KROWS) {
                 const int k = 2 * sg + (lane >> 5);
                 voff[q] = (uint32_t)((k * ld + 4 * (lane & 31)) * 4);
@@ -627,7 +631,7 @@ struct LdsOperandSmall {
     __device__ __forceinline__ void load(const float *base, const float *lds) const {
         const uint32_t at = lds_address(lds);
 #pragma unroll
-        for (int q = 0; q < 2; q++) lds_dma16(base, voff[q], at + seg[q]);
+        for (int q = 0; q < kSegs; q++) lds_dma16(base, voff[q], at + seg[q]);
     }
     // Element (row, k) of a k-contiguous tile for a lane whose row has
     // swizzle sw (its row's r & 7), at k step kk (k = kk + fk).
@@ -640,8 +644,9 @@ struct LdsOperandSmall {
     }
 };
 
-// The small tile qualifies when 128 rows of a row stride stay below 2^31
-// bytes (its loads need only dword alignment, as the large tile's).
+// The 128x128 and 64x128 tiles qualify when 128 rows of a row stride stay
+// below 2^31 bytes (their loads need only dword alignment, as the large
+// tile's).
 inline bool lds_small_ok(const GemmArgs &g) {
     const bool aligned = (uintptr_t)g.a % 4 == 0 && (uintptr_t)g.b % 4 == 0;
     const bool fits = g.lda >= 0 && g.ldb >= 0 && 128 * g.lda * 4 < ((int64_t)1 << 31) &&
@@ -649,11 +654,13 @@ inline bool lds_small_ok(const GemmArgs &g) {
     return aligned && fits && g.K % 32 == 0;
 }
 
-template <bool TA, bool TB>
-__global__ void __launch_bounds__(512, 2) gemm_f32_mfma_lds_small(GemmArgs args) {
-    constexpr int BM = 128, BN = 128, BK = 32, WGN = 2, WM = 32, WN = 64, TM = WM / 16, TN = WN / 16;
-    using LA = LdsOperandSmall<TA>;
-    using LB = LdsOperandSmall<!TB>;
+// BM 128: 8 waves (4x2); BM 64 (the 64x128 tile, A not transposed): 4
+// waves (2x2).  Each wave owns 32x64 either way.
+template <int BM, bool TA, bool TB>
+__global__ void __launch_bounds__(BM * 4, 2) gemm_f32_mfma_lds_small(GemmArgs args) {
+    constexpr int NW = BM / 16, BN = 128, BK = 32, WGN = 2, WM = 32, WN = 64, TM = WM / 16, TN = WN / 16;
+    using LA = LdsOperandSmall<TA, BM, NW>;
+    using LB = LdsOperandSmall<!TB, 128, NW>;
     constexpr int ASIZE = LA::kFloats, BSIZE = LB::kFloats;
     __shared__ __attribute__((aligned(16))) float lds[2 * (ASIZE + BSIZE)];
 
@@ -870,13 +877,13 @@ int launch_tiled(GemmArgs g, bool full, hipStream_t s) {
     return TRS_OK;
 }
 
-template <bool TA, bool TB>
+template <int BM, bool TA, bool TB>
 int launch_lds_small(GemmArgs g, hipStream_t s) {
-    g.tiles_m = (int32_t)(g.M / 128);
+    g.tiles_m = (int32_t)(g.M / BM);
     g.tiles_n = (int32_t)(g.N / 128);
     const int64_t blocks = (int64_t)g.tiles_m * g.tiles_n * g.batch;
     g.xcd_remap = blocks % kXcds == 0 ? 1 : 0;
-    hipLaunchKernelGGL((gemm_f32_mfma_lds_small<TA, TB>), dim3((unsigned)blocks), dim3(512), 0, s, g);
+    hipLaunchKernelGGL((gemm_f32_mfma_lds_small<BM, TA, TB>), dim3((unsigned)blocks), dim3(BM * 4), 0, s, g);
     TRS_LAUNCH_CHECK("gemm kernel launch");
     return TRS_OK;
 }
@@ -888,12 +895,20 @@ int launch_layout(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipS
 // lds_small_ok allows.
 int launch_small(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipStream_t s) {
     if (full && lds_small_ok(g)) {
-        if (a_plain && b_plain) return launch_lds_small<false, false>(g, s);
-        if (a_plain) return launch_lds_small<false, true>(g, s);
-        if (b_plain) return launch_lds_small<true, false>(g, s);
-        return launch_lds_small<true, true>(g, s);
+        if (a_plain && b_plain) return launch_lds_small<128, false, false>(g, s);
+        if (a_plain) return launch_lds_small<128, false, true>(g, s);
+        if (b_plain) return launch_lds_small<128, true, false>(g, s);
+        return launch_lds_small<128, true, true>(g, s);
     }
     return launch_layout<SmallTiles>(g, a_plain, b_plain, full, s);
+}
+
+// The 64x128 tile (whole tiles only); with A not transposed its slices load
+// straight into LDS where lds_small_ok allows.
+int launch_medium(const GemmArgs &g, bool a_plain, bool b_plain, hipStream_t s) {
+    if (a_plain && lds_small_ok(g))
+        return b_plain ? launch_lds_small<64, false, false>(g, s) : launch_lds_small<64, false, true>(g, s);
+    return launch_layout<MediumTiles>(g, a_plain, b_plain, true, s);
 }
 
 template <class T>
@@ -1121,7 +1136,7 @@ int launch_split_k(const GemmPlan &p, GemmArgs g, bool a_plain, bool b_plain, in
     g.batch = S;
     switch (p.split_tile) {
     case GemmKind::Large: rc = launch_large(g, a_plain, b_plain, p.full, s); break;
-    case GemmKind::Medium: rc = launch_layout<MediumTiles>(g, a_plain, b_plain, true, s); break;
+    case GemmKind::Medium: rc = launch_medium(g, a_plain, b_plain, s); break;
     default: rc = launch_small(g, a_plain, b_plain, p.full, s); break;
     }
     if (rc == TRS_OK) {
@@ -1257,7 +1272,7 @@ int run_unsplit(const GemmPlan &p, const GemmArgs &g, bool a_plain, bool b_plain
     switch (p.kind) {
     case GemmKind::Large:
     case GemmKind::SplitK: return launch_large(g, a_plain, b_plain, p.full, s);
-    case GemmKind::Medium: return launch_layout<MediumTiles>(g, a_plain, b_plain, true, s);
+    case GemmKind::Medium: return launch_medium(g, a_plain, b_plain, s);
     default: return launch_small(g, a_plain, b_plain, p.full, s);
     }
 }
