@@ -465,7 +465,9 @@ inline int lds_tile_depth(const GemmArgs &g, bool a_trans) {
     return (!a_trans && whole32 && g.K >= 2048) ? 32 : 16;
 }
 
-template <int BK, bool TA, bool TB>
+// TAIL: some product's k ends inside a slice (compiled apart: the branch in
+// the slice loop cost 1% at 4096^3 and on the MLP step).
+template <int BK, bool TA, bool TB, bool TAIL>
 __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
     constexpr int BM = 256, BN = 256, WGN = 4, WM = 64, WN = 64, TM = WM / 16, TN = WN / 16;
     using LA = LdsOperand<BK, TA>;
@@ -522,10 +524,10 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
     // Whole slices load straight into LDS; a k that ends inside a slice
     // ends with one more, partial slice loaded through registers.
     const int64_t kwhole = Kb / BK;
-    const int tail = (int)(Kb - kwhole * BK);
+    const int tail = TAIL ? (int)(Kb - kwhole * BK) : 0;
     const int64_t kslices = kwhole + (tail ? 1 : 0);
     auto fetch = [&](int64_t s, float *dst) {
-        if (s < kwhole) {
+        if (!TAIL || s < kwhole) {
             la.load(abase + s * astep, dst);
             lb.load(bbase + s * bstep, dst + ASIZE);
         } else {
@@ -925,7 +927,9 @@ int launch_lds_tile(GemmArgs g, hipStream_t s) {
     g.tiles_n = (int32_t)(g.N / 256);
     const int64_t blocks = (int64_t)g.tiles_m * g.tiles_n * g.batch;
     g.xcd_remap = blocks % kXcds == 0 ? 1 : 0;
-    hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB>), dim3((unsigned)blocks), dim3(1024), 0, s, g);
+    const bool tail = g.K % BK != 0 || (g.ktotal != 0 && g.ktotal % BK != 0);
+    if (tail) hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, true>), dim3((unsigned)blocks), dim3(1024), 0, s, g);
+    else hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, false>), dim3((unsigned)blocks), dim3(1024), 0, s, g);
     TRS_LAUNCH_CHECK("gemm kernel launch");
     return TRS_OK;
 }
