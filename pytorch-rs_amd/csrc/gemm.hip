@@ -369,9 +369,22 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
 // KiB of LDS with no registers in between.  Against the register-staged
 // kernel above this drops the slice's four float4 LDS stores per lane and
 // the registers that hold the prefetch; the result bits are the same (each
-// lane's MFMA sequence is unchanged).  256x256 tile, 16 waves, tiles whole
-// in M and N (a k that ends inside a slice ends with a partial slice loaded
-// through registers), row offsets within 2^31 bytes.
+// lane's MFMA sequence is unchanged).  256x256 tile, 16 waves (a k that
+// ends inside a slice ends with a partial slice loaded through registers),
+// row offsets within 2^31 bytes.
+//
+// Ragged M or N (the EDGE form): a tile reaching past the matrix keeps its
+// loads inside it and its LDS layout unchanged.
+//   - An operand read along k clamps its rows past the edge to the last row.
+//   - An operand of k rows (its 256 columns contiguous) with v < 256 valid
+//     columns points each chunk past v at the tile's first chunk.  A chunk
+//     that straddles v (v not a multiple of 4) is read from v - 4 instead,
+//     so that its valid columns c land at c + d, d = 4 - v % 4, and the
+//     fragment reads of those columns add d.  The host requires v >= 4.
+//   - Whatever lands in the rows or columns past the edge only feeds outputs
+//     past it, which are not stored.
+// The interior tiles of a ragged product run the same code with nothing
+// clamped and d = 0.
 //
 // LDS layouts, per operand and buffer:
 //   - a tile read along k (A not transposed, B transposed): 256 rows of BK
@@ -401,20 +414,24 @@ struct LdsOperand {
     uint32_t voff[kSegs], seg[kSegs];
     int k0[kSegs];  // the slice k of this lane's first float in each segment
 
-    // ld: the operand's row stride (elements).
-    __device__ __forceinline__ void plan(int64_t ld, int lane, int wave) {
+    // ld: the operand's row stride (elements).  valid: the tile's rows (read
+    // along k) or columns (k rows) inside the matrix, 4..256.
+    __device__ __forceinline__ void plan(int64_t ld, int lane, int wave, int valid = 256) {
 #pragma unroll
         for (int q = 0; q < kSegs; q++) {
             const int sg = wave + 16 * q;
             if constexpr (KROWS) {
-                voff[q] = (uint32_t)((sg * ld + 4 * lane) * 4);
+                int col = 4 * lane;
+                if (col + 4 > valid) col = col < valid ? valid - 4 : 0;
+                voff[q] = (uint32_t)((sg * ld + col) * 4);
                 seg[q] = sg * kLdsRowPitch * 4;
                 k0[q] = sg;
             } else {
                 constexpr int kChunks = BK / 4, kRowsPerSeg = 256 / BK;
+                // Tile row r's slot holds chunk c of matrix row min(r, valid - 1).
                 const int r = sg * kRowsPerSeg + lane / kChunks;
                 const int c = (lane % kChunks) ^ lds_swizzle<BK>(r);
-                voff[q] = (uint32_t)((r * ld + 4 * c) * 4);
+                voff[q] = (uint32_t)((std::min(r, valid - 1) * ld + 4 * c) * 4);
                 seg[q] = sg * 1024;
                 k0[q] = 4 * c;
             }
@@ -452,12 +469,18 @@ struct LdsOperand {
 // of one product (of one slice of a split K).  Measured at 4096^3: BK = 32
 // runs 0.925-0.934 of the FP32 MFMA peak with A not transposed, against
 // 0.919-0.924 at 16; with A transposed 16 is better (0.909-0.913 against
-// 0.904-0.911), and so it is at K = 1024 (0.889 against 0.864).
-inline int lds_tile_depth(const GemmArgs &g, bool a_trans) {
+// 0.904-0.911), and so it is at K = 1024 (0.889 against 0.864).  Ragged M
+// or N run at 16 (the EDGE form), where each k-row operand's edge tile has
+// at least 4 valid columns (M or N not 1-3 past a multiple of 256).
+inline int lds_tile_depth(const GemmArgs &g, bool a_trans, bool b_trans) {
     const bool aligned = (uintptr_t)g.a % 4 == 0 && (uintptr_t)g.b % 4 == 0;
     const bool fits = g.lda >= 0 && g.ldb >= 0 && 256 * g.lda * 4 < ((int64_t)1 << 31) &&
                       256 * g.ldb * 4 < ((int64_t)1 << 31);
     if (!aligned || !fits) return 0;
+    if (g.M % 256 != 0 || g.N % 256 != 0) {
+        const auto edge_ok = [](int64_t d) { return d % 256 == 0 || d % 256 >= 4; };
+        return (a_trans && !edge_ok(g.M)) || (!b_trans && !edge_ok(g.N)) ? 0 : 16;
+    }
     // Depth 32 only where every product's k is whole slices of 32: where k
     // ends inside a slice, the last slice is padded with zeros to 16, as in
     // the register-staged kernel, so that the steps (and any -0.0 sum) match.
@@ -466,8 +489,10 @@ inline int lds_tile_depth(const GemmArgs &g, bool a_trans) {
 }
 
 // TAIL: some product's k ends inside a slice (compiled apart: the branch in
-// the slice loop cost 1% at 4096^3 and on the MLP step).
-template <int BK, bool TA, bool TB, bool TAIL>
+// the slice loop cost 1% at 4096^3 and on the MLP step).  EDGE: M or N is
+// not a multiple of 256 (compiled apart too, so that whole-tile products
+// keep the loop they had).
+template <int BK, bool TA, bool TB, bool TAIL, bool EDGE>
 __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
     constexpr int BM = 256, BN = 256, WGN = 4, WM = 64, WN = 64, TM = WM / 16, TN = WN / 16;
     using LA = LdsOperand<BK, TA>;
@@ -503,10 +528,21 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
     const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
     const int fi = lane & 15, fk = lane >> 4;
 
+    // The tile's rows and columns inside C (256 but on the edge tiles).
+    const int vm = EDGE ? (int)std::min<int64_t>(BM, args.M - m0) : BM;
+    const int vn = EDGE ? (int)std::min<int64_t>(BN, args.N - n0) : BN;
     LA la;
     LB lb;
-    la.plan(args.lda, lane, wave);
-    lb.plan(args.ldb, lane, wave);
+    la.plan(args.lda, lane, wave, vm);
+    lb.plan(args.ldb, lane, wave, vn);
+    // Fragment columns of a k-row operand that a straddling chunk moved
+    // (see above): column c in [v & ~3, v) is read at c + 4 - v % 4.
+    const auto moved = [](int c, int v) { return (v & 3) && c >= (v & ~3) && c < v ? 4 - (v & 3) : 0; };
+    int adja[TM], adjb[TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) adja[i] = EDGE && TA ? moved(wm0 + i * 16 + fi, vm) : 0;
+#pragma unroll
+    for (int j = 0; j < TN; j++) adjb[j] = EDGE && !TB ? moved(wn0 + j * 16 + fi, vn) : 0;
     // Slice s starts at abase + s * astep and bbase + s * bstep.
     const float *abase = TA ? A + m0 : A + m0 * args.lda;
     const float *bbase = TB ? B + n0 * args.ldb : B + n0;
@@ -562,10 +598,10 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
                 float af[TM], bf[TN];
 #pragma unroll
                 for (int i = 0; i < TM; i++)
-                    af[i] = TA ? As[(k4 + e) * kLdsRowPitch + wm0 + i * 16 + fi] : a4[i][e];
+                    af[i] = TA ? As[(k4 + e) * kLdsRowPitch + wm0 + i * 16 + fi + adja[i]] : a4[i][e];
 #pragma unroll
                 for (int j = 0; j < TN; j++)
-                    bf[j] = TB ? b4[j][e] : Bs[(k4 + e) * kLdsRowPitch + wn0 + j * 16 + fi];
+                    bf[j] = TB ? b4[j][e] : Bs[(k4 + e) * kLdsRowPitch + wn0 + j * 16 + fi + adjb[j]];
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -585,7 +621,7 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int64_t m = m0 + wm0 + i * 16 + 4 * fk + r;
-                Cp[m * args.ldc + n] = acc[i][j][r];
+                if (!EDGE || (m < args.M && n < args.N)) Cp[m * args.ldc + n] = acc[i][j][r];
             }
         }
     }
@@ -923,13 +959,25 @@ int launch_layout(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipS
 
 template <int BK, bool TA, bool TB>
 int launch_lds_tile(GemmArgs g, hipStream_t s) {
-    g.tiles_m = (int32_t)(g.M / 256);
-    g.tiles_n = (int32_t)(g.N / 256);
+    g.tiles_m = (int32_t)((g.M + 255) / 256);
+    g.tiles_n = (int32_t)((g.N + 255) / 256);
     const int64_t blocks = (int64_t)g.tiles_m * g.tiles_n * g.batch;
     g.xcd_remap = blocks % kXcds == 0 ? 1 : 0;
     const bool tail = g.K % BK != 0 || (g.ktotal != 0 && g.ktotal % BK != 0);
-    if (tail) hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, true>), dim3((unsigned)blocks), dim3(1024), 0, s, g);
-    else hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, false>), dim3((unsigned)blocks), dim3(1024), 0, s, g);
+    const dim3 grid((unsigned)blocks), block(1024);
+    if (g.M % 256 != 0 || g.N % 256 != 0) {
+        // lds_tile_depth gives ragged outputs depth 16 only.
+        if constexpr (BK == 16) {
+            if (tail) hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, true, true>), grid, block, 0, s, g);
+            else hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, false, true>), grid, block, 0, s, g);
+        } else {
+            return set_error(TRS_E_INVALID_ARGUMENT, "ragged gemm tile at depth %d", BK);
+        }
+    } else if (tail) {
+        hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, true, false>), grid, block, 0, s, g);
+    } else {
+        hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, false, false>), grid, block, 0, s, g);
+    }
     TRS_LAUNCH_CHECK("gemm kernel launch");
     return TRS_OK;
 }
@@ -939,17 +987,15 @@ int launch_lds_layout(const GemmArgs &g, int bk, hipStream_t s) {
     return bk == 32 ? launch_lds_tile<32, TA, TB>(g, s) : launch_lds_tile<16, TA, TB>(g, s);
 }
 
-// The large tile in each layout; `full` when it divides M, N and K.  Tiles
-// whole in M and N (any K) load their slices straight into LDS where
-// lds_tile_depth allows.
+// The large tile in each layout; `full` when it divides M, N and K.  Slices
+// load straight into LDS where lds_tile_depth allows (any K, ragged M and N
+// too), else through registers.
 int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipStream_t s) {
-    if (g.M % 256 == 0 && g.N % 256 == 0) {
-        if (const int bk = lds_tile_depth(g, !a_plain)) {
-            if (a_plain && b_plain) return launch_lds_layout<false, false>(g, bk, s);
-            if (a_plain) return launch_lds_layout<false, true>(g, bk, s);
-            if (b_plain) return launch_lds_layout<true, false>(g, bk, s);
-            return launch_lds_layout<true, true>(g, bk, s);
-        }
+    if (const int bk = lds_tile_depth(g, !a_plain, !b_plain)) {
+        if (a_plain && b_plain) return launch_lds_layout<false, false>(g, bk, s);
+        if (a_plain) return launch_lds_layout<false, true>(g, bk, s);
+        if (b_plain) return launch_lds_layout<true, false>(g, bk, s);
+        return launch_lds_layout<true, true>(g, bk, s);
     }
     if (a_plain && b_plain)
         return full ? launch_tiled<LargeTiles, false, false>(g, true, s)
@@ -1030,7 +1076,7 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
     const auto large_depth = [&](int64_t k) -> int {
         GemmArgs t = g;
         t.K = k;
-        const int d = lds_tile_depth(t, !a_plain);
+        const int d = lds_tile_depth(t, !a_plain, !b_plain);
         return d ? d : (int)large_bk;
     };
     const int64_t large_tiles = ceil_div(M, L) * ceil_div(N, L) * batch;

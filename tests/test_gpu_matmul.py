@@ -393,6 +393,8 @@ RAGGED_LARGE = [
     ((4096 + 31, 129, 4096), 0, (256, 256, 16, 1, 256)),   # a 31-row rim, full-width tile
     ((4096, 77, 4096 + 5), 0, (256, 256, 16, 1, 256)),     # a 5-column rim
     ((4352 + 3, 65, 4096 + 32), 0, (256, 256, 16, 1, 272)),  # both rims, 17 x 16 main tiles
+    ((4094, 100, 4093), 0, (256, 256, 16, 1, 256)),     # edge tiles 254 x 253: straddling chunks
+    ((3841, 64, 3842), 0, (256, 256, 16, 1, 256)),      # edge tiles 1 x 2: k-row operands through registers
 ]
 
 
@@ -417,6 +419,41 @@ def test_ragged_large_tile_and_rims_exact_on_small_integers(mkn, batch, plan, ta
     got = U.matmul(sa, *la, sb, *lb).reshape(nb, m, n)
     want = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("m,k,n,batch", [(1001, 300, 1003, 16), (1002, 77, 1000, 16), (4094, 100, 4093, 0)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_ragged_large_tile_bits_match_the_padded_product(m, k, n, batch, ta, tb):
+    """The 256x256 tile on ragged M and N (edge tiles clamp their rows, move
+    straddling chunks, and mask their stores) gives every element the bits it
+    has in the product of the operands zero-padded to whole tiles: the same
+    lane computes it over the same k steps.  Edge tiles of 233, 234 and 254
+    rows and 235, 232 and 253 columns cover every straddle (v % 4 = 0..3), in
+    all four layouts, with normal inputs and a partial last slice."""
+    if _cu_count() != 256:
+        pytest.skip("the ragged shapes take the 256x256 tile on a 256-CU device")
+    rng = np.random.default_rng(m + 5 * k + 11 * n + 2 * ta + tb)
+    nb = max(batch, 1)
+    mp, np_ = -(-m // 256) * 256, -(-n // 256) * 256
+    a = np.zeros((nb, mp, k), np.float32)
+    b = np.zeros((nb, k, np_), np.float32)
+    a[:, :m] = rng.standard_normal((nb, m, k)).astype(np.float32)
+    b[:, :, :n] = rng.standard_normal((nb, k, n)).astype(np.float32)
+
+    def run(mm, nn):
+        aa, bb = np.ascontiguousarray(a[:, :mm]), np.ascontiguousarray(b[:, :, :nn])
+        sa = (np.ascontiguousarray(aa.transpose(0, 2, 1)) if ta else aa).ravel()
+        sb = (np.ascontiguousarray(bb.transpose(0, 2, 1)) if tb else bb).ravel()
+        ast, bst = ((1, mm) if ta else (k, 1)), ((1, k) if tb else (nn, 1))
+        if batch:
+            la, lb = ((batch, mm, k), (mm * k,) + ast, 0), ((batch, k, nn), (k * nn,) + bst, 0)
+        else:
+            la, lb = ((mm, k), ast, 0), ((k, nn), bst, 0)
+            assert _plan(mm, k, nn, ta, tb) == (256, 256, 16, 1, 256)
+        return U.matmul(sa, *la, sb, *lb).reshape(nb, mm, nn)
+
+    got, padded = run(m, n), run(mp, np_)
+    assert np.array_equal(got.view(np.uint32), padded[:, :m, :n].view(np.uint32))
 
 
 @pytest.mark.parametrize("s", [4095, 4097])
