@@ -58,6 +58,11 @@ struct GemmArgs {
     int64_t ktotal;
     int32_t tiles_m, tiles_n;
     int32_t xcd_remap;
+    // Stream-K (gemm_f32_mfma_lds_sk and its fix-up pass): blocks, slices
+    // per tile, (tile, slice) units, and the workspace of two partial tiles
+    // per block.
+    int64_t sk_blocks, sk_q, sk_units;
+    float *sk_ws;
 };
 
 constexpr int kGroupM = 8;
@@ -373,18 +378,15 @@ __global__ void __launch_bounds__(WGM *WGN * 64, MINB) gemm_f32_mfma(GemmArgs ar
 // ends inside a slice ends with a partial slice loaded through registers),
 // row offsets within 2^31 bytes.
 //
-// Ragged M or N (the EDGE form): a tile reaching past the matrix keeps its
-// loads inside it and its LDS layout unchanged.
-//   - An operand read along k clamps its rows past the edge to the last row.
-//   - An operand of k rows (its 256 columns contiguous) with v < 256 valid
-//     columns points each chunk past v at the tile's first chunk.  A chunk
-//     that straddles v (v not a multiple of 4) is read from v - 4 instead,
-//     so that its valid columns c land at c + d, d = 4 - v % 4, and the
-//     fragment reads of those columns add d.  The host requires v >= 4.
-//   - Whatever lands in the rows or columns past the edge only feeds outputs
-//     past it, which are not stored.
-// The interior tiles of a ragged product run the same code with nothing
-// clamped and d = 0.
+// Ragged M or N (the EDGE form, M and N at least 256): the last tile row
+// and column are moved back to end at the matrix's edge (rows M - 256 .. M,
+// columns N - 256 .. N), so that every tile is whole and runs the same loads
+// and loop; a moved tile stores only the outputs past the tile before it
+// (those of its own row and column index).  Each output has one tile that
+// stores it, with the k steps of any other tile, so the result bits are
+// those of the zero-padded product.  (Clamping the edge tiles' loads
+// instead took a per-lane shift of the chunks that straddle the edge, which
+// cost the stream-K form registers or each slice an LDS round trip.)
 //
 // LDS layouts, per operand and buffer:
 //   - a tile read along k (A not transposed, B transposed): 256 rows of BK
@@ -414,24 +416,20 @@ struct LdsOperand {
     uint32_t voff[kSegs], seg[kSegs];
     int k0[kSegs];  // the slice k of this lane's first float in each segment
 
-    // ld: the operand's row stride (elements).  valid: the tile's rows (read
-    // along k) or columns (k rows) inside the matrix, 4..256.
-    __device__ __forceinline__ void plan(int64_t ld, int lane, int wave, int valid = 256) {
+    // ld: the operand's row stride (elements).
+    __device__ __forceinline__ void plan(int64_t ld, int lane, int wave) {
 #pragma unroll
         for (int q = 0; q < kSegs; q++) {
             const int sg = wave + 16 * q;
             if constexpr (KROWS) {
-                int col = 4 * lane;
-                if (col + 4 > valid) col = col < valid ? valid - 4 : 0;
-                voff[q] = (uint32_t)((sg * ld + col) * 4);
+                voff[q] = (uint32_t)((sg * ld + 4 * lane) * 4);
                 seg[q] = sg * kLdsRowPitch * 4;
                 k0[q] = sg;
             } else {
                 constexpr int kChunks = BK / 4, kRowsPerSeg = 256 / BK;
-                // Tile row r's slot holds chunk c of matrix row min(r, valid - 1).
                 const int r = sg * kRowsPerSeg + lane / kChunks;
                 const int c = (lane % kChunks) ^ lds_swizzle<BK>(r);
-                voff[q] = (uint32_t)((std::min(r, valid - 1) * ld + 4 * c) * 4);
+                voff[q] = (uint32_t)((r * ld + 4 * c) * 4);
                 seg[q] = sg * 1024;
                 k0[q] = 4 * c;
             }
@@ -470,17 +468,14 @@ struct LdsOperand {
 // runs 0.925-0.934 of the FP32 MFMA peak with A not transposed, against
 // 0.919-0.924 at 16; with A transposed 16 is better (0.909-0.913 against
 // 0.904-0.911), and so it is at K = 1024 (0.889 against 0.864).  Ragged M
-// or N run at 16 (the EDGE form), where each k-row operand's edge tile has
-// at least 4 valid columns (M or N not 1-3 past a multiple of 256).
-inline int lds_tile_depth(const GemmArgs &g, bool a_trans, bool b_trans) {
+// or N (the EDGE form) need M and N of at least 256.
+inline int lds_tile_depth(const GemmArgs &g, bool a_trans) {
     const bool aligned = (uintptr_t)g.a % 4 == 0 && (uintptr_t)g.b % 4 == 0;
     const bool fits = g.lda >= 0 && g.ldb >= 0 && 256 * g.lda * 4 < ((int64_t)1 << 31) &&
                       256 * g.ldb * 4 < ((int64_t)1 << 31);
     if (!aligned || !fits) return 0;
-    if (g.M % 256 != 0 || g.N % 256 != 0) {
-        const auto edge_ok = [](int64_t d) { return d % 256 == 0 || d % 256 >= 4; };
-        return (a_trans && !edge_ok(g.M)) || (!b_trans && !edge_ok(g.N)) ? 0 : 16;
-    }
+    // Ragged M or N: the edge tiles move back inside the matrix.
+    if ((g.M % 256 != 0 || g.N % 256 != 0) && (g.M < 256 || g.N < 256)) return 0;
     // Depth 32 only where every product's k is whole slices of 32: where k
     // ends inside a slice, the last slice is padded with zeros to 16, as in
     // the register-staged kernel, so that the steps (and any -0.0 sum) match.
@@ -488,61 +483,90 @@ inline int lds_tile_depth(const GemmArgs &g, bool a_trans, bool b_trans) {
     return (!a_trans && whole32 && g.K >= 2048) ? 32 : 16;
 }
 
+// Tile t of a launch (t over batch * tiles_m * tiles_n): tiles in groups of
+// kGroupM tile rows, the group's tiles taken down its columns.
+// min by value: std::min of a kernel argument and a temporary returns a
+// reference the compiler may have to keep in scratch memory.
+__device__ __forceinline__ int64_t imin(int64_t a, int64_t b) { return a < b ? a : b; }
+
+struct TileCoord {
+    int64_t batch, m, n;
+};
+__device__ __forceinline__ TileCoord decode_tile(const GemmArgs &args, int64_t t) {
+    const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
+    TileCoord c;
+    c.batch = t / tiles;
+    t -= c.batch * tiles;
+    const int64_t group_span = (int64_t)kGroupM * args.tiles_n;
+    const int64_t group = t / group_span;
+    const int64_t first_m = group * kGroupM;
+    const int64_t gm = imin(args.tiles_m - first_m, kGroupM);
+    const int64_t within = t - group * group_span;
+    c.m = first_m + within % gm;
+    c.n = within / gm;
+    return c;
+}
+
+// decode_tile in 32 bits (t and the tile counts below 2^31): the stream-K
+// loop decodes a tile per segment, and the 64-bit divisions' loop-invariant
+// parts, kept in VGPRs across segments, spilled.
+__device__ __forceinline__ TileCoord decode_tile32(const GemmArgs &args, uint32_t t) {
+    const uint32_t tm = (uint32_t)args.tiles_m, tn = (uint32_t)args.tiles_n, tiles = tm * tn;
+    TileCoord c;
+    const uint32_t batch = t / tiles;
+    t -= batch * tiles;
+    const uint32_t group_span = (uint32_t)kGroupM * tn;
+    const uint32_t group = t / group_span;
+    const uint32_t first_m = group * kGroupM;
+    const uint32_t gm = tm - first_m < (uint32_t)kGroupM ? tm - first_m : (uint32_t)kGroupM;
+    const uint32_t within = t - group * group_span;
+    c.batch = batch;
+    c.m = first_m + within % gm;
+    c.n = within / gm;
+    return c;
+}
+
+constexpr int64_t kLargeTileFloats = 256 * 256;
+
+// One 256x256 tile of the LDS-loading kernel over its slices [q0, q1) (q1
+// past the last slice: to the end).  Stores the tile into C (masked on the
+// edge, EDGE), or with `ws` set its partial sums into ws[r * 256 + c], all
+// 256 x 256 of them.  tid: threadIdx.x (the stream-K loop passes a copy the
+// compiler cannot see through, so that the lane values derived from it are
+// not kept live across segments: they spilled there).
+//
 // TAIL: some product's k ends inside a slice (compiled apart: the branch in
 // the slice loop cost 1% at 4096^3 and on the MLP step).  EDGE: M or N is
 // not a multiple of 256 (compiled apart too, so that whole-tile products
 // keep the loop they had).
 template <int BK, bool TA, bool TB, bool TAIL, bool EDGE>
-__global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
+__device__ __forceinline__ void lds_tile_slices(const GemmArgs &args, float *lds, TileCoord tc, int64_t q0,
+                                                int64_t q1, float *ws, unsigned tid) {
     constexpr int BM = 256, BN = 256, WGN = 4, WM = 64, WN = 64, TM = WM / 16, TN = WN / 16;
     using LA = LdsOperand<BK, TA>;
     using LB = LdsOperand<BK, !TB>;
     constexpr int ASIZE = LA::kFloats, BSIZE = LB::kFloats;
-    __shared__ __attribute__((aligned(16))) float lds[2 * (ASIZE + BSIZE)];
 
-    const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
-    int64_t bid = blockIdx.x;
-    if (args.xcd_remap) {
-        const int64_t total = tiles * args.batch;
-        const int64_t per_xcd = total / kXcds;
-        bid = (bid % kXcds) * per_xcd + bid / kXcds;
-    }
-    const int64_t batch_idx = bid / tiles;
-    int64_t t = bid - batch_idx * tiles;
-    const int64_t group_span = (int64_t)kGroupM * args.tiles_n;
-    const int64_t group = t / group_span;
-    const int64_t first_m = group * kGroupM;
-    const int64_t gm = std::min<int64_t>(args.tiles_m - first_m, kGroupM);
-    const int64_t within = t - group * group_span;
-    const int64_t tile_m = first_m + within % gm;
-    const int64_t tile_n = within / gm;
-
-    const int64_t Kb = args.ktotal ? std::min<int64_t>(args.K, args.ktotal - batch_idx * args.K) : args.K;
+    const int64_t batch_idx = tc.batch;
+    const int64_t Kb = args.ktotal ? imin(args.K, args.ktotal - batch_idx * args.K) : args.K;
     const float *A = args.a + batch_idx * args.bsa;
     const float *B = args.b + batch_idx * args.bsb;
     float *Cp = args.c + batch_idx * args.bsc;
-    const int64_t m0 = tile_m * BM, n0 = tile_n * BN;
+    // The tile's own first row and column, and its origin: on the edge,
+    // moved back to end at the matrix's (EDGE: M, N >= 256).
+    const int64_t own_m = tc.m * BM, own_n = tc.n * BN;
+    const int64_t m0 = EDGE ? imin(own_m, args.M - BM) : own_m;
+    const int64_t n0 = EDGE ? imin(own_n, args.N - BN) : own_n;
 
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
     const int fi = lane & 15, fk = lane >> 4;
 
-    // The tile's rows and columns inside C (256 but on the edge tiles).
-    const int vm = EDGE ? (int)std::min<int64_t>(BM, args.M - m0) : BM;
-    const int vn = EDGE ? (int)std::min<int64_t>(BN, args.N - n0) : BN;
     LA la;
     LB lb;
-    la.plan(args.lda, lane, wave, vm);
-    lb.plan(args.ldb, lane, wave, vn);
-    // Fragment columns of a k-row operand that a straddling chunk moved
-    // (see above): column c in [v & ~3, v) is read at c + 4 - v % 4.
-    const auto moved = [](int c, int v) { return (v & 3) && c >= (v & ~3) && c < v ? 4 - (v & 3) : 0; };
-    int adja[TM], adjb[TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++) adja[i] = EDGE && TA ? moved(wm0 + i * 16 + fi, vm) : 0;
-#pragma unroll
-    for (int j = 0; j < TN; j++) adjb[j] = EDGE && !TB ? moved(wn0 + j * 16 + fi, vn) : 0;
+    la.plan(args.lda, lane, wave);
+    lb.plan(args.ldb, lane, wave);
     // Slice s starts at abase + s * astep and bbase + s * bstep.
     const float *abase = TA ? A + m0 : A + m0 * args.lda;
     const float *bbase = TB ? B + n0 * args.ldb : B + n0;
@@ -557,27 +581,9 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
 
     // Row wm0 + 16i + fi (or wn0 + 16j + fi) has the swizzle of fi.
     const int aswz = lds_swizzle<BK>(fi), bswz = aswz;
-    // Whole slices load straight into LDS; a k that ends inside a slice
-    // ends with one more, partial slice loaded through registers.
-    const int64_t kwhole = Kb / BK;
-    const int tail = TAIL ? (int)(Kb - kwhole * BK) : 0;
-    const int64_t kslices = kwhole + (tail ? 1 : 0);
-    auto fetch = [&](int64_t s, float *dst) {
-        if (!TAIL || s < kwhole) {
-            la.load(abase + s * astep, dst);
-            lb.load(bbase + s * bstep, dst + ASIZE);
-        } else {
-            la.load_tail(abase + s * astep, dst, tail, lane);
-            lb.load_tail(bbase + s * bstep, dst + ASIZE, tail, lane);
-        }
-    };
-    fetch(0, lds);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int64_t s = 0; s < kslices; s++) {
-        const float *As = lds + (s & 1) * (ASIZE + BSIZE);
+    // Slices of BK MFMA steps from one LDS buffer.
+    auto slice_mfma = [&](const float *As) {
         const float *Bs = As + ASIZE;
-        if (s + 1 < kslices) fetch(s + 1, lds + ((s + 1) & 1) * (ASIZE + BSIZE));
 #pragma unroll 1
         for (int kg = 0; kg < BK; kg += 16) {
             const int k4 = kg + 4 * fk;
@@ -598,10 +604,10 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
                 float af[TM], bf[TN];
 #pragma unroll
                 for (int i = 0; i < TM; i++)
-                    af[i] = TA ? As[(k4 + e) * kLdsRowPitch + wm0 + i * 16 + fi + adja[i]] : a4[i][e];
+                    af[i] = TA ? As[(k4 + e) * kLdsRowPitch + wm0 + i * 16 + fi] : a4[i][e];
 #pragma unroll
                 for (int j = 0; j < TN; j++)
-                    bf[j] = TB ? b4[j][e] : Bs[(k4 + e) * kLdsRowPitch + wn0 + j * 16 + fi + adjb[j]];
+                    bf[j] = TB ? b4[j][e] : Bs[(k4 + e) * kLdsRowPitch + wn0 + j * 16 + fi];
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -609,10 +615,50 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
         }
+    };
+    // Whole slices load straight into LDS, each prefetched during the one
+    // before.  A k that ends inside a slice ends with one more, partial
+    // slice, loaded through registers once the last whole slice is done
+    // (prefetched with the others, its loads' wait fell among the MFMAs:
+    // stream-K at 5000^3 ran 0.75 of peak against 0.84 at K = 4992).
+    const int64_t kwhole = Kb / BK;
+    const int tail = TAIL ? (int)(Kb - kwhole * BK) : 0;
+    const int64_t kend = imin(q1, kwhole + (tail ? 1 : 0));
+    const int64_t kmain = TAIL ? imin(kend, kwhole) : kend;
+    auto fetch = [&](int64_t s, float *dst) {
+        la.load(abase + s * astep, dst);
+        lb.load(bbase + s * bstep, dst + ASIZE);
+    };
+    auto fetch_tail = [&](float *dst) {
+        la.load_tail(abase + kwhole * astep, dst, tail, lane);
+        lb.load_tail(bbase + kwhole * bstep, dst + ASIZE, tail, lane);
+    };
+    if (TAIL && q0 == kwhole) fetch_tail(lds);
+    else fetch(q0, lds);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int64_t s = q0; s < kend; s++) {
+        const float *As = lds + ((s - q0) & 1) * (ASIZE + BSIZE);
+        float *next = lds + ((s - q0 + 1) & 1) * (ASIZE + BSIZE);
+        if (s + 1 < kmain) fetch(s + 1, next);
+        slice_mfma(As);
         __builtin_amdgcn_s_waitcnt(0);  // this slice's loads into the other buffer have landed
         __syncthreads();
+        if (TAIL && s + 1 == kwhole && s + 1 < kend) {
+            fetch_tail(next);
+            __syncthreads();
+        }
     }
 
+    if (ws) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) ws[(wm0 + i * 16 + 4 * fk + r) * 256 + wn0 + j * 16 + fi] = acc[i][j][r];
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++) {
 #pragma unroll
@@ -621,9 +667,89 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int64_t m = m0 + wm0 + i * 16 + 4 * fk + r;
-                if (!EDGE || (m < args.M && n < args.N)) Cp[m * args.ldc + n] = acc[i][j][r];
+                if (!EDGE || (m >= own_m && n >= own_n)) Cp[m * args.ldc + n] = acc[i][j][r];
             }
         }
+    }
+}
+
+template <int BK, bool TA, bool TB>
+constexpr int lds_tile_floats() {
+    return 2 * (LdsOperand<BK, TA>::kFloats + LdsOperand<BK, !TB>::kFloats);
+}
+
+// One block per tile.
+template <int BK, bool TA, bool TB, bool TAIL, bool EDGE>
+__global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds(GemmArgs args) {
+    __shared__ __attribute__((aligned(16))) float lds[lds_tile_floats<BK, TA, TB>()];
+    int64_t bid = blockIdx.x;
+    if (args.xcd_remap) {
+        const int64_t total = (int64_t)args.tiles_m * args.tiles_n * args.batch;
+        const int64_t per_xcd = total / kXcds;
+        bid = (bid % kXcds) * per_xcd + bid / kXcds;
+    }
+    lds_tile_slices<BK, TA, TB, TAIL, EDGE>(args, lds, decode_tile(args, bid), 0, INT64_MAX, nullptr, threadIdx.x);
+}
+
+// Stream-K: one persistent block per CU, block b taking the (tile, slice)
+// units [b*U/G, (b+1)*U/G) of the U = tiles * Q of the product (G blocks, Q
+// slices per tile, tile-major).  A tile whose units fall to one block is
+// stored into C; a block's first and last segments that cover only part of
+// a tile's slices go to its two workspace slots (slot 0 the first segment,
+// slot 1 the last), which gemm_streamk_fixup adds in k order.  No block waits
+// for another.  Logical block b runs as blockIdx (b % (G/8)) * 8 + b / (G/8),
+// so each XCD takes one contiguous eighth of the units.
+template <int BK, bool TA, bool TB, bool TAIL, bool EDGE>
+__global__ void __launch_bounds__(1024, 1) gemm_f32_mfma_lds_sk(GemmArgs args) {
+    __shared__ __attribute__((aligned(16))) float lds[lds_tile_floats<BK, TA, TB>()];
+    const int64_t G = args.sk_blocks, U = args.sk_units, Q = args.sk_q;
+    const int64_t b = args.xcd_remap ? (blockIdx.x % kXcds) * (G / kXcds) + blockIdx.x / kXcds : blockIdx.x;
+    const int64_t u0 = b * U / G, u1 = (b + 1) * U / G;
+    // Segment: slices [qb, qe) of tile t; the next starts the next tile.
+    int64_t t = u0 / Q, qb = u0 - t * Q;
+    for (int64_t u = u0; u < u1; t++, qb = 0) {
+        const int64_t qe = imin(Q, qb + (u1 - u));
+        float *ws = (qb == 0 && qe == Q) ? nullptr : args.sk_ws + (2 * b + (u == u0 ? 0 : 1)) * kLargeTileFloats;
+        unsigned tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        lds_tile_slices<BK, TA, TB, TAIL, EDGE>(args, lds, decode_tile32(args, (uint32_t)t), qb, qe, ws, tid);
+        u += qe - qb;
+    }
+}
+
+// The pieces of the tiles stream-K split between blocks, added in k order
+// (block order) into C.  Block (t, y) takes rows 16y..16y+15 of tile t; a
+// tile that one block ran whole was stored by it and is skipped.
+__global__ void __launch_bounds__(256) gemm_streamk_fixup(GemmArgs args) {
+    const int64_t G = args.sk_blocks, U = args.sk_units, Q = args.sk_q;
+    const int64_t t = blockIdx.x;
+    // The block whose units hold unit u: the largest b with b*U/G <= u.
+    const auto block_of = [&](int64_t u) { return imin(G - 1, ((u + 1) * G - 1) / U); };
+    const int64_t bf = block_of(t * Q), bl = block_of((t + 1) * Q - 1);
+    if (bf == bl) return;
+    const TileCoord tc = decode_tile32(args, (uint32_t)t);
+    float *Cp = args.c + tc.batch * args.bsc;
+    // The tile's origin, moved back on the edge as in lds_tile_slices, and
+    // the outputs it owns: rows and columns from its own index on.
+    const int64_t own_m = tc.m * 256, own_n = tc.n * 256;
+    const int64_t m0 = imin(own_m, args.M - 256), n0 = imin(own_n, args.N - 256);
+    const int r = (int)blockIdx.y * 16 + (int)(threadIdx.x >> 4);
+    const int64_t m = m0 + r;
+    if (m < own_m) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = 4 * ((int)(threadIdx.x & 15) + 16 * i);
+        vf4 v;
+        for (int64_t p = bf; p <= bl; p++) {
+            // Slot 0 when the tile holds block p's first unit, else slot 1.
+            const int64_t slot = p * U / G >= t * Q ? 0 : 1;
+            const vf4 x = *(const vf4 *)(args.sk_ws + (2 * p + slot) * kLargeTileFloats + r * 256 + c);
+            v = p == bf ? x : v + x;
+        }
+        const int64_t n = n0 + c;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (n + e >= own_n) Cp[m * args.ldc + n + e] = v[e];
     }
 }
 
@@ -957,28 +1083,45 @@ int launch_layout(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipS
     return launch_tiled<T, true, true>(g, full, s);
 }
 
+// The LDS-loading large tile: one block per tile, or with g.sk_ws set the
+// stream-K form (g.sk_blocks blocks) followed by its fix-up pass.
 template <int BK, bool TA, bool TB>
 int launch_lds_tile(GemmArgs g, hipStream_t s) {
     g.tiles_m = (int32_t)((g.M + 255) / 256);
     g.tiles_n = (int32_t)((g.N + 255) / 256);
-    const int64_t blocks = (int64_t)g.tiles_m * g.tiles_n * g.batch;
+    const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n * g.batch;
+    const bool sk = g.sk_ws != nullptr;
+    if (sk) {
+        g.sk_q = (g.K + BK - 1) / BK;
+        g.sk_units = tiles * g.sk_q;
+    }
+    const int64_t blocks = sk ? g.sk_blocks : tiles;
     g.xcd_remap = blocks % kXcds == 0 ? 1 : 0;
     const bool tail = g.K % BK != 0 || (g.ktotal != 0 && g.ktotal % BK != 0);
+    const bool edge = g.M % 256 != 0 || g.N % 256 != 0;
     const dim3 grid((unsigned)blocks), block(1024);
-    if (g.M % 256 != 0 || g.N % 256 != 0) {
-        // lds_tile_depth gives ragged outputs depth 16 only.
-        if constexpr (BK == 16) {
-            if (tail) hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, true, true>), grid, block, 0, s, g);
-            else hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, false, true>), grid, block, 0, s, g);
-        } else {
-            return set_error(TRS_E_INVALID_ARGUMENT, "ragged gemm tile at depth %d", BK);
-        }
+    auto go = [&]<bool TL, bool ED>() {
+        if (sk) hipLaunchKernelGGL((gemm_f32_mfma_lds_sk<BK, TA, TB, TL, ED>), grid, block, 0, s, g);
+        else hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, TL, ED>), grid, block, 0, s, g);
+    };
+    // lds_tile_depth gives depth 32 to whole slices only.
+    if constexpr (BK == 32) {
+        if (tail) return set_error(TRS_E_INVALID_ARGUMENT, "gemm tile depth 32 needs whole slices");
+        if (edge) go.template operator()<false, true>();
+        else go.template operator()<false, false>();
+    } else if (edge) {
+        if (tail) go.template operator()<true, true>();
+        else go.template operator()<false, true>();
     } else if (tail) {
-        hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, true, false>), grid, block, 0, s, g);
+        go.template operator()<true, false>();
     } else {
-        hipLaunchKernelGGL((gemm_f32_mfma_lds<BK, TA, TB, false, false>), grid, block, 0, s, g);
+        go.template operator()<false, false>();
     }
     TRS_LAUNCH_CHECK("gemm kernel launch");
+    if (sk) {
+        hipLaunchKernelGGL(gemm_streamk_fixup, dim3((unsigned)tiles, 16), dim3(256), 0, s, g);
+        TRS_LAUNCH_CHECK("stream-k fix-up launch");
+    }
     return TRS_OK;
 }
 
@@ -991,7 +1134,7 @@ int launch_lds_layout(const GemmArgs &g, int bk, hipStream_t s) {
 // load straight into LDS where lds_tile_depth allows (any K, ragged M and N
 // too), else through registers.
 int launch_large(const GemmArgs &g, bool a_plain, bool b_plain, bool full, hipStream_t s) {
-    if (const int bk = lds_tile_depth(g, !a_plain, !b_plain)) {
+    if (const int bk = lds_tile_depth(g, !a_plain)) {
         if (a_plain && b_plain) return launch_lds_layout<false, false>(g, bk, s);
         if (a_plain) return launch_lds_layout<false, true>(g, bk, s);
         if (b_plain) return launch_lds_layout<true, false>(g, bk, s);
@@ -1041,16 +1184,18 @@ constexpr double kSmallPairOverLarge = 0.575;
 //     64x128 divides the shape (76% against 69% of peak measured at
 //     4096x1024x8192), else 128x128 (full or edge-guarded);
 //   - a single matrix whose tile gives at most one block per CU splits K
-//     over that tile (above).
-enum class GemmKind { Strided, Large, SplitK, Medium, Small };
+//     over that tile (above);
+//   - then stream-K on the 256x256 tile (below) replaces the plan where it
+//     is estimated at least kStreamKGain faster.
+enum class GemmKind { Strided, Large, SplitK, Medium, Small, StreamK };
 struct GemmPlan {
     GemmKind kind = GemmKind::Strided;
     int bm = 0, bn = 0, bk = 0;
     int64_t splits = 1;
     int64_t blocks = 0;
     bool full = false;
-    // SplitK only: the tile each slice runs on, the k per slice, and the
-    // unsplit plan, run when no workspace can be allocated.
+    // SplitK only: the tile each slice runs on and the k per slice.
+    // SplitK and StreamK: the plan run when no workspace can be allocated.
     GemmKind split_tile = GemmKind::Large;
     int64_t ks = 0;
     GemmKind fallback = GemmKind::Small;
@@ -1060,7 +1205,7 @@ struct GemmPlan {
     int64_t main_m = 0, main_n = 0;
 };
 
-GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, bool b_trans, int cu_count) {
+GemmPlan plan_gemm_tiles(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, bool b_trans, int cu_count) {
     GemmPlan p;
     const int64_t M = g.M, N = g.N, K = g.K, batch = g.batch;
     if (!(a_plain || a_trans) || !(b_plain || b_trans)) {
@@ -1071,13 +1216,15 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
     constexpr int64_t L = LargeTiles::BM;  // 256, both dims
     const int64_t large_bk = (a_plain && b_plain) ? LargeTiles::BK : LargeTilesK16::BK;
     const auto ceil_div = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
-    // The depth a whole-tile product of depth k runs at: the LDS-loading
-    // kernel's where its load offsets fit, else the register-staged tile's.
-    const auto large_depth = [&](int64_t k) -> int {
+    // The depth the large tile runs an mm x nn product of depth k at (ktotal:
+    // the full depth of a split K, else 0): the LDS-loading kernel's where
+    // it applies, else the register-staged tile's (BK = 32 only for whole
+    // tiles and slices).
+    const auto large_depth = [&](int64_t mm, int64_t nn, int64_t k, int64_t ktotal, bool full) -> int {
         GemmArgs t = g;
-        t.K = k;
-        const int d = lds_tile_depth(t, !a_plain, !b_plain);
-        return d ? d : (int)large_bk;
+        t.M = mm, t.N = nn, t.K = k, t.ktotal = ktotal;
+        const int d = lds_tile_depth(t, !a_plain);
+        return d ? d : full ? (int)large_bk : LargeTilesK16::BK;
     };
     const int64_t large_tiles = ceil_div(M, L) * ceil_div(N, L) * batch;
     const int64_t small_tiles = ceil_div(M, 128) * ceil_div(N, 128) * batch;
@@ -1087,7 +1234,7 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
         p.bm = L, p.bn = L;
         p.blocks = tiles;
         p.full = mm % L == 0 && nn % L == 0 && K % large_bk == 0;
-        p.bk = p.full ? large_depth(K) : LargeTilesK16::BK;
+        p.bk = large_depth(mm, nn, K, 0, p.full);
     };
     if (large_div && large_tiles >= cu_count) {
         use_large(M, N, large_tiles);
@@ -1142,7 +1289,7 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
             p.ks = ks;
             p.blocks = large_tiles * p.splits;
             p.full = large_div && K % ks == 0;
-            p.bk = p.full ? large_depth(ks) : LargeTilesK16::BK;
+            p.bk = large_depth(M, N, ks, K, p.full);
             return p;
         }
     }
@@ -1165,6 +1312,76 @@ GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, 
         }
     }
     return p;
+}
+
+// Stream-K on the LDS-loading 256x256 tile: one block per CU, each taking
+// an equal share of the product's (tile, slice) units, then one pass adding
+// the pieces of the tiles split between blocks (gemm_f32_mfma_lds_sk).  It
+// removes the idle CUs of a last, partial round of tiles (6144^3: 576
+// tiles, three rounds of 256 for 2.25 rounds of work) and of outputs with
+// fewer tiles than CUs that no power-of-two K split fills (3072^3: 144).
+//
+// The choice compares estimated times in k steps of one 256x256 tile on one
+// CU (0.21 us at the measured 0.92 of peak): the plan above by its rounds of
+// blocks, and stream-K by its even share plus kStreamKCost for the pieces'
+// extra traffic (two 256 KiB pieces per split tile written, read back and
+// added, at most one split tile per block), the fix-up launch and a block's
+// extra segment starts.  The 128x128 and 64x128 tiles cost 0.30 and 0.175
+// of a large k step per k (their measured rates and areas).  Stream-K needs
+// tiles at least 85% covered, no K split of its own (ktotal), and at least
+// kStreamKMinWork k steps per CU.
+constexpr double kStreamKCost = 150.0;
+constexpr double kStreamKMinWork = 192.0;
+constexpr double kStreamKGain = 1.15;
+constexpr double kSmallStep = 0.30, kMediumStep = 0.175;
+
+double plan_k_steps(const GemmPlan &p, int64_t K, int cu_count) {
+    const auto rounds = [&](int64_t blocks) { return (double)((blocks + cu_count - 1) / cu_count); };
+    switch (p.kind) {
+    case GemmKind::Large: return rounds(p.blocks) * (double)K;
+    case GemmKind::SplitK: {
+        const double step = p.split_tile == GemmKind::Large ? 1.0 : p.split_tile == GemmKind::Medium ? kMediumStep : kSmallStep;
+        return rounds(p.blocks) * (double)p.ks * step + 50.0;
+    }
+    case GemmKind::Medium: return rounds(p.blocks) * (double)K * kMediumStep;
+    case GemmKind::Small: return rounds(p.blocks) * (double)K * kSmallStep;
+    default: return 0.0;
+    }
+}
+
+GemmPlan plan_gemm(const GemmArgs &g, bool a_plain, bool a_trans, bool b_plain, bool b_trans, int cu_count) {
+    GemmPlan p = plan_gemm_tiles(g, a_plain, a_trans, b_plain, b_trans, cu_count);
+    if (p.kind == GemmKind::Strided || p.main_m || g.ktotal) return p;
+    const int bk = lds_tile_depth(g, !a_plain);
+    if (!bk) return p;
+    const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
+    if ((double)(g.M * g.N * g.batch) < 0.85 * (double)(tiles * kLargeTileFloats)) return p;
+    const double work = (double)tiles * (double)g.K / cu_count;
+    if (work < kStreamKMinWork || plan_k_steps(p, g.K, cu_count) < kStreamKGain * (work + kStreamKCost)) return p;
+    GemmPlan sk;
+    sk.kind = GemmKind::StreamK;
+    sk.bm = 256, sk.bn = 256, sk.bk = bk;
+    sk.splits = 0;
+    sk.blocks = cu_count;
+    sk.fallback = p.kind == GemmKind::SplitK ? p.fallback : p.kind;
+    sk.fallback_full = p.kind == GemmKind::SplitK ? p.fallback_full : p.full;
+    return sk;
+}
+
+// Runs a stream-K plan; TRS_E_ALLOCATION_FAILED, with nothing launched, when
+// the workspace (two partial tiles per block, 512 KiB per CU) cannot be had.
+int launch_stream_k(const GemmPlan &p, GemmArgs g, bool a_plain, bool b_plain, int cu_count, hipStream_t s) {
+    void *ws = nullptr;
+    int rc = trs_alloc((size_t)(2 * (int64_t)cu_count * kLargeTileFloats) * sizeof(float), &ws);
+    if (rc) return rc;
+    g.sk_blocks = cu_count;
+    g.sk_ws = (float *)ws;
+    if (a_plain && b_plain) rc = launch_lds_layout<false, false>(g, p.bk, s);
+    else if (a_plain) rc = launch_lds_layout<false, true>(g, p.bk, s);
+    else if (b_plain) rc = launch_lds_layout<true, false>(g, p.bk, s);
+    else rc = launch_lds_layout<true, true>(g, p.bk, s);
+    const int frc = trs_free(ws);
+    return rc ? rc : frc;
 }
 
 // Runs a split plan; returns TRS_E_ALLOCATION_FAILED without launching
@@ -1410,6 +1627,15 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
                            g.N, g.K, st.sam, st.sak, st.sbk, st.sbn, g.bsa, g.bsb, g.batch);
         TRS_LAUNCH_CHECK("strided gemm launch");
         return TRS_OK;
+    }
+    if (p.kind == GemmKind::StreamK) {
+        rc = launch_stream_k(p, g, st.a_plain, st.b_plain, dev->cu_count, dev->stream);
+        if (rc != TRS_E_ALLOCATION_FAILED) return rc;
+        // No workspace: run the plan stream-K replaced, unsplit.
+        GemmPlan fb;
+        fb.kind = p.fallback;
+        fb.full = p.fallback_full;
+        return run_unsplit(fb, g, st.a_plain, st.b_plain, dev->stream);
     }
     if (p.kind == GemmKind::SplitK) {
         rc = launch_split_k(p, g, st.a_plain, st.b_plain, st.sak, st.sbk, dev->cu_count, dev->stream);

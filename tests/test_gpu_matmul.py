@@ -210,7 +210,7 @@ def _plan(m, k, n, ta=False, tb=False):
 # Outputs with fewer 256x256 tiles than CUs and a long K.  On a 256-CU device
 # K is split into S slices (the value given here) summed in slice order: S
 # slices fill half the CUs, or give as many blocks as the unsplit tile.
-SPLIT_K = [(256, 8192, 256, 8), (1024, 8192, 1024, 8), (4096, 8192, 1024, 4), (8192, 4096, 1024, 2)]
+SPLIT_K = [(256, 8192, 256, 8), (1024, 8192, 2048, 8), (4096, 8192, 1024, 4), (8192, 4096, 1024, 2)]
 
 
 def _expect_split(m, k, n, s, ta, tb):
@@ -381,8 +381,8 @@ def test_empty_dimensions_on_the_device():
     assert (no_inner.numpy().view(np.uint32) == 0).all()
 
 
-# Ragged products on the 256x256 tile (BK=16 form, edge tiles bounds-checked,
-# interior tiles loading dword-aligned float4 from rows of any length), and
+# Ragged products on the 256x256 tile (edge tiles moved back inside the
+# matrix, slices loaded straight into LDS from rows of any length), and
 # single matrices that exceed a multiple of 256 by at most 32 rows or columns,
 # whose rims run as skinny products.  Plans are those of a 256-CU device.
 RAGGED_LARGE = [
@@ -394,7 +394,7 @@ RAGGED_LARGE = [
     ((4096, 77, 4096 + 5), 0, (256, 256, 16, 1, 256)),     # a 5-column rim
     ((4352 + 3, 65, 4096 + 32), 0, (256, 256, 16, 1, 272)),  # both rims, 17 x 16 main tiles
     ((4094, 100, 4093), 0, (256, 256, 16, 1, 256)),     # edge tiles 254 x 253: straddling chunks
-    ((3841, 64, 3842), 0, (256, 256, 16, 1, 256)),      # edge tiles 1 x 2: k-row operands through registers
+    ((3841, 64, 3842), 0, (256, 256, 16, 1, 256)),      # edge tiles of 1 row and 2 columns, moved back 255 and 254
 ]
 
 
@@ -424,12 +424,13 @@ def test_ragged_large_tile_and_rims_exact_on_small_integers(mkn, batch, plan, ta
 @pytest.mark.parametrize("m,k,n,batch", [(1001, 300, 1003, 16), (1002, 77, 1000, 16), (4094, 100, 4093, 0)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
 def test_ragged_large_tile_bits_match_the_padded_product(m, k, n, batch, ta, tb):
-    """The 256x256 tile on ragged M and N (edge tiles clamp their rows, move
-    straddling chunks, and mask their stores) gives every element the bits it
-    has in the product of the operands zero-padded to whole tiles: the same
-    lane computes it over the same k steps.  Edge tiles of 233, 234 and 254
-    rows and 235, 232 and 253 columns cover every straddle (v % 4 = 0..3), in
-    all four layouts, with normal inputs and a partial last slice."""
+    """The 256x256 tile on ragged M and N (the last tile row and column moved
+    back to end at the matrix's edge, each storing only the outputs past the
+    tile before it) gives every element the bits it has in the product of
+    the operands zero-padded to whole tiles: the same k steps.  Edge tiles of
+    233, 234 and 254 rows and 235, 232 and 253 columns (every residue mod 4,
+    so every float offset of the moved tiles' rows), in all four layouts,
+    with normal inputs and a partial last slice."""
     if _cu_count() != 256:
         pytest.skip("the ragged shapes take the 256x256 tile on a 256-CU device")
     rng = np.random.default_rng(m + 5 * k + 11 * n + 2 * ta + tb)
@@ -454,6 +455,57 @@ def test_ragged_large_tile_bits_match_the_padded_product(m, k, n, batch, ta, tb)
 
     got, padded = run(m, n), run(mp, np_)
     assert np.array_equal(got.view(np.uint32), padded[:, :m, :n].view(np.uint32))
+
+
+# Stream-K on the 256x256 tile: one block per CU takes an equal share of the
+# product's (tile, k-slice) units, and a second pass adds, in k order, the
+# pieces of the tiles split between blocks.  Plans of a 256-CU device
+# (splits 0 = stream-K, 256 blocks).
+STREAM_K = [
+    ((3072, 1024, 3072), 0, 16),   # 144 tiles for 256 CUs: two or three pieces per tile
+    ((512, 4096, 4096), 0, 32),    # 32 tiles, eight pieces each
+    ((2999, 1000, 2901), 0, 16),   # edge tiles 183 x 85 (straddling chunks), a K tail of 8
+    ((1000, 2048, 1000), 6, 16),   # a batch of ragged outputs, 96 tiles
+]
+
+
+@pytest.mark.parametrize("mkn,batch,bk", STREAM_K)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_stream_k_exact_on_small_integers(mkn, batch, bk, ta, tb):
+    m, k, n = mkn
+    if _cu_count() != 256:
+        pytest.skip("plan expectations are those of a 256-CU device")
+    rng = np.random.default_rng(m + 3 * k + 7 * n + batch + 2 * ta + tb)
+    nb = max(batch, 1)
+    a = rng.integers(-3, 4, (nb, m, k)).astype(np.float32)
+    b = rng.integers(-3, 4, (nb, k, n)).astype(np.float32)
+    sa = (np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a).ravel()
+    sb = (np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b).ravel()
+    ast, bst = ((1, m) if ta else (k, 1)), ((1, k) if tb else (n, 1))
+    if batch:
+        la, lb = ((batch, m, k), (m * k,) + ast, 0), ((batch, k, n), (k * n,) + bst, 0)
+    else:
+        la, lb = ((m, k), ast, 0), ((k, n), bst, 0)
+        # depth 32 only with A not transposed
+        assert _plan(m, k, n, ta, tb) == (256, 256, 16 if ta else bk, 0, 256)
+    got = U.matmul(sa, *la, sb, *lb).reshape(nb, m, n)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_stream_k_normal_inputs_within_tolerance_and_deterministic():
+    """A ragged stream-K product with N(0, 1/sqrt(K)) entries: every element
+    against the reference-order oracle within 1e-5*sqrt(K)*(|A||B|), and the
+    same bits from a second call."""
+    m, k, n = 2999, 1000, 2901
+    rng = np.random.default_rng(77)
+    a = (rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
+    b = (rng.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
+    got = U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0)
+    again = U.matmul(a.ravel(), (m, k), (k, 1), 0, b.ravel(), (k, n), (n, 1), 0)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    want = O.matmul_threads(a, b, threads=_oracle_threads())
+    _check_tol(got.reshape(m, n), want.reshape(m, n), _abs_bound(a, b), k)
 
 
 @pytest.mark.parametrize("s", [4095, 4097])
@@ -507,9 +559,9 @@ def test_fallbacks_when_no_workspace_can_be_allocated():
     want = O.matmul(ab.ravel(), *la, bb.ravel(), *lb).reshape(m, n)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     cases = [(1024, 8192, 1024, False, False), (1000, 1000, 1000, False, False), (1, 4096, 4096, False, False),
-             (32, 4096, 4096, False, True), (4097, 300, 4097, False, False)]
+             (32, 4096, 4096, False, True), (4097, 300, 4097, False, False), (2999, 1000, 2901, False, False)]
     for m, k, n, ta, tb in cases:
-        assert _plan(m, k, n, ta, tb)[3] > 1 or m == 4097, (m, k, n)
+        assert _plan(m, k, n, ta, tb)[3] != 1 or m == 4097, (m, k, n)
         a = rng.integers(-3, 4, (m, k)).astype(np.float32)
         b = rng.integers(-3, 4, (k, n)).astype(np.float32)
         sa, la, sb, lb = _layouts(a, b, ta, tb)
