@@ -250,7 +250,15 @@ int trs_accumulate_f32(float *dst, const float *src, size_t n);
  * partial products then take S*M*N floats of device memory from the
  * library's block cache for the duration of the call (at most 65,536
  * floats per CU: 64 MiB on a 256-CU device).  If that memory cannot be
- * allocated the call runs the unsplit tile instead.  An output with at most 32 rows or columns (a matrix-vector
+ * allocated the call runs the unsplit tile instead.  A product whose
+ * 256x256 tiles would leave CUs idle in their last round, or number fewer
+ * than the CUs with no power-of-two split filling them (6144^3: 576 tiles;
+ * 3072^3: 144), may instead run stream-K: one block per CU takes an equal
+ * share of all (tile, k-slice) steps, and a tile split between blocks has
+ * its pieces added in k order by a second pass; its workspace is two 256x256
+ * tiles per CU (128 MiB on a 256-CU device) from the block cache, and
+ * without it the call runs the plan stream-K replaced.  An output with at
+ * most 32 rows or columns (a matrix-vector
  * product, a small-batch linear layer) runs a kernel that streams the long
  * operand once; it splits K to fill the device when the partial products
  * (splits * M * N * batch floats, from the block cache) move at most 1/8 of
@@ -270,8 +278,8 @@ int trs_matmul_f32(const float *a, const trs_layout *la, const float *b, const t
  * when nothing is launched; operands with no unit stride report the tile
  * their contiguous copies run on; a short output side reports its padded
  * rows, 16 or 32, by 64 and the k per slice),
- * *splits the number of K slices (1 = unsplit), *blocks the blocks of the
- * main launch.  Any out pointer may be null. */
+ * *splits the number of K slices (1 = unsplit, 0 = stream-K), *blocks the
+ * blocks of the main launch.  Any out pointer may be null. */
 int trs_matmul_plan_f32(const float *a, const trs_layout *la, const float *b, const trs_layout *lb,
                         const float *c, const trs_layout *lc, int *tile_m, int *tile_n, int *tile_k,
                         int64_t *splits, int64_t *blocks);

@@ -243,8 +243,9 @@ def matmul(log, reps: int = 20) -> dict:
 
 # (name, M, K, N, A transposed, B transposed, bound): outputs with a short
 # side (matrix-vector products and small-batch linear layers, x @ W or
-# x @ W.mT), which stream the long operand once and are HBM-bound, and
-# shapes whose square tiles alone would leave CUs idle (K split over them).
+# x @ W.mT), which stream the long operand once and are HBM-bound, shapes
+# whose square tiles alone would leave CUs idle (K split over them), ragged
+# squares, and tile counts whose last round leaves CUs idle (stream-K).
 MATMUL_SHAPES = [
     ("matvec [1,4096]@[4096,4096]", 1, 4096, 4096, False, False, "hbm"),
     ("matvec [1,4096]@W.mT", 1, 4096, 4096, False, True, "hbm"),
@@ -257,6 +258,11 @@ MATMUL_SHAPES = [
     ("2047^3", 2047, 2047, 2047, False, False, "mfma"),
     ("4095^3", 4095, 4095, 4095, False, False, "mfma"),
     ("4097^3", 4097, 4097, 4097, False, False, "mfma"),
+    # tile counts that leave CUs idle in whole rounds (stream-K)
+    ("[512,4096]@[4096,4096]", 512, 4096, 4096, False, False, "mfma"),
+    ("3072^3", 3072, 3072, 3072, False, False, "mfma"),
+    ("5000^3", 5000, 5000, 5000, False, False, "mfma"),
+    ("6144^3", 6144, 6144, 6144, False, False, "mfma"),
 ]
 
 
