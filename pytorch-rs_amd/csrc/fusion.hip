@@ -207,7 +207,7 @@ int generate(const std::string &ir, Program *prog) {
     wrap("trs_fused_flat_c", "trs::pw_flat_contig_body<TrsFused, " + mask + ">", "trs::kFlatBlock");
     wrap("trs_fused_flat_s", "trs::pw_flat_body<TrsFused, " + mask + ", false>", "trs::kFlatBlock");
     wrap("trs_fused_rows_s", "trs::pw_rows_body<TrsFused, " + mask + ", false>");
-    wrap("trs_fused_generic", "trs::pw_generic_body<TrsFused, " + mask + ">");
+    wrap("trs_fused_generic", "trs::pw_generic_body<TrsFused, " + mask + ">", "trs::kGenericBlock");
     prog->nin = nin;
     prog->nout = nout;
     prog->u8mask = u8mask;

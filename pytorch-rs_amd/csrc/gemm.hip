@@ -933,9 +933,9 @@ __global__ void __launch_bounds__(BM * 4, 2) gemm_f32_mfma_lds_small(GemmArgs ar
 // slice, with no branch between the loads, where a copy at a branch join
 // waits for every load issued before it), else 0 and S is read at run time.
 template <int NS>
-__global__ void __launch_bounds__(256) splitk_sum(const float4 *__restrict__ parts, float4 *__restrict__ c,
+__global__ void __launch_bounds__(kHelperLanes) splitk_sum(const float4 *__restrict__ parts, float4 *__restrict__ c,
                                                   int64_t n4, int S) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i = (int64_t)blockIdx.x * kHelperLanes + threadIdx.x;
     if (i >= n4) return;
     auto add = [](float4 &acc, const float4 &v) {
         acc.x += v.x;
@@ -964,20 +964,20 @@ __global__ void __launch_bounds__(256) splitk_sum(const float4 *__restrict__ par
 
 template <int NS = 2>
 void launch_splitk_sum(int S, dim3 grid, hipStream_t s, const float4 *parts, float4 *c, int64_t n4) {
-    if constexpr (NS > 16) hipLaunchKernelGGL(splitk_sum<0>, grid, dim3(256), 0, s, parts, c, n4, S);
-    else if (S == NS) hipLaunchKernelGGL(splitk_sum<NS>, grid, dim3(256), 0, s, parts, c, n4, S);
+    if constexpr (NS > 16) hipLaunchKernelGGL(splitk_sum<0>, grid, dim3(kHelperLanes), 0, s, parts, c, n4, S);
+    else if (S == NS) hipLaunchKernelGGL(splitk_sum<NS>, grid, dim3(kHelperLanes), 0, s, parts, c, n4, S);
     else launch_splitk_sum<NS + 1>(S, grid, s, parts, c, n4);
 }
 
 // Simple fallback for operands with no unit stride: one thread per output,
 // sequential k (the reference's own order).
-__global__ void __launch_bounds__(256) gemm_f32_strided(const float *a, const float *b, float *c, int64_t M,
+__global__ void __launch_bounds__(kHelperLanes) gemm_f32_strided(const float *a, const float *b, float *c, int64_t M,
                                                         int64_t N, int64_t K, int64_t sam, int64_t sak,
                                                         int64_t sbk, int64_t sbn, int64_t bsa, int64_t bsb,
                                                         int64_t batch) {
     const int64_t total = M * N * batch;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kHelperLanes;
+    for (int64_t e = (int64_t)blockIdx.x * kHelperLanes + threadIdx.x; e < total; e += stride) {
         const int64_t t = e / (M * N), rem = e - t * M * N, i = rem / N, j = rem - i * N;
         const float *A = a + t * bsa, *B = b + t * bsb;
         float acc = 0.0f;
@@ -1418,7 +1418,7 @@ int launch_split_k(const GemmPlan &p, GemmArgs g, bool a_plain, bool b_plain, in
             if (n4 <= 2 * 256 * (int64_t)cu_count)
                 launch_splitk_sum((int)S, grid, s, (const float4 *)ws, (float4 *)C, n4);
             else
-                hipLaunchKernelGGL(splitk_sum<0>, grid, dim3(256), 0, s, (const float4 *)ws, (float4 *)C, n4, (int)S);
+                hipLaunchKernelGGL(splitk_sum<0>, grid, dim3(kHelperLanes), 0, s, (const float4 *)ws, (float4 *)C, n4, (int)S);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) rc = hip_fail(e, "split-k sum launch");
         } else {
@@ -1623,7 +1623,7 @@ extern "C" int trs_matmul_f32(const float *a, const trs_layout *la, const float 
         if (ta) trs_free(ta);
         if (tb) trs_free(tb);
         if (!no_memory) return rc;
-        hipLaunchKernelGGL(gemm_f32_strided, dim3((unsigned)p.blocks), dim3(256), 0, dev->stream, g.a, g.b, g.c, g.M,
+        hipLaunchKernelGGL(gemm_f32_strided, dim3((unsigned)p.blocks), dim3(kHelperLanes), 0, dev->stream, g.a, g.b, g.c, g.M,
                            g.N, g.K, st.sam, st.sak, st.sbk, st.sbn, g.bsa, g.bsb, g.batch);
         TRS_LAUNCH_CHECK("strided gemm launch");
         return TRS_OK;

@@ -550,10 +550,10 @@ __global__ void __launch_bounds__(256) gemm_f32_skinny_lds(SkinnyArgs g) {
 // copy at a branch join waits for every load issued before it; conditional
 // loads made this pass 1.2 us slower).
 template <bool WIDE, int NS>
-__global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, float *__restrict__ c, int64_t mn,
+__global__ void __launch_bounds__(kHelperLanes) slice_sum(const float *__restrict__ ws, float *__restrict__ c, int64_t mn,
                                                   int64_t total, int S, SliceOut out) {
     typedef std::conditional_t<WIDE, int64_t, uint32_t> Index;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t e = (int64_t)blockIdx.x * kHelperLanes + threadIdx.x;
     if (e >= total) return;
     const Index b = total > mn ? (Index)e / (Index)mn : 0;
     const Index r = (Index)e - b * (Index)mn;
@@ -585,8 +585,8 @@ __global__ void __launch_bounds__(256) slice_sum(const float *__restrict__ ws, f
 template <bool WIDE, int NS = 2>
 void launch_slices(int S, dim3 grid, hipStream_t s, const float *ws, float *c, int64_t mn, int64_t total,
                    const SliceOut &out) {
-    if constexpr (NS > 16) hipLaunchKernelGGL((slice_sum<WIDE, 0>), grid, dim3(256), 0, s, ws, c, mn, total, S, out);
-    else if (S == NS) hipLaunchKernelGGL((slice_sum<WIDE, NS>), grid, dim3(256), 0, s, ws, c, mn, total, S, out);
+    if constexpr (NS > 16) hipLaunchKernelGGL((slice_sum<WIDE, 0>), grid, dim3(kHelperLanes), 0, s, ws, c, mn, total, S, out);
+    else if (S == NS) hipLaunchKernelGGL((slice_sum<WIDE, NS>), grid, dim3(kHelperLanes), 0, s, ws, c, mn, total, S, out);
     else launch_slices<WIDE, NS + 1>(S, grid, s, ws, c, mn, total, out);
 }
 

@@ -89,10 +89,10 @@ __global__ void __launch_bounds__(256) sum_pass2(const float *partial, int n, fl
 // memory: kernels receive only the address setup_sum_scratch looks up.
 static __device__ __align__(256) float scratch[kSumBlocks];
 
-__global__ void __launch_bounds__(256) fill_kernel(float *out, size_t n, float value, const float *src) {
+__global__ void __launch_bounds__(kHelperLanes) fill_kernel(float *out, size_t n, float value, const float *src) {
     const float v = src ? src[0] : value;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = v;
+    const size_t stride = (size_t)gridDim.x * kHelperLanes;
+    for (size_t i = (size_t)blockIdx.x * kHelperLanes + threadIdx.x; i < n; i += stride) out[i] = v;
 }
 
 // Broadcast-reduction: grad[j] = sum over the reduced dims (row-major order)
@@ -120,10 +120,10 @@ struct ReduceGeom {
 constexpr int kRedUnroll = 8;
 
 template <bool HAS_OTHER>
-__global__ void __launch_bounds__(256) reduce_bcast_kernel(const float *up, const float *other, ReduceGeom rg,
+__global__ void __launch_bounds__(kHelperLanes) reduce_bcast_kernel(const float *up, const float *other, ReduceGeom rg,
                                                            float *grad) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < rg.nself; j += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kHelperLanes;
+    for (int64_t j = (int64_t)blockIdx.x * kHelperLanes + threadIdx.x; j < rg.nself; j += stride) {
         int64_t ub = 0, ob = rg.other_off, rem = j;
         for (int d = rg.nkept - 1; d >= 0; d--) {
             const int64_t c = rem % rg.kept_size[d];
@@ -541,7 +541,7 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
     if (rg.nself == 0) return TRS_OK;
     if (layout_numel(lout) == 0) {  // nothing reaches the operand: +0.0
         const int64_t grid = std::min<int64_t>((rg.nself + 255) / 256, (int64_t)dev->cu_count * 8);
-        hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream, grad,
+        hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(kHelperLanes), 0, dev->stream, grad,
                            (size_t)rg.nself, 0.0f, (const float *)nullptr);
         TRS_LAUNCH_CHECK("fill kernel");
         return TRS_OK;
@@ -587,10 +587,10 @@ int reduce_to_operand(const float *up, const trs_layout *lout, const float *othe
     }
     const int64_t grid = std::min<int64_t>((rg.nself + 255) / 256, (int64_t)dev->cu_count * 8);
     if (other)
-        hipLaunchKernelGGL(reduce_bcast_kernel<true>, dim3((unsigned)grid), dim3(256), 0, dev->stream, up,
+        hipLaunchKernelGGL(reduce_bcast_kernel<true>, dim3((unsigned)grid), dim3(kHelperLanes), 0, dev->stream, up,
                            other, rg, grad);
     else
-        hipLaunchKernelGGL(reduce_bcast_kernel<false>, dim3((unsigned)grid), dim3(256), 0, dev->stream, up,
+        hipLaunchKernelGGL(reduce_bcast_kernel<false>, dim3((unsigned)grid), dim3(kHelperLanes), 0, dev->stream, up,
                            (const float *)nullptr, rg, grad);
     TRS_LAUNCH_CHECK("broadcast reduction kernel");
     return TRS_OK;
@@ -726,7 +726,7 @@ int trs_fill_f32(float *out, size_t n, float value) {
     if (n == 0) return TRS_OK;
     if (!out) return set_error(TRS_E_INVALID_ARGUMENT, "null output");
     const int64_t grid = std::min<int64_t>(((int64_t)n + 255) / 256, (int64_t)dev->cu_count * 8);
-    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream, out, n, value,
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(kHelperLanes), 0, dev->stream, out, n, value,
                        (const float *)nullptr);
     TRS_LAUNCH_CHECK("fill kernel");
     return TRS_OK;
@@ -738,7 +738,7 @@ int trs_fill_from_device_f32(float *out, size_t n, const float *value) {
     if (n == 0) return TRS_OK;
     if (!out || !value) return set_error(TRS_E_INVALID_ARGUMENT, "null pointer");
     const int64_t grid = std::min<int64_t>(((int64_t)n + 255) / 256, (int64_t)dev->cu_count * 8);
-    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream, out, n, 0.0f, value);
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(kHelperLanes), 0, dev->stream, out, n, 0.0f, value);
     TRS_LAUNCH_CHECK("fill kernel");
     return TRS_OK;
 }

@@ -49,11 +49,15 @@ constexpr int kRowChunkVec = 2048;  // columns per vector pw_rows tile (256 lane
 // Largest grid a launch uses (256-lane blocks).  Launches are one-shot --
 // one tile per block -- up to this many blocks; beyond it the bodies loop.
 constexpr int64_t kMaxGrid = 1 << 20;
-// Lanes per block of the flat kernels.  On gfx950 the 4 GiB three-input
-// chain measured 64, 128 and 256 within 2% of each other (their order changes
-// from board to board, ~79-82% of HBM peak) and 512/1024 2-3% slower, while
-// at 128 MiB (an MLP activation) 128 was ~4% slower than 64 or 256.
-constexpr int kFlatBlock = 256;
+// Lanes per block of the flat kernels: one wave, one float4 per lane per
+// operand, so a block reads 1 KiB of each operand and retires as soon as its
+// one store is issued.  On gfx950 a standalone three-input chain over 2^28
+// elements took 642 us with 64-lane blocks against 654 (128), 667 (256) and
+// 685 (512) in interleaved runs on two boards; two or four float4 per lane
+// were slower at every block size (670-707 us).  The bodies index with this
+// constant, not blockDim: reading blockDim costs each wave a memory load and
+// a wait before its first data load.
+constexpr int kFlatBlock = 64;
 
 // Unsigned 32-bit division by a runtime-invariant divisor (Granlund-Montgomery
 // round-up method): q = (umulhi(n, mul) + n) >> shift, exact for all n < 2^32.
@@ -292,8 +296,8 @@ __device__ __forceinline__ void pw_flat_body(const F &f, const PwGeom &g, const 
     constexpr int NIN = F::NIN;
     constexpr int NOUT = nout_of<F>();
     const int64_t n = g.numel;
-    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+    const int64_t tid = (int64_t)blockIdx.x * kFlatBlock + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * kFlatBlock;
     bool unit[NIN > 0 ? NIN : 1];
     for (int i = 0; i < NIN; i++) unit[i] = g.istride[i][0] != 0;
     int64_t tail_start = 0;
@@ -346,8 +350,8 @@ __device__ __forceinline__ void pw_flat_contig_body(const F &f, const PwGeom &g,
     constexpr int NIN = F::NIN;
     constexpr int NOUT = nout_of<F>();
     const int64_t n = g.numel;
-    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+    const int64_t tid = (int64_t)blockIdx.x * kFlatBlock + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * kFlatBlock;
     const int64_t groups = n >> 2;
     for (int64_t gi = tid; gi < groups; gi += nthreads) {
         const int64_t e = gi << 2;
@@ -779,12 +783,13 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
 
 // ---- pw_generic -----------------------------------------------------------
 // Any strides: every element decoded on its own by magic-number division.  A
-// block takes kGenericUnroll * blockDim consecutive elements per step, lane t
-// the elements t, t + blockDim, ... of them, so each load instruction still
+// block takes kGenericUnroll * kGenericBlock consecutive elements per step,
+// lane t the elements t, t + kGenericBlock, ... of them, so each load still
 // covers consecutive elements; the lane issues all its loads before any
 // arithmetic.  With one element per lane, x[::2] + y[::2] over 2^25 elements
 // took 171 us, each lane waiting for its loads before the next element.
 constexpr int kGenericUnroll = 4;
+constexpr int kGenericBlock = 256;  // lanes per block of pw_generic
 
 template <class F, unsigned U8MASK>
 __device__ __forceinline__ void pw_generic_body(const F &f, const PwGeom &g, const PwPtrs &p) {
@@ -792,13 +797,14 @@ __device__ __forceinline__ void pw_generic_body(const F &f, const PwGeom &g, con
     constexpr int NIN1 = NIN > 0 ? NIN : 1;
     constexpr int NOUT = nout_of<F>();
     constexpr int U = kGenericUnroll;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x * U;
-    for (int64_t base = (int64_t)blockIdx.x * blockDim.x * U; base < g.numel; base += step) {
+    constexpr int B = kGenericBlock;
+    const int64_t step = (int64_t)gridDim.x * B * U;
+    for (int64_t base = (int64_t)blockIdx.x * B * U; base < g.numel; base += step) {
         int64_t oo[U], io[U][NIN1];
         float a[U][NIN1];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int64_t e = base + (int64_t)u * blockDim.x + threadIdx.x;
+            const int64_t e = base + (int64_t)u * B + threadIdx.x;
             if (e < g.numel) {
                 decode_outer<NIN>(g, g.rank, e, oo[u], io[u]);
                 static_for<NIN>([&]<int I>() { a[u][I] = ld1<U8MASK, I>(p, io[u][I]); });
@@ -806,7 +812,7 @@ __device__ __forceinline__ void pw_generic_body(const F &f, const PwGeom &g, con
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int64_t e = base + (int64_t)u * blockDim.x + threadIdx.x;
+            const int64_t e = base + (int64_t)u * B + threadIdx.x;
             if (e < g.numel) {
                 float o[NOUT];
                 eval1(f, a[u], o);

@@ -413,7 +413,8 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         }
     }
     plan->variant = PwVariant::Generic;
-    const int64_t per_block = 256 * kGenericUnroll;
+    plan->block = kGenericBlock;
+    const int64_t per_block = kGenericBlock * kGenericUnroll;
     plan->grid = std::min<int64_t>(std::max<int64_t>(1, (numel + per_block - 1) / per_block), want);
     return TRS_OK;
 }

@@ -105,7 +105,7 @@ __global__ void __launch_bounds__(64 * kXposeWT * kXposeWX) k_xpose(PwGeom, PwPt
     pw_xpose_body<F, M, V, kXposeWT, kXposeWX, TR, 0u, 0u, 1, S>(f, kernarg_geom(), p);
 }
 template <class F, unsigned M>
-__global__ void __launch_bounds__(256) k_generic(PwGeom, PwPtrs p, F f) { pw_generic_body<F, M>(f, kernarg_geom(), p); }
+__global__ void __launch_bounds__(kGenericBlock) k_generic(PwGeom, PwPtrs p, F f) { pw_generic_body<F, M>(f, kernarg_geom(), p); }
 
 // Calls fn.template operator()<K>() with K the compile-time value of the
 // run-time mask `m` over NIN bits (NIN is 1 or 2 here).

@@ -27,14 +27,14 @@ DeviceState *const g_devices = new DeviceState[kMaxDevices];
 std::mutex g_init_mu;
 int g_device_count = -1;
 
-__global__ void __launch_bounds__(256) fill_u32_kernel(uint32_t *dst, size_t n, uint32_t value) {
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = value;
+__global__ void __launch_bounds__(kHelperLanes) fill_u32_kernel(uint32_t *dst, size_t n, uint32_t value) {
+    const size_t stride = (size_t)gridDim.x * kHelperLanes;
+    for (size_t i = (size_t)blockIdx.x * kHelperLanes + threadIdx.x; i < n; i += stride) dst[i] = value;
 }
 
-__global__ void __launch_bounds__(256) fill_u8_kernel(uint8_t *dst, size_t n) {
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = 0;
+__global__ void __launch_bounds__(kHelperLanes) fill_u8_kernel(uint8_t *dst, size_t n) {
+    const size_t stride = (size_t)gridDim.x * kHelperLanes;
+    for (size_t i = (size_t)blockIdx.x * kHelperLanes + threadIdx.x; i < n; i += stride) dst[i] = 0;
 }
 
 int count_devices() {
@@ -372,11 +372,11 @@ int trs_memset_zero(void *dst, size_t bytes) {
     if (bytes % 4 == 0 && ((uintptr_t)dst % 4) == 0) {
         const size_t n = bytes / 4;
         const int64_t grid = std::min<int64_t>(std::max<int64_t>(1, (int64_t)((n + 255) / 256)), want);
-        hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream,
+        hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)grid), dim3(kHelperLanes), 0, dev->stream,
                            (uint32_t *)dst, n, 0u);
     } else {
         const int64_t grid = std::min<int64_t>(std::max<int64_t>(1, (int64_t)((bytes + 255) / 256)), want);
-        hipLaunchKernelGGL(fill_u8_kernel, dim3((unsigned)grid), dim3(256), 0, dev->stream,
+        hipLaunchKernelGGL(fill_u8_kernel, dim3((unsigned)grid), dim3(kHelperLanes), 0, dev->stream,
                            (uint8_t *)dst, bytes);
     }
     TRS_LAUNCH_CHECK("memset kernel");

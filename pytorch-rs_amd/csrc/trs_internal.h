@@ -16,6 +16,13 @@
 
 namespace trs {
 
+// Lanes per block of the one-dimensional helper kernels (fills, slice and
+// split-K sums, the per-element reduction).  Their bodies index with this
+// constant rather than blockDim: reading blockDim costs each wave a memory
+// load and a wait before its first load, one more memory latency in a pass
+// whose time is load latency.
+constexpr int kHelperLanes = 256;
+
 // Per-device state: one in-order stream carries every entry point's work, so
 // stream order gives the reference's eager semantics.
 struct DeviceState {
