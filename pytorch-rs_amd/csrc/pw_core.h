@@ -44,8 +44,15 @@ namespace trs {
 constexpr int kMaxRank = 8;
 constexpr int kMaxIn = 8;
 constexpr int kMaxOut = 8;  // outputs of one program (all share one layout)
-constexpr int kRowChunk = 1024;     // columns per scalar pw_rows tile (256 lanes x 4)
-constexpr int kRowChunkVec = 2048;  // columns per vector pw_rows tile (256 lanes x 2 float4)
+constexpr int kRowChunk = 1024;  // columns per scalar pw_rows tile (256 lanes x 4)
+// Vector pw_rows tiles: one wave per block, one float4 per lane, 256
+// columns.  relu(x + b) over [4096, 4096] with the inputs rotated past the
+// cache measured 21.2 us per launch on such tiles against 22.8 us on
+// 2,048-column tiles of 256 lanes (two float4 each), 23.6 on 128 lanes and
+// 22.8 on 64 lanes with two float4; a flat copy of the same bytes took 21.1.
+constexpr int kRowLanesVec = 64;
+constexpr int kRowVecPerLane = 1;
+constexpr int kRowChunkVec = kRowLanesVec * 4 * kRowVecPerLane;
 // Largest grid a launch uses (256-lane blocks).  Launches are one-shot --
 // one tile per block -- up to this many blocks; beyond it the bodies loop.
 constexpr int64_t kMaxGrid = 1 << 20;
@@ -374,11 +381,12 @@ __device__ __forceinline__ void pw_flat_contig_body(const F &f, const PwGeom &g,
 // Innermost dim (size[rank-1] columns) has ostride 1 and istride in {0, 1}.
 // g.rows = product of the outer dims, g.chunks = ceil(cols / chunk) with
 // chunk = kRowChunkVec under VEC, else kRowChunk.
-// VEC: cols % 4 == 0 and every unit-stride row start 16-byte aligned.  A lane
-// then takes two float4 of the row, 1024 columns apart, and issues all their
-// loads before any arithmetic: with one float4 per lane, relu(x + b) over
-// [4096, 4096] measured 5% slower than a plain copy of the same shape, with
-// two it is within 1%.
+// VEC: cols % 4 == 0 and every unit-stride row start 16-byte aligned.  A
+// block is one wave (kRowLanesVec lanes) and a lane takes kRowVecPerLane
+// float4 of the row, issuing all their loads before any arithmetic.  On
+// 256-lane blocks one float4 per lane measured 5% slower than a plain copy of
+// the same shape and two within 1%; one-wave blocks of one float4 run at the
+// copy's speed and both faster than either 256-lane form.
 // STRM: as for pw_flat.
 // RANK = 2, 3 or 4: the rank is fixed, so the row splits into its outer
 // indices by RANK - 2 multiply-shifts with every geometry field at a constant
@@ -446,13 +454,13 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
             decode_outer<NIN, !VEC>(g, inner, row, oo, io);
         }
         if constexpr (VEC) {
-            constexpr int RV = kRowChunkVec / 1024;  // float4 per lane
+            constexpr int RV = kRowVecPerLane;
             const int64_t c0 = chunk * kRowChunkVec;
             auto run = [&]<bool FULL>() {
                 float v[RV][NIN > 0 ? NIN : 1][4];
 #pragma unroll
                 for (int j = 0; j < RV; j++) {
-                    const int64_t c = c0 + ((int64_t)threadIdx.x + 256 * j) * 4;
+                    const int64_t c = c0 + ((int64_t)threadIdx.x + kRowLanesVec * j) * 4;
                     if (FULL || c < cols)
                         static_for<NIN>([&]<int I>() {
                             ld4<U8MASK, I, ((STRM >> I) & 1u) != 0u>(p, io[I] + (unit[I] ? c : 0), unit[I], v[j][I]);
@@ -460,7 +468,7 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
                 }
 #pragma unroll
                 for (int j = 0; j < RV; j++) {
-                    const int64_t c = c0 + ((int64_t)threadIdx.x + 256 * j) * 4;
+                    const int64_t c = c0 + ((int64_t)threadIdx.x + kRowLanesVec * j) * 4;
                     if (FULL || c < cols) {
                         float r[NOUT][4];
                         eval4(f, v[j], r);

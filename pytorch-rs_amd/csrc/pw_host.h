@@ -332,6 +332,7 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         } else {
             plan->variant = PwVariant::Rows;
             plan->vec = vec && size[inner] % 4 == 0;
+            plan->block = plan->vec ? kRowLanesVec : 256;
             g.rows = numel / size[inner];
             const int64_t chunk = plan->vec ? kRowChunkVec : kRowChunk;
             g.chunks = (size[inner] + chunk - 1) / chunk;

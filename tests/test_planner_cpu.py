@@ -29,7 +29,8 @@ def test_size_one_dims_are_dropped_before_merging():
 def test_config0_row_broadcast_is_the_rank2_rows_kernel():
     p = plan(layout_of((4096, 4096)), layout_of((4096,)), out=layout_of((4096, 4096)))
     assert (p.variant, p.rank, p.vec, p.fixed_rank) == (ROWS, 2, 1, 2)
-    assert p.grid == 4096 * 2  # one 2,048-column tile per block
+    assert p.grid == 4096 * 16  # one 256-column tile per one-wave block
+    assert p.block == 64
 
 
 def test_config2_fused_roles_and_walk():
