@@ -421,7 +421,7 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
         return get_spec_function(prog, dev, name,
                                  "trs::pw_rows_body<TrsFused, " + mask + ", true, " + std::to_string(strm) + "u, " +
                                      std::to_string(rk) + ">",
-                                 kRowLanesVec, fn);
+                                 kRowLanesMax, fn);
     }
     case PwVariant::Xpose: {
         // The scalar form reads every input plainly, so the streamed mask is

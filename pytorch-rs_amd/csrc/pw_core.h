@@ -45,14 +45,10 @@ constexpr int kMaxRank = 8;
 constexpr int kMaxIn = 8;
 constexpr int kMaxOut = 8;  // outputs of one program (all share one layout)
 constexpr int kRowChunk = 1024;  // columns per scalar pw_rows tile (256 lanes x 4)
-// Vector pw_rows tiles: one wave per block, one float4 per lane, 256
-// columns.  relu(x + b) over [4096, 4096] with the inputs rotated past the
-// cache measured 21.2 us per launch on such tiles against 22.8 us on
-// 2,048-column tiles of 256 lanes (two float4 each), 23.6 on 128 lanes and
-// 22.8 on 64 lanes with two float4; a flat copy of the same bytes took 21.1.
-constexpr int kRowLanesVec = 64;
-constexpr int kRowVecPerLane = 1;
-constexpr int kRowChunkVec = kRowLanesVec * 4 * kRowVecPerLane;
+// Vector pw_rows tiles: one float4 per lane, g.chunkcols = 4 x lanes
+// columns, the lanes per block (64, 128 or 256) chosen per launch by
+// rows_lanes() in pw_host.h.  At most this many:
+constexpr int kRowLanesMax = 256;
 // Largest grid a launch uses (256-lane blocks).  Launches are one-shot --
 // one tile per block -- up to this many blocks; beyond it the bodies loop.
 constexpr int64_t kMaxGrid = 1 << 20;
@@ -107,6 +103,7 @@ struct PwGeom {
     FastDiv fdxtiles;     // pw_xpose: divides by the x tiles of a tuple (skewed order)
     int64_t ttiles;       // pw_xpose: tiles along tdim
     int64_t groups;       // pw_xpose: block groups G; a block walks outer tuples c, c+G, c+2G, ...
+    int64_t chunkcols;    // pw_rows (vector): columns per tile, 4 per lane
 };
 
 // The launch geometry, read in place in the kernel-argument segment: every
@@ -380,13 +377,10 @@ __device__ __forceinline__ void pw_flat_contig_body(const F &f, const PwGeom &g,
 // ---- pw_rows --------------------------------------------------------------
 // Innermost dim (size[rank-1] columns) has ostride 1 and istride in {0, 1}.
 // g.rows = product of the outer dims, g.chunks = ceil(cols / chunk) with
-// chunk = kRowChunkVec under VEC, else kRowChunk.
-// VEC: cols % 4 == 0 and every unit-stride row start 16-byte aligned.  A
-// block is one wave (kRowLanesVec lanes) and a lane takes kRowVecPerLane
-// float4 of the row, issuing all their loads before any arithmetic.  On
-// 256-lane blocks one float4 per lane measured 5% slower than a plain copy of
-// the same shape and two within 1%; one-wave blocks of one float4 run at the
-// copy's speed and both faster than either 256-lane form.
+// chunk = g.chunkcols under VEC, else kRowChunk.
+// VEC: cols % 4 == 0 and every unit-stride row start 16-byte aligned.  A lane
+// takes one float4 of the row; the block's lanes (g.chunkcols / 4) are
+// chosen per launch for the HBM bytes a block moves (rows_lanes()).
 // STRM: as for pw_flat.
 // RANK = 2, 3 or 4: the rank is fixed, so the row splits into its outer
 // indices by RANK - 2 multiply-shifts with every geometry field at a constant
@@ -454,30 +448,27 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
             decode_outer<NIN, !VEC>(g, inner, row, oo, io);
         }
         if constexpr (VEC) {
-            constexpr int RV = kRowVecPerLane;
-            const int64_t c0 = chunk * kRowChunkVec;
-            auto run = [&]<bool FULL>() {
-                float v[RV][NIN > 0 ? NIN : 1][4];
-#pragma unroll
-                for (int j = 0; j < RV; j++) {
-                    const int64_t c = c0 + ((int64_t)threadIdx.x + kRowLanesVec * j) * 4;
-                    if (FULL || c < cols)
-                        static_for<NIN>([&]<int I>() {
-                            ld4<U8MASK, I, ((STRM >> I) & 1u) != 0u>(p, io[I] + (unit[I] ? c : 0), unit[I], v[j][I]);
-                        });
-                }
-#pragma unroll
-                for (int j = 0; j < RV; j++) {
-                    const int64_t c = c0 + ((int64_t)threadIdx.x + kRowLanesVec * j) * 4;
-                    if (FULL || c < cols) {
-                        float r[NOUT][4];
-                        eval4(f, v[j], r);
-                        store4(p, oo + c, r);
-                    }
-                }
-            };
-            if (c0 + kRowChunkVec <= cols) run.template operator()<true>();
-            else run.template operator()<false>();
+            const int64_t c0 = chunk * g.chunkcols;
+            const int64_t c = c0 + (int64_t)threadIdx.x * 4;
+            // cols % 4 == 0, so a lane's float4 lies wholly inside or past
+            // the row.  Lanes past it load the row's last float4 and store
+            // nothing: no branch around the loads, which would hold back the
+            // geometry reads they depend on until the lane test.  A streamed
+            // operand (read once, no broadcast dim) is unit-stride here, so
+            // its load kind is fixed at compile time, and the streamed loads
+            // are issued first, ahead of the other operands' run-time choice
+            // between a vector and a broadcast load.
+            const int64_t cl = c < cols ? c : cols - 4;
+            float v[NIN > 0 ? NIN : 1][4];
+            static_for<NIN>([&]<int I>() {
+                if constexpr (((STRM >> I) & 1u) != 0u) ld4<U8MASK, I, true>(p, io[I] + cl, true, v[I]);
+            });
+            static_for<NIN>([&]<int I>() {
+                if constexpr (((STRM >> I) & 1u) == 0u) ld4<U8MASK, I, false>(p, io[I] + (unit[I] ? cl : 0), unit[I], v[I]);
+            });
+            float r[NOUT][4];
+            eval4(f, v, r);
+            if (c < cols) store4(p, oo + c, r);
         } else {
             const int64_t c0 = chunk * kRowChunk;
             for (int k = 0; k < 4; k++) {
@@ -494,7 +485,10 @@ __device__ __forceinline__ void pw_rows_loop(const F &f, const PwGeom &g, const 
             }
         }
     };
-    if ((int64_t)blockIdx.x >= ntiles) return;
+    // The host launches at most ntiles blocks (grid = min(tiles, kMaxGrid),
+    // checked before every launch), so the first tile needs no bounds check.
+    // With one, every geometry load behind it waited for the tile count: four
+    // dependent rounds of scalar loads before a block's first data load.
     do_tile(blockIdx.x);
     for (int64_t tile = (int64_t)blockIdx.x + gridDim.x; tile < ntiles; tile += gridDim.x) do_tile(tile);
 }

@@ -69,6 +69,10 @@ struct PwPlan {
 // disjoint output elements, so their order does not change any result.
 template <class L>
 int for_each_part(const PwPlan &pl, L &&launch) {
+    // pw_rows takes its block's first tile unchecked: never more blocks than tiles.
+    if (pl.variant == PwVariant::Rows && (pl.grid < 1 || pl.grid > pl.g.rows * pl.g.chunks))
+        return set_error(TRS_E_INVALID_ARGUMENT, "pw_rows launch of %lld blocks over %lld tiles", (long long)pl.grid,
+                         (long long)(pl.g.rows * pl.g.chunks));
     if (pl.nsplit == 0) return launch(pl.g);
     PwGeom g = pl.g;
     int64_t idx[kMaxSplit] = {};
@@ -97,6 +101,26 @@ inline FastDiv make_fast_div(uint32_t d) {
     f.mul = (uint32_t)m;
     f.shift = shift;
     return f;
+}
+
+// Lanes per vector pw_rows block (one float4 per lane): the fewest that give
+// a block at least 2 KiB of HBM traffic, counting the outputs and the inputs
+// read once (`streamed`; broadcast operands come from cache).  The GPU starts
+// about 4.4 blocks per nanosecond, so a kernel whose blocks each move 1 KiB
+// is bound by block dispatch, not HBM: a write-only pass over 128 MiB took
+// 29.9 us on one-wave blocks and 20.4 us on 256-lane blocks, and a [64, 512,
+// 1024] broadcast add (a and b from cache, the output written) 30.1 us on
+// one wave against 20.6 on two.  Where inputs stream as well, one wave is
+// fastest: relu(x + b) over [4096, 4096] measured 21.2 us per launch on
+// one-wave blocks, 22.7 on 256 lanes and 22.8 on 2,048-column tiles of 256
+// lanes with two float4 each.
+inline int rows_lanes(uint32_t streamed, int nin, const int *elem_bytes, int nout) {
+    int per_element = 4 * nout;
+    for (int i = 0; i < nin; i++)
+        if ((streamed >> i) & 1u) per_element += elem_bytes[i];
+    for (int lanes = 64; lanes < kRowLanesMax; lanes *= 2)
+        if (lanes * 4 * per_element >= 2048) return lanes;
+    return kRowLanesMax;
 }
 
 // `elem_bytes[i]` is 4 for f32 inputs and 1 for u8 inputs.  A program with
@@ -332,9 +356,10 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
         } else {
             plan->variant = PwVariant::Rows;
             plan->vec = vec && size[inner] % 4 == 0;
-            plan->block = plan->vec ? kRowLanesVec : 256;
+            plan->block = plan->vec ? rows_lanes(g.streamed, nin, elem_bytes, nout) : 256;
+            g.chunkcols = plan->vec ? 4 * plan->block : 0;
             g.rows = numel / size[inner];
-            const int64_t chunk = plan->vec ? kRowChunkVec : kRowChunk;
+            const int64_t chunk = plan->vec ? g.chunkcols : kRowChunk;
             g.chunks = (size[inner] + chunk - 1) / chunk;
             g.fdchunks = make_fast_div(g.chunks > (int64_t)UINT32_MAX ? 1u : (uint32_t)g.chunks);
             const bool fast = g.rows * g.chunks <= (int64_t)UINT32_MAX && offsets_fit32();

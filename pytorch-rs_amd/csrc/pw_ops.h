@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(kFlatBlock) k_flat_contig(PwGeom, PwPtrs p, F 
     pw_flat_contig_body<F, M>(f, kernarg_geom(), p);
 }
 template <class F, unsigned M, bool V, unsigned S, int RK = 0>
-__global__ void __launch_bounds__(V ? kRowLanesVec : 256) k_rows(PwGeom, PwPtrs p, F f) {
+__global__ void __launch_bounds__(kRowLanesMax) k_rows(PwGeom, PwPtrs p, F f) {
     pw_rows_body<F, M, V, S, RK>(f, kernarg_geom(), p);
 }
 template <class F, unsigned M, bool V, unsigned TR, unsigned S>

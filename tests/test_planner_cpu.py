@@ -33,6 +33,26 @@ def test_config0_row_broadcast_is_the_rank2_rows_kernel():
     assert p.block == 64
 
 
+def test_rows_blocks_with_streamed_inputs_are_one_wave():
+    # The MLP's fused activation: x (f32) and the u8 keep-mask stream, the
+    # bias row comes from cache; with the f32 output 9 B per element, so 64
+    # lanes of one float4 move 2 KiB through HBM.
+    x, mask, b = layout_of((8192, 4096)), layout_of((8192, 4096)), layout_of((4096,))
+    p = plan(x, mask, b, out=layout_of((8192, 4096)), elem_bytes=[4, 1, 4])
+    assert (p.variant, p.vec, p.block) == (ROWS, 1, 64)
+    assert p.grid == 8192 * 16
+
+
+def test_write_only_rows_blocks_are_wider():
+    # a [64,1,1024] + b [1,512,1024]: both from cache, only the output
+    # streams (4 B per element), so a block takes 128 lanes (2 KiB): one-wave
+    # blocks of 1 KiB are bound by how fast the GPU starts blocks.
+    p = plan(layout_of((64, 1, 1024)), layout_of((1, 512, 1024)), out=layout_of((64, 512, 1024)))
+    assert (p.variant, p.rank, p.vec, p.fixed_rank) == (ROWS, 3, 1, 3)
+    assert p.block == 128
+    assert p.grid == 64 * 512 * 2  # 512-column tiles of 1,024-column rows
+
+
 def test_config2_fused_roles_and_walk():
     a = layout_of((64, 1, 1024))
     b = layout_of((1, 512, 1024))
