@@ -777,8 +777,8 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
         }
     };
     // The first tile runs outside the loop: a block with one tile ends
-    // without waiting at the loop's back edge for its own stores.
-    if ((int64_t)blockIdx.x >= ntiles) return;
+    // without waiting at the loop's back edge for its own stores.  As in
+    // pw_rows, the host launches at most ntiles blocks, so it is unchecked.
     do_tile(blockIdx.x);
     for (int64_t tile = (int64_t)blockIdx.x + gridDim.x; tile < ntiles; tile += gridDim.x) do_tile(tile);
 }

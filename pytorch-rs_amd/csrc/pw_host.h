@@ -69,10 +69,14 @@ struct PwPlan {
 // disjoint output elements, so their order does not change any result.
 template <class L>
 int for_each_part(const PwPlan &pl, L &&launch) {
-    // pw_rows takes its block's first tile unchecked: never more blocks than tiles.
-    if (pl.variant == PwVariant::Rows && (pl.grid < 1 || pl.grid > pl.g.rows * pl.g.chunks))
-        return set_error(TRS_E_INVALID_ARGUMENT, "pw_rows launch of %lld blocks over %lld tiles", (long long)pl.grid,
-                         (long long)(pl.g.rows * pl.g.chunks));
+    // pw_rows and pw_xpose take a block's first tile unchecked: never more
+    // blocks than tiles.
+    const int64_t tiles = pl.variant == PwVariant::Rows    ? pl.g.rows * pl.g.chunks
+                          : pl.variant == PwVariant::Xpose ? pl.g.groups * pl.g.chunks
+                                                           : INT64_MAX;
+    if (pl.grid < 1 || pl.grid > tiles)
+        return set_error(TRS_E_INVALID_ARGUMENT, "pointwise launch of %lld blocks over %lld tiles", (long long)pl.grid,
+                         (long long)tiles);
     if (pl.nsplit == 0) return launch(pl.g);
     PwGeom g = pl.g;
     int64_t idx[kMaxSplit] = {};
