@@ -64,6 +64,10 @@ BINARY_CASES = {
     "rank4_broadcast_wide": lambda rng: (_view(rng, (8, 1, 16, 1024)), _view(rng, (1, 8, 1, 1024))),
     "rank4_broadcast_ragged": lambda rng: (_view(rng, (5, 1, 7, 2051)), _view(rng, (1, 3, 1, 2051))),
     "rank5_broadcast": lambda rng: (_view(rng, (2, 1, 3, 1, 64)), _view(rng, (1, 3, 1, 4, 64))),
+    # rows tiles of one float4 per lane with a partial last tile: 64-lane
+    # blocks when an input streams, 128-lane blocks when only the output does
+    "rows_partial_tile": lambda rng: (_view(rng, (64, 260)), _view(rng, (260,))),
+    "rows_write_only_partial": lambda rng: (_view(rng, (8, 1, 516)), _view(rng, (1, 16, 516))),
     # more tiles in one tuple than the GPU holds at once: diagonal tile order
     "skewed_transposed": lambda rng: (_view(rng, (4096, 4096)), _transposed(rng, (4096, 4096))),
     "skewed_transposed_ragged": lambda rng: (_transposed(rng, (4099, 4100)), _view(rng, (4100, 4099))),
