@@ -10,9 +10,10 @@
 // that are contiguous for every operand are merged.  The kernels below then
 // cover four cases:
 //   pw_flat  -- rank 1, every operand unit-stride or broadcast: one 16-byte
-//               vector per lane, one-shot grid.
+//               vector per lane, one-wave blocks, one-shot grid.
 //   pw_rows  -- innermost dim unit-stride or broadcast for every operand:
-//               one (outer row, 2048-column chunk) tile per block;
+//               one (outer row, column chunk) tile per block, one 16-byte
+//               vector per lane;
 //               the outer-row decode is wave-uniform (scalar registers), the
 //               lanes stream 16-byte vectors along the row.
 //   pw_xpose -- an operand is unit-stride along another dim (a transposed or
@@ -49,7 +50,7 @@ constexpr int kRowChunk = 1024;  // columns per scalar pw_rows tile (256 lanes x
 // columns, the lanes per block (64, 128 or 256) chosen per launch by
 // rows_lanes() in pw_host.h.  At most this many:
 constexpr int kRowLanesMax = 256;
-// Largest grid a launch uses (256-lane blocks).  Launches are one-shot --
+// Largest grid a launch uses, in blocks.  Launches are one-shot --
 // one tile per block -- up to this many blocks; beyond it the bodies loop.
 constexpr int64_t kMaxGrid = 1 << 20;
 // Lanes per block of the flat kernels: one wave, one float4 per lane per
