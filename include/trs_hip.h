@@ -99,6 +99,13 @@ int trs_alloc(size_t bytes, void **ptr);
  * operands with no unit stride cannot be had runs the one-lane-per-output
  * kernel; a split K whose workspace cannot be had runs unsplit. */
 int trs_debug_fail_allocs_after(int64_t n);
+/* Test hook (no counterpart in the reference; for the tests of the
+ * pointwise kernels' grid-stride loops, which only launches of more than
+ * 2^22 blocks reach otherwise): every pointwise launch planned after it uses
+ * at most `blocks` blocks, its blocks looping over the remaining tiles;
+ * blocks = 0 restores the default cap.  Process-wide; negative is
+ * TRS_E_INVALID_ARGUMENT. */
+int trs_debug_pointwise_grid_cap(int64_t blocks);
 int trs_free(void *ptr);
 /* Return every cached block to HIP (after draining the device stream). */
 int trs_empty_cache(void);

@@ -50,9 +50,14 @@ constexpr int kRowChunk = 1024;  // columns per scalar pw_rows tile (256 lanes x
 // columns, the lanes per block (64, 128 or 256) chosen per launch by
 // rows_lanes() in pw_host.h.  At most this many:
 constexpr int kRowLanesMax = 256;
-// Largest grid a launch uses, in blocks.  Launches are one-shot --
-// one tile per block -- up to this many blocks; beyond it the bodies loop.
-constexpr int64_t kMaxGrid = 1 << 20;
+// Largest grid a launch uses, in blocks.  Launches are one-shot -- one tile
+// per block -- up to this many blocks; beyond it the bodies loop.  A
+// dispatch counts at most 2^32 - 1 lanes per dimension, and the widest
+// block here has 512 lanes, so 2^22 blocks always fit.  On gfx950 the
+// three-input chain over 2^30 elements (16 GiB per launch, one-wave blocks)
+// took 2,536 us one-shot against 2,830 us capped at 2^20 blocks, each lane
+// then taking 4 groups in a grid-stride loop.
+constexpr int64_t kMaxGrid = 1 << 22;
 // Lanes per block of the flat kernels: one wave, one float4 per lane per
 // operand, so a block reads 1 KiB of each operand and retires as soon as its
 // one store is issued.  On gfx950 a standalone three-input chain over 2^28

@@ -342,7 +342,8 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
     };
     bool unit_or_bcast = os[inner] == 1;
     for (int i = 0; i < nin; i++) unit_or_bcast &= is[i][inner] == 0 || is[i][inner] == 1;
-    const int64_t want = kMaxGrid;
+    const int64_t cap = g_pw_grid_cap.load(std::memory_order_relaxed);
+    const int64_t want = cap > 0 ? cap : kMaxGrid;
 
     if (unit_or_bcast) {
         bool vec = outputs_aligned();

@@ -210,6 +210,7 @@ using namespace trs;
 namespace trs {
 // Allocations trs_alloc grants before it refuses every one (-1: no limit).
 std::atomic<int64_t> g_allocs_before_failure{-1};
+std::atomic<int64_t> g_pw_grid_cap{0};
 }  // namespace trs
 
 extern "C" {
@@ -260,6 +261,12 @@ int trs_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz) 
 
 int trs_debug_fail_allocs_after(int64_t n) {
     trs::g_allocs_before_failure.store(n < 0 ? -1 : n);
+    return TRS_OK;
+}
+
+int trs_debug_pointwise_grid_cap(int64_t blocks) {
+    if (blocks < 0) return set_error(TRS_E_INVALID_ARGUMENT, "negative grid cap");
+    trs::g_pw_grid_cap.store(blocks);
     return TRS_OK;
 }
 

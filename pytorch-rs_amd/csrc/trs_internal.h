@@ -1,6 +1,7 @@
 // trs_internal.h -- host-side internals shared by the libtrs_hip.so sources.
 #pragma once
 
+#include <atomic>
 #include <exception>
 #include <new>
 
@@ -15,6 +16,9 @@
 #include "trs_hip.h"
 
 namespace trs {
+
+// Pointwise grid cap set by trs_debug_pointwise_grid_cap (0: kMaxGrid).
+extern std::atomic<int64_t> g_pw_grid_cap;
 
 // Lanes per block of the one-dimensional helper kernels (fills, slice and
 // split-K sums, the per-element reduction).  Their bodies index with this

@@ -111,6 +111,7 @@ _SIGNATURES = {
     "trs_memcpy_h2d": ([c_void_p, c_void_p, c_size_t], c_int),
     "trs_memcpy_d2h": ([c_void_p, c_void_p, c_size_t], c_int),
     "trs_debug_fail_allocs_after": ([c_int64], c_int),
+    "trs_debug_pointwise_grid_cap": ([c_int64], c_int),
     "trs_memcpy_d2d": ([c_void_p, c_void_p, c_size_t], c_int),
     "trs_memset_zero": ([c_void_p, c_size_t], c_int),
     "trs_synchronize": ([], c_int),

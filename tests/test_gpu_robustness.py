@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import gpu_util as U
+from helpers import assert_bitwise_equal
 import oracle as O
 from trs_backend import abi
 from trs_backend.abi import DeviceArray, check, layout_of
@@ -230,3 +231,58 @@ def test_square_sum_backward_smoke_matches_closed_form_and_is_fast():
     want = 10 * float(((2.0 * values.astype(np.float64)) ** 2).sum())
     assert abs(checksum - want) <= 1e-9 * want
     assert statistics.median(samples) < 2e-3
+
+
+def test_grid_stride_loops_of_every_pointwise_kernel_bit_exact():
+    """Launches capped at a few blocks (trs_debug_pointwise_grid_cap), so each
+    block loops over many tiles: the flat kernels (contiguous, broadcast,
+    scalar tail), the rows kernel (vector on one-wave and wider blocks,
+    scalar), the transposing kernel (eager, and fused with a held operand
+    walked over outer tuples) and the generic kernel, each bit-exact against
+    the oracle.  Without the cap only launches of more than 2^22 blocks loop."""
+    rng = np.random.default_rng(77)
+
+    def bin_case(ash, ast, aoff, bsh, bst, boff, op=O.ADD):
+        a = U.special_mix(rng, O.storage_size(ash, ast, aoff))
+        b = U.special_mix(rng, O.storage_size(bsh, bst, boff))
+        osh, ost = O.binary_output_layout(ash, ast, bsh, bst)
+        want = O.binary(op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ost)
+        return (op, a, ash, ast, aoff, b, bsh, bst, boff, osh, ost), want
+
+    cs = O.contiguous_strides
+    cases = {
+        "flat_contig_tail": bin_case((100_003,), (1,), 0, (100_003,), (1,), 0),
+        "flat_broadcast": bin_case((50_000,), (1,), 0, (), (), 0, O.MUL),
+        "rows_one_wave": bin_case((300, 1028), cs((300, 1028)), 0, (1028,), (1,), 0),
+        "rows_wider_blocks": bin_case((6, 1, 516), cs((6, 1, 516)), 0, (1, 40, 516), cs((1, 40, 516)), 0),
+        "rows_scalar": bin_case((333, 37), cs((333, 37)), 0, (37,), (1,), 0),
+        "xpose": bin_case((300, 260), (1, 300), 0, (300, 260), cs((300, 260)), 0),
+        "generic": bin_case((5000,), (3,), 1, (5000,), (2,), 0),
+    }
+    B, M, N = 16, 96, 160
+    a = rng.standard_normal(B * N).astype(np.float32)
+    b = rng.standard_normal(M * N).astype(np.float32)
+    c = rng.standard_normal(B * N * M).astype(np.float32)
+    sh1, st1 = O.binary_output_layout((B, 1, N), (N, N, 1), (1, M, N), (M * N, N, 1))
+    s1 = O.binary(O.ADD, a, (B, 1, N), (N, N, 1), 0, b, (1, M, N), (M * N, N, 1), 0, sh1, st1)
+    sh2, st2 = O.binary_output_layout(sh1, st1, (B, M, N), (N * M, 1, M))
+    want_fused = O.binary(O.MUL, s1, sh1, st1, 0, c, (B, M, N), (N * M, 1, M), 0, sh2, st2)
+    kid = U.fusion_compile("in f32\nin f32\nin f32\nadd %0 %1\nmul %3 %2\nout %4\n")
+    for cap in (1, 7):
+        print(f"grid cap {cap}", flush=True)
+        try:
+            check(abi.lib.trs_debug_pointwise_grid_cap(cap))
+            for name, (args, want) in cases.items():
+                got = U.binary(*args)
+                try:
+                    assert_bitwise_equal(got, want)
+                except AssertionError as e:
+                    raise AssertionError(f"{name}, cap {cap}: {e}") from None
+            devs = [U.dev(x) for x in (a, b, c)]
+            out = U.out_buffer(B * M * N)
+            U.fusion_launch(kid, devs, [layout_of((B, 1, N)), layout_of((1, M, N)), layout_of((B, M, N), (N * M, 1, M))],
+                            out, layout_of((B, M, N)))
+            assert_bitwise_equal(out.to_numpy(count=B * M * N), want_fused)
+        finally:
+            check(abi.lib.trs_debug_pointwise_grid_cap(0))
+

@@ -191,3 +191,23 @@ def test_shape_mismatch_and_bad_arguments_are_errors():
     assert e.value.code == abi.TRS_E_SHAPE_MISMATCH
     with pytest.raises(abi.TrsError):
         plan(layout_of((3, 4)), out=layout_of((3, 4)), cu_count=0)
+
+
+def test_grid_cap_hook_bounds_every_pointwise_launch_and_resets():
+    # trs_debug_pointwise_grid_cap: the tests of the kernels' grid-stride
+    # loops plan launches with fewer blocks than tiles through it.
+    x, b = layout_of((4096, 4096)), layout_of((4096,))
+    c_mt = layout_of((64, 512, 1024), (512 * 1024, 1, 512))
+    try:
+        abi.check(abi.lib.trs_debug_pointwise_grid_cap(5))
+        assert plan(x, b, out=x).grid == 5
+        assert plan(layout_of((1 << 20,)), layout_of((1 << 20,)), out=layout_of((1 << 20,))).grid == 5
+        assert plan(layout_of((64, 512, 1024)), c_mt, out=layout_of((64, 512, 1024))).grid == 5
+        assert abi.lib.trs_debug_pointwise_grid_cap(-1) == abi.TRS_E_INVALID_ARGUMENT
+    finally:
+        abi.check(abi.lib.trs_debug_pointwise_grid_cap(0))
+    assert plan(x, b, out=x).grid == 4096 * 16
+    # one-shot up to 2^22 blocks: 2^30 contiguous floats on one-wave blocks
+    n = 1 << 30
+    assert plan(layout_of((n,)), layout_of((n,)), out=layout_of((n,))).grid == 1 << 22
+
