@@ -426,12 +426,16 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
     case PwVariant::Xpose: {
         // The scalar form reads every input plainly, so the streamed mask is
         // not part of its name (one kernel for every mask).
-        std::snprintf(name, sizeof name, "trs_fused_xpose_%c%d_%u_%u_%u_%u_%d_%u", pl.vec ? 'v' : 's', pl.rk,
-                      pl.trans, pl.held, pl.once, pl.xbc, pl.walk, pl.vec ? strm : 0u);
+        // Rank 3 fixes the t dim (0 or 1) too; other ranks read it at run time.
+        const int td = pl.rk == 3 ? (int)pl.g.tdim : -1;
+        std::snprintf(name, sizeof name, "trs_fused_xpose_%c%d_%u_%u_%u_%u_%d_%u%s%s", pl.vec ? 'v' : 's', pl.rk,
+                      pl.trans, pl.held, pl.once, pl.xbc, pl.walk, pl.vec ? strm : 0u,
+                      td == 0 ? "_t0" : td == 1 ? "_t1" : "", pl.plain ? "_p" : "");
         std::ostringstream b;
         b << "trs::pw_xpose_body<TrsFused, " << mask << ", " << (pl.vec ? "true" : "false") << ", " << kXposeWT << ", "
           << kXposeWX << ", " << pl.trans << "u, " << pl.held << "u, " << pl.once << "u, " << pl.walk << ", "
-          << (pl.vec ? strm : 0u) << "u, " << pl.xbc << "u, " << pl.rk << ">";
+          << (pl.vec ? strm : 0u) << "u, " << pl.xbc << "u, " << pl.rk << ", " << td << ", "
+          << (pl.plain ? "true" : "false") << ">";
         return get_spec_function(prog, dev, name, b.str(), 64 * kXposeWT * kXposeWX, fn);
     }
     case PwVariant::Generic: return get_function(&prog->base, dev, "trs_fused_generic", fn);
@@ -441,8 +445,8 @@ int resolve_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hip
 }
 
 // The kernel of a launch plan: looked up by the plan's signature (variant,
-// vector access, role masks, walk, streamed inputs, fixed rank), resolved on
-// a miss.
+// vector access, role masks, walk, streamed inputs, fixed rank and, at rank
+// 3, the transposing kernel's t dim and plain tiles), resolved on a miss.
 int get_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunction_t *fn) {
     // The streamed mask selects among vector kernels only (the scalar
     // transposing kernel ignores it).
@@ -450,7 +454,8 @@ int get_plan_function(Program *prog, DeviceState *dev, const PwPlan &pl, hipFunc
         (pl.variant == PwVariant::Xpose && !pl.vec) ? 0 : pl.g.streamed & ((1u << prog->nin) - 1u);
     const uint64_t key = (uint64_t)pl.variant | (uint64_t)pl.vec << 3 | (uint64_t)pl.contig << 4 |
                          (uint64_t)pl.walk << 5 | strm << 9 | (uint64_t)pl.trans << 17 | (uint64_t)pl.held << 25 |
-                         (uint64_t)pl.once << 33 | (uint64_t)pl.xbc << 41 | (uint64_t)pl.rk << 49;
+                         (uint64_t)pl.once << 33 | (uint64_t)pl.xbc << 41 | (uint64_t)pl.rk << 49 |
+                         (uint64_t)(pl.rk == 3 ? pl.g.tdim : 0) << 52 | (uint64_t)pl.plain << 53;
     {
         std::lock_guard<std::mutex> lock(prog->spec_mu);
         auto it = prog->by_plan[dev->index].find(key);

@@ -554,17 +554,25 @@ constexpr unsigned kRuntimeMask = 0xffffffffu;
 // element offset below 2^32, compiled with no run-time geometry branches, a
 // direct offset for the one outer dim and 32-bit offsets; RK = 0: any launch,
 // dispatched at run time with 64-bit offsets.  Tile indices below 2^32 split
-// into (tuple, t tile, x tile) by multiply-shift either way.
+// into (tuple, t tile, x tile) by multiply-shift either way.  TD (0 or 1,
+// with RK = 3): the t dim fixed at compile time, so the geometry fields a
+// block reads sit at constant offsets.  PLAIN (with RK = 3 and VEC): every
+// tile is interior and the tiles are taken in plain order, so no block tests
+// either.  Without both, the scalar loads of the geometry waited behind the
+// run-time t dim and the two tests: five rounds of them before a walking
+// block's first data load.
 template <class F, unsigned U8MASK, bool VEC, int WT, int WX, unsigned TRANS, unsigned HELD, unsigned ONCE, int NW,
-          unsigned STRM, unsigned XBC = kRuntimeMask, int RK = 0>
+          unsigned STRM, unsigned XBC = kRuntimeMask, int RK = 0, int TD = -1, bool PLAIN = false>
 __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const PwPtrs &p) {
+    static_assert(TD < 0 || (RK == 3 && TD <= 1), "a fixed t dim is 0 or 1 of a rank-3 launch");
+    static_assert(!PLAIN || (RK == 3 && VEC), "plain tiles are a vector rank-3 case");
     constexpr int NIN = F::NIN;
     constexpr int NIN1 = NIN > 0 ? NIN : 1;
     constexpr int NOUT = nout_of<F>();
     constexpr int NH = __builtin_popcount(HELD);
     constexpr int BT = 32 * WT, BX = 32 * WX;
     using Off = typename OffsetT<RK == 3>::type;
-    const int xd = RK == 3 ? 2 : g.rank - 1, td = g.tdim;
+    const int xd = RK == 3 ? 2 : g.rank - 1, td = TD >= 0 ? TD : g.tdim;
     const int64_t xs = g.size[xd], ts = g.size[td];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t ntiles = g.groups * g.chunks;
@@ -615,7 +623,7 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
             c = q;
             xt = q2;
             tt = rest - q2 * g.fdttiles.div;
-            if (g.skew) {  // xt + tt < xtiles * ttiles < 2^32
+            if (!PLAIN && g.skew) {  // xt + tt < xtiles * ttiles < 2^32
                 const uint32_t sk = q2 + (uint32_t)tt;
                 xt = sk - fast_div(sk, g.fdxtiles) * g.fdxtiles.div;
             }
@@ -771,7 +779,7 @@ __device__ __forceinline__ void pw_xpose_body(const F &f, const PwGeom &g, const
                 compute(v, ocur);
             }
         };
-        const bool fast = VEC && t0 + BT <= ts && x0 + BX <= xs;
+        const bool fast = PLAIN || (VEC && t0 + BT <= ts && x0 + BX <= xs);
         if (RK == 3 || g.rank == 3) {
             if (fast) run.template operator()<true, true>();
             else run.template operator()<false, true>();

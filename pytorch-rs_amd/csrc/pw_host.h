@@ -48,6 +48,9 @@ struct PwPlan {
     // Xpose: 3) of a launch with fewer than 2^32 tiles and every element
     // offset below 2^32.
     int rk = 0;
+    // Xpose with rk = 3 and vector access: every tile interior and taken in
+    // plain order (no diagonal skew), so the kernel tests neither per block.
+    bool plain = false;
     int nin = 0;
     int block = 256;  // lanes per block (kFlatBlock for the flat variants)
     int64_t grid = 0;
@@ -439,6 +442,8 @@ inline int plan_pointwise(const trs_layout *lo, float *out, int nin, const void 
             g.skew = xtiles > 1 && g.chunks > (int64_t)kXposeResident * cu_count;
             g.fdxtiles = make_fast_div(small ? (uint32_t)xtiles : 1u);
             plan->rk = rank == 3 && small && offsets_fit32() ? 3 : 0;
+            plan->plain = plan->rk == 3 && vec && !g.skew && size[tdim] % kXposeBT == 0 &&
+                          size[inner] % kXposeBX == 0;
             plan->grid = std::min<int64_t>(g.groups * g.chunks, want);
             return TRS_OK;
         }
