@@ -31,8 +31,9 @@ struct SkinnyPlan {
     // The VALU matrix-vector kernel (dot form, R <= 4): row_groups is then
     // the short rows it is compiled for (1, 2 or 4) and kc the k per wave.
     bool gemv = false;
-    // The VALU kernel for the other form (Y unit-stride along j, R <= 2):
-    // row_groups is then R and kc the rows of Y per slice.
+    // The VALU kernel for the other form (Y unit-stride along j, R <= 8):
+    // row_groups is then the rows it is compiled for (1, 2, 4 or 8, at
+    // least R) and kc the rows of Y per slice.
     bool axpy = false;
     // The MFMA kernel that streams Y through LDS (dot form, 5..32 short
     // rows): kLdsSkinnyCols columns per block, kc a multiple of 32.
@@ -47,7 +48,7 @@ struct SkinnyPlan {
 
 constexpr int64_t kSkinnyMaxRows = 32;
 constexpr int kSkinnyCols = 64;  // output columns per block
-constexpr int kAxpyCols = 128;   // output columns per block of the VALU axpy kernel
+constexpr int kAxpyCols = 256;   // output columns per block of the VALU axpy kernel
 constexpr int kLdsSkinnyCols = 64;  // output columns per block of the LDS-streaming kernel
 
 // Fills `plan` and returns true when the kernel takes the problem (R at

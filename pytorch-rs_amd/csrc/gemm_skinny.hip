@@ -371,76 +371,111 @@ __global__ void __launch_bounds__(256) gemv_f32_dot(SkinnyArgs g) {
 }
 
 // The other form (Y unit-stride along the output columns j, e.g. x @ W)
-// with one or two short rows, on the VALU: padded to 16 MFMA rows it does 8
-// to 16 times the arithmetic it needs, and its fragments read each row of Y
-// in 256-byte pieces.  A block owns kAxpyCols columns and one slice of kc
-// rows of Y: 32 lanes read one 512-byte run of a row (a float4 each) and the
-// block's 8 such lane groups take every 8th row of the slice, eight rows in
-// flight per lane, each with its X elements (read per row: the 32 lanes of
-// a group load the same address).  Each lane adds its rows in increasing k
-// with one fused multiply-add per element, the 8 lane groups' sums are added
-// in group order through LDS, and the slices in slice order.
-// Measured on the box for x[1,4096] @ W[4096,4096] with the slices added by
-// slice_sum: 16.7 us per call (14.8 us once the slice pass issued all its
-// loads at once) against 18.5 us for the MFMA form's 16 x 64 tiles; staging X in LDS (17.2 us), or that with the next rows' loads
-// issued before the current rows' FMAs (18.8 us), was slower.  With 8 short
-// rows this kernel took 21.9 us (X in LDS) or 32 us (X per row) against
-// 19.5 us on the MFMA tiles, so it takes at most 2.
-constexpr int kAxpyMaxRows = 2;
-constexpr int kAxpyRowGroups = 8;    // lane groups of 32 lanes, one row each
-constexpr int kAxpyInFlight = 8;     // rows of Y loaded before their FMAs per lane
+// with at most 8 short rows, on the VALU: padded to 16 MFMA rows it does 2
+// to 16 times the arithmetic it needs, and the MFMA fragments read each row
+// of Y in 256-byte pieces.  A block of kAxpyWaves waves owns kAxpyCols
+// columns (one float4 per lane, so one load instruction reads 1 KiB of a row
+// of Y) and one slice of kc rows of Y, which its waves split into
+// consecutive parts.  A wave loads kAxpyInFlight rows of Y before their
+// FMAs.  The X elements those rows need are the same for every lane of the
+// wave, so they come through scalar loads and cost no vector-memory
+// instruction.  Each lane adds its rows in increasing k with one fused
+// multiply-add per element, the waves' sums are added in wave order through
+// LDS, and the slices in slice order.  Measured on the box (a standalone
+// probe of this form with the inputs rotated past the cache, main pass
+// only): x[8,4096] @ W 12.5 us against 15.8 us for the MFMA form's 16 x 64
+// tiles; x[1,4096] @ W 11.2 us against 13.6 us for the former VALU form
+// (32-lane groups each reading one row's X through vector loads, at most 2
+// rows); 16 rows 15.8 us, no gain over the MFMA form, so it takes at most 8.
+// 8 waves per block and one block per CU measured fastest (256 blocks of
+// 4 waves, 512 blocks and 16 waves per block: 13.3-15.6 us).
+constexpr int kAxpyMaxRows = 8;
+constexpr int kAxpyWaves = 8;
+constexpr int kAxpyInFlight = 8;  // rows of Y loaded before their FMAs per lane
 
-template <int RR>
-__global__ void __launch_bounds__(256) gemv_f32_axpy(SkinnyArgs g) {
+//
+// X's offsets within a batch are 32-bit (the host takes this kernel only
+// when they fit), and XK1 (X unit-stride along k) lets a row's U values come
+// in one scalar load: with 64-bit offsets and a run-time k stride the 8-row
+// kernel spilled 24 scalar registers to VGPR lanes.
+template <int RR, bool XK1>
+__global__ void __launch_bounds__(64 * kAxpyWaves) gemv_f32_axpy(SkinnyArgs g) {
     constexpr int U = kAxpyInFlight;
-    constexpr int BR = kAxpyRowGroups * U;  // rows of a batch: U per lane group
-    const int lc = threadIdx.x & 31, lr = threadIdx.x >> 5;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const BlockCoords bc = block_coords(g);
     const int64_t jb = bc.jb, s = bc.s, b = bc.b;
     const int64_t j0 = jb * kAxpyCols;
-    const int64_t kbeg = s * g.kc, kend = std::min(g.K, kbeg + g.kc);
-    const int64_t nrows = kend - kbeg;
-    const int64_t j = j0 + 4 * lc;
+    const int64_t j = j0 + 4 * lane;
     const bool jin = j < g.L;  // L is a multiple of 4: a lane's float4 is all in or all out
-    const float *yp = g.y + b * g.by + kbeg * g.yl + (jin ? j : 0);
-    // This lane's X elements: row i's at xp[i] + r * xk for slice row r.
-    const float *xp[RR];
+    // The slice's rows, split among the waves in parts of a whole number of
+    // U-row steps (kc is a multiple of kAxpyWaves * U when K is split; an
+    // unsplit product has kc = K, any length, and its last parts are short
+    // or empty).
+    const int64_t kbeg = s * g.kc, kend = std::min(g.K, kbeg + g.kc);
+    const int64_t kw = ((g.kc + kAxpyWaves - 1) / kAxpyWaves + U - 1) / U * U;
+    const int64_t wbeg = std::min(kend, kbeg + wave * kw), wend = std::min(kend, wbeg + kw);
+    const float *yp = g.y + b * g.by + (jin ? j : 0);
+    const float *xb = g.x + b * g.bx;
+    // Row i's X at xb[xrow[i] + k * xk]; rows past R read row 0 into sums
+    // that are never stored.
+    const uint32_t xk = XK1 ? 1u : (uint32_t)g.xk;
+    uint32_t xrow[RR];
 #pragma unroll
-    for (int i = 0; i < RR; i++) xp[i] = g.x + b * g.bx + (i < g.R ? i : 0) * g.xi + kbeg * g.xk;
+    for (int i = 0; i < RR; i++) xrow[i] = (uint32_t)((i < g.R ? i : 0) * g.xi);
 
-    __shared__ float red[kAxpyRowGroups][RR][kAxpyCols];
     vf4 acc[RR];
 #pragma unroll
     for (int i = 0; i < RR; i++) acc[i] = (vf4){0.f, 0.f, 0.f, 0.f};
-    for (int64_t r0 = lr; r0 < nrows; r0 += BR) {
+    // A step: U rows of Y (lanes past L read column 0 of each, into sums
+    // that are never stored, so no load waits on a lane test), then every
+    // row's X values in one scalar load each, then the FMAs in increasing k,
+    // each row of Y used as soon as it lands.
+    int64_t k = wbeg;
+    for (; k + U <= wend; k += U) {
         vf4 v[U];
-        float xv[U][RR];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int64_t r = r0 + kAxpyRowGroups * u;
-            const bool in = r < nrows;
-            v[u] = (jin && in) ? load4_stream(yp + r * g.yl) : (vf4){0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < U; u++) v[u] = load4_stream(yp + (k + u) * g.yl);
+        const uint32_t xo = (uint32_t)k * xk;
+        float xv[RR][U];
 #pragma unroll
-            for (int i = 0; i < RR; i++) xv[u][i] = (in && i < g.R) ? xp[i][r * g.xk] : 0.f;
+        for (int i = 0; i < RR; i++) {
+            // Indexed from the row's pointer, so that with XK1 the U values
+            // are known to be adjacent and come in one scalar load (offsets
+            // summed in 32 bits could wrap, which kept them apart).
+            const float *xr = xb + (xrow[i] + xo);
+#pragma unroll
+            for (int u = 0; u < U; u++) xv[i][u] = xr[XK1 ? u : (int64_t)u * xk];
         }
 #pragma unroll
         for (int u = 0; u < U; u++)
 #pragma unroll
             for (int i = 0; i < RR; i++)
 #pragma unroll
-                for (int c = 0; c < 4; c++) acc[i][c] = __builtin_fmaf(xv[u][i], v[u][c], acc[i][c]);
+                for (int c = 0; c < 4; c++) acc[i][c] = __builtin_fmaf(xv[i][u], v[u][c], acc[i][c]);
     }
+    for (; k < wend; k++) {
+        const vf4 v = load4_stream(yp + k * g.yl);
+#pragma unroll
+        for (int i = 0; i < RR; i++) {
+            const float xv = xb[xrow[i] + (uint32_t)k * xk];
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[i][c] = __builtin_fmaf(xv, v[c], acc[i][c]);
+        }
+    }
+
+    __shared__ float red[kAxpyWaves][RR][kAxpyCols];
 #pragma unroll
     for (int i = 0; i < RR; i++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) red[lr][i][4 * lc + c] = acc[i][c];
+        for (int c = 0; c < 4; c++) red[wave][i][4 * lane + c] = acc[i][c];
     __syncthreads();
     float *O = g.o + b * g.bo + s * g.os;
-    for (int q = threadIdx.x; q < RR * kAxpyCols; q += 256) {
+    for (int q = threadIdx.x; q < RR * kAxpyCols; q += 64 * kAxpyWaves) {
         const int i = q / kAxpyCols, cc = q - i * kAxpyCols;
         float r = red[0][i][cc];
 #pragma unroll
-        for (int w = 1; w < kAxpyRowGroups; w++) r += red[w][i][cc];
+        for (int w = 1; w < kAxpyWaves; w++) r += red[w][i][cc];
         if (i < g.R && j0 + cc < g.L) O[i * g.oi + (j0 + cc) * g.oj] = r;
     }
 }
@@ -633,23 +668,27 @@ bool plan_skinny(const SkinnyProblem &p, int cu_count, SkinnyPlan *plan) {
     }
     // The VALU axpy kernel: Y unit-stride along j and read as float4, at most
     // kAxpyMaxRows short rows, and K deep enough for a 64-row slice per
-    // block.  About 2
-    // blocks per CU (the probe's fastest grid: 512 blocks of 512 KiB-slices
-    // of 4 KiB rows ran 12.0 us where 256 blocks ran 16.3 us), slices of a
-    // multiple of 64 rows, and the partial products' traffic (written and
-    // read back) at most 1/8 of Y's.
-    if (!p.dot && pl.yvec && p.R <= kAxpyMaxRows && p.L % 4 == 0 && p.K >= 64) {
+    // block, X unit-stride along k when it has more than 2 rows (a strided
+    // X's values load one by one, and 4 or 8 rows of them spilled scalar
+    // registers), and X's offsets within a batch below 2^31.  About one block (8
+    // waves) per CU, slices of a multiple of kAxpyWaves * kAxpyInFlight
+    // rows, and the partial products' traffic (written and read back) at
+    // most 1/8 of Y's.  Compiled for 1, 2, 4 or 8 rows; R rounds up to the
+    // next.
+    if (!p.dot && pl.yvec && p.R <= kAxpyMaxRows && p.L % 4 == 0 && p.K >= 64 && (p.xk == 1 || p.R <= 2) &&
+        (p.R - 1) * p.xi + (p.K - 1) * p.xk < ((int64_t)1 << 31)) {
+        constexpr int64_t kStep = kAxpyWaves * kAxpyInFlight;
         const int64_t jb = (p.L + kAxpyCols - 1) / kAxpyCols;
         const int64_t ab = jb * p.batch;
-        const int64_t want = (2 * (int64_t)cu_count + ab - 1) / ab;
-        const int64_t cap = std::max<int64_t>(1, std::min(p.K / 64, p.K / (16 * p.R)));
+        const int64_t want = ((int64_t)cu_count + ab - 1) / ab;
+        const int64_t cap = std::max<int64_t>(1, std::min(p.K / kStep, p.K / (16 * p.R)));
         int64_t S = std::clamp<int64_t>(want, 1, cap);
         int64_t kc = (p.K + S - 1) / S;
-        kc = (kc + 63) / 64 * 64;
+        kc = (kc + kStep - 1) / kStep * kStep;
         S = (p.K + kc - 1) / kc;
         if (ab * S <= INT32_MAX && jb <= INT32_MAX) {
             pl.axpy = true;
-            pl.row_groups = (int)p.R;
+            pl.row_groups = p.R <= 1 ? 1 : p.R <= 2 ? 2 : p.R <= 4 ? 4 : 8;
             pl.kc = kc;
             pl.splits = S;
             pl.blocks = ab * S;
@@ -780,8 +819,15 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
     const dim3 grid((unsigned)((int64_t)g.jblocks * S * p.batch));
     int rc = TRS_OK;
     if (plan.axpy) {
-        if (plan.row_groups == 1) hipLaunchKernelGGL((gemv_f32_axpy<1>), grid, dim3(256), 0, s, g);
-        else hipLaunchKernelGGL((gemv_f32_axpy<2>), grid, dim3(256), 0, s, g);
+        const dim3 block(64 * kAxpyWaves);
+        auto axpy = [&]<bool XK1>() {
+            if (plan.row_groups == 1) hipLaunchKernelGGL((gemv_f32_axpy<1, XK1>), grid, block, 0, s, g);
+            else if (plan.row_groups == 2) hipLaunchKernelGGL((gemv_f32_axpy<2, XK1>), grid, block, 0, s, g);
+            else if (plan.row_groups == 4) hipLaunchKernelGGL((gemv_f32_axpy<4, XK1>), grid, block, 0, s, g);
+            else hipLaunchKernelGGL((gemv_f32_axpy<8, XK1>), grid, block, 0, s, g);
+        };
+        if (p.xk == 1) axpy.template operator()<true>();
+        else axpy.template operator()<false>();
         TRS_LAUNCH_CHECK("axpy gemv launch");
     } else if (plan.lds) {
         if (plan.row_groups == 1) hipLaunchKernelGGL((gemm_f32_skinny_lds<1>), grid, dim3(256), 0, s, g);

@@ -75,7 +75,7 @@ SHAPES = [
 def test_short_sides_plan_the_skinny_kernel():
     """Rows of the short side are padded to 16 or 32 by 64 columns a block;
     33 rows go to the square tiles; K is split to fill the device.  x @ W
-    with at most 2 short rows runs the VALU axpy kernel instead (below)."""
+    with at most 8 short rows runs the VALU axpy kernel instead (below)."""
     plain = lambda m, k, n: _plan((m, k), (k, 1), 0, (k, n), (n, 1), 0)
     assert plain(9, 4096, 4096)[:2] == (16, 64) and plain(9, 4096, 4096)[3] > 1
     assert plain(4096, 100, 1)[:2] == (64, 16)
@@ -185,22 +185,29 @@ def test_dot_form_with_four_rows_or_fewer_plans_the_matrix_vector_kernel():
     assert _plan((4096, 4096), (4096, 1), 0, (4096, 1), (1, 1), 0)[:2] == (4, 1)  # W @ x
 
 
-def test_axpy_form_with_two_rows_or_fewer_plans_the_valu_kernel():
-    """x @ W (W unit-stride along the output columns) with one or two short
+def test_axpy_form_with_eight_rows_or_fewer_plans_the_valu_kernel():
+    """x @ W (W unit-stride along the output columns) with at most 8 short
     rows, the long side a multiple of 4 and K >= 64 runs the VALU axpy
-    kernel: the plan reports its rows by the 128 columns a block takes, and
-    slices of a multiple of 64 rows for about 2 blocks per CU."""
+    kernel, compiled for 1, 2, 4 or 8 rows: the plan reports those rows by
+    the 256 columns a block takes, and slices of a multiple of 64 rows for
+    about one block per CU."""
     plain = lambda m, k, n: _plan((m, k), (k, 1), 0, (k, n), (n, 1), 0)
     tm, tn, tk, s, blocks = plain(1, 4096, 4096)
-    assert (tm, tn) == (1, 128) and tk % 64 == 0 and s * tk >= 4096 > (s - 1) * tk and blocks == 32 * s
-    assert 256 <= blocks <= 1024
-    assert plain(2, 4096, 4096)[:2] == (2, 128)
-    assert plain(3, 4096, 4096)[:2] == (16, 64)               # three rows: the MFMA kernel
-    assert plain(1, 100, 4096)[:4] == (1, 128, 128, 1)        # one slice
+    assert (tm, tn) == (1, 256) and tk % 64 == 0 and s * tk >= 4096 > (s - 1) * tk and blocks == 16 * s
+    assert 128 <= blocks <= 512
+    assert plain(2, 4096, 4096)[:2] == (2, 256)
+    assert plain(3, 4096, 4096)[:2] == (4, 256)                # three rows: the 4-row kernel
+    assert plain(5, 4096, 4096)[:2] == (8, 256)
+    assert plain(8, 4096, 4096)[:2] == (8, 256)
+    assert plain(9, 4096, 4096)[:2] == (16, 64)               # nine rows: the MFMA kernel
+    assert plain(1, 100, 4096)[:4] == (1, 256, 128, 1)        # one slice
     assert plain(1, 63, 4096)[:2] == (16, 64)                 # K < 64: the MFMA kernel
     assert plain(1, 4096, 4098)[:2] == (16, 64)               # long side not a multiple of 4
+    # X strided along k (A read transposed): the VALU kernel up to 2 rows only
+    at = lambda m, k, n: _plan((m, k), (1, m), 0, (k, n), (n, 1), 0)
+    assert at(2, 4096, 4096)[:2] == (2, 256) and at(3, 4096, 4096)[:2] == (16, 64)
     # W^T @ x^T: the short side is N and A is read transposed (unit stride along M).
-    assert _plan((4096, 4096), (1, 4096), 0, (4096, 1), (1, 1), 0)[:2] == (128, 1)
+    assert _plan((4096, 4096), (1, 4096), 0, (4096, 1), (1, 1), 0)[:2] == (256, 1)
 
 
 @pytest.mark.parametrize("m,k,n,ta,tb,batch", [
@@ -208,15 +215,21 @@ def test_axpy_form_with_two_rows_or_fewer_plans_the_valu_kernel():
     (2, 257, 260, False, False, 0), (1, 8192, 132, False, False, 0), (2, 64, 128, False, False, 0),
     (1, 100, 8, False, False, 0), (1, 513, 2048, False, False, 3), (2, 1000, 644, False, False, 5),
     (4096, 4096, 1, True, False, 0), (1000, 3000, 2, True, False, 0), (2048, 300, 2, True, True, 2),
+    # 3..8 rows (the 4- and 8-row kernels): ragged K and long sides, batches,
+    # and the W^T @ x^T form; X strided along k (A read transposed) with 2 rows
+    (3, 4100, 1000, False, False, 0), (5, 777, 4100, False, False, 0), (8, 4096, 4096, False, False, 0),
+    (7, 257, 260, False, False, 0), (8, 1000, 644, False, False, 5), (6, 64, 128, False, False, 0),
+    (2, 1000, 300, True, False, 0), (2, 3000, 2052, True, False, 2), (4096, 4096, 8, True, True, 0),
+    (1000, 3000, 5, True, True, 2),
 ])
 def test_axpy_kernel_exact(m, k, n, ta, tb, batch):
     """The VALU axpy kernel on ragged K (slices that end early), long sides
-    that leave a block's columns partly past the edge, one or two short
-    rows, either side short (x @ W and W^T @ x^T) and batches: exact on small
-    integers."""
+    that leave a block's columns partly past the edge, 1 to 8 short rows,
+    either side short (x @ W and W^T @ x^T), X strided along k, and batches:
+    exact on small integers."""
     rng = np.random.default_rng(m + 5 * k + 11 * n + batch)
     a, b, sa, la, sb, lb = _operands(rng, m, k, n, ta, tb, batch=batch)
-    assert _plan(*la, *lb)[1 if m <= n else 0] == 128, "not the axpy kernel"
+    assert _plan(*la, *lb)[1 if m <= n else 0] == 256, "not the axpy kernel"
     got = U.matmul(sa, *la, sb, *lb)
     want = np.matmul(a.astype(np.int64), b.astype(np.int64)).astype(np.float32)
     assert np.array_equal(got.reshape(want.shape), want)
@@ -260,7 +273,7 @@ def test_lds_streaming_skinny_kernel_plan_and_normal_inputs():
 
 def test_axpy_kernel_normal_inputs_within_tolerance():
     rng = np.random.default_rng(31)
-    for m, k, n in [(1, 4096, 4096), (2, 4096, 4096), (2, 3000, 1000)]:
+    for m, k, n in [(1, 4096, 4096), (2, 4096, 4096), (2, 3000, 1000), (8, 4096, 4096), (5, 3000, 1000)]:
         a, b, sa, la, sb, lb = _operands(rng, m, k, n, False, False, ints=False)
         got = U.matmul(sa, *la, sb, *lb)
         want = O.matmul(sa, *la, sb, *lb).reshape(m, n)
