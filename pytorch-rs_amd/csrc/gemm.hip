@@ -828,22 +828,17 @@ __global__ void __launch_bounds__(BM * 4, 2) gemm_f32_mfma_lds_small(GemmArgs ar
     constexpr int ASIZE = LA::kFloats, BSIZE = LB::kFloats;
     __shared__ __attribute__((aligned(16))) float lds[2 * (ASIZE + BSIZE)];
 
-    const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
-    int64_t bid = blockIdx.x;
+    // The block's tile, decoded in 32 bits: the grid is one block per tile
+    // and below 2^23 blocks (a dispatch counts under 2^32 lanes), so every
+    // count fits.  In 64 bits the four divisions by run-time counts were
+    // software loops, some 600 instructions before a block's first load.
+    uint32_t bid = blockIdx.x;
     if (args.xcd_remap) {
-        const int64_t total = tiles * args.batch;
-        const int64_t per_xcd = total / kXcds;
+        const uint32_t per_xcd = (uint32_t)args.tiles_m * (uint32_t)args.tiles_n * (uint32_t)args.batch / kXcds;
         bid = (bid % kXcds) * per_xcd + bid / kXcds;
     }
-    const int64_t batch_idx = bid / tiles;
-    int64_t t = bid - batch_idx * tiles;
-    const int64_t group_span = (int64_t)kGroupM * args.tiles_n;
-    const int64_t group = t / group_span;
-    const int64_t first_m = group * kGroupM;
-    const int64_t gm = std::min<int64_t>(args.tiles_m - first_m, kGroupM);
-    const int64_t within = t - group * group_span;
-    const int64_t tile_m = first_m + within % gm;
-    const int64_t tile_n = within / gm;
+    const TileCoord tc = decode_tile32(args, bid);
+    const int64_t batch_idx = tc.batch, tile_m = tc.m, tile_n = tc.n;
 
     const int64_t Kb = args.ktotal ? std::min<int64_t>(args.K, args.ktotal - batch_idx * args.K) : args.K;
     const float *A = args.a + batch_idx * args.bsa;
