@@ -584,8 +584,7 @@ __device__ __forceinline__ void lds_tile_slices(const GemmArgs &args, float *lds
     // Slices of BK MFMA steps from one LDS buffer.
     auto slice_mfma = [&](const float *As) {
         const float *Bs = As + ASIZE;
-#pragma unroll 1
-        for (int kg = 0; kg < BK; kg += 16) {
+        auto kgroup = [&](int kg) {
             const int k4 = kg + 4 * fk;
             const int chunk = kg / 4 + fk;
             vf4 a4[TM], b4[TN];
@@ -614,6 +613,17 @@ __device__ __forceinline__ void lds_tile_slices(const GemmArgs &args, float *lds
                     for (int j = 0; j < TN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
+        };
+        // The k groups of a slice unrolled, so the next group's fragment reads
+        // can be issued among this group's MFMAs (0.3% on the MLP step and at
+        // 4096^3); the stream-K form with B transposed and ragged M or N then
+        // spills, so it keeps the rolled loop.
+        if constexpr (TB && EDGE) {
+#pragma unroll 1
+            for (int kg = 0; kg < BK; kg += 16) kgroup(kg);
+        } else {
+#pragma unroll
+            for (int kg = 0; kg < BK; kg += 16) kgroup(kg);
         }
     };
     // Whole slices load straight into LDS, each prefetched during the one
