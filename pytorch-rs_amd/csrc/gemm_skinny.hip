@@ -393,11 +393,11 @@ constexpr int kAxpyMaxRows = 8;
 constexpr int kAxpyWaves = 8;
 constexpr int kAxpyInFlight = 8;  // rows of Y loaded before their FMAs per lane
 
-//
-// X's offsets within a batch are 32-bit (the host takes this kernel only
-// when they fit), and XK1 (X unit-stride along k) lets a row's U values come
-// in one scalar load: with 64-bit offsets and a run-time k stride the 8-row
-// kernel spilled 24 scalar registers to VGPR lanes.
+// RR: the rows compiled for (1, 2, 4 or 8, at least R).  X's offsets within
+// a batch are 32-bit (the host takes this kernel only when they fit), and
+// XK1 (X unit-stride along k) lets a row's U values come in one scalar load:
+// with 64-bit offsets and a run-time k stride the 8-row kernel spilled 24
+// scalar registers to VGPR lanes.
 template <int RR, bool XK1>
 __global__ void __launch_bounds__(64 * kAxpyWaves) gemv_f32_axpy(SkinnyArgs g) {
     constexpr int U = kAxpyInFlight;
