@@ -401,6 +401,9 @@ constexpr int kAxpyInFlight = 8;  // rows of Y loaded before their FMAs per lane
 template <int RR, bool XK1>
 __global__ void __launch_bounds__(64 * kAxpyWaves) gemv_f32_axpy(SkinnyArgs g) {
     constexpr int U = kAxpyInFlight;
+    // X values held in scalar registers at once: 8 rows x 8 steps (64) left
+    // too few for the addresses and spilled 17 to VGPR lanes.
+    constexpr int UH = RR * U > 32 ? U / 2 : U;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const BlockCoords bc = block_coords(g);
@@ -437,22 +440,28 @@ __global__ void __launch_bounds__(64 * kAxpyWaves) gemv_f32_axpy(SkinnyArgs g) {
 #pragma unroll
         for (int u = 0; u < U; u++) v[u] = load4_stream(yp + (k + u) * g.yl);
         const uint32_t xo = (uint32_t)k * xk;
-        float xv[RR][U];
 #pragma unroll
-        for (int i = 0; i < RR; i++) {
-            // Indexed from the row's pointer, so that with XK1 the U values
-            // are known to be adjacent and come in one scalar load (offsets
-            // summed in 32 bits could wrap, which kept them apart).
-            const float *xr = xb + (xrow[i] + xo);
+        for (int h = 0; h < U; h += UH) {
+            float xv[RR][UH];
 #pragma unroll
-            for (int u = 0; u < U; u++) xv[i][u] = xr[XK1 ? u : (int64_t)u * xk];
+            for (int i = 0; i < RR; i++) {
+                // Indexed from the row's pointer, so that with XK1 the
+                // values are known to be adjacent and come in one scalar
+                // load (offsets summed in 32 bits could wrap, which kept
+                // them apart).
+                const float *xr = xb + (xrow[i] + xo);
+#pragma unroll
+                for (int u = 0; u < UH; u++) xv[i][u] = xr[XK1 ? h + u : (int64_t)(h + u) * xk];
+            }
+#pragma unroll
+            for (int u = 0; u < UH; u++)
+#pragma unroll
+                for (int i = 0; i < RR; i++)
+#pragma unroll
+                    for (int c = 0; c < 4; c++) acc[i][c] = __builtin_fmaf(xv[i][u], v[h + u][c], acc[i][c]);
+            // Keeps the scheduler from hoisting the next half's scalar loads.
+            if constexpr (UH < U) __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (int u = 0; u < U; u++)
-#pragma unroll
-            for (int i = 0; i < RR; i++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) acc[i][c] = __builtin_fmaf(xv[i][u], v[u][c], acc[i][c]);
     }
     for (; k < wend; k++) {
         const vf4 v = load4_stream(yp + k * g.yl);
