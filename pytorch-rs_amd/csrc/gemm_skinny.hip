@@ -829,11 +829,16 @@ int run_skinny(const SkinnyProblem &p, const SkinnyPlan &plan, hipStream_t s) {
     int rc = TRS_OK;
     if (plan.axpy) {
         const dim3 block(64 * kAxpyWaves);
+        // X with a k stride other than 1 is planned here only for R <= 2, so
+        // only those row counts are compiled without XK1.
+        if (p.xk != 1 && plan.row_groups > 2) return TRS_E_INVALID_ARGUMENT;
         auto axpy = [&]<bool XK1>() {
             if (plan.row_groups == 1) hipLaunchKernelGGL((gemv_f32_axpy<1, XK1>), grid, block, 0, s, g);
-            else if (plan.row_groups == 2) hipLaunchKernelGGL((gemv_f32_axpy<2, XK1>), grid, block, 0, s, g);
-            else if (plan.row_groups == 4) hipLaunchKernelGGL((gemv_f32_axpy<4, XK1>), grid, block, 0, s, g);
-            else hipLaunchKernelGGL((gemv_f32_axpy<8, XK1>), grid, block, 0, s, g);
+            else if (!XK1 || plan.row_groups == 2) hipLaunchKernelGGL((gemv_f32_axpy<2, XK1>), grid, block, 0, s, g);
+            else if constexpr (XK1) {
+                if (plan.row_groups == 4) hipLaunchKernelGGL((gemv_f32_axpy<4, true>), grid, block, 0, s, g);
+                else hipLaunchKernelGGL((gemv_f32_axpy<8, true>), grid, block, 0, s, g);
+            }
         };
         if (p.xk == 1) axpy.template operator()<true>();
         else axpy.template operator()<false>();
